@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""bench.py — DenseCore's quantized mul_mat hot path on one MI355X.
+
+A step is one pass of the hot path over one batch: quantize X (the
+vec_dot_type from_float) + the mul_mat kernel, Y[M, N] = W[N, K] . Xq[M, K]^T,
+on inputs already resident in HBM. Steps cycle through enough copies of W to
+exceed the 256 MB Infinity Cache, so every step streams its weights from HBM.
+Steps are captured in one HIP graph (torch.cuda.CUDAGraph around the C ABI
+calls) and replayed, so host launch overhead does not enter GPU time.
+
+Printed: one JSON line. `value` is the headline configuration's
+(Q4_K GEMV, M = 1) weight GB/s over whole steps; every
+configuration is listed under "configs" with its kernel-only rate and roofline
+fraction. The CPU baseline is the oracle's restatement of the reference CPU path
+(quantize once, row-partitioned vec_dot, threaded), timed on this host.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "quant mul_mat: weight GB/s at M=1, int8 TOPS at M=2048; % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POP/s
+HEADLINE = 2
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--rotate-mb", type=int, default=1024, help="total bytes of W copies cycled through")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--replays", type=int, default=3)
+    return ap.parse_args()
+
+
+def make_config_inputs(cfg, dev):
+    """W fp32 N(0, w_std) quantized on the GPU (dcq_quantize_weights) and X fp32 N(0, 1)."""
+    import torch
+    import densecore_amd as dc
+    from densecore_amd import synth
+    w = synth.normal(cfg.N * cfg.K, cfg.w_seed, 0.0, cfg.w_std).reshape(cfg.N, cfg.K)
+    x = synth.normal(cfg.M * cfg.K, cfg.x_seed).reshape(cfg.M, cfg.K)
+    if cfg.n_outliers:
+        for m in range(cfg.M):
+            synth.set_outliers(x[m], cfg.n_outliers, cfg.outlier_value, cfg.x_seed + 17 * m)
+    wd = torch.from_numpy(w).to(dev)
+    wq = dc.quantize_weights(cfg.wtype, wd)
+    del wd
+    xd = torch.from_numpy(x).to(dev)
+    torch.cuda.synchronize()
+    return wq, xd, {"w_f32": synth.digest(w), "x_f32": synth.digest(x)}
+
+
+def time_graph(fn_steps, steps, warmup, replays):
+    """Capture `steps` calls into one graph; return (mean ms per step, stream)."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(warmup):  # eager warmup (also loads the kernels)
+            fn_steps(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(steps):
+            fn_steps(i)
+    torch.cuda.synchronize()
+    g.replay()  # warm replay
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / steps)
+    del g
+    return float(np.median(times))
+
+
+def bench_config(cfg, args, dev):
+    import torch
+    import densecore_amd as dc
+    wq, x, digests = make_config_inputs(cfg, dev)
+    rb = dc.row_size(cfg.wtype, cfg.K)
+    wbytes = cfg.N * rb
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    big = torch.empty((copies, cfg.N, rb), dtype=torch.uint8, device=dev)
+    for r in range(copies):
+        big[r].copy_(wq)
+    ws = torch.empty(dc.mul_mat_workspace_size(cfg.wtype, cfg.M, cfg.K), dtype=torch.uint8, device=dev)
+    y = torch.empty((cfg.M, cfg.N), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        dc.mul_mat(cfg.wtype, big[i % copies], cfg.N, cfg.K, x, y=y, workspace=ws,
+                   stream=torch.cuda.current_stream().cuda_stream)
+
+    def kernel_only(i):
+        dc.mul_mat_q(cfg.wtype, big[i % copies], cfg.N, cfg.K, ws, cfg.M, y=y,
+                     stream=torch.cuda.current_stream().cuda_stream)
+
+    step_ms = time_graph(step, args.steps, args.warmup, args.replays)
+    dc.quantize_src1(cfg.wtype, x, ws)
+    torch.cuda.synchronize()
+    kern_ms = time_graph(kernel_only, args.steps, args.warmup, args.replays)
+
+    xq_bytes = dc.mul_mat_workspace_size(cfg.wtype, cfg.M, cfg.K)
+    ops = 2.0 * cfg.M * cfg.N * cfg.K
+    boundary = wbytes + cfg.M * cfg.K * 4 + cfg.M * cfg.N * 4
+    kernel_name = "gemv_kernel" if cfg.M <= 8 else "mmq_kernel"
+    out = {
+        "config": cfg.index, "name": cfg.name, "type": dc.TYPE_NAMES[cfg.wtype], "M": cfg.M, "N": cfg.N, "K": cfg.K,
+        "w_bytes": wbytes, "w_copies": copies, "step_us": step_ms * 1e3, "kernel_us": kern_ms * 1e3,
+        "kernel": kernel_name, "digests": digests,
+    }
+    if cfg.bound == "hbm":
+        achieved = wbytes / (kern_ms * 1e-3) / 1e9
+        out.update({
+            "weight_GBps_step": wbytes / (step_ms * 1e-3) / 1e9,
+            "weight_GBps_kernel": achieved,
+            "boundary_GBps_step": boundary / (step_ms * 1e-3) / 1e9,
+            "TOPS_kernel": ops / (kern_ms * 1e-3) / 1e12,
+            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                         "algorithmic_bytes_per_launch": wbytes},
+        })
+    else:
+        achieved = ops / (kern_ms * 1e-3) / 1e12
+        out.update({
+            "TOPS_step": ops / (step_ms * 1e-3) / 1e12,
+            "TOPS_kernel": achieved,
+            "weight_GBps_step": wbytes / (step_ms * 1e-3) / 1e9,
+            "roofline": {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                         "frac": achieved / INT8_PEAK_TOPS, "traffic": None,
+                         "algorithmic_ops_per_launch": ops},
+        })
+    out["xq_workspace_bytes"] = xq_bytes
+    del big, ws, y, x, wq
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(cfg, seconds, threads):
+    """The oracle's restatement of the reference CPU path on this host's cores, bounded sample."""
+    from oracle import oracle as O
+    from densecore_amd import synth
+    w = synth.normal(cfg.N * cfg.K, cfg.w_seed, 0.0, cfg.w_std).reshape(cfg.N, cfg.K)
+    wq = O.quantize_matrix(cfg.wtype, w)
+    x = synth.normal(cfg.M * cfg.K, cfg.x_seed).reshape(cfg.M, cfg.K)
+    nt = threads or min(16, os.cpu_count() or 1)
+    O.mul_mat(cfg.wtype, wq, x, nthreads=nt, want_l1=False)  # warm
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        O.mul_mat(cfg.wtype, wq, x, nthreads=nt, want_l1=False)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    wbytes = wq.nbytes
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": wbytes / med / 1e9, "unit": "GB/s", "cores": nt, "kind": "port",
+            "sample": f"config {cfg.index} full ({cfg.M}x{cfg.N}x{cfg.K} {cfg.name}): quantize X once + "
+                      f"row-partitioned scalar vec_dot (oracle/dcq_oracle.c), {len(times)} runs over "
+                      f"{sum(times):.1f} s, median {med * 1e3:.2f} ms",
+            "host_cpu": model, "nproc": os.cpu_count()}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "Run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+    import densecore_amd as dc
+    dc.lib()
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(0)
+    wanted = [int(c) for c in args.configs.split(",") if c.strip()]
+    results = []
+    for c in dc.CONFIGS:
+        if c.index in wanted:
+            r = bench_config(c, args, dev)
+            results.append(r)
+            print(f"# config {c.index} {c.name}: step {r['step_us']:.2f} us, kernel {r['kernel_us']:.2f} us, "
+                  f"roofline {r['roofline']['achieved']:.1f} {r['roofline']['unit']} "
+                  f"({100 * r['roofline']['frac']:.1f} %)", file=sys.stderr, flush=True)
+    head = next((r for r in results if r["config"] == HEADLINE), results[0])
+    hcfg = dc.by_index(head["config"])
+    line = {
+        "metric": METRIC,
+        "value": head.get("weight_GBps_step", head.get("TOPS_step")),
+        "unit": "GB/s" if hcfg.bound == "hbm" else "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["step_us"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded SplitMix64/Box-Muller; W quantized on the GPU by dcq_quantize_weights)",
+        "config": {"workload": f"config {hcfg.index}: {dc.TYPE_NAMES[hcfg.wtype]} mul_mat M={hcfg.M} "
+                               f"N={hcfg.N} K={hcfg.K} ({hcfg.name}), quantize + kernel per step, "
+                               f"W rotated over {head['w_copies']} copies",
+                   "M": hcfg.M, "N": hcfg.N, "K": hcfg.K, "type": dc.TYPE_NAMES[hcfg.wtype]},
+        "roofline": head["roofline"],
+        "device": props.name, "gcn_arch": getattr(props, "gcnArchName", ""), "host": platform.node(),
+        "configs": results,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(hcfg, args.cpu_seconds, args.cpu_threads)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

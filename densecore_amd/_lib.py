@@ -1,0 +1,208 @@
+"""ctypes binding of libdcq (include/dcq.h) with torch-tensor conveniences.
+
+Every function maps 1:1 onto an extern "C" entry point. Non-zero status codes
+raise DcqError carrying dcq_status_string(). Device tensors are passed as raw
+pointers; the stream is torch's current stream unless one is given.
+"""
+import ctypes
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libdcq.so")
+SYMBOLS = [
+    "dcq_version", "dcq_status_string", "dcq_block_size", "dcq_type_size", "dcq_row_size", "dcq_vec_dot_type",
+    "dcq_supports_mul_mat", "dcq_quantize_rows", "dcq_mul_mat_workspace_size", "dcq_mul_mat", "dcq_mul_mat_ex",
+    "dcq_block_sums_per_row", "dcq_dot_rows", "dcq_quantize_weights", "dcq_dequantize_rows",
+    "dcq_quantize_src1", "dcq_mul_mat_q",
+]
+
+PATH_AUTO, PATH_GEMV, PATH_MMQ = 0, 1, 2
+
+_lib = None
+
+
+class DcqError(RuntimeError):
+    def __init__(self, fn, status):
+        self.status = status
+        super().__init__(f"{fn} failed: status {status} ({status_string(status)})")
+
+
+def build():
+    """Compile libdcq.so for gfx950 in-tree (hipcc cross-compiles without a GPU)."""
+    subprocess.check_call(["make", "-s", "-j8", "-C", os.path.join(HERE, "csrc")])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with densecore_amd.build() "
+                              "(there is no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        i64, i32, vp, sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+        sig = {
+            "dcq_version": (ctypes.c_char_p, []),
+            "dcq_status_string": (ctypes.c_char_p, [i32]),
+            "dcq_block_size": (i64, [i32]),
+            "dcq_type_size": (i64, [i32]),
+            "dcq_row_size": (sz, [i32, i64]),
+            "dcq_vec_dot_type": (i32, [i32]),
+            "dcq_supports_mul_mat": (i32, [i32, i32, i32]),
+            "dcq_quantize_rows": (i32, [i32, vp, i64, i64, sz, vp, vp]),
+            "dcq_mul_mat_workspace_size": (sz, [i32, i64, i64]),
+            "dcq_mul_mat": (i32, [i32, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp, sz, vp]),
+            "dcq_mul_mat_ex": (i32, [i32, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp, sz, i32, vp, vp]),
+            "dcq_block_sums_per_row": (i64, [i32, i64]),
+            "dcq_dot_rows": (i32, [i32, vp, sz, vp, i64, vp, i64, i64, vp]),
+            "dcq_quantize_weights": (i32, [i32, vp, i64, i64, vp, vp]),
+            "dcq_dequantize_rows": (i32, [i32, vp, i64, i64, sz, vp, vp]),
+            "dcq_quantize_src1": (i32, [i32, vp, i64, i64, sz, vp, sz, vp]),
+            "dcq_mul_mat_q": (i32, [i32, vp, i64, i64, sz, vp, sz, i64, vp, sz, i32, vp]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def status_string(s):
+    return lib().dcq_status_string(s).decode()
+
+
+def _check(fn, status):
+    if status != 0:
+        raise DcqError(fn, status)
+
+
+def version():
+    return lib().dcq_version().decode()
+
+
+def block_size(t):
+    return int(lib().dcq_block_size(t))
+
+
+def type_size(t):
+    return int(lib().dcq_type_size(t))
+
+
+def row_size(t, k):
+    return int(lib().dcq_row_size(t, k))
+
+
+def vec_dot_type(t):
+    return int(lib().dcq_vec_dot_type(t))
+
+
+def supports_mul_mat(wt, xt=0, yt=0):
+    return bool(lib().dcq_supports_mul_mat(wt, xt, yt))
+
+
+def block_sums_per_row(wt, k):
+    return int(lib().dcq_block_sums_per_row(wt, k))
+
+
+def mul_mat_workspace_size(wt, m, k):
+    return int(lib().dcq_mul_mat_workspace_size(wt, m, k))
+
+
+def _stream(stream):
+    if stream is not None:
+        return ctypes.c_void_p(stream)
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def quantize_rows(vdt, x, out=None, stream=None):
+    """x: float32 cuda [M, K] -> uint8 cuda [M, row_size(vdt, K)] in ggml block layout."""
+    import torch
+    m, k = x.shape
+    if out is None:
+        out = torch.empty((m, row_size(vdt, k)), dtype=torch.uint8, device=x.device)
+    _check("dcq_quantize_rows", lib().dcq_quantize_rows(vdt, _ptr(x), m, k, x.stride(0) * 4, _ptr(out),
+                                                        _stream(stream)))
+    return out
+
+
+def mul_mat_ex(wt, wq, n, k, x, y=None, workspace=None, path=PATH_AUTO, block_sums=None, w_row_bytes=None,
+               stream=None):
+    """Y[M, N] = W[N, K] (quantized rows, uint8 cuda) x X[M, K]^T (float32 cuda)."""
+    import torch
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("dcq_mul_mat_ex", lib().dcq_mul_mat_ex(
+        wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace), ws_bytes,
+        path, _ptr(block_sums), _stream(stream)))
+    return y
+
+
+def mul_mat(wt, wq, n, k, x, y=None, workspace=None, w_row_bytes=None, stream=None):
+    import torch
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("dcq_mul_mat", lib().dcq_mul_mat(
+        wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace), ws_bytes,
+        _stream(stream)))
+    return y
+
+
+def dot_rows(wt, wq, xq_row, k, n0, n1, y=None, w_row_bytes=None, stream=None):
+    """ComputeDotProductBatch: y[r - n0] = vec_dot(W row r, xq_row), xq_row pre-quantized (ggml layout)."""
+    import torch
+    if y is None:
+        y = torch.empty((max(n1 - n0, 0),), dtype=torch.float32, device=wq.device)
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    _check("dcq_dot_rows", lib().dcq_dot_rows(wt, _ptr(wq), wrb, _ptr(xq_row), k, _ptr(y), n0, n1,
+                                              _stream(stream)))
+    return y
+
+
+def quantize_weights(wt, w, out=None, stream=None):
+    """w: float32 cuda [N, K] -> uint8 cuda [N, row_size(wt, K)] (ggml_quantize_chunk)."""
+    import torch
+    n, k = w.shape
+    if out is None:
+        out = torch.empty((n, row_size(wt, k)), dtype=torch.uint8, device=w.device)
+    _check("dcq_quantize_weights", lib().dcq_quantize_weights(wt, _ptr(w), n, k, _ptr(out), _stream(stream)))
+    return out
+
+
+def dequantize_rows(t, wq, n, k, y=None, w_row_bytes=None, stream=None):
+    import torch
+    if y is None:
+        y = torch.empty((n, k), dtype=torch.float32, device=wq.device)
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(t, k)
+    _check("dcq_dequantize_rows", lib().dcq_dequantize_rows(t, _ptr(wq), n, k, wrb, _ptr(y), _stream(stream)))
+    return y
+
+
+def quantize_src1(wt, x, workspace, stream=None):
+    """Quantize X [M, K] once into `workspace` (uint8 cuda, mul_mat_workspace_size bytes)."""
+    m, k = x.shape
+    _check("dcq_quantize_src1", lib().dcq_quantize_src1(wt, _ptr(x), m, k, x.stride(0) * 4, _ptr(workspace),
+                                                        workspace.numel(), _stream(stream)))
+    return workspace
+
+
+def mul_mat_q(wt, wq, n, k, workspace, m, y=None, path=PATH_AUTO, w_row_bytes=None, stream=None):
+    """Y[M, N] from W and activations already quantized by quantize_src1 into `workspace`."""
+    import torch
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=wq.device)
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    _check("dcq_mul_mat_q", lib().dcq_mul_mat_q(wt, _ptr(wq), n, k, wrb, _ptr(workspace), workspace.numel(), m,
+                                                _ptr(y), y.stride(0) * 4, path, _stream(stream)))
+    return y

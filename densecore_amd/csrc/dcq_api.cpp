@@ -1,0 +1,304 @@
+// dcq_api.cpp — the extern "C" boundary of libdcq (declared in include/dcq.h).
+//
+// Every entry point validates its arguments on the host before touching the
+// device, so a bad call returns a status and launches nothing. Device work is
+// stream-ordered on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+#include <string.h>
+
+#include "../../include/dcq.h"
+#include "dcq_common.h"
+#include "dcq_kernels.h"
+
+namespace dcq {
+
+size_t planar_bytes(int vdt, int64_t M, int64_t K, PlanarBuffers* pb, void* base) {
+    const int64_t bs = vdt == kTypeQ8_0 ? QK8_0 : QK_K;
+    const int64_t m_ld = round_up(M, 64);  // >= every MMQ m-tile, so float4 scale loads stay in bounds
+    const size_t qs_b = (size_t)round_up(M * K, 256);
+    const size_t d_b = (size_t)round_up((K / bs) * m_ld * 4, 256);
+    const size_t bs_b = vdt == kTypeQ8_K ? (size_t)round_up(M * (K / 16) * 2, 256) : 0;
+    if (pb) {
+        char* p = (char*)base;
+        pb->qs = (int8_t*)p;
+        pb->d = (float*)(p + qs_b);
+        pb->bs = vdt == kTypeQ8_K ? (int16_t*)(p + qs_b + d_b) : nullptr;
+        pb->m_ld = m_ld;
+    }
+    return qs_b + d_b + bs_b;
+}
+
+}  // namespace dcq
+
+using namespace dcq;
+
+namespace {
+
+bool is_weight_type(int t) { return t == kTypeQ8_0 || t == kTypeQ4_K || t == kTypeQ6_K; }
+
+// The kernels are built for gfx950 only; refuse other devices loudly.
+int check_device() {
+    static std::mutex mu;
+    static int ok_for[64] = {0};  // 0 unknown, 1 ok, -1 bad
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return DCQ_ERR_NO_DEVICE;
+    if (dev < 0 || dev >= 64) return DCQ_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(mu);
+    if (ok_for[dev] == 0) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return DCQ_ERR_NO_DEVICE;
+        ok_for[dev] = strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : -1;
+    }
+    return ok_for[dev] == 1 ? DCQ_OK : DCQ_ERR_NO_DEVICE;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+int hip_status(hipError_t e) { return e == hipSuccess ? DCQ_OK : DCQ_ERR_HIP; }
+
+// Validation of dcq_mul_mat-style arguments (no device calls).
+int validate_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X, int64_t M,
+                     size_t x_stride_bytes, const float* Y, size_t y_stride_bytes) {
+    if (!is_weight_type(wtype)) return DCQ_ERR_UNSUPPORTED;
+    if (!W || !X || !Y) return DCQ_ERR_INVALID_ARG;
+    if (N <= 0 || M <= 0 || K <= 0) return DCQ_ERR_BAD_SHAPE;
+    if (K % dcq_block_size(wtype)) return DCQ_ERR_BAD_SHAPE;
+    if (K > (int64_t)1 << 30 || N > (int64_t)1 << 31 || M > (int64_t)1 << 31) return DCQ_ERR_BAD_SHAPE;
+    if (w_row_bytes < dcq_row_size(wtype, K)) return DCQ_ERR_INVALID_ARG;
+    if (x_stride_bytes < (size_t)K * 4 || y_stride_bytes < (size_t)N * 4) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(W, 16) || !aligned(X, 16) || !aligned(Y, 4)) return DCQ_ERR_MISALIGNED;
+    if (x_stride_bytes % 16 || y_stride_bytes % 4) return DCQ_ERR_MISALIGNED;
+    if (w_row_bytes % 2) return DCQ_ERR_MISALIGNED;
+    if (wtype == kTypeQ4_K && w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
+    return DCQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dcq_version(void) { return "dcq 0.1.0 gfx950"; }
+
+const char* dcq_status_string(int s) {
+    switch (s) {
+        case DCQ_OK: return "ok";
+        case DCQ_ERR_INVALID_ARG: return "invalid argument";
+        case DCQ_ERR_UNSUPPORTED: return "unsupported type";
+        case DCQ_ERR_BAD_SHAPE: return "bad shape (K must be a multiple of the block size; dims > 0)";
+        case DCQ_ERR_MISALIGNED: return "misaligned pointer or stride";
+        case DCQ_ERR_WORKSPACE: return "workspace too small";
+        case DCQ_ERR_HIP: return "HIP runtime error";
+        case DCQ_ERR_NO_DEVICE: return "no gfx950 device";
+        default: return "unknown status";
+    }
+}
+
+int64_t dcq_block_size(int type) {
+    switch (type) {
+        case DCQ_TYPE_F32:
+        case DCQ_TYPE_F16: return 1;
+        case DCQ_TYPE_Q8_0: return QK8_0;
+        case DCQ_TYPE_Q4_K:
+        case DCQ_TYPE_Q6_K:
+        case DCQ_TYPE_Q8_K: return QK_K;
+        default: return 0;
+    }
+}
+
+int64_t dcq_type_size(int type) {
+    switch (type) {
+        case DCQ_TYPE_F32: return 4;
+        case DCQ_TYPE_F16: return 2;
+        case DCQ_TYPE_Q8_0: return (int64_t)sizeof(BlockQ8_0);
+        case DCQ_TYPE_Q4_K: return (int64_t)sizeof(BlockQ4_K);
+        case DCQ_TYPE_Q6_K: return (int64_t)sizeof(BlockQ6_K);
+        case DCQ_TYPE_Q8_K: return (int64_t)sizeof(BlockQ8_K);
+        default: return 0;
+    }
+}
+
+size_t dcq_row_size(int type, int64_t k) {
+    const int64_t bs = dcq_block_size(type);
+    if (bs <= 0 || k < 0 || k % bs) return 0;
+    return (size_t)((k / bs) * dcq_type_size(type));
+}
+
+int dcq_vec_dot_type(int wtype) {
+    switch (wtype) {
+        case DCQ_TYPE_Q8_0: return DCQ_TYPE_Q8_0;
+        case DCQ_TYPE_Q4_K:
+        case DCQ_TYPE_Q6_K: return DCQ_TYPE_Q8_K;
+        default: return DCQ_ERR_UNSUPPORTED;
+    }
+}
+
+int dcq_supports_mul_mat(int wtype, int xtype, int ytype) {
+    return is_weight_type(wtype) && xtype == DCQ_TYPE_F32 && ytype == DCQ_TYPE_F32;
+}
+
+int64_t dcq_block_sums_per_row(int wtype, int64_t k) {
+    if (!is_weight_type(wtype) || k <= 0 || k % dcq_block_size(wtype)) return 0;
+    switch (wtype) {
+        case DCQ_TYPE_Q8_0: return k / QK8_0;
+        case DCQ_TYPE_Q4_K: return 2 * (k / QK_K);
+        default: return k / QK_K;
+    }
+}
+
+size_t dcq_mul_mat_workspace_size(int wtype, int64_t M, int64_t K) {
+    const int vdt = dcq_vec_dot_type(wtype);
+    if (vdt < 0 || M <= 0 || K <= 0 || K % dcq_block_size(wtype)) return 0;
+    return planar_bytes(vdt, M, K, nullptr, nullptr);
+}
+
+int dcq_quantize_rows(int vdt, const float* X, int64_t M, int64_t K, size_t x_stride_bytes, void* Xq, void* stream) {
+    if (vdt != DCQ_TYPE_Q8_0 && vdt != DCQ_TYPE_Q8_K) return DCQ_ERR_UNSUPPORTED;
+    if (!X || !Xq) return DCQ_ERR_INVALID_ARG;
+    if (M <= 0 || K <= 0 || K % dcq_block_size(vdt)) return DCQ_ERR_BAD_SHAPE;
+    if (x_stride_bytes < (size_t)K * 4) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(X, 16) || x_stride_bytes % 16) return DCQ_ERR_MISALIGNED;
+    if (!aligned(Xq, vdt == DCQ_TYPE_Q8_K ? 4 : 2)) return DCQ_ERR_MISALIGNED;
+    int rc = check_device();
+    if (rc) return rc;
+    return hip_status(launch_quantize_ggml(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, Xq,
+                                           (int64_t)dcq_row_size(vdt, K), (hipStream_t)stream));
+}
+
+int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X, int64_t M,
+                   size_t x_stride_bytes, float* Y, size_t y_stride_bytes, void* workspace, size_t workspace_bytes,
+                   int path, int32_t* block_sums, void* stream) {
+    int rc = validate_mul_mat(wtype, W, N, K, w_row_bytes, X, M, x_stride_bytes, Y, y_stride_bytes);
+    if (rc) return rc;
+    if (path != DCQ_PATH_AUTO && path != DCQ_PATH_GEMV && path != DCQ_PATH_MMQ) return DCQ_ERR_INVALID_ARG;
+    if (block_sums && !aligned(block_sums, 4)) return DCQ_ERR_MISALIGNED;
+    const int vdt = dcq_vec_dot_type(wtype);
+    const size_t need = planar_bytes(vdt, M, K, nullptr, nullptr);
+    if (workspace) {
+        if (workspace_bytes < need) return DCQ_ERR_WORKSPACE;
+        if (!aligned(workspace, 256)) return DCQ_ERR_MISALIGNED;
+    }
+    rc = check_device();
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    void* ws = workspace;
+    if (!ws) {
+        if (hipMallocAsync(&ws, need, st) != hipSuccess) return DCQ_ERR_HIP;
+    }
+    PlanarBuffers pb;
+    planar_bytes(vdt, M, K, &pb, ws);
+    hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
+    if (e == hipSuccess) {
+        const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
+        const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= 8);
+        if (use_gemv)
+            e = launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, block_sums, N, st);
+        else
+            e = launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, block_sums, st);
+    }
+    if (!workspace) {
+        hipError_t e2 = hipFreeAsync(ws, st);
+        if (e == hipSuccess) e = e2;
+    }
+    return hip_status(e);
+}
+
+int dcq_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X, int64_t M,
+                size_t x_stride_bytes, float* Y, size_t y_stride_bytes, void* workspace, size_t workspace_bytes,
+                void* stream) {
+    return dcq_mul_mat_ex(wtype, W, N, K, w_row_bytes, X, M, x_stride_bytes, Y, y_stride_bytes, workspace,
+                          workspace_bytes, DCQ_PATH_AUTO, nullptr, stream);
+}
+
+int dcq_quantize_src1(int wtype, const float* X, int64_t M, int64_t K, size_t x_stride_bytes, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    if (!is_weight_type(wtype)) return DCQ_ERR_UNSUPPORTED;
+    if (!X || !workspace) return DCQ_ERR_INVALID_ARG;
+    if (M <= 0 || K <= 0 || K % dcq_block_size(wtype)) return DCQ_ERR_BAD_SHAPE;
+    if (K > (int64_t)1 << 30 || M > (int64_t)1 << 31) return DCQ_ERR_BAD_SHAPE;
+    if (x_stride_bytes < (size_t)K * 4) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(X, 16) || x_stride_bytes % 16 || !aligned(workspace, 256)) return DCQ_ERR_MISALIGNED;
+    const int vdt = dcq_vec_dot_type(wtype);
+    if (workspace_bytes < planar_bytes(vdt, M, K, nullptr, nullptr)) return DCQ_ERR_WORKSPACE;
+    int rc = check_device();
+    if (rc) return rc;
+    PlanarBuffers pb;
+    planar_bytes(vdt, M, K, &pb, workspace);
+    return hip_status(launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, (hipStream_t)stream));
+}
+
+int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const void* workspace,
+                  size_t workspace_bytes, int64_t M, float* Y, size_t y_stride_bytes, int path, void* stream) {
+    if (!workspace) return DCQ_ERR_INVALID_ARG;
+    // X is already quantized: validate the rest with a stand-in X of the right alignment
+    int rc = validate_mul_mat(wtype, W, N, K, w_row_bytes, (const float*)workspace, M, (size_t)K * 4 + 16, Y,
+                              y_stride_bytes);
+    if (rc) return rc;
+    if (path != DCQ_PATH_AUTO && path != DCQ_PATH_GEMV && path != DCQ_PATH_MMQ) return DCQ_ERR_INVALID_ARG;
+    const int vdt = dcq_vec_dot_type(wtype);
+    if (workspace_bytes < planar_bytes(vdt, M, K, nullptr, nullptr)) return DCQ_ERR_WORKSPACE;
+    if (!aligned(workspace, 256)) return DCQ_ERR_MISALIGNED;
+    rc = check_device();
+    if (rc) return rc;
+    PlanarBuffers pb;
+    planar_bytes(vdt, M, K, &pb, (void*)workspace);
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
+    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= 8);
+    hipError_t e = use_gemv ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
+                            : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st);
+    return hip_status(e);
+}
+
+int dcq_dot_rows(int wtype, const void* W, size_t w_row_bytes, const void* Xq, int64_t K, float* Y, int64_t n0,
+                 int64_t n1, void* stream) {
+    if (!is_weight_type(wtype)) return DCQ_ERR_UNSUPPORTED;
+    if (!W || !Xq || !Y) return DCQ_ERR_INVALID_ARG;
+    if (K <= 0 || K % dcq_block_size(wtype) || n0 < 0 || n1 < n0) return DCQ_ERR_BAD_SHAPE;
+    if (w_row_bytes < dcq_row_size(wtype, K)) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(W, 16) || !aligned(Y, 4)) return DCQ_ERR_MISALIGNED;
+    if (w_row_bytes % 2) return DCQ_ERR_MISALIGNED;
+    if (wtype == kTypeQ4_K && w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
+    const int vdt = dcq_vec_dot_type(wtype);
+    if (!aligned(Xq, vdt == kTypeQ8_K ? 4 : 2)) return DCQ_ERR_MISALIGNED;
+    if (n1 == n0) return DCQ_OK;
+    int rc = check_device();
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const size_t need = planar_bytes(vdt, 1, K, nullptr, nullptr);
+    void* ws = nullptr;
+    if (hipMallocAsync(&ws, need, st) != hipSuccess) return DCQ_ERR_HIP;
+    PlanarBuffers pb;
+    planar_bytes(vdt, 1, K, &pb, ws);
+    hipError_t e = launch_unpack_ggml_rows(vdt, Xq, (int64_t)dcq_row_size(vdt, K), 1, K, pb, st);
+    if (e == hipSuccess)
+        e = launch_gemv(wtype, (const uint8_t*)W, (int64_t)w_row_bytes, n0, n1, K, pb, 1, Y, n1 - n0, nullptr,
+                        n1 - n0, st);
+    hipError_t e2 = hipFreeAsync(ws, st);
+    if (e == hipSuccess) e = e2;
+    return hip_status(e);
+}
+
+int dcq_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, void* stream) {
+    if (!is_weight_type(wtype)) return DCQ_ERR_UNSUPPORTED;
+    if (!W || !Wq) return DCQ_ERR_INVALID_ARG;
+    if (N <= 0 || K <= 0 || K % dcq_block_size(wtype)) return DCQ_ERR_BAD_SHAPE;
+    if (!aligned(W, 4) || !aligned(Wq, 16)) return DCQ_ERR_MISALIGNED;
+    int rc = check_device();
+    if (rc) return rc;
+    return hip_status(launch_quantize_weights(wtype, W, N, K, Wq, (hipStream_t)stream));
+}
+
+int dcq_dequantize_rows(int type, const void* Wq, int64_t N, int64_t K, size_t w_row_bytes, float* Y, void* stream) {
+    if (!is_weight_type(type) && type != DCQ_TYPE_Q8_K) return DCQ_ERR_UNSUPPORTED;
+    if (!Wq || !Y) return DCQ_ERR_INVALID_ARG;
+    if (N <= 0 || K <= 0 || K % dcq_block_size(type)) return DCQ_ERR_BAD_SHAPE;
+    if (w_row_bytes < dcq_row_size(type, K)) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(Y, 4) || w_row_bytes % 2 || !aligned(Wq, 4)) return DCQ_ERR_MISALIGNED;
+    int rc = check_device();
+    if (rc) return rc;
+    return hip_status(launch_dequantize(type, Wq, N, K, (int64_t)w_row_bytes, Y, (hipStream_t)stream));
+}
+
+}  // extern "C"

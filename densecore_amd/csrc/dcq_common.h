@@ -1,0 +1,127 @@
+// dcq_common.h — shared definitions of the gfx950 quantized mul_mat library.
+//
+// GGUF block layouts (little-endian, `half` = IEEE fp16), as the reference's
+// ggml stores weights in host memory (core/src/model_loader.cpp:103-122) and
+// DenseCore's own Metal shader restates for Q8_0
+// (core/shaders/quantized_gemv.metal:85-88):
+//   Q8_0 (32 elems, 34 B):  { half d; int8 qs[32]; }                 value = d*qs[i]
+//   Q4_K (256 elems, 144 B):{ half d; half dmin; u8 scales[12]; u8 qs[128]; }
+//   Q6_K (256 elems, 210 B):{ u8 ql[128]; u8 qh[64]; i8 scales[16]; half d; }
+//   Q8_K (256 elems, 292 B):{ float d; i8 qs[256]; i16 bsums[16]; }
+//
+// Planar activation layout (library-internal, in the caller's workspace). The
+// GPU kernels consume quantized activations in this split form rather than
+// the ggml block array; dcq_quantize_rows still emits the ggml bytes.
+//   qs : int8  [M][K]                 row m at qs + m*K (K % 32 == 0, so rows stay 16-B aligned)
+//   d  : float [K/bs][M_ld]           block-major scales (fp16 d widened exactly for Q8_0,
+//                                     fp32 d for Q8_K); M_ld = M rounded up to 64, rows
+//                                     M..M_ld-1 hold 0
+//   bs : int16 [M][K/16]              Q8_K bsums (sum of 16 consecutive qs)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dcq {
+
+constexpr int kTypeF32 = 0;
+constexpr int kTypeF16 = 1;
+constexpr int kTypeQ8_0 = 8;
+constexpr int kTypeQ4_K = 12;
+constexpr int kTypeQ6_K = 14;
+constexpr int kTypeQ8_K = 15;
+
+constexpr int QK8_0 = 32;
+constexpr int QK_K = 256;
+
+struct __attribute__((packed)) BlockQ8_0 {
+    uint16_t d;
+    int8_t qs[QK8_0];
+};
+struct BlockQ4_K {
+    uint16_t d;
+    uint16_t dmin;
+    uint8_t scales[12];
+    uint8_t qs[QK_K / 2];
+};
+struct BlockQ6_K {
+    uint8_t ql[QK_K / 2];
+    uint8_t qh[QK_K / 4];
+    int8_t scales[QK_K / 16];
+    uint16_t d;
+};
+struct BlockQ8_K {
+    float d;
+    int8_t qs[QK_K];
+    int16_t bsums[QK_K / 16];
+};
+static_assert(sizeof(BlockQ8_0) == 34, "Q8_0 block is 34 bytes");
+static_assert(sizeof(BlockQ4_K) == 144, "Q4_K block is 144 bytes");
+static_assert(sizeof(BlockQ6_K) == 210, "Q6_K block is 210 bytes");
+static_assert(sizeof(BlockQ8_K) == 292, "Q8_K block is 292 bytes");
+
+// Quantized activations in the planar layout (device pointers into the workspace).
+struct ActPlanar {
+    const int8_t* qs;   // [M][K]
+    const float* d;     // [K/bs][m_ld]
+    const int16_t* bs;  // [M][K/16] (Q8_K only)
+    int64_t M;
+    int64_t K;
+    int64_t m_ld;
+};
+
+inline __host__ __device__ int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
+
+// ---- device helpers ----
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
+    _Float16 h;
+    uint16_t b = (uint16_t)h16;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+// fp32 -> fp16 bits, IEEE round-to-nearest-even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+    _Float16 h = (_Float16)f;
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// (hi:lo) >> (8*shift), low 32 bits; shift in bytes (0..3).
+__device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t shift) {
+    return __builtin_amdgcn_alignbyte(hi, lo, shift);
+}
+
+// Global loads with the alignment the data actually has. 16 B at 4-B alignment is a
+// single global_load_dwordx4 (gfx9 needs dword alignment for multi-dword accesses).
+struct __attribute__((aligned(4))) U32x4 {
+    uint32_t x, y, z, w;
+};
+struct __attribute__((aligned(4))) U32x2 {
+    uint32_t x, y;
+};
+__device__ __forceinline__ U32x4 ld4(const void* p) { return *reinterpret_cast<const U32x4*>(p); }
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ uint32_t ld1(const void* p) { return *reinterpret_cast<const uint32_t*>(p); }
+__device__ __forceinline__ uint32_t ldu16(const void* p) { return *reinterpret_cast<const uint16_t*>(p); }
+
+// 16 bytes starting at a 2-byte aligned address p, reading only [p - (p & 3), p + 16):
+// 4 dwords from the dword at or below p, then the last 2 bytes with a halfword
+// load when p is not dword aligned (so a piece that ends a tensor never reads past it).
+__device__ __forceinline__ void ld16_a2(const uint8_t* p, uint32_t out[4]) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t sh = (uint32_t)(a & 3u);
+    const U32x4 w = ld4(p - sh);
+    const uint32_t w4 = ldu16(p + (sh ? 14 : 12));
+    out[0] = align_bytes(w.y, w.x, sh);
+    out[1] = align_bytes(w.z, w.y, sh);
+    out[2] = align_bytes(w.w, w.z, sh);
+    out[3] = align_bytes(w4, w.w, sh);
+}
+
+}  // namespace dcq

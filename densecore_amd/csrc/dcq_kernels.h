@@ -1,0 +1,41 @@
+// dcq_kernels.h — internal launcher declarations shared by the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dcq {
+
+// Planar quantized activations inside a workspace (see dcq_common.h for the layout).
+struct PlanarBuffers {
+    int8_t* qs;   // [M][K]
+    float* d;     // [K/bs][m_ld]
+    int16_t* bs;  // [M][K/16] (Q8_K) or nullptr
+    int64_t m_ld;
+};
+
+// Workspace carve-up for `vdt` activations of M x K; returns total bytes (256-B granules).
+size_t planar_bytes(int vdt, int64_t M, int64_t K, PlanarBuffers* pb, void* base);
+
+hipError_t launch_quantize_ggml(int vdt, const float* X, int64_t x_stride, int64_t M, int64_t K, void* out,
+                                int64_t out_row_bytes, hipStream_t st);
+hipError_t launch_quantize_planar(int vdt, const float* X, int64_t x_stride, int64_t M, int64_t K,
+                                  const PlanarBuffers& pb, hipStream_t st);
+hipError_t launch_unpack_ggml_rows(int vdt, const void* in, int64_t in_row_bytes, int64_t M, int64_t K,
+                                   const PlanarBuffers& pb, hipStream_t st);
+
+// Decode GEMV / small-M: wave-per-row-group int8 dot products.
+// Y[m*y_stride + n] for m < M, n in [n0, n1); block_sums optional (atomics, pre-zeroed).
+hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
+                       const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                       int64_t sums_n_stride, hipStream_t st);
+
+// Int8-MFMA tiles for any M.
+hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                      int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+
+hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, hipStream_t st);
+hipError_t launch_dequantize(int type, const void* Wq, int64_t N, int64_t K, int64_t w_row_bytes, float* Y,
+                             hipStream_t st);
+
+}  // namespace dcq

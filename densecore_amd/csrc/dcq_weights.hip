@@ -1,0 +1,357 @@
+// dcq_weights.hip — weight quantization (ggml_quantize_chunk without an importance
+// matrix) and dequantization (type_traits->to_float).
+//
+// Weight quantization is the offline step before the hot path
+// (core/src/quantize.cpp:214, 285 call ggml_quantize_chunk); dequantization is
+// the reference GEMV's fallback (core/src/inference.cpp:938-945). One thread per
+// block / superblock; the scalar search below is ggml's published algorithm
+// (make_qkx2_quants for Q4_K, make_qx_quants with rmse_type 1 for Q6_K,
+// roundf scaling for Q8_0). This file is compiled with -ffp-contract=off so
+// each fp32 operation rounds on its own, as the CPU code does, and the bytes
+// match a CPU build of the same algorithm exactly.
+#include "dcq_common.h"
+#include "dcq_kernels.h"
+
+namespace dcq {
+
+__device__ __forceinline__ int nearest_int(float v) {
+    float t = v + 12582912.f;
+    int32_t i;
+    __builtin_memcpy(&i, &t, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+// ---- Q8_0: quantize_row_q8_0_ref (id = 1/d, roundf) ----
+__global__ void __launch_bounds__(256) quantize_w_q8_0_kernel(const float* __restrict__ W, int64_t N, int64_t K,
+                                                              uint8_t* __restrict__ out) {
+    const int64_t nb = K / QK8_0;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= N * nb) return;
+    const int64_t r = gid / nb, b = gid - (gid / nb) * nb;
+    const float* x = W + r * K + b * QK8_0;
+    float amax = 0.0f;
+    for (int j = 0; j < QK8_0; ++j) amax = fmaxf(amax, fabsf(x[j]));
+    const float d = amax / 127.f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint8_t* blk = out + r * nb * 34 + b * 34;
+    uint16_t* p16 = reinterpret_cast<uint16_t*>(blk);
+    p16[0] = float_to_half_bits(d);
+    for (int j = 0; j < QK8_0; j += 2) {
+        float v0 = fminf(fmaxf(roundf(x[j] * id), -128.f), 127.f);
+        float v1 = fminf(fmaxf(roundf(x[j + 1] * id), -128.f), 127.f);
+        p16[1 + j / 2] = (uint16_t)(((uint32_t)(int32_t)v0 & 0xFFu) | (((uint32_t)(int32_t)v1 & 0xFFu) << 8));
+    }
+}
+
+// ---- Q4_K ----
+__device__ float make_qkx2_quants(int n, int nmax, const float* x, const float* weights, uint8_t* L, float* the_min,
+                                  uint8_t* Laux, float rmin, float rdelta, int nstep) {
+    float min = x[0], max = x[0];
+    float sum_w = weights[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        float w = weights[i];
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (min > 0) min = 0;
+    if (max == min) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        *the_min = -min;
+        return 0.f;
+    }
+    float iscale = nmax / (max - min);
+    float scale = 1 / iscale;
+    float best_error = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * (x[i] - min));
+        L[i] = (uint8_t)(l < 0 ? 0 : (l > nmax ? nmax : l));
+        float diff = scale * L[i] + min - x[i];
+        best_error += weights[i] * (diff * diff);
+    }
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * is + nmax) / (max - min);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale * (x[i] - min));
+            l = l < 0 ? 0 : (l > nmax ? nmax : l);
+            Laux[i] = (uint8_t)l;
+            float w = weights[i];
+            sum_l += w * l;
+            sum_l2 += w * l * l;
+            sum_xl += w * l * x[i];
+        }
+        float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) {
+                this_min = 0;
+                this_scale = sum_xl / sum_l2;
+            }
+            float mad = 0;
+            for (int i = 0; i < n; ++i) {
+                float diff = this_scale * Laux[i] + this_min - x[i];
+                mad += weights[i] * (diff * diff);
+            }
+            if (mad < best_error) {
+                for (int i = 0; i < n; ++i) L[i] = Laux[i];
+                best_error = mad;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+    *the_min = -min;
+    return scale;
+}
+
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4));
+    }
+}
+
+__global__ void __launch_bounds__(64) quantize_w_q4_K_kernel(const float* __restrict__ W, int64_t N, int64_t K,
+                                                             uint8_t* __restrict__ out) {
+    const int64_t nsb = K / QK_K;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= N * nsb) return;
+    const int64_t r = gid / nsb, sbi = gid - (gid / nsb) * nsb;
+    const float* x = W + r * K + sbi * QK_K;
+    BlockQ4_K y __attribute__((aligned(16)));
+    uint8_t L[QK_K], Laux[32];
+    float weights[32], mins[8], scales[8];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < 8; ++j) {
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+        float av_x = sqrtf(sum_x2 / 32);
+        for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+        scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    for (int i = 0; i < 12; ++i) y.scales[i] = 0;
+    for (int j = 0; j < 8; ++j) {
+        int ls = nearest_int(inv_scale * scales[j]);
+        int lm = nearest_int(inv_min * mins[j]);
+        ls = ls < 63 ? ls : 63;
+        lm = lm < 63 ? lm : 63;
+        if (j < 4) {
+            y.scales[j] = (uint8_t)ls;
+            y.scales[j + 4] = (uint8_t)lm;
+        } else {
+            y.scales[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+            y.scales[j - 4] |= (uint8_t)((ls >> 4) << 6);
+            y.scales[j - 0] |= (uint8_t)((lm >> 4) << 6);
+        }
+    }
+    y.d = float_to_half_bits(max_scale / 63.f);
+    y.dmin = float_to_half_bits(max_min / 63.f);
+    for (int j = 0; j < 8; ++j) {
+        uint8_t sc, m;
+        scale_min_k4(j, y.scales, &sc, &m);
+        const float d = half_bits_to_float(y.d) * sc;
+        if (!d) continue;
+        const float dm = half_bits_to_float(y.dmin) * m;
+        for (int ii = 0; ii < 32; ++ii) {
+            int l = nearest_int((x[32 * j + ii] + dm) / d);
+            L[32 * j + ii] = (uint8_t)(l < 0 ? 0 : (l > 15 ? 15 : l));
+        }
+    }
+    for (int c = 0; c < 4; ++c)
+        for (int l = 0; l < 32; ++l) y.qs[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + l + 32] << 4));
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out + (r * nsb + sbi) * 144);
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(&y);
+    for (int i = 0; i < 36; ++i) dst[i] = src[i];
+}
+
+// ---- Q6_K ----
+__device__ float make_qx_quants_rmse1(int n, int nmax, const float* x, int8_t* L) {
+    float max = 0, amax = 0;
+    for (int i = 0; i < n; ++i) {
+        float ax = fabsf(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            max = x[i];
+        }
+    }
+    if (amax < 1e-15f) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        return 0.f;
+    }
+    float iscale = -nmax / max;
+    float sumlx = 0, suml2 = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * x[i]);
+        l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+        L[i] = (int8_t)(l + nmax);
+        float w = x[i] * x[i];
+        sumlx += w * x[i] * l;
+        suml2 += w * l * l;
+    }
+    float scale = suml2 ? sumlx / suml2 : 0.0f;
+    float best = scale * sumlx;
+    for (int is = -9; is <= 9; ++is) {
+        if (is == 0) continue;
+        iscale = -(nmax + 0.1f * is) / max;
+        sumlx = suml2 = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale * x[i]);
+            l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+            float w = x[i] * x[i];
+            sumlx += w * x[i] * l;
+            suml2 += w * l * l;
+        }
+        if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < n; ++i) {
+                int l = nearest_int(iscale * x[i]);
+                l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+                L[i] = (int8_t)(l + nmax);
+            }
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+    return scale;
+}
+
+__global__ void __launch_bounds__(64) quantize_w_q6_K_kernel(const float* __restrict__ W, int64_t N, int64_t K,
+                                                             uint8_t* __restrict__ out) {
+    const int64_t nsb = K / QK_K;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= N * nsb) return;
+    const int64_t r = gid / nsb, sbi = gid - (gid / nsb) * nsb;
+    const float* x = W + r * K + sbi * QK_K;
+    uint8_t* dstb = out + (r * nsb + sbi) * 210;
+    int8_t L[QK_K];
+    float scales[16];
+    float max_scale = 0, max_abs_scale = 0;
+    for (int ib = 0; ib < 16; ++ib) {
+        const float scale = make_qx_quants_rmse1(16, 32, x + 16 * ib, L + 16 * ib);
+        scales[ib] = scale;
+        const float abs_scale = fabsf(scale);
+        if (abs_scale > max_abs_scale) {
+            max_abs_scale = abs_scale;
+            max_scale = scale;
+        }
+    }
+    uint8_t y[210];
+    for (int i = 0; i < 210; ++i) y[i] = 0;
+    if (!(max_abs_scale < 1e-15f)) {
+        float iscale = -128.f / max_scale;
+        const uint16_t dh = float_to_half_bits(1 / iscale);
+        y[208] = (uint8_t)dh;
+        y[209] = (uint8_t)(dh >> 8);
+        int8_t* ysc = reinterpret_cast<int8_t*>(y + 192);
+        for (int ib = 0; ib < 16; ++ib) {
+            int v = nearest_int(iscale * scales[ib]);
+            ysc[ib] = (int8_t)(v < 127 ? v : 127);
+        }
+        for (int j = 0; j < 16; ++j) {
+            float d = half_bits_to_float(dh) * ysc[j];
+            if (!d) continue;
+            for (int ii = 0; ii < 16; ++ii) {
+                int l = nearest_int(x[16 * j + ii] / d);
+                l = l < -32 ? -32 : (l > 31 ? 31 : l);
+                L[16 * j + ii] = (int8_t)(l + 32);
+            }
+        }
+        uint8_t* ql = y;
+        uint8_t* qh = y + 128;
+        for (int j = 0; j < QK_K; j += 128) {
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t q1 = L[j + l + 0] & 0xF;
+                const uint8_t q2 = L[j + l + 32] & 0xF;
+                const uint8_t q3 = L[j + l + 64] & 0xF;
+                const uint8_t q4 = L[j + l + 96] & 0xF;
+                ql[l + 0] = (uint8_t)(q1 | (q3 << 4));
+                ql[l + 32] = (uint8_t)(q2 | (q4 << 4));
+                qh[l] = (uint8_t)((L[j + l] >> 4) | ((L[j + l + 32] >> 4) << 2) | ((L[j + l + 64] >> 4) << 4) |
+                                  ((L[j + l + 96] >> 4) << 6));
+            }
+            ql += 64;
+            qh += 32;
+        }
+    }
+    uint16_t* d16 = reinterpret_cast<uint16_t*>(dstb);  // superblocks are 2-byte aligned
+    for (int i = 0; i < 105; ++i) d16[i] = (uint16_t)(y[2 * i] | (y[2 * i + 1] << 8));
+}
+
+// ---- dequantization: one thread per 32 output elements ----
+__global__ void __launch_bounds__(256) dequantize_kernel(int type, const uint8_t* __restrict__ Wq, int64_t N,
+                                                         int64_t K, int64_t w_row_bytes, float* __restrict__ Y) {
+    const int64_t per_row = K / 32;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= N * per_row) return;
+    const int64_t r = gid / per_row, c = gid - (gid / per_row) * per_row;  // chunk of 32 elements
+    const uint8_t* row = Wq + r * w_row_bytes;
+    float* y = Y + r * K + c * 32;
+    if (type == kTypeQ8_0) {
+        const uint8_t* b = row + c * 34;
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b));
+        for (int j = 0; j < 32; ++j) y[j] = (float)(int8_t)b[2 + j] * d;
+    } else if (type == kTypeQ4_K) {
+        const uint8_t* b = row + (c / 8) * 144;
+        const int j = (int)(c % 8);  // sub-block
+        uint8_t sc, m;
+        scale_min_k4(j, b + 4, &sc, &m);
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b)) * sc;
+        const float dm = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b + 2)) * m;
+        const uint8_t* qs = b + 16 + 32 * (j / 2);
+        for (int l = 0; l < 32; ++l) {
+            const int q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 0xF);
+            y[l] = d * q - dm;
+        }
+    } else if (type == kTypeQ6_K) {
+        const uint8_t* b = row + (c / 8) * 210;
+        const float d = half_bits_to_float((uint32_t)b[208] | ((uint32_t)b[209] << 8));
+        for (int l = 0; l < 32; ++l) {
+            const int e = (int)(c % 8) * 32 + l;
+            const int h = e / 128, ep = e % 128, t = ep / 32, ll = ep % 32;
+            const int lo = (b[64 * h + ll + 32 * (t & 1)] >> (4 * (t >> 1))) & 0xF;
+            const int hi = (b[128 + 32 * h + ll] >> (2 * t)) & 3;
+            y[l] = d * (float)(int8_t)b[192 + e / 16] * (float)((lo | (hi << 4)) - 32);
+        }
+    } else if (type == kTypeQ8_K) {
+        const uint8_t* b = row + (c / 8) * 292;
+        const float d = *reinterpret_cast<const float*>(b);
+        for (int l = 0; l < 32; ++l) y[l] = d * (float)(int8_t)b[4 + (c % 8) * 32 + l];
+    }
+}
+
+hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, hipStream_t st) {
+    if (wtype == kTypeQ8_0) {
+        const int64_t t = N * (K / QK8_0);
+        hipLaunchKernelGGL(quantize_w_q8_0_kernel, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, W, N, K,
+                           (uint8_t*)Wq);
+    } else if (wtype == kTypeQ4_K) {
+        const int64_t t = N * (K / QK_K);
+        hipLaunchKernelGGL(quantize_w_q4_K_kernel, dim3((unsigned)((t + 63) / 64)), dim3(64), 0, st, W, N, K,
+                           (uint8_t*)Wq);
+    } else {
+        const int64_t t = N * (K / QK_K);
+        hipLaunchKernelGGL(quantize_w_q6_K_kernel, dim3((unsigned)((t + 63) / 64)), dim3(64), 0, st, W, N, K,
+                           (uint8_t*)Wq);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize(int type, const void* Wq, int64_t N, int64_t K, int64_t w_row_bytes, float* Y,
+                             hipStream_t st) {
+    const int64_t t = N * (K / 32);
+    hipLaunchKernelGGL(dequantize_kernel, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, type,
+                       (const uint8_t*)Wq, N, K, w_row_bytes, Y);
+    return hipGetLastError();
+}
+
+}  // namespace dcq

@@ -1,0 +1,154 @@
+/*
+ * dcq.h — C ABI of libdcq, the MI355X (gfx950) quantized mul_mat backend.
+ *
+ * It replaces the compute behind ggml's MUL_MAT for GGUF Q8_0 / Q4_K / Q6_K
+ * weights times fp32 activations with fp32 output, the operator DenseCore's
+ * graph emits for every FFN / attention projection:
+ *   core/src/inference.cpp:1063, 1794-1797, 1817 (ggml_mul_mat call sites),
+ *   core/src/worker.cpp:544 (ggml_backend_graph_compute executes them),
+ *   core/src/inference.cpp:840-948 (cb_gemv_custom, the M == 1 custom op).
+ * Paths in citations are relative to the DenseCore source tree.
+ *
+ * Conventions
+ *   - Plain C types only. `stream` is a hipStream_t passed as void* (NULL =
+ *     the null stream). Every call is stream-ordered and asynchronous.
+ *   - All data pointers are device pointers owned by the caller; nothing is
+ *     freed across the ABI.
+ *   - Type ids are ggml's: F32 = 0, F16 = 1, Q8_0 = 8, Q4_K = 12, Q6_K = 14,
+ *     Q8_K = 15.
+ *   - Dimensions: W is [N][K] (N output rows, K reduction), row r starts at
+ *     W + r * w_row_bytes. X is [M][K] fp32 with row stride x_stride_bytes.
+ *     Y is [M][N] fp32 with row stride y_stride_bytes:
+ *       Y[m][n] = vec_dot(W row n, quantize_{vec_dot_type}(X row m)).
+ *   - Status: 0 on success, a negative DCQ_ERR_* otherwise. Arguments are
+ *     validated before any device work, so an error never leaves a partial
+ *     result (unlike the reference's silent zero-fill / early return,
+ *     core/src/inference.cpp:842-879, core/src/simd_ops.cpp:193-196).
+ *   - The quantized activation bytes are bit-exact with ggml's from_float
+ *     for the vec_dot_type (Q8_0: x86 SIMD semantics, round-half-even with
+ *     id = 127/amax; Q8_K: quantize_row_q8_K_ref); the per-block int32 sums
+ *     are exact; fp32 outputs differ from a CPU vec_dot only by summation
+ *     order.
+ */
+#ifndef DCQ_H
+#define DCQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids */
+#define DCQ_TYPE_F32 0
+#define DCQ_TYPE_F16 1
+#define DCQ_TYPE_Q8_0 8
+#define DCQ_TYPE_Q4_K 12
+#define DCQ_TYPE_Q6_K 14
+#define DCQ_TYPE_Q8_K 15
+
+/* status codes */
+#define DCQ_OK 0
+#define DCQ_ERR_INVALID_ARG (-1)     /* null pointer, negative size, bad stride */
+#define DCQ_ERR_UNSUPPORTED (-2)     /* type (or type pair) not supported */
+#define DCQ_ERR_BAD_SHAPE (-3)       /* K not a multiple of the block size, empty dims */
+#define DCQ_ERR_MISALIGNED (-4)      /* pointer / stride alignment the kernels need */
+#define DCQ_ERR_WORKSPACE (-5)       /* workspace smaller than dcq_mul_mat_workspace_size */
+#define DCQ_ERR_HIP (-6)             /* a HIP runtime call failed */
+#define DCQ_ERR_NO_DEVICE (-7)       /* no usable gfx950 device */
+
+/* kernel path selection for dcq_mul_mat_ex */
+#define DCQ_PATH_AUTO 0
+#define DCQ_PATH_GEMV 1 /* wave-per-row-group int8 dot (sdot4), any M (tiled by 8) */
+#define DCQ_PATH_MMQ 2  /* int8 MFMA tiles, any M */
+
+/* Library version string, e.g. "dcq 0.1.0 gfx950". */
+const char* dcq_version(void);
+/* Human-readable text for a status code. */
+const char* dcq_status_string(int status);
+
+/* ---- type traits (ggml_type_traits / ggml_row_size equivalents) ---- */
+/* Elements per block: Q8_0 32, Q4_K/Q6_K/Q8_K 256, F32/F16 1; 0 if unknown. */
+int64_t dcq_block_size(int type);
+/* Bytes per block: Q8_0 34, Q4_K 144, Q6_K 210, Q8_K 292, F32 4, F16 2; 0 if unknown. */
+int64_t dcq_type_size(int type);
+/* Bytes of one row of K elements (ggml_row_size, core/src/inference.cpp:977); 0 if K is not
+ * a multiple of the block size. */
+size_t dcq_row_size(int type, int64_t k);
+/* vec_dot_type of a weight type (core/src/inference.cpp:970-984, core/include/simd_ops.h:
+ * 3298-3305): Q8_0 -> Q8_0, Q4_K/Q6_K -> Q8_K; DCQ_ERR_UNSUPPORTED otherwise. */
+int dcq_vec_dot_type(int wtype);
+/* 1 if MUL_MAT(src0 = wtype, src1 = xtype) -> ytype is computed by this library, else 0
+ * (the check a ggml backend's supports_op answers). */
+int dcq_supports_mul_mat(int wtype, int xtype, int ytype);
+
+/* ---- activation quantization: from_float of the vec_dot_type ----
+ * Replaces type_traits_cpu(vec_dot_type)->from_float (core/src/inference.cpp:889-892).
+ * Quantizes M rows of K floats into the ggml block layout, rows packed
+ * (row r at Xq + r * dcq_row_size(vec_dot_type, K)). vec_dot_type: Q8_0 or Q8_K. */
+int dcq_quantize_rows(int vec_dot_type, const float* X, int64_t M, int64_t K, size_t x_stride_bytes,
+                      void* Xq, void* stream);
+
+/* ---- the operator ----
+ * GGML_OP_MUL_MAT for src0 = W (wtype in {Q8_0, Q4_K, Q6_K}), src1 = X (F32), dst = Y (F32):
+ * quantizes X once into the workspace, then computes every (m, n) dot
+ * (replaces the quantize + chunked vec_dot of ggml's CPU MUL_MAT, executed from
+ * core/src/worker.cpp:544, and cb_gemv_custom, core/src/inference.cpp:840-948).
+ * Requirements: K % block_size(wtype) == 0; W 16-byte aligned; w_row_bytes >= row_size, even, and
+ * a multiple of 16 for Q4_K; X 16-byte aligned with x_stride_bytes % 16 == 0; Y 4-byte aligned
+ * with y_stride_bytes % 4 == 0.
+ * workspace may be NULL (the library then takes stream-ordered scratch); otherwise it must
+ * hold dcq_mul_mat_workspace_size(wtype, M, K) bytes and be 256-byte aligned. */
+size_t dcq_mul_mat_workspace_size(int wtype, int64_t M, int64_t K);
+int dcq_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X,
+                int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* dcq_mul_mat with an explicit kernel path and, optionally, the per-block int32 sums the
+ * kernel scaled (block_sums != NULL: int32 [M][N][dcq_block_sums_per_row(wtype, K)], written
+ * with atomics, so it must be zeroed by the caller; a debugging aid — slower). */
+int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes,
+                   const float* X, int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes,
+                   void* workspace, size_t workspace_bytes, int path, int32_t* block_sums,
+                   void* stream);
+/* Number of int32 block sums per (m, n): Q8_0 K/32 (I_b = sum qw*qa over a 32-block);
+ * Q4_K 2*K/256 (per superblock: sum_j sc_j*I_j, then sum_j m_j*S_j); Q6_K K/256 (per
+ * superblock: sum_g sc_g*I_g). 0 if unsupported. */
+int64_t dcq_block_sums_per_row(int wtype, int64_t k);
+
+/* ---- the operator in two halves (ggml MUL_MAT's wdata step made explicit) ----
+ * dcq_quantize_src1 quantizes X once into `workspace` (the library's planar layout, sized by
+ * dcq_mul_mat_workspace_size(wtype, M, K)); dcq_mul_mat_q then computes Y from W and that
+ * workspace. One quantization can feed several weights that share X (ffn gate and up,
+ * core/src/inference.cpp:1794-1797). dcq_mul_mat == dcq_quantize_src1 + dcq_mul_mat_q. The
+ * workspace must not be written between the two calls. */
+int dcq_quantize_src1(int wtype, const float* X, int64_t M, int64_t K, size_t x_stride_bytes,
+                      void* workspace, size_t workspace_bytes, void* stream);
+int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes,
+                  const void* workspace, size_t workspace_bytes, int64_t M, float* Y,
+                  size_t y_stride_bytes, int path, void* stream);
+
+/* ---- row-range dot with pre-quantized input ----
+ * ComputeDotProductBatch (core/src/simd_ops.cpp:140-197): Y[r - n0] = vec_dot(K, W row r, Xq)
+ * for r in [n0, n1); Xq is ONE row already quantized to the vec_dot_type (ggml layout, as
+ * dcq_quantize_rows writes it). Unsupported types return DCQ_ERR_UNSUPPORTED instead of the
+ * reference's zero-fill. */
+int dcq_dot_rows(int wtype, const void* W, size_t w_row_bytes, const void* Xq, int64_t K, float* Y,
+                 int64_t n0, int64_t n1, void* stream);
+
+/* ---- weight quantization (ggml_quantize_chunk equivalent, core/src/quantize.cpp:285) ----
+ * Quantizes an fp32 [N][K] matrix into wtype rows (packed, row stride dcq_row_size):
+ * Q8_0 = quantize_row_q8_0_ref, Q4_K = quantize_row_q4_K_ref, Q6_K = quantize_row_q6_K_ref
+ * (no importance matrix). */
+int dcq_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, void* stream);
+
+/* ---- dequantization (type_traits->to_float, core/src/inference.cpp:938-945) ----
+ * Y[r][k] = value of element k of row r; N rows of K elements, Y rows packed. */
+int dcq_dequantize_rows(int type, const void* Wq, int64_t N, int64_t K, size_t w_row_bytes, float* Y,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DCQ_H */

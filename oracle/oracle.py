@@ -1,0 +1,218 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as
+the checker, and by bench.py's cpu_baseline leg. The product library never
+imports it. See dcq_oracle.h for what it restates and how each part is pinned.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
+Q8_0_X86, Q8_0_REF = 0, 1
+
+_lib = None
+
+
+def build():
+    subprocess.check_call(["make", "-s", "-C", HERE])
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        i64, i32, vp, fp = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float
+        sz = ctypes.c_size_t
+        sig = {
+            "dcqo_block_size": (i64, [i32]),
+            "dcqo_type_size": (i64, [i32]),
+            "dcqo_row_size": (i64, [i32, i64]),
+            "dcqo_vec_dot_type": (i32, [i32]),
+            "dcqo_fp32_to_fp16": (ctypes.c_uint16, [fp]),
+            "dcqo_fp16_to_fp32": (fp, [ctypes.c_uint16]),
+            "dcqo_fp32_to_fp16_array": (None, [vp, vp, i64]),
+            "dcqo_fp16_to_fp32_array": (None, [vp, vp, i64]),
+            "dcqo_quantize_row_q8_0": (None, [vp, vp, i64, i32]),
+            "dcqo_quantize_row_q8_K": (None, [vp, vp, i64]),
+            "dcqo_quantize_rows": (None, [i32, vp, i64, i64, i64, vp, i32]),
+            "dcqo_quantize_matrix": (i32, [i32, vp, i64, i64, vp, i32]),
+            "dcqo_dequantize_row": (i32, [i32, vp, vp, i64]),
+            "dcqo_vec_dot": (fp, [i32, i64, vp, vp]),
+            "dcqo_vec_dot_f64": (ctypes.c_double, [i32, i64, vp, vp]),
+            "dcqo_vec_dot_l1": (ctypes.c_double, [i32, i64, vp, vp]),
+            "dcqo_block_sums_per_row": (i64, [i32, i64]),
+            "dcqo_block_sums": (i32, [i32, i64, vp, vp, vp]),
+            "dcqo_block_sums_bruteforce": (i32, [i32, i64, vp, vp, vp]),
+            "dcqo_dot_rows": (i32, [i32, vp, sz, vp, i64, vp, i64, i64]),
+            "dcqo_mul_mat": (i32, [i32, vp, i64, i64, sz, vp, i64, i64, vp, i64, vp, i32, i32]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def row_size(t, k):
+    return int(lib().dcqo_row_size(t, k))
+
+
+def block_size(t):
+    return int(lib().dcqo_block_size(t))
+
+
+def vec_dot_type(t):
+    return int(lib().dcqo_vec_dot_type(t))
+
+
+def fp32_to_fp16(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().dcqo_fp32_to_fp16_array(_p(x), _p(y), x.size)
+    return y
+
+
+def fp16_to_fp32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().dcqo_fp16_to_fp32_array(_p(h), _p(y), h.size)
+    return y
+
+
+def quantize_rows(vdt, x, variant=Q8_0_X86):
+    """Activation quantization of every row of x [m, k] -> uint8 [m, row_size]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    m, k = x.shape
+    rs = row_size(vdt, k)
+    assert rs > 0, (vdt, k)
+    y = np.zeros((m, rs), dtype=np.uint8)
+    lib().dcqo_quantize_rows(vdt, _p(x), m, k, k, _p(y), variant)
+    return y
+
+
+def quantize_matrix(t, w, nthreads=0):
+    """Weight quantization of w [n, k] -> uint8 [n, row_size] (rows packed)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    rs = row_size(t, k)
+    y = np.zeros((n, rs), dtype=np.uint8)
+    rc = lib().dcqo_quantize_matrix(t, _p(w), n, k, _p(y), nthreads)
+    assert rc == 0, rc
+    return y
+
+
+def dequantize_row(t, q, k):
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    y = np.empty(k, dtype=np.float32)
+    rc = lib().dcqo_dequantize_row(t, _p(q), _p(y), k)
+    assert rc == 0
+    return y
+
+
+def vec_dot(wt, k, w_row, xq_row):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
+    return float(lib().dcqo_vec_dot(wt, k, _p(w_row), _p(xq_row)))
+
+
+def vec_dot_f64(wt, k, w_row, xq_row):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
+    return float(lib().dcqo_vec_dot_f64(wt, k, _p(w_row), _p(xq_row)))
+
+
+def vec_dot_l1(wt, k, w_row, xq_row):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
+    return float(lib().dcqo_vec_dot_l1(wt, k, _p(w_row), _p(xq_row)))
+
+
+def block_sums_per_row(wt, k):
+    return int(lib().dcqo_block_sums_per_row(wt, k))
+
+
+def block_sums(wt, k, w_row, xq_row):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
+    out = np.zeros(block_sums_per_row(wt, k), dtype=np.int32)
+    assert lib().dcqo_block_sums(wt, k, _p(w_row), _p(xq_row), _p(out)) == 0
+    return out
+
+
+def block_sums_bruteforce(wt, k, w_row, xq_row):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
+    out = np.zeros(block_sums_per_row(wt, k), dtype=np.int64)
+    assert lib().dcqo_block_sums_bruteforce(wt, k, _p(w_row), _p(xq_row), _p(out)) == 0
+    return out
+
+
+def block_sums_matrix(wt, k, wq, xq):
+    """int32 [m, n, per_row] block sums of every (activation row, weight row)."""
+    m, n = xq.shape[0], wq.shape[0]
+    per = block_sums_per_row(wt, k)
+    out = np.zeros((m, n, per), dtype=np.int32)
+    for mi in range(m):
+        for ni in range(n):
+            out[mi, ni] = block_sums(wt, k, wq[ni], xq[mi])
+    return out
+
+
+def dot_rows(wt, wq, xq_row, k, n0, n1):
+    wq = np.ascontiguousarray(wq, dtype=np.uint8)
+    xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
+    y = np.zeros(max(n1 - n0, 0), dtype=np.float32)
+    rc = lib().dcqo_dot_rows(wt, _p(wq), wq.shape[1], _p(xq_row), k, _p(y), n0, n1)
+    assert rc == 0
+    return y
+
+
+def mul_mat(wt, wq, x, variant=Q8_0_X86, nthreads=0, want_l1=True):
+    """GGML_OP_MUL_MAT: Y[m, n] = vec_dot(W row n, quantize(X row m)); also L1 guard."""
+    wq = np.ascontiguousarray(wq, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    m, k = x.shape
+    n = wq.shape[0]
+    y = np.zeros((m, n), dtype=np.float32)
+    l1 = np.zeros((m, n), dtype=np.float32) if want_l1 else None
+    rc = lib().dcqo_mul_mat(wt, _p(wq), n, k, wq.shape[1], _p(x), m, k, _p(y), n,
+                            _p(l1) if want_l1 else None, variant, nthreads)
+    assert rc == 0, rc
+    return (y, l1) if want_l1 else y
+
+
+def assert_close(y, y_ref, l1, rtol=1e-4, what=""):
+    """The output tolerance: |y - y_ref| <= rtol * max(|y_ref|, L1), elementwise.
+
+    L1 = sum over blocks of |scale_b * int_b| guards outputs whose blocks cancel:
+    their fp32 rounding error scales with L1, not with |y_ref|.
+    """
+    y = np.asarray(y, dtype=np.float64)
+    y_ref = np.asarray(y_ref, dtype=np.float64)
+    bound = rtol * np.maximum(np.abs(y_ref), np.asarray(l1, dtype=np.float64))
+    err = np.abs(y - y_ref)
+    bad = err > bound
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {bad.size} outputs outside tolerance; first {idx.tolist()}: "
+            f"got {y[tuple(idx[0])]}, want {y_ref[tuple(idx[0])]}, bound {bound[tuple(idx[0])]}")
+    rel = err / np.maximum(np.abs(y_ref), 1e-30)
+    return float(np.max(err / np.maximum(bound / rtol, 1e-30))), float(np.median(rel))

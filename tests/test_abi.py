@@ -1,0 +1,110 @@
+"""The C ABI of libdcq without a GPU: symbols, type traits, argument validation.
+
+Validation runs on the host before any device call, so every error path here is
+exercised on the CPU; a well-formed call on a machine without a gfx950 device
+must fail loudly with DCQ_ERR_NO_DEVICE (no CPU fallback).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+import densecore_amd as dc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+OK, INVALID, UNSUPPORTED, BAD_SHAPE, MISALIGNED, WORKSPACE, HIP, NO_DEVICE = 0, -1, -2, -3, -4, -5, -6, -7
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "dcq.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dcq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = dc.lib()
+    names = declared_symbols()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(L, name), name
+    assert set(names) == set(dc._lib.SYMBOLS)
+
+
+def test_version_and_status_strings():
+    assert "gfx950" in dc.version()
+    for s in (OK, INVALID, UNSUPPORTED, BAD_SHAPE, MISALIGNED, WORKSPACE, HIP, NO_DEVICE):
+        assert dc._lib.status_string(s) != "unknown status"
+
+
+def test_type_traits_match_gguf():
+    assert [dc.block_size(t) for t in (0, 1, 8, 12, 14, 15, 2)] == [1, 1, 32, 256, 256, 256, 0]
+    assert [dc.type_size(t) for t in (0, 1, 8, 12, 14, 15)] == [4, 2, 34, 144, 210, 292]
+    assert dc.row_size(8, 1024) == 1088
+    assert dc.row_size(12, 2560) == 1440
+    assert dc.row_size(14, 9728) == 7980
+    assert dc.row_size(15, 2560) == 2920
+    assert dc.row_size(12, 100) == 0
+    assert [dc.vec_dot_type(t) for t in (8, 12, 14)] == [8, 15, 15]
+    assert dc.vec_dot_type(0) == UNSUPPORTED
+    assert dc.supports_mul_mat(12, 0, 0) and not dc.supports_mul_mat(12, 1, 0) and not dc.supports_mul_mat(2, 0, 0)
+    assert dc.block_sums_per_row(8, 1024) == 32
+    assert dc.block_sums_per_row(12, 2560) == 20
+    assert dc.block_sums_per_row(14, 9728) == 38
+
+
+def test_workspace_size():
+    # planar: int8 [M][K] + fp32 scales [K/bs][roundup(M, 64)] (+ int16 bsums [M][K/16] for Q8_K)
+    assert dc.mul_mat_workspace_size(8, 1, 1024) == 1024 + 32 * 64 * 4
+    assert dc.mul_mat_workspace_size(12, 64, 2048) == 64 * 2048 + 8 * 64 * 4 + 64 * 128 * 2
+    assert dc.mul_mat_workspace_size(12, 1, 100) == 0
+
+
+def _mm(wt=12, W=0x1000, N=16, K=256, wrb=None, X=0x2000, M=1, xs=None, Y=0x3000, ys=None, ws=None, wsb=0,
+        path=0, sums=None):
+    wrb = dc.row_size(wt, K) if wrb is None else wrb
+    xs = K * 4 if xs is None else xs
+    ys = N * 4 if ys is None else ys
+    return dc.lib().dcq_mul_mat_ex(wt, W, N, K, wrb, X, M, xs, Y, ys, ws, wsb, path, sums, None)
+
+
+def test_mul_mat_validation_order():
+    """Argument errors are reported before any device call."""
+    assert _mm(wt=2) == UNSUPPORTED
+    assert _mm(W=None) == INVALID
+    assert _mm(K=100) == BAD_SHAPE
+    assert _mm(N=0) == BAD_SHAPE
+    assert _mm(M=0) == BAD_SHAPE
+    assert _mm(wrb=100) == INVALID
+    assert _mm(xs=16) == INVALID
+    assert _mm(W=0x1004) == MISALIGNED
+    assert _mm(X=0x2004) == MISALIGNED
+    assert _mm(wt=12, wrb=152) == MISALIGNED  # Q4_K rows must keep 16-byte alignment
+    assert _mm(path=7) == INVALID
+    assert _mm(ws=0x4000, wsb=16) == WORKSPACE
+    assert _mm(ws=0x4010, wsb=1 << 20) == MISALIGNED
+
+
+def test_well_formed_call_without_gpu_fails_loudly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    assert _mm() == NO_DEVICE
+    assert dc.lib().dcq_quantize_rows(8, 0x1000, 1, 64, 256, 0x2000, None) == NO_DEVICE
+
+
+def test_dot_rows_and_quantize_validation():
+    L = dc.lib()
+    assert L.dcq_dot_rows(2, 0x1000, 64, 0x2000, 256, 0x3000, 0, 4, None) == UNSUPPORTED
+    assert L.dcq_dot_rows(12, 0x1000, 144, 0x2000, 256, 0x3000, 4, 2, None) == BAD_SHAPE
+    assert L.dcq_dot_rows(12, 0x1000, 144, 0x2000, 256, 0x3000, 3, 3, None) == OK  # empty range: no work
+    assert L.dcq_quantize_rows(12, 0x1000, 1, 256, 1024, 0x2000, None) == UNSUPPORTED
+    assert L.dcq_quantize_rows(15, 0x1000, 1, 100, 1024, 0x2000, None) == BAD_SHAPE
+    assert L.dcq_quantize_rows(15, 0x1004, 1, 256, 1024, 0x2000, None) == MISALIGNED
+    assert L.dcq_quantize_weights(15, 0x1000, 1, 256, 0x2000, None) == UNSUPPORTED
+    assert L.dcq_dequantize_rows(2, 0x1000, 1, 256, 64, 0x2000, None) == UNSUPPORTED
+
+
+def test_binding_raises_on_error():
+    with pytest.raises(dc.DcqError):
+        dc._lib._check("dcq_mul_mat", MISALIGNED)

@@ -1,0 +1,291 @@
+"""Pins of the CPU oracle (oracle/dcq_oracle.c) — no GPU.
+
+The reference has no golden vectors for this path (its tests never touch GGUF
+quant types), so each oracle function is pinned here by what the mathematics
+fixes: IEEE fp16 (numpy), closed forms and constructed ties, int64 brute force,
+fp64 dequantize-and-dot, and round-trip error bounds. Each test names the
+plausible mistake it would catch.
+"""
+import numpy as np
+import pytest
+
+from densecore_amd import synth
+
+Q8_0, Q4_K, Q6_K, Q8_K = 8, 12, 14, 15
+
+
+# ---------------------------------------------------------------- format parsers (GGUF spec)
+def parse_q8_0(row, k):
+    b = np.frombuffer(np.ascontiguousarray(row).tobytes(), dtype=np.uint8).reshape(k // 32, 34)
+    d = b[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    qs = b[:, 2:].copy().view(np.int8)
+    return d, qs
+
+
+def parse_q8_K(row, k):
+    b = np.frombuffer(np.ascontiguousarray(row).tobytes(), dtype=np.uint8).reshape(k // 256, 292)
+    d = b[:, 0:4].copy().view(np.float32).reshape(-1)
+    qs = b[:, 4:260].copy().view(np.int8)
+    bsums = b[:, 260:292].copy().view(np.int16)
+    return d, qs, bsums
+
+
+# ---------------------------------------------------------------- fp16
+def test_fp16_matches_numpy_random(O):
+    """RNE fp32->fp16 against numpy (catches truncation, wrong subnormal shift, overflow)."""
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(1 << 20) * np.exp(rng.uniform(-25, 12, 1 << 20))).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(O.fp32_to_fp16(x), want)
+
+
+def test_fp16_ties_and_specials(O):
+    """Exact midpoints between adjacent fp16 values (normal and subnormal) round to even."""
+    h = np.arange(0, 0x7BFF, dtype=np.uint16)
+    lo = h.view(np.float16).astype(np.float64)
+    hi = (h + 1).view(np.float16).astype(np.float64)
+    mid = ((lo + hi) / 2).astype(np.float32)  # exactly representable in fp32
+    assert np.all(mid.astype(np.float64) == (lo + hi) / 2)
+    want = mid.astype(np.float16).view(np.uint16)
+    got = O.fp32_to_fp16(mid)
+    assert np.array_equal(got, want)
+    assert np.all(got % 2 == 0)  # ties go to the even neighbour
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, 65504.0, 65519.99, 65520.0, 6e-8, 2.9e-8, 3.0e-8, 1e-45],
+                        dtype=np.float32)
+    with np.errstate(over="ignore"):
+        assert np.array_equal(O.fp32_to_fp16(specials), specials.astype(np.float16).view(np.uint16))
+    allh = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    f = allh.view(np.float16).astype(np.float32)
+    ok = ~np.isnan(f)
+    assert np.array_equal(O.fp16_to_fp32(allh)[ok].view(np.uint32), f[ok].view(np.uint32))
+
+
+# ---------------------------------------------------------------- Q8_0 activation quantizer
+def test_q8_0_zero_block_and_single_nonzero(O):
+    x = np.zeros(64, np.float32)
+    x[40] = -3.0  # second block: single non-zero
+    q = O.quantize_rows(Q8_0, x, O.Q8_0_X86)[0]
+    d, qs = parse_q8_0(q, 64)
+    assert d[0] == 0 and not qs[0].any()
+    assert np.float16(d[1]) == np.float16(np.float32(3.0) / np.float32(127))
+    assert qs[1][8] == -127 and np.count_nonzero(qs[1]) == 1
+
+
+def test_q8_0_x86_vs_ref_ties(O):
+    """amax = 127 makes id = 1 exactly; x = k + 0.5 is an exact tie: the x86 SIMD form rounds
+    half to even, quantize_row_q8_0_ref rounds half away from zero."""
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:7] = [2.5, -2.5, 3.5, -0.5, 0.5, 126.5]
+    _, qx = parse_q8_0(O.quantize_rows(Q8_0, x, O.Q8_0_X86)[0], 32)
+    _, qr = parse_q8_0(O.quantize_rows(Q8_0, x, O.Q8_0_REF)[0], 32)
+    assert list(qx[0][:7]) == [127, 2, -2, 4, 0, 0, 126]
+    assert list(qr[0][:7]) == [127, 3, -3, 4, -1, 1, 127]
+
+
+def test_q8_0_invariants_random(O):
+    """max|q| = 127 in every non-zero block; |x - d*q| <= d/2 (with the fp16 rounding of d)."""
+    x = synth.normal(32 * 4096, 7).reshape(64, -1)
+    q = O.quantize_rows(Q8_0, x, O.Q8_0_X86)
+    for r in range(x.shape[0]):
+        d, qs = parse_q8_0(q[r], x.shape[1])
+        xb = x[r].reshape(-1, 32)
+        amax = np.abs(xb).max(axis=1)
+        assert np.all(np.abs(qs).max(axis=1) == 127)
+        dexact = amax / 127.0
+        err = np.abs(xb - qs * dexact[:, None])
+        assert np.all(err <= dexact[:, None] * 0.5 * (1 + 1e-5))
+        assert np.all(np.abs(d - dexact) <= dexact * 2.0 ** -11)
+
+
+# ---------------------------------------------------------------- Q8_K activation quantizer
+def test_q8_K_extreme_first_occurrence_and_sign(O):
+    """The first element of largest |x| sets the scale and maps to -127 (catches taking the
+    last occurrence, or |max| instead of the signed extreme)."""
+    x = np.zeros(256, np.float32)
+    x[3], x[10], x[200] = -5.0, 5.0, 1.0
+    d, qs, bs = parse_q8_K(O.quantize_rows(Q8_K, x)[0], 256)
+    assert qs[0][3] == -127 and qs[0][10] == 127
+    iscale = np.float32(-127.0) / np.float32(-5.0)
+    assert d[0] == np.float32(1.0) / iscale
+    assert qs[0][200] == np.rint(np.float32(iscale) * np.float32(1.0))
+    x2 = x.copy()
+    x2[3], x2[10] = 5.0, -5.0
+    _, qs2, _ = parse_q8_K(O.quantize_rows(Q8_K, x2)[0], 256)
+    assert qs2[0][3] == -127 and qs2[0][10] == 127
+
+
+def test_q8_K_zero_block_bsums_and_bounds(O):
+    x = synth.normal(256 * 64, 8)
+    synth.set_outliers(x, 97, 20.0, 9)
+    x[256:512] = 0.0
+    q = O.quantize_rows(Q8_K, x)[0]
+    d, qs, bs = parse_q8_K(q, x.size)
+    assert d[1] == 0 and not qs[1].any() and not bs[1].any()
+    assert np.array_equal(bs, qs.reshape(-1, 16, 16).sum(axis=2).astype(np.int16))
+    xb = x.reshape(-1, 256)
+    nz = d != 0
+    err = np.abs(xb[nz] - qs[nz] * d[nz, None])
+    assert np.all(err <= np.abs(d[nz, None]) * 0.5 * (1 + 1e-5))
+    assert np.all(np.abs(qs[nz]).max(axis=1) == 127)
+    # the signed extreme maps to exactly -127
+    first = np.argmax(np.abs(xb), axis=1)
+    assert np.all(qs[nz, first[nz]] == -127)
+
+
+# ---------------------------------------------------------------- integer block sums
+@pytest.mark.parametrize("wt,k", [(Q8_0, 1024), (Q4_K, 2560), (Q6_K, 2048)])
+def test_block_sums_match_bruteforce(O, wt, k):
+    """Structured (ggml loop order, bsums for Q4_K mins) vs element-wise int64 brute force."""
+    w = synth.normal(6 * k, 11, 0, 0.02).reshape(6, k)
+    w[1, :256] = 0.0
+    wq = O.quantize_matrix(wt, w)
+    x = synth.normal(3 * k, 12).reshape(3, k)
+    synth.set_outliers(x[2], 20, 20.0, 13)
+    xq = O.quantize_rows(O.vec_dot_type(wt), x)
+    for n in range(6):
+        for m in range(3):
+            bs = O.block_sums(wt, k, wq[n], xq[m])
+            bf = O.block_sums_bruteforce(wt, k, wq[n], xq[m])
+            assert np.array_equal(bs.astype(np.int64), bf), (n, m)
+
+
+def test_block_sums_extreme_magnitudes(O):
+    """All-(-128)/127 activations with the largest weight codes stay exact in int32."""
+    k = 512
+    for wt in (Q8_0, Q4_K, Q6_K):
+        w = np.where(np.arange(k) % 2 == 0, 1.0, -1.0).astype(np.float32)[None, :] * 0.05
+        wq = O.quantize_matrix(wt, w)
+        x = np.full((1, k), -3.0, np.float32)
+        xq = O.quantize_rows(O.vec_dot_type(wt), x)
+        assert np.array_equal(O.block_sums(wt, k, wq[0], xq[0]).astype(np.int64),
+                              O.block_sums_bruteforce(wt, k, wq[0], xq[0]))
+
+
+# ---------------------------------------------------------------- vec_dot vs fp64
+@pytest.mark.parametrize("wt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2560), (Q6_K, 9728)])
+def test_vec_dot_matches_fp64(O, wt, k):
+    """The fp32 vec_dot is within fp32 rounding of the exact dequantized dot (catches a dropped
+    mins term, a wrong scale index, a sign error)."""
+    w = synth.normal(8 * k, 21, 0, 0.02).reshape(8, k)
+    wq = O.quantize_matrix(wt, w)
+    x = synth.normal(k, 22)
+    xq = O.quantize_rows(O.vec_dot_type(wt), x)[0]
+    for n in range(8):
+        v = O.vec_dot(wt, k, wq[n], xq)
+        v64 = O.vec_dot_f64(wt, k, wq[n], xq)
+        l1 = O.vec_dot_l1(wt, k, wq[n], xq)
+        assert abs(v - v64) <= 1e-5 * max(abs(v64), l1), (n, v, v64, l1)
+
+
+def test_vec_dot_approximates_float_dot(O):
+    """The quantized dot is close to the float dot of the original data (catches an element
+    permutation that is consistent between dequantize and vec_dot but wrong)."""
+    k = 4096
+    for wt, tol in ((Q8_0, 0.02), (Q6_K, 0.05), (Q4_K, 0.15)):
+        w = synth.normal(16 * k, 31, 0, 0.02).reshape(16, k)
+        x = synth.normal(k, 32)
+        wq = O.quantize_matrix(wt, w)
+        xq = O.quantize_rows(O.vec_dot_type(wt), x)[0]
+        got = np.array([O.vec_dot(wt, k, wq[n], xq) for n in range(16)])
+        want = w.astype(np.float64) @ x.astype(np.float64)
+        rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+        assert rel < tol, (wt, rel)
+
+
+# ---------------------------------------------------------------- weight quantizers (round trip)
+@pytest.mark.parametrize("wt,bound", [(Q8_0, 0.006), (Q6_K, 0.03), (Q4_K, 0.11)])
+def test_weight_quantizer_round_trip(O, wt, bound):
+    k = 2048
+    w = synth.normal(32 * k, 41, 0, 0.02).reshape(32, k)
+    wq = O.quantize_matrix(wt, w)
+    deq = np.stack([O.dequantize_row(wt, wq[n], k) for n in range(32)])
+    rel = np.sqrt(((deq - w) ** 2).mean()) / 0.02
+    assert rel < bound, rel
+
+
+def test_q8_0_weight_dequant_closed_form(O):
+    k = 256
+    w = synth.normal(k, 42, 0, 0.02)[None, :]
+    wq = O.quantize_matrix(Q8_0, w)
+    d, qs = parse_q8_0(wq[0], k)
+    assert np.array_equal(O.dequantize_row(Q8_0, wq[0], k), (qs * d[:, None]).reshape(-1).astype(np.float32))
+
+
+def test_q4_K_element_layout_constructed(O):
+    """A hand-packed Q4_K block (d = 1, dmin = 0, distinct 6-bit scales incl. j >= 4) dequantizes
+    to sc_j * q with q read from the documented nibble positions."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([1.0], np.float16).view(np.uint8)   # d
+    blk[2:4] = np.array([0.0], np.float16).view(np.uint8)   # dmin
+    sc = [1, 2, 3, 4, 37, 45, 50, 63]
+    for j in range(4):
+        blk[4 + j] = sc[j]
+    for j in range(4, 8):
+        blk[4 + j + 4] = sc[j] & 0xF
+        blk[4 + j - 4] |= (sc[j] >> 4) << 6
+    q = np.arange(256) % 16
+    for c in range(4):
+        for l in range(32):
+            blk[16 + 32 * c + l] = q[64 * c + l] | (q[64 * c + 32 + l] << 4)
+    got = O.dequantize_row(Q4_K, blk, 256)
+    want = np.array([sc[e // 32] * q[e] for e in range(256)], np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_q6_K_element_layout_constructed(O):
+    """A hand-packed Q6_K block: element e has quant (e * 7) % 64 and scale (g + 1) * (-1)^g."""
+    q = (np.arange(256) * 7) % 64
+    sc = np.array([(g + 1) * (-1) ** g for g in range(16)], np.int8)
+    blk = np.zeros(210, np.uint8)
+    for e in range(256):
+        h, ep = divmod(e, 128)
+        t, l = divmod(ep, 32)
+        blk[64 * h + l + 32 * (t & 1)] |= (q[e] & 0xF) << (4 * (t >> 1))
+        blk[128 + 32 * h + l] |= (q[e] >> 4) << (2 * t)
+    blk[192:208] = sc.view(np.uint8)
+    blk[208:210] = np.array([0.5], np.float16).view(np.uint8)
+    got = O.dequantize_row(Q6_K, blk, 256)
+    want = np.array([0.5 * sc[e // 16] * (q[e] - 32) for e in range(256)], np.float32)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- mul_mat driver
+def test_mul_mat_one_hot_columns(O):
+    """X = one-hot rows picks columns of the dequantized W (scaled by the Q8 code of 1.0)."""
+    k, n = 512, 12
+    for wt in (Q8_0, Q4_K, Q6_K):
+        w = synth.normal(n * k, 51, 0, 0.02).reshape(n, k)
+        wq = O.quantize_matrix(wt, w)
+        deq = np.stack([O.dequantize_row(wt, wq[r], k) for r in range(n)])
+        cols = [0, 31, 255, 300, 511]
+        x = np.zeros((len(cols), k), np.float32)
+        for i, c in enumerate(cols):
+            x[i, c] = 1.0
+        y, _ = O.mul_mat(wt, wq, x)
+        xq = O.quantize_rows(O.vec_dot_type(wt), x)
+        for i, c in enumerate(cols):
+            if wt == Q8_0:
+                d, qs = parse_q8_0(xq[i], k)
+                scale = d[c // 32] * qs[c // 32][c % 32]
+            else:
+                d, qs, _ = parse_q8_K(xq[i], k)
+                scale = d[c // 256] * qs[c // 256][c % 256]
+            np.testing.assert_allclose(y[i], deq[:, c] * scale, rtol=1e-5, atol=1e-7)
+
+
+def test_mul_mat_rows_and_dot_rows(O):
+    """Y[m, n] = vec_dot(W row n, Xq row m); dot_rows writes y[r - n0] (simd_ops.cpp:140-171)."""
+    k, n = 768, 20
+    w = synth.normal(n * k, 61, 0, 0.02).reshape(n, k)
+    wq = O.quantize_matrix(Q6_K, np.pad(w, ((0, 0), (0, 256)))[:, :768])
+    x = synth.normal(3 * k, 62).reshape(3, k)
+    y, l1 = O.mul_mat(Q6_K, wq, x)
+    xq = O.quantize_rows(Q8_K, x)
+    for m in range(3):
+        for r in range(n):
+            assert y[m, r] == O.vec_dot(Q6_K, k, wq[r], xq[m])
+            assert l1[m, r] == np.float32(O.vec_dot_l1(Q6_K, k, wq[r], xq[m]))
+    part = O.dot_rows(Q6_K, wq, xq[1], k, 5, 17)
+    assert np.array_equal(part, y[1, 5:17])
