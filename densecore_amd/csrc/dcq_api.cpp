@@ -182,6 +182,13 @@ int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_
     rc = check_device();
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
+    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= 8);
+    if (use_gemv) {
+        // decode: the activation quantization runs inside the GEMV kernel where it can
+        hipError_t e = launch_decode_fused(wtype, W, (int64_t)w_row_bytes, N, K, X, (int64_t)(x_stride_bytes / 4), M,
+                                           Y, (int64_t)(y_stride_bytes / 4), block_sums, st);
+        if (e != hipErrorNotSupported) return hip_status(e);
+    }
     void* ws = workspace;
     if (!ws) {
         if (hipMallocAsync(&ws, need, st) != hipSuccess) return DCQ_ERR_HIP;
@@ -191,7 +198,6 @@ int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
     if (e == hipSuccess) {
         const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
-        const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= 8);
         if (use_gemv)
             e = launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, block_sums, N, st);
         else

@@ -124,4 +124,67 @@ __device__ __forceinline__ void ld16_a2(const uint8_t* p, uint32_t out[4]) {
     out[3] = align_bytes(w4, w.w, sh);
 }
 
+// ---- cross-lane reductions inside a 16-lane DPP row (no LDS traffic) ----
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror: after the four
+// steps every lane of the row holds the reduction over its 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));
+    return v;
+}
+__device__ __forceinline__ int row16_min(int v) {
+    v = min(v, dpp_mov<0xB1>(v));
+    v = min(v, dpp_mov<0x4E>(v));
+    v = min(v, dpp_mov<0x141>(v));
+    v = min(v, dpp_mov<0x140>(v));
+    return v;
+}
+
+// One Q8_K superblock (quantize_row_q8_K_ref semantics) quantized by the 16 lanes of a
+// DPP row; lane g (= lane % 16) holds elements 16g .. 16g+15 in x[16]. Returns the lane's
+// 16 quantized bytes (4 dwords), the sum of its 16-element group (bsums[g]) and d.
+//   max = first element of largest |x| (strict '>' scan); iscale = -127/max;
+//   q = min(127, round-half-even(iscale*x)); d = 1/iscale; an all-zero block is all zero.
+// max |x| and the first index holding it do not depend on the reduction order, so the
+// bytes equal the sequential scan's.
+__device__ __forceinline__ void quantize_q8k_row16(const float (&x)[16], int g, uint32_t (&packed)[4], int& bsum,
+                                                   float& dval) {
+    float best = -1.0f;
+    int bkey = 0;  // (index << 1) | sign of this lane's first maximum
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const float a = fabsf(x[j]);
+        if (a > best) {
+            best = a;
+            bkey = ((16 * g + j) << 1) | (int)(__float_as_uint(x[j]) >> 31);
+        }
+    }
+    const float amax = row16_max(best);
+    // the smallest index holding the maximum wins
+    const int key = (best == amax) ? bkey : 0x7FFFFFFF;
+    const int win = row16_min(key);
+    const float maxv = (win & 1) ? -amax : amax;
+    bsum = 0;
+    dval = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) packed[i] = 0u;
+    if (amax != 0.0f) {
+        const float iscale = -127.f / maxv;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int qv = (int)__builtin_rintf(iscale * x[j]);
+            qv = qv < 127 ? qv : 127;
+            bsum += qv;
+            packed[j >> 2] |= ((uint32_t)qv & 0xFFu) << (8 * (j & 3));
+        }
+        dval = 1.0f / iscale;
+    }
+}
+
 }  // namespace dcq

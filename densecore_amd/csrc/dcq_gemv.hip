@@ -342,6 +342,11 @@ static int env_int(const char* name, int dflt) {
 hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                        const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                        int64_t sums_n_stride, hipStream_t st) {
+    if (wtype == kTypeQ4_K && env_int("DCQ_GEMV_GENERIC", 0) == 0) {
+        const hipError_t e = launch_decode_q4k(W, w_row_bytes, n0, n1, K, act, M, Y, y_stride, block_sums,
+                                               sums_n_stride, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     int f;
     if (wtype == kTypeQ8_0)
         f = (K % 64 == 0 && w_row_bytes % 4 == 0) ? kQ8_0Pair : kQ8_0Single;

@@ -8,7 +8,8 @@
 //     q = round-half-even(x*id) (v_rndne_f32 of the rounded product).
 //   Q8_K (quantize_row_q8_K_ref): max = first element of largest |x|;
 //     iscale = -127/max; q = min(127, round-half-even(iscale*x)); d = 1/iscale;
-//     bsums[g] = sum of q[16g..16g+15]; an all-zero block is all zero.
+//     bsums[g] = sum of q[16g..16g+15]; an all-zero block is all zero. 16 lanes per
+//     superblock, reduced with DPP (quantize_q8k_row16).
 // Memory-bound: reads 4 B and writes ~1.06 B (Q8_0) / ~1.14 B (Q8_K) per element.
 #include "dcq_common.h"
 #include "dcq_kernels.h"
@@ -65,7 +66,7 @@ __global__ void __launch_bounds__(256) quantize_q8_0_kernel(const float* __restr
     }
 }
 
-// ---- Q8_K: one wave per 256-element superblock, 4 floats per lane ----
+// ---- Q8_K: 16 lanes (one DPP row) per 256-element superblock, 16 floats per lane ----
 template <bool kPlanar>
 __global__ void __launch_bounds__(256) quantize_q8_K_kernel(const float* __restrict__ X, int64_t x_stride,
                                                             int64_t M, int64_t K, uint8_t* __restrict__ out,
@@ -73,68 +74,43 @@ __global__ void __launch_bounds__(256) quantize_q8_K_kernel(const float* __restr
                                                             float* __restrict__ dpl, int16_t* __restrict__ bsp,
                                                             int64_t m_ld) {
     const int64_t nsb = K / QK_K;
-    const int lane = threadIdx.x & 63;
-    const int64_t sbg = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // global superblock
+    const int g = threadIdx.x & 15;
+    const int64_t sbg = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // global superblock
     const int64_t m = sbg / nsb;
     const int64_t s = sbg - m * nsb;
-    if (m >= m_ld) return;  // whole waves exit together
+    if (m >= m_ld) return;  // whole 16-lane rows exit together
     if (m >= M) {
-        if (kPlanar && lane == 0) dpl[s * m_ld + m] = 0.0f;
+        if (kPlanar && g == 0) dpl[s * m_ld + m] = 0.0f;
         return;
     }
-    const float4 v = *reinterpret_cast<const float4*>(X + m * x_stride + s * QK_K + lane * 4);
-    const float xs[4] = {v.x, v.y, v.z, v.w};
-    // first index of the largest |x| (the reference scans with a strict '>')
-    float best = -1.0f;
-    int bidx = 0;
+    const float4* xp = reinterpret_cast<const float4*>(X + m * x_stride + s * QK_K + 16 * g);
+    float x[16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float a = fabsf(xs[j]);
-        if (a > best) {
-            best = a;
-            bidx = lane * 4 + j;
-        }
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = xp[i];
+        x[4 * i] = v.x;
+        x[4 * i + 1] = v.y;
+        x[4 * i + 2] = v.z;
+        x[4 * i + 3] = v.w;
     }
-    float amax = best;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    int cand = (best == amax) ? bidx : 1 << 30;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) cand = min(cand, __shfl_xor(cand, o, 64));
-    float mine = xs[0];
-    const int slot = cand & 3;
-    mine = slot == 1 ? xs[1] : mine;
-    mine = slot == 2 ? xs[2] : mine;
-    mine = slot == 3 ? xs[3] : mine;
-    const float maxv = __shfl(mine, cand >> 2, 64);
-
-    uint32_t packed = 0u;
-    int bsum = 0;
-    float dval = 0.0f;
-    if (amax != 0.0f) {
-        const float iscale = -127.f / maxv;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            int qv = (int)__builtin_rintf(iscale * xs[j]);
-            qv = qv < 127 ? qv : 127;
-            bsum += qv;
-            packed |= ((uint32_t)qv & 0xFFu) << (8 * j);
-        }
-        dval = 1.0f / iscale;
-    }
-    // groups of 16 elements = 4 lanes
-    bsum += __shfl_xor(bsum, 1, 4);
-    bsum += __shfl_xor(bsum, 2, 4);
-    const int g = lane >> 2;
+    uint32_t packed[4];
+    int bsum;
+    float dval;
+    quantize_q8k_row16(x, g, packed, bsum, dval);
     if (kPlanar) {
-        *reinterpret_cast<uint32_t*>(qs + m * K + s * QK_K + lane * 4) = packed;
-        if ((lane & 3) == 0) bsp[m * (K / 16) + s * 16 + g] = (int16_t)bsum;
-        if (lane == 0) dpl[s * m_ld + m] = dval;
+        *reinterpret_cast<uint4*>(qs + m * K + s * QK_K + 16 * g) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+        bsp[m * (K / 16) + s * 16 + g] = (int16_t)bsum;
+        if (g == 0) dpl[s * m_ld + m] = dval;
     } else {
         uint8_t* blkp = out + m * out_row_bytes + s * (int64_t)sizeof(BlockQ8_K);
-        *reinterpret_cast<uint32_t*>(blkp + 4 + lane * 4) = packed;
-        if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(blkp + 4 + QK_K + 2 * g) = (int16_t)bsum;
-        if (lane == 0) *reinterpret_cast<float*>(blkp) = dval;
+        U32x4 w;
+        w.x = packed[0];
+        w.y = packed[1];
+        w.z = packed[2];
+        w.w = packed[3];
+        *reinterpret_cast<U32x4*>(blkp + 4 + 16 * g) = w;  // 4-byte aligned block
+        *reinterpret_cast<int16_t*>(blkp + 4 + QK_K + 2 * g) = (int16_t)bsum;
+        if (g == 0) *reinterpret_cast<float*>(blkp) = dval;
     }
 }
 
@@ -188,7 +164,7 @@ hipError_t launch_quantize_ggml(int vdt, const float* X, int64_t x_stride, int64
         hipLaunchKernelGGL(quantize_q8_0_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
                            (uint8_t*)out, out_row_bytes, (int8_t*)nullptr, (float*)nullptr, M);
     } else {
-        const int64_t threads = M * (K / QK_K) * 64;
+        const int64_t threads = M * (K / QK_K) * 16;
         const int64_t grid = (threads + 255) / 256;
         hipLaunchKernelGGL(quantize_q8_K_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
                            (uint8_t*)out, out_row_bytes, (int8_t*)nullptr, (float*)nullptr, (int16_t*)nullptr, M);
@@ -204,7 +180,7 @@ hipError_t launch_quantize_planar(int vdt, const float* X, int64_t x_stride, int
         hipLaunchKernelGGL(quantize_q8_0_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
                            (uint8_t*)nullptr, (int64_t)0, pb.qs, pb.d, pb.m_ld);
     } else {
-        const int64_t threads = pb.m_ld * (K / QK_K) * 64;
+        const int64_t threads = pb.m_ld * (K / QK_K) * 16;
         const int64_t grid = (threads + 255) / 256;
         hipLaunchKernelGGL(quantize_q8_K_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
                            (uint8_t*)nullptr, (int64_t)0, pb.qs, pb.d, pb.bs, pb.m_ld);

@@ -184,3 +184,21 @@ def test_baseline_config_parity(O, dev, cfg):
     # the GPU weight quantizer produces the same bytes as the oracle on the config shape
     if cfg.index in (1, 2, 3):
         assert np.array_equal(to_host(dc.quantize_weights(cfg.wtype, to_dev(w, dev))), wq)
+
+
+# ---------------------------------------------------------------- split operator (shared quantization)
+@pytest.mark.parametrize("path", [dc.PATH_AUTO, dc.PATH_GEMV, dc.PATH_MMQ])
+@pytest.mark.parametrize("wt,M,N,K", [(Q8_0, 1, 70, 1024), (Q4_K, 1, 96, 2560), (Q4_K, 5, 64, 2048),
+                                      (Q4_K, 8, 40, 768), (Q6_K, 3, 33, 1024)])
+def test_quantize_src1_then_mul_mat_q(O, dev, wt, M, N, K, path):
+    """dcq_quantize_src1 once, then dcq_mul_mat_q for two weights sharing X (ffn gate and up):
+    the planar-activation kernels, against the oracle."""
+    import torch
+    wq_a, x = make_inputs(O, wt, M, N, K, seed=11 + M)
+    wq_b, _ = make_inputs(O, wt, M, N, K, seed=12 + M)
+    ws = torch.empty(dc.mul_mat_workspace_size(wt, M, K), dtype=torch.uint8, device=dev)
+    dc.quantize_src1(wt, to_dev(x, dev), ws)
+    for wq in (wq_a, wq_b):
+        y = dc.mul_mat_q(wt, to_dev(wq, dev), N, K, ws, M, path=path)
+        y_ref, l1 = O.mul_mat(wt, wq, x)
+        O.assert_close(to_host(y), y_ref, l1, RTOL, what=f"split type {wt} M{M} path {path}")
