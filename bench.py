@@ -1,18 +1,24 @@
 #!/usr/bin/env python3
 """bench.py — DenseCore's quantized mul_mat hot path on one MI355X.
 
-A step is one pass of the hot path over one batch: quantize X (the
-vec_dot_type from_float) + the mul_mat kernel, Y[M, N] = W[N, K] . Xq[M, K]^T,
-on inputs already resident in HBM. Steps cycle through enough copies of W to
-exceed the 256 MB Infinity Cache, so every step streams its weights from HBM.
-Steps are captured in one HIP graph (torch.cuda.CUDAGraph around the C ABI
-calls) and replayed, so host launch overhead does not enter GPU time.
+A step is one dcq_mul_mat call over one batch: Y[M, N] = W[N, K] . quantize(X[M, K])^T
+(activation quantization to the vec_dot_type + the int8 dots), on inputs already
+resident in HBM. Steps cycle through enough copies of W (1 GiB) to exceed the 256 MB
+Infinity Cache, so every step streams its weights from HBM. Steps are captured in
+one HIP graph (torch.cuda.CUDAGraph around the C ABI calls) and replayed, so host
+launch overhead does not enter GPU time; HIP events on the replay stream time them.
 
-Printed: one JSON line. `value` is the headline configuration's
-(Q4_K GEMV, M = 1) weight GB/s over whole steps; every
-configuration is listed under "configs" with its kernel-only rate and roofline
-fraction. The CPU baseline is the oracle's restatement of the reference CPU path
-(quantize once, row-partitioned vec_dot, threaded), timed on this host.
+Printed: one JSON line. `value` is the headline configuration's (
+Q4_K GEMV, M = 1) weight GB/s over whole steps. `roofline` is for the dominant kernel
+of that step: the whole step when it is one kernel (decode with fused activation
+quantization), else the mul_mat kernel timed alone on pre-quantized activations.
+Every configuration is listed under "configs". The CPU baseline is the oracle's
+restatement of the reference CPU path (quantize once, row-partitioned vec_dot,
+threaded), timed on this host on a bounded sample.
+
+--profile runs the same steps eagerly (no graph) followed by a device-to-device copy
+of known size, for rocprofv3 counter passes (the copy calibrates FETCH_SIZE /
+WRITE_SIZE); it prints no JSON line.
 """
 import argparse
 import json
@@ -43,6 +49,7 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--replays", type=int, default=3)
+    ap.add_argument("--profile", action="store_true", help="eager steps + a calibration copy, for rocprofv3 --pmc")
     return ap.parse_args()
 
 
@@ -64,8 +71,33 @@ def make_config_inputs(cfg, dev):
     return wq, xd, {"w_f32": synth.digest(w), "x_f32": synth.digest(x)}
 
 
+def _graph_kernel_nodes(g):
+    """Kernel nodes in a captured graph (hipGraphGetNodes / hipGraphNodeGetType), or None."""
+    try:
+        import ctypes
+        import torch
+        raw = g.raw_cuda_graph()
+        hip = ctypes.CDLL(os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so"))
+        n = ctypes.c_size_t(0)
+        if hip.hipGraphGetNodes(ctypes.c_void_p(raw), None, ctypes.byref(n)) != 0:
+            return None
+        nodes = (ctypes.c_void_p * n.value)()
+        if hip.hipGraphGetNodes(ctypes.c_void_p(raw), nodes, ctypes.byref(n)) != 0:
+            return None
+        kinds = ctypes.c_int(0)
+        kernels = 0
+        for i in range(n.value):
+            if hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(kinds)) == 0 and kinds.value == 0:
+                kernels += 1
+        return kernels
+    except Exception:  # introspection is best-effort: timing does not depend on it
+        return None
+
+
 def time_graph(fn_steps, steps, warmup, replays):
-    """Capture `steps` calls into one graph; return (mean ms per step, stream)."""
+    """Capture `steps` calls into one graph and replay it; return (mean ms per step, kernels per step).
+
+    The events are recorded on the stream the graph replays on (the kernels' stream)."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -73,11 +105,15 @@ def time_graph(fn_steps, steps, warmup, replays):
         for i in range(warmup):  # eager warmup (also loads the kernels)
             fn_steps(i)
     torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
+    try:
+        g = torch.cuda.CUDAGraph(keep_graph=True)
+    except TypeError:
+        g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         for i in range(steps):
             fn_steps(i)
     torch.cuda.synchronize()
+    kernels = _graph_kernel_nodes(g)
     g.replay()  # warm replay
     torch.cuda.synchronize()
     times = []
@@ -92,7 +128,28 @@ def time_graph(fn_steps, steps, warmup, replays):
         torch.cuda.synchronize()
         times.append(e0.elapsed_time(e1) / steps)
     del g
-    return float(np.median(times))
+    return float(np.median(times)), (kernels / steps if kernels is not None else None)
+
+
+def load_traffic(cfg_index):
+    """HBM bytes per launch of a config's dominant kernel from the committed PMC summary
+    (profiles/traffic.txt: FETCH_SIZE / WRITE_SIZE in KiB per dispatch, each scaled by the
+    same counter's reading for a device copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("#") or not line.strip():
+                continue
+            kv = dict(tok.split("=", 1) for tok in line.split() if "=" in tok)
+            if kv.get("config") == str(cfg_index):
+                try:
+                    return (float(kv["fetch_kib"]) * 1024 * float(kv["fetch_scale"]) +
+                            float(kv["write_kib"]) * 1024 * float(kv["write_scale"]))
+                except (KeyError, ValueError):
+                    return None
+    return None
 
 
 def bench_config(cfg, args, dev):
@@ -117,45 +174,70 @@ def bench_config(cfg, args, dev):
         dc.mul_mat_q(cfg.wtype, big[i % copies], cfg.N, cfg.K, ws, cfg.M, y=y,
                      stream=torch.cuda.current_stream().cuda_stream)
 
-    step_ms = time_graph(step, args.steps, args.warmup, args.replays)
-    dc.quantize_src1(cfg.wtype, x, ws)
-    torch.cuda.synchronize()
-    kern_ms = time_graph(kernel_only, args.steps, args.warmup, args.replays)
+    step_ms, step_kernels = time_graph(step, args.steps, args.warmup, args.replays)
+    if step_kernels == 1:
+        # the whole step is one kernel (decode with the activation quantization fused in)
+        dom_ms, dom = step_ms, "decode kernel with fused activation quantization (the whole step)"
+    else:
+        dc.quantize_src1(cfg.wtype, x, ws)
+        torch.cuda.synchronize()
+        dom_ms, _ = time_graph(kernel_only, args.steps, args.warmup, args.replays)
+        dom = "mul_mat kernel on pre-quantized activations (dcq_mul_mat_q)"
 
-    xq_bytes = dc.mul_mat_workspace_size(cfg.wtype, cfg.M, cfg.K)
     ops = 2.0 * cfg.M * cfg.N * cfg.K
     boundary = wbytes + cfg.M * cfg.K * 4 + cfg.M * cfg.N * 4
-    kernel_name = "gemv_kernel" if cfg.M <= 8 else "mmq_kernel"
     out = {
         "config": cfg.index, "name": cfg.name, "type": dc.TYPE_NAMES[cfg.wtype], "M": cfg.M, "N": cfg.N, "K": cfg.K,
-        "w_bytes": wbytes, "w_copies": copies, "step_us": step_ms * 1e3, "kernel_us": kern_ms * 1e3,
-        "kernel": kernel_name, "digests": digests,
+        "w_bytes": wbytes, "boundary_bytes": boundary, "w_copies": copies, "step_us": step_ms * 1e3,
+        "kernels_per_step": step_kernels, "dominant_kernel": dom, "dominant_us": dom_ms * 1e3,
+        "weight_GBps_step": wbytes / (step_ms * 1e-3) / 1e9,
+        "boundary_GBps_step": boundary / (step_ms * 1e-3) / 1e9,
+        "TOPS_step": ops / (step_ms * 1e-3) / 1e12, "digests": digests,
     }
+    traffic = load_traffic(cfg.index)
     if cfg.bound == "hbm":
-        achieved = wbytes / (kern_ms * 1e-3) / 1e9
-        out.update({
-            "weight_GBps_step": wbytes / (step_ms * 1e-3) / 1e9,
-            "weight_GBps_kernel": achieved,
-            "boundary_GBps_step": boundary / (step_ms * 1e-3) / 1e9,
-            "TOPS_kernel": ops / (kern_ms * 1e-3) / 1e12,
-            "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                         "algorithmic_bytes_per_launch": wbytes},
-        })
+        achieved = wbytes / (dom_ms * 1e-3) / 1e9
+        out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                           "algorithmic_bytes_per_launch": wbytes}
     else:
-        achieved = ops / (kern_ms * 1e-3) / 1e12
-        out.update({
-            "TOPS_step": ops / (step_ms * 1e-3) / 1e12,
-            "TOPS_kernel": achieved,
-            "weight_GBps_step": wbytes / (step_ms * 1e-3) / 1e9,
-            "roofline": {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                         "frac": achieved / INT8_PEAK_TOPS, "traffic": None,
-                         "algorithmic_ops_per_launch": ops},
-        })
-    out["xq_workspace_bytes"] = xq_bytes
+        achieved = ops / (dom_ms * 1e-3) / 1e12
+        out["roofline"] = {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                           "frac": achieved / INT8_PEAK_TOPS, "traffic": traffic,
+                           "algorithmic_ops_per_launch": ops}
     del big, ws, y, x, wq
     torch.cuda.empty_cache()
     return out
+
+
+def profile_config(cfg, args, dev):
+    """Eager steps of one config (counter collection needs plain dispatches)."""
+    import torch
+    import densecore_amd as dc
+    wq, x, _ = make_config_inputs(cfg, dev)
+    rb = dc.row_size(cfg.wtype, cfg.K)
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / (cfg.N * rb))))
+    big = torch.empty((copies, cfg.N, rb), dtype=torch.uint8, device=dev)
+    for r in range(copies):
+        big[r].copy_(wq)
+    ws = torch.empty(dc.mul_mat_workspace_size(cfg.wtype, cfg.M, cfg.K), dtype=torch.uint8, device=dev)
+    y = torch.empty((cfg.M, cfg.N), dtype=torch.float32, device=dev)
+    for i in range(args.warmup + args.steps):
+        dc.mul_mat(cfg.wtype, big[i % copies], cfg.N, cfg.K, x, y=y, workspace=ws)
+    torch.cuda.synchronize()
+    print(f"# profiled config {cfg.index}: {args.warmup + args.steps} eager steps", file=sys.stderr, flush=True)
+    del big, ws, y, x, wq
+    torch.cuda.empty_cache()
+
+
+def calibration_copy(dev, nbytes=64 << 20):
+    """One device-to-device copy of nbytes: the known-size kernel the traffic counters are scaled by."""
+    import torch
+    src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"# calibration copy: {nbytes} bytes read, {nbytes} bytes written", file=sys.stderr, flush=True)
 
 
 def cpu_baseline(cfg, seconds, threads):
@@ -200,19 +282,25 @@ def main():
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(0)
     wanted = [int(c) for c in args.configs.split(",") if c.strip()]
+    if args.profile:
+        for c in dc.CONFIGS:
+            if c.index in wanted:
+                profile_config(c, args, dev)
+        calibration_copy(dev)
+        return 0
     results = []
     for c in dc.CONFIGS:
         if c.index in wanted:
             r = bench_config(c, args, dev)
             results.append(r)
-            print(f"# config {c.index} {c.name}: step {r['step_us']:.2f} us, kernel {r['kernel_us']:.2f} us, "
-                  f"roofline {r['roofline']['achieved']:.1f} {r['roofline']['unit']} "
-                  f"({100 * r['roofline']['frac']:.1f} %)", file=sys.stderr, flush=True)
+            print(f"# config {c.index} {c.name}: step {r['step_us']:.2f} us ({r['kernels_per_step']} kernels), "
+                  f"dominant kernel {r['dominant_us']:.2f} us, roofline {r['roofline']['achieved']:.1f} "
+                  f"{r['roofline']['unit']} ({100 * r['roofline']['frac']:.1f} %)", file=sys.stderr, flush=True)
     head = next((r for r in results if r["config"] == HEADLINE), results[0])
     hcfg = dc.by_index(head["config"])
     line = {
         "metric": METRIC,
-        "value": head.get("weight_GBps_step", head.get("TOPS_step")),
+        "value": head["weight_GBps_step"] if hcfg.bound == "hbm" else head["TOPS_step"],
         "unit": "GB/s" if hcfg.bound == "hbm" else "TOPS",
         "n_gpus": 1,
         "steps": args.steps,
@@ -224,8 +312,9 @@ def main():
         "dtype": "int8",
         "data": "synthetic (seeded SplitMix64/Box-Muller; W quantized on the GPU by dcq_quantize_weights)",
         "config": {"workload": f"config {hcfg.index}: {dc.TYPE_NAMES[hcfg.wtype]} mul_mat M={hcfg.M} "
-                               f"N={hcfg.N} K={hcfg.K} ({hcfg.name}), quantize + kernel per step, "
-                               f"W rotated over {head['w_copies']} copies",
+                               f"N={hcfg.N} K={hcfg.K} ({hcfg.name}); a step is one dcq_mul_mat call "
+                               f"(activation quantization + dots, {head['kernels_per_step']} kernel(s)); "
+                               f"W rotated over {head['w_copies']} copies ({head['w_copies'] * head['w_bytes'] >> 20} MiB)",
                    "M": hcfg.M, "N": hcfg.N, "K": hcfg.K, "type": dc.TYPE_NAMES[hcfg.wtype]},
         "roofline": head["roofline"],
         "device": props.name, "gcn_arch": getattr(props, "gcnArchName", ""), "host": platform.node(),
