@@ -16,7 +16,7 @@ namespace dcq {
 
 size_t planar_bytes(int vdt, int64_t M, int64_t K, PlanarBuffers* pb, void* base) {
     const int64_t bs = vdt == kTypeQ8_0 ? QK8_0 : QK_K;
-    const int64_t m_ld = round_up(M, 64);  // >= every MMQ m-tile, so float4 scale loads stay in bounds
+    const int64_t m_ld = round_up(M, 128);  // >= every MFMA m-tile, so float4 scale loads stay in bounds
     const size_t qs_b = (size_t)round_up(M * K, 256);
     const size_t d_b = (size_t)round_up((K / bs) * m_ld * 4, 256);
     const size_t bs_b = vdt == kTypeQ8_K ? (size_t)round_up(M * (K / 16) * 2, 256) : 0;

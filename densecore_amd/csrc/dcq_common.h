@@ -14,7 +14,7 @@
 // the ggml block array; dcq_quantize_rows still emits the ggml bytes.
 //   qs : int8  [M][K]                 row m at qs + m*K (K % 32 == 0, so rows stay 16-B aligned)
 //   d  : float [K/bs][M_ld]           block-major scales (fp16 d widened exactly for Q8_0,
-//                                     fp32 d for Q8_K); M_ld = M rounded up to 64, rows
+//                                     fp32 d for Q8_K); M_ld = M rounded up to 128, rows
 //                                     M..M_ld-1 hold 0
 //   bs : int16 [M][K/16]              Q8_K bsums (sum of 16 consecutive qs)
 #pragma once

@@ -487,6 +487,10 @@ static MmqFn pick(int wtype, const MmqShape& s) {
 
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                       int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+    if (wtype == kTypeQ8_0 && M > 32) {
+        const hipError_t e = launch_prefill_q8_0(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     MmqShape s;
     // Large M: 4 waves along n, 64 x 256 workgroup tiles. Small M: 4 waves split K,
     // so N/32 workgroups still fill the chip.

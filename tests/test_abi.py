@@ -54,9 +54,10 @@ def test_type_traits_match_gguf():
 
 
 def test_workspace_size():
-    # planar: int8 [M][K] + fp32 scales [K/bs][roundup(M, 64)] (+ int16 bsums [M][K/16] for Q8_K)
-    assert dc.mul_mat_workspace_size(8, 1, 1024) == 1024 + 32 * 64 * 4
-    assert dc.mul_mat_workspace_size(12, 64, 2048) == 64 * 2048 + 8 * 64 * 4 + 64 * 128 * 2
+    # planar: int8 [M][K] + fp32 scales [K/bs][roundup(M, 128)] (+ int16 bsums [M][K/16] for Q8_K)
+    assert dc.mul_mat_workspace_size(8, 1, 1024) == 1024 + 32 * 128 * 4
+    assert dc.mul_mat_workspace_size(12, 64, 2048) == 64 * 2048 + 8 * 128 * 4 + 64 * 128 * 2
+    assert dc.mul_mat_workspace_size(8, 130, 1024) == 130 * 1024 + 32 * 256 * 4
     assert dc.mul_mat_workspace_size(12, 1, 100) == 0
 
 
