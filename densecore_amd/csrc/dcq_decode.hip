@@ -1,4 +1,4 @@
-// dcq_decode.hip — decode GEMV (M <= 8 per launch) for Q4_K weights.
+// dcq_decode.hip — decode GEMV (M <= 8 per launch) for the K-quant weights (Q4_K, Q6_K).
 //
 // Replaces the per-row vec_dot loop of cb_gemv_custom (core/src/inference.cpp:896-923)
 // and ggml's CPU MUL_MAT at small M (core/src/inference.cpp:1794-1797, executed at
@@ -16,10 +16,17 @@
 // with the same wave quantizer (bit-identical bytes) — the fused form saves the
 // separate quantize launch of a decode step.
 //
-// Arithmetic per lane and superblock: 16 v_dot4 over the unpacked nibbles, the two 6-bit
-// sub-block scales applied to exact sums, the mins term from the 16-element bsums:
-//   iA = sc_2c*I_2c + sc_2c+1*I_2c+1,  iB = m_2c*S_2c + m_2c+1*S_2c+1   (exact int32)
-//   acc += dA * (d * iA - dmin * iB)      (vec_dot_q4_K_q8_K's per-superblock form)
+// The per-format work of a lane (one quarter of a superblock, 64 weights) is a policy:
+// Q4_K (144 B): lane c holds the 32 nibble bytes of sub-blocks 2c and 2c+1; 16 v_dot4,
+//   the two 6-bit scales applied to exact sums, the mins term from the 16-element bsums:
+//     iA = sc_2c*I_2c + sc_2c+1*I_2c+1,  iB = m_2c*S_2c + m_2c+1*S_2c+1   (exact int32)
+//     acc += dA * (d * iA - dmin * iB)      (vec_dot_q4_K_q8_K's per-superblock form)
+// Q6_K (210 B, 2-byte aligned): lane (h, lh) holds elements l in [16lh, 16lh+16) of half h
+//   for all four quarters t: 16 bytes of ql low/high nibbles twice, 16 bytes of qh, the 16
+//   int8 scales and d; q = (nibble | 2 qh bits << 4) - 32 with the -32 taken through the
+//   bsums, 16 v_dot4:
+//     iS = sum_t sc_t * (sum q6*q8 - 32 * bsum_t)                        (exact int32)
+//     acc += (d * dA) * iS                   (vec_dot_q6_K_q8_K's per-superblock form)
 // The 4*P lanes of a row are reduced once at the end.
 #include "dcq_common.h"
 #include "dcq_kernels.h"
@@ -57,6 +64,119 @@ int env_int(const char* name, int dflt) {
 
 }  // namespace
 
+
+// ---------------------------------------------------------------- per-format policies
+struct FmtQ4K {
+    static constexpr int kBytes = 144;    // superblock bytes
+    static constexpr int kSumsPerSb = 2;  // dumped int32 per superblock: sum sc*I, sum m*S
+    struct Raw {
+        uint4 hdr, n0, n1;
+    };
+    __device__ __forceinline__ static void load(const uint8_t* sb, int c, Raw& r) {
+        r.hdr = ld16(sb);
+        r.n0 = ld16(sb + 16 + 32 * c);
+        r.n1 = ld16(sb + 32 + 32 * c);
+    }
+    // exact integer sums of this lane's quarter against activation row mi; returns the fp32 term
+    __device__ __forceinline__ static float dot(const Raw& r, const ActLds& act, int mi, int s, int c, int K, int MT,
+                                                int nsb, int (&ints)[2]) {
+        const bool lo_sc = c < 2;  // sub-blocks 0..3 keep their 6 bits in one byte
+        const uint32_t sh = (uint32_t)(c & 1) * 16u;
+        const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
+        const uint32_t scw = lo_sc ? (s0 & 0x3F3F3F3Fu) : ((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u));
+        const uint32_t mnw = lo_sc ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
+        const int sc0 = (int)((scw >> sh) & 0xFFu), sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
+        const int mn0 = (int)((mnw >> sh) & 0xFFu), mn1 = (int)((mnw >> (sh + 8)) & 0xFFu);
+        const uint32_t lo = 0x0F0F0F0Fu;
+        const int8_t* aq = act.qs + mi * K + 256 * s + 64 * c;
+        const uint4 a0 = *reinterpret_cast<const uint4*>(aq);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(aq + 16);
+        const uint4 a2 = *reinterpret_cast<const uint4*>(aq + 32);
+        const uint4 a3 = *reinterpret_cast<const uint4*>(aq + 48);
+        const uint2 bq = *reinterpret_cast<const uint2*>(act.bs + mi * (K / 16) + 16 * s + 4 * c);
+        int il = sdot4((int)(r.n0.x & lo), (int)a0.x, 0);
+        il = sdot4((int)(r.n0.y & lo), (int)a0.y, il);
+        il = sdot4((int)(r.n0.z & lo), (int)a0.z, il);
+        il = sdot4((int)(r.n0.w & lo), (int)a0.w, il);
+        il = sdot4((int)(r.n1.x & lo), (int)a1.x, il);
+        il = sdot4((int)(r.n1.y & lo), (int)a1.y, il);
+        il = sdot4((int)(r.n1.z & lo), (int)a1.z, il);
+        il = sdot4((int)(r.n1.w & lo), (int)a1.w, il);
+        int ih = sdot4((int)((r.n0.x >> 4) & lo), (int)a2.x, 0);
+        ih = sdot4((int)((r.n0.y >> 4) & lo), (int)a2.y, ih);
+        ih = sdot4((int)((r.n0.z >> 4) & lo), (int)a2.z, ih);
+        ih = sdot4((int)((r.n0.w >> 4) & lo), (int)a2.w, ih);
+        ih = sdot4((int)((r.n1.x >> 4) & lo), (int)a3.x, ih);
+        ih = sdot4((int)((r.n1.y >> 4) & lo), (int)a3.y, ih);
+        ih = sdot4((int)((r.n1.z >> 4) & lo), (int)a3.z, ih);
+        ih = sdot4((int)((r.n1.w >> 4) & lo), (int)a3.w, ih);
+        // S_2c = bsums[4c] + bsums[4c+1], S_2c+1 = bsums[4c+2] + bsums[4c+3]
+        const int S0 = (int)(int16_t)(bq.x & 0xFFFFu) + (int)(int16_t)(bq.x >> 16);
+        const int S1 = (int)(int16_t)(bq.y & 0xFFFFu) + (int)(int16_t)(bq.y >> 16);
+        const int iA = sc0 * il + sc1 * ih;
+        const int iB = mn0 * S0 + mn1 * S1;
+        ints[0] = iA;
+        ints[1] = iB;
+        const float d = half_bits_to_float(r.hdr.x & 0xFFFFu), dmin = half_bits_to_float(r.hdr.x >> 16);
+        const float dA = act.d[s * MT + mi];
+        return dA * fmaf(-dmin, (float)iB, d * (float)iA);
+    }
+};
+
+struct FmtQ6K {
+    static constexpr int kBytes = 210;
+    static constexpr int kSumsPerSb = 1;  // sum_g sc_g * I_g
+    struct Raw {
+        uint32_t a[4], b[4], h[4], sc[4];
+        uint32_t d;
+    };
+    // lane c = (h, lh): ql[64h + 16lh ..] (quarters 0/2), ql[64h + 32 + 16lh ..] (1/3),
+    // qh[32h + 16lh ..], scales[16], d — every piece 2-byte aligned
+    __device__ __forceinline__ static void load(const uint8_t* sb, int c, Raw& r) {
+        const int h = c >> 1, lh = c & 1;
+        ld16_a2(sb + 64 * h + 16 * lh, r.a);
+        ld16_a2(sb + 64 * h + 32 + 16 * lh, r.b);
+        ld16_a2(sb + 128 + 32 * h + 16 * lh, r.h);
+        ld16_a2(sb + 192, r.sc);
+        r.d = ldu16(sb + 208);
+    }
+    __device__ __forceinline__ static float dot(const Raw& r, const ActLds& act, int mi, int s, int c, int K, int MT,
+                                                int nsb, int (&ints)[2]) {
+        const int h = c >> 1, lh = c & 1;
+        const int8_t* aq = act.qs + mi * K + 256 * s + 128 * h + 16 * lh;
+        // bsums of groups 8h + 2t + lh, t = 0..3: int16 [16s + 8h .. +8), every other one
+        const uint4 bq = *reinterpret_cast<const uint4*>(act.bs + mi * (K / 16) + 16 * s + 8 * h);
+        const uint32_t bsh = (uint32_t)lh * 16u;
+        const int bs[4] = {(int)(int16_t)(bq.x >> bsh), (int)(int16_t)(bq.y >> bsh), (int)(int16_t)(bq.z >> bsh),
+                           (int)(int16_t)(bq.w >> bsh)};
+        // scales of the same groups: bytes 8h + lh + 2t of the 16 scales
+        const uint32_t scw0 = r.sc[2 * h], scw1 = r.sc[2 * h + 1];
+        const uint32_t ssh = (uint32_t)lh * 8u;
+        const int sc[4] = {(int)(int8_t)(scw0 >> ssh), (int)(int8_t)(scw0 >> (16 + ssh)), (int)(int8_t)(scw1 >> ssh),
+                           (int)(int8_t)(scw1 >> (16 + ssh))};
+        int iS = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint4 av = *reinterpret_cast<const uint4*>(aq + 32 * t);
+            const uint32_t* src = (t & 1) ? r.b : r.a;
+            const uint32_t nsh = (t >> 1) ? 4u : 0u;
+            int I = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo4 = (src[i] >> nsh) & 0x0F0F0F0Fu;
+                const uint32_t hi2 = ((r.h[i] >> (2 * t)) & 0x03030303u) << 4;
+                const uint32_t a = i == 0 ? av.x : i == 1 ? av.y : i == 2 ? av.z : av.w;
+                I = sdot4((int)(lo4 | hi2), (int)a, I);
+            }
+            iS += sc[t] * (I - 32 * bs[t]);
+        }
+        ints[0] = iS;
+        ints[1] = 0;
+        const float dA = act.d[s * MT + mi];
+        return (half_bits_to_float(r.d) * dA) * (float)iS;
+    }
+};
+
 // Staging passes for the largest K a (P, NS) shape covers (nsb <= P*NS):
 // FUSE: (superblock, m) pairs, 16 per workgroup pass (one per 16-lane DPP row);
 // else: 16-byte chunks of the planar activation per thread.
@@ -66,8 +186,8 @@ __host__ __device__ constexpr int stage_chunks(int P, int NS, int MT, bool fuse)
 
 // FUSE: X is fp32 [M][x_stride], quantized in the workgroup; else planar Q8_K
 // (xqs, xd, xbs, m_ld). M <= MT activation rows; LDS holds MT rows, rows >= M unused.
-template <int P, int MT, int NS, bool FUSE, bool DUMP, int QC = stage_chunks(P, NS, MT, FUSE)>
-__global__ void __launch_bounds__(kWG) decode_q4k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+template <class Fmt, int P, int MT, int NS, bool FUSE, bool DUMP, int QC = stage_chunks(P, NS, MT, FUSE)>
+__global__ void __launch_bounds__(kWG) decode_kq_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                          int64_t n0, int64_t n1, int nsb,
                                                          const float* __restrict__ X, int64_t x_stride,
                                                          const int8_t* __restrict__ xqs, const float* __restrict__ xd,
@@ -118,16 +238,13 @@ __global__ void __launch_bounds__(kWG) decode_q4k_kernel(const uint8_t* __restri
     const int64_t row = n0 + ((int64_t)blockIdx.x * 4 + wave) * RPW + lane / L;
     const bool row_ok = row < n1;
     const uint8_t* wrow = W + (row_ok ? row : n1 - 1) * w_row_bytes;
-    const int q = lane % L, p = q >> 2, c = q & 3;
-    uint4 hdr[NS], nb0[NS], nb1[NS];
-#pragma unroll
+    const int q = lane % L, p = q >> 2, c = q & 3;  // superblock p of the step, quarter c
+    typename Fmt::Raw raw[NS];
+#pragma clang loop unroll(full)
     for (int t = 0; t < NS; ++t) {
         int s = t * P + p;
         s = s < nsb ? s : nsb - 1;
-        const uint8_t* sb = wrow + s * 144;
-        hdr[t] = ld16(sb);
-        nb0[t] = ld16(sb + 16 + 32 * c);
-        nb1[t] = ld16(sb + 32 + 32 * c);
+        Fmt::load(wrow + s * Fmt::kBytes, c, raw[t]);
     }
 
     // ---- 3. activation into LDS ----
@@ -170,68 +287,28 @@ __global__ void __launch_bounds__(kWG) decode_q4k_kernel(const uint8_t* __restri
     __syncthreads();
 
     // ---- 4. per step: exact integer sums, one fp32 update per superblock ----
-    const bool lo_sc = c < 2;  // sub-blocks 0..3 keep their 6 bits in one byte
-    const uint32_t sh = (uint32_t)(c & 1) * 16u;
     float acc[MT];
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
-#pragma unroll
+    // fully unrolled: raw[t] must stay in registers (a rolled loop indexes it dynamically)
+#pragma clang loop unroll(full)
     for (int t = 0; t < NS; ++t) {
         const int s_raw = t * P + p;
         const bool valid = s_raw < nsb;
         const int s = valid ? s_raw : nsb - 1;
-        const uint4 hd = hdr[t], w0 = nb0[t], w1 = nb1[t];
-        const uint32_t s0 = hd.y, s1 = hd.z, s2 = hd.w;
-        const uint32_t scw = lo_sc ? (s0 & 0x3F3F3F3Fu) : ((s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u));
-        const uint32_t mnw = lo_sc ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
-        const int sc0 = (int)((scw >> sh) & 0xFFu), sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
-        const int mn0 = (int)((mnw >> sh) & 0xFFu), mn1 = (int)((mnw >> (sh + 8)) & 0xFFu);
-        const float d = half_bits_to_float(hd.x & 0xFFFFu), dmin = half_bits_to_float(hd.x >> 16);
-        const uint32_t lo = 0x0F0F0F0Fu;
-        const int l0 = (int)(w0.x & lo), l1 = (int)(w0.y & lo), l2 = (int)(w0.z & lo), l3 = (int)(w0.w & lo);
-        const int l4 = (int)(w1.x & lo), l5 = (int)(w1.y & lo), l6 = (int)(w1.z & lo), l7 = (int)(w1.w & lo);
-        const int h0 = (int)((w0.x >> 4) & lo), h1 = (int)((w0.y >> 4) & lo), h2 = (int)((w0.z >> 4) & lo),
-                  h3 = (int)((w0.w >> 4) & lo);
-        const int h4 = (int)((w1.x >> 4) & lo), h5 = (int)((w1.y >> 4) & lo), h6 = (int)((w1.z >> 4) & lo),
-                  h7 = (int)((w1.w >> 4) & lo);
+        // all MT rows, also those >= M (their LDS rows hold stale bytes and their sums are
+        // never stored): a guard here lets the compiler merge the unrolled steps into one
+        // block fed by selects
 #pragma unroll
         for (int mi = 0; mi < MT; ++mi) {
-            if (mi >= M) break;  // wave-uniform
-            const int8_t* aq = act.qs + mi * K + 256 * s + 64 * c;
-            const uint4 a0 = *reinterpret_cast<const uint4*>(aq);
-            const uint4 a1 = *reinterpret_cast<const uint4*>(aq + 16);
-            const uint4 a2 = *reinterpret_cast<const uint4*>(aq + 32);
-            const uint4 a3 = *reinterpret_cast<const uint4*>(aq + 48);
-            const uint2 bq = *reinterpret_cast<const uint2*>(act.bs + mi * (K / 16) + 16 * s + 4 * c);
-            const float dA = act.d[s * MT + mi];
-            int il = sdot4(l0, (int)a0.x, 0);
-            il = sdot4(l1, (int)a0.y, il);
-            il = sdot4(l2, (int)a0.z, il);
-            il = sdot4(l3, (int)a0.w, il);
-            il = sdot4(l4, (int)a1.x, il);
-            il = sdot4(l5, (int)a1.y, il);
-            il = sdot4(l6, (int)a1.z, il);
-            il = sdot4(l7, (int)a1.w, il);
-            int ih = sdot4(h0, (int)a2.x, 0);
-            ih = sdot4(h1, (int)a2.y, ih);
-            ih = sdot4(h2, (int)a2.z, ih);
-            ih = sdot4(h3, (int)a2.w, ih);
-            ih = sdot4(h4, (int)a3.x, ih);
-            ih = sdot4(h5, (int)a3.y, ih);
-            ih = sdot4(h6, (int)a3.z, ih);
-            ih = sdot4(h7, (int)a3.w, ih);
-            // S_2c = bsums[4c] + bsums[4c+1], S_2c+1 = bsums[4c+2] + bsums[4c+3]
-            const int S0 = (int)(int16_t)(bq.x & 0xFFFFu) + (int)(int16_t)(bq.x >> 16);
-            const int S1 = (int)(int16_t)(bq.y & 0xFFFFu) + (int)(int16_t)(bq.y >> 16);
-            const int iA = sc0 * il + sc1 * ih;
-            const int iB = mn0 * S0 + mn1 * S1;
-            if (DUMP && valid && row_ok) {
-                int32_t* srow = sums + ((int64_t)mi * sums_n_stride + (row - n0)) * (2 * nsb);
-                atomicAdd(srow + 2 * s, iA);
-                atomicAdd(srow + 2 * s + 1, iB);
+            int ints[2];
+            const float v = Fmt::dot(raw[t], act, mi, s, c, K, MT, nsb, ints);
+            if (DUMP && valid && row_ok && mi < M) {
+                int32_t* srow = sums + ((int64_t)mi * sums_n_stride + (row - n0)) * (Fmt::kSumsPerSb * nsb);
+#pragma unroll
+                for (int k = 0; k < Fmt::kSumsPerSb; ++k) atomicAdd(srow + Fmt::kSumsPerSb * s + k, ints[k]);
             }
-            const float y = fmaf(-dmin, (float)iB, d * (float)iA);
-            acc[mi] = valid ? fmaf(dA, y, acc[mi]) : acc[mi];
+            acc[mi] = valid ? acc[mi] + v : acc[mi];
         }
     }
     // ---- 5. reduce the L lanes of each row ----
@@ -263,35 +340,41 @@ struct Shape {
 constexpr Shape kShapes[] = {{8, 1}, {4, 3}, {2, 5}, {16, 1}, {4, 5}, {8, 3}, {16, 2}, {8, 5}, {8, 6}, {16, 4}};
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
 
-template <int I, int MT, bool FUSE, bool DUMP>
+template <class Fmt, int I, int MT, bool FUSE, bool DUMP>
 DecodeFn fn_of() {
-    return decode_q4k_kernel<kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP>;
+    return decode_kq_kernel<Fmt, kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP>;
 }
 
-template <int I, bool FUSE, bool DUMP>
+template <class Fmt, int I, bool FUSE, bool DUMP>
 DecodeFn pick_mt(int mt) {
     switch (mt) {
-        case 1: return fn_of<I, 1, FUSE, DUMP>();
-        case 2: return fn_of<I, 2, FUSE, DUMP>();
-        case 4: return fn_of<I, 4, FUSE, DUMP>();
-        default: return fn_of<I, 8, FUSE, DUMP>();
+        case 1: return fn_of<Fmt, I, 1, FUSE, DUMP>();
+        case 2: return fn_of<Fmt, I, 2, FUSE, DUMP>();
+        case 4: return fn_of<Fmt, I, 4, FUSE, DUMP>();
+        default: return fn_of<Fmt, I, 8, FUSE, DUMP>();
     }
 }
 
-template <bool FUSE, bool DUMP>
+template <class Fmt, bool FUSE, bool DUMP>
 DecodeFn pick_shape(int idx, int mt) {
     switch (idx) {
-        case 0: return pick_mt<0, FUSE, DUMP>(mt);
-        case 1: return pick_mt<1, FUSE, DUMP>(mt);
-        case 2: return pick_mt<2, FUSE, DUMP>(mt);
-        case 3: return pick_mt<3, FUSE, DUMP>(mt);
-        case 4: return pick_mt<4, FUSE, DUMP>(mt);
-        case 5: return pick_mt<5, FUSE, DUMP>(mt);
-        case 6: return pick_mt<6, FUSE, DUMP>(mt);
-        case 7: return pick_mt<7, FUSE, DUMP>(mt);
-        case 8: return pick_mt<8, FUSE, DUMP>(mt);
-        default: return pick_mt<9, FUSE, DUMP>(mt);
+        case 0: return pick_mt<Fmt, 0, FUSE, DUMP>(mt);
+        case 1: return pick_mt<Fmt, 1, FUSE, DUMP>(mt);
+        case 2: return pick_mt<Fmt, 2, FUSE, DUMP>(mt);
+        case 3: return pick_mt<Fmt, 3, FUSE, DUMP>(mt);
+        case 4: return pick_mt<Fmt, 4, FUSE, DUMP>(mt);
+        case 5: return pick_mt<Fmt, 5, FUSE, DUMP>(mt);
+        case 6: return pick_mt<Fmt, 6, FUSE, DUMP>(mt);
+        case 7: return pick_mt<Fmt, 7, FUSE, DUMP>(mt);
+        case 8: return pick_mt<Fmt, 8, FUSE, DUMP>(mt);
+        default: return pick_mt<Fmt, 9, FUSE, DUMP>(mt);
     }
+}
+
+template <class Fmt>
+DecodeFn pick_fn(bool fuse, bool dump, int idx, int mt) {
+    return fuse ? (dump ? pick_shape<Fmt, true, true>(idx, mt) : pick_shape<Fmt, true, false>(idx, mt))
+                : (dump ? pick_shape<Fmt, false, true>(idx, mt) : pick_shape<Fmt, false, false>(idx, mt));
 }
 static_assert(kNumShapes == 10, "pick_shape covers every shape");
 
@@ -319,17 +402,18 @@ int choose_shape(int nsb) {
     return best;
 }
 
-hipError_t launch_q4k(bool fuse, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
-                      const float* X, int64_t x_stride, const PlanarBuffers* act, int64_t M, float* Y,
-                      int64_t y_stride, int32_t* block_sums, int64_t sums_n_stride, hipStream_t st) {
+hipError_t launch_kq(int wtype, bool fuse, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
+                     const float* X, int64_t x_stride, const PlanarBuffers* act, int64_t M, float* Y,
+                     int64_t y_stride, int32_t* block_sums, int64_t sums_n_stride, hipStream_t st) {
     const int nsb = (int)(K / 256);
-    if (w_row_bytes % 16) return hipErrorNotSupported;
+    if (wtype != kTypeQ4_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
+    if (wtype == kTypeQ4_K ? (w_row_bytes % 16 != 0) : (w_row_bytes % 2 != 0)) return hipErrorNotSupported;
     const int idx = choose_shape(nsb);
     if (idx < 0) return hipErrorNotSupported;
     const int P = kShapes[idx].P;
     const int rows_per_block = 4 * (64 / (4 * P));
     const unsigned grid = (unsigned)((n1 - n0 + rows_per_block - 1) / rows_per_block);
-    const int64_t per_row_sums = 2 * (K / 256);
+    const int64_t per_row_sums = (wtype == kTypeQ4_K ? 2 : 1) * (K / 256);
     // validate every M tile before launching anything
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
@@ -341,8 +425,8 @@ hipError_t launch_q4k(bool fuse, const void* W, int64_t w_row_bytes, int64_t n0,
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         const size_t lds = act_lds_bytes_q8k(mt, K);
-        DecodeFn fn = fuse ? (block_sums ? pick_shape<true, true>(idx, mt) : pick_shape<true, false>(idx, mt))
-                           : (block_sums ? pick_shape<false, true>(idx, mt) : pick_shape<false, false>(idx, mt));
+        DecodeFn fn = wtype == kTypeQ4_K ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, idx, mt)
+                                         : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, idx, mt);
         // rows beyond mc in an MT tile stage the last real activation row and are never stored
         hipLaunchKernelGGL(fn, dim3(grid), dim3(kWG), lds, st, (const uint8_t*)W, w_row_bytes, n0, n1, nsb,
                            fuse ? X + m0 * x_stride : nullptr, x_stride, fuse ? nullptr : act->qs + m0 * K,
@@ -355,18 +439,19 @@ hipError_t launch_q4k(bool fuse, const void* W, int64_t w_row_bytes, int64_t n0,
 
 }  // namespace
 
-hipError_t launch_decode_q4k(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
-                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                             int64_t sums_n_stride, hipStream_t st) {
-    return launch_q4k(false, W, w_row_bytes, n0, n1, K, nullptr, 0, &act, M, Y, y_stride, block_sums, sums_n_stride,
-                      st);
+hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
+                            const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                            int64_t sums_n_stride, hipStream_t st) {
+    return launch_kq(wtype, false, W, w_row_bytes, n0, n1, K, nullptr, 0, &act, M, Y, y_stride, block_sums,
+                     sums_n_stride, st);
 }
 
 hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
                                int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                hipStream_t st) {
-    if (wtype != kTypeQ4_K || env_int("DCQ_NO_FUSE", 0)) return hipErrorNotSupported;
-    return launch_q4k(true, W, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums, N, st);
+    if (env_int("DCQ_NO_FUSE", 0)) return hipErrorNotSupported;
+    if (wtype != kTypeQ4_K && !(wtype == kTypeQ6_K && env_int("DCQ_Q6K_DECODE", 0))) return hipErrorNotSupported;
+    return launch_kq(wtype, true, W, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums, N, st);
 }
 
 }  // namespace dcq

@@ -32,9 +32,9 @@ hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0
 
 // LDS-staged decode kernels (M <= 8 per launch, tiled by 8). hipErrorNotSupported means the
 // shape is outside what they cover and nothing was launched.
-hipError_t launch_decode_q4k(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
-                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                             int64_t sums_n_stride, hipStream_t st);
+hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
+                            const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                            int64_t sums_n_stride, hipStream_t st);
 
 // Decode with the activation quantization fused in (X fp32, no workspace): one launch per
 // 8 rows of M. hipErrorNotSupported: the caller quantizes and uses launch_gemv.
