@@ -1,0 +1,210 @@
+// dcq_batch.hip — batched-decode mul_mat (8 < M <= 64 per m-tile) for Q4_K weights on int8 MFMA.
+//
+// Replaces ggml's CPU MUL_MAT at small M > 1 (continuous-batching decode; every M > 1
+// projection goes there: core/src/inference.cpp:1049-1063, executed at
+// core/src/worker.cpp:544). HBM-bound at M = 64: each weight byte feeds 64 activation
+// rows, so the kernel must stream W once at full bandwidth and keep the MFMA work
+// off the critical path.
+//
+// Launch shape. A workgroup of 8 waves owns 32 weight rows (one MFMA n-tile) and 64
+// activation rows (two MFMA m-tiles); its waves split K by superblock (wave w takes
+// superblocks w, w + 8, ...). Per superblock a wave
+//   - loads the 64 x 256 activation bytes and 64 scales straight into its own LDS
+//     region (global_load_lds_dwordx4: coalesced, no registers in flight, no barrier:
+//     only this wave reads the region), 16-byte slots XOR-swizzled by row % 16;
+//   - loads its weight fragments (row = lane % 32, 16 nibble bytes per 32-element
+//     sub-block half, plus the 16-byte header) into registers;
+//   - runs v_mfma_i32_32x32x32_i8 per 32-element sub-block j: I_j (weight nibbles) and
+//     the mins term (a weight operand whose bytes all equal m_j, so the MFMA yields
+//     m_j * S_j); the 6-bit scale is applied to the exact I_j with v_mad_i32_i24;
+//   - per superblock: acc += dA * (d * sum_j sc_j I_j - dmin * sum_j m_j S_j)
+//     (vec_dot_q4_K_q8_K's per-superblock form).
+// The 8 partial tiles are summed in wave order through LDS at the end (deterministic).
+#include "dcq_common.h"
+#include "dcq_kernels.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 in the clobber list (see dma16)
+
+namespace dcq {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int kWaves = 8;
+constexpr int kMT = 64;         // activation rows per workgroup
+constexpr int kNT = 32;         // weight rows per workgroup
+constexpr int kRegion = 17408;  // per-wave LDS: 64 rows x 256 B activation + 1 KB scales
+
+// 16 bytes per lane from global memory straight into LDS at base + 16 * lane (base
+// wave-uniform, in M0). Inline asm: the builtin form makes the compiler wait for every
+// earlier LDS-direct load before the next. The compiler does not count these loads, so
+// they are issued before the ordinary loads they must precede, and the wave waits with
+// an explicit s_waitcnt vmcnt(0) before reading the region. M0 has no other use here.
+__device__ __forceinline__ void dma16(const void* g, const void* lds_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// LDS byte offset of logical 16-byte slot `slot` (0..15) of activation row `row` (256 B rows)
+__device__ __forceinline__ int aswz(int row, int slot) { return row * 256 + 16 * (slot ^ (row & 15)); }
+
+}  // namespace
+
+template <bool DUMP>
+__global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+                                                                   int N, int nsb, const int8_t* __restrict__ xqs,
+                                                                   const float* __restrict__ xd, int64_t m_ld, int M,
+                                                                   float* __restrict__ Y, int64_t y_stride,
+                                                                   int32_t* __restrict__ sums) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int K = nsb * 256;
+    const int n0 = blockIdx.x * kNT, m0 = blockIdx.y * kMT;
+    const int col = lane & 31, hl = lane >> 5;
+    uint8_t* region = smem + wave * kRegion;
+    int8_t* a_lds = reinterpret_cast<int8_t*>(region);
+    float* d_lds = reinterpret_cast<float*>(region + 64 * 256);
+
+    // activation DMA: instruction i (0..15) fills rows 4i .. 4i+3; lane l the physical slot
+    // l % 16 of row 4i + l / 16, which holds logical slot (l % 16) ^ (row % 16)
+    const int8_t* a_src[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int row = 4 * i + (lane >> 4);
+        const int slot = (lane & 15) ^ (row & 15);
+        a_src[i] = xqs + (int64_t)min(m0 + row, M - 1) * K + 16 * slot;
+    }
+    // activation scales: lanes 0..15 carry rows 4l .. 4l+3 (the other lanes repeat lane 15)
+    const float* d_src = xd + m0 + 4 * min(lane, 15);
+    // weight row of this lane (MFMA B operand: column n = lane % 32)
+    const uint8_t* wrow = W + (int64_t)min(n0 + col, N - 1) * w_row_bytes;
+
+    float acc[2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+
+    for (int s = wave; s < nsb; s += kWaves) {
+        // ---- loads: activation + scales into this wave's LDS region, weights into registers ----
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dma16(a_src[i] + 256 * s, a_lds + 1024 * i);
+        dma16(d_src + (int64_t)s * m_ld, d_lds);
+        const uint8_t* sb = wrow + (int64_t)s * 144;
+        const uint4 hdr = ld16(sb);
+        uint4 qw[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qw[c] = ld16(sb + 16 + 32 * c + 16 * hl);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
+        __builtin_amdgcn_wave_barrier();
+
+        // 6-bit scales / mins of the 8 sub-blocks (get_scale_min_k4)
+        const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+        const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
+        const uint32_t mnw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
+        const float d = half_bits_to_float(hdr.x & 0xFFFFu), dmin = half_bits_to_float(hdr.x >> 16);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            v16i ai, amin;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                ai[v] = 0;
+                amin[v] = 0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint4 q = qw[j >> 1];
+                const uint32_t sh = (j & 1) ? 4u : 0u;
+                v4i bv;
+                bv.x = (int)((q.x >> sh) & 0x0F0F0F0Fu);
+                bv.y = (int)((q.y >> sh) & 0x0F0F0F0Fu);
+                bv.z = (int)((q.z >> sh) & 0x0F0F0F0Fu);
+                bv.w = (int)((q.w >> sh) & 0x0F0F0F0Fu);
+                const int sc = (int)((scw[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+                const uint32_t mb = ((mnw[j >> 2] >> (8 * (j & 3))) & 0xFFu) * 0x01010101u;
+                v4i bm;
+                bm.x = bm.y = bm.z = bm.w = (int)mb;
+                // activation fragment: rows 32i + col, k = 32j + 16hl .. +16 (logical slot 2j + hl)
+                const v4i av = *reinterpret_cast<const v4i*>(a_lds + aswz(32 * i + col, 2 * j + hl));
+                v16i zero;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) zero[v] = 0;
+                const v16i I = mfma32(av, bv, zero);
+                amin = mfma32(av, bm, amin);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) ai[v] = __mul24(sc, I[v]) + ai[v];
+            }
+            // lane owns weight row n = n0 + col and activation rows m_v = 32i + 8(v/4) + 4hl + v%4
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 dav = *reinterpret_cast<const float4*>(d_lds + 32 * i + 8 * q + 4 * hl);
+                const float da4[4] = {dav.x, dav.y, dav.z, dav.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int v = 4 * q + e;
+                    const float y = fmaf(-dmin, (float)amin[v], d * (float)ai[v]);
+                    acc[i][v] = fmaf(da4[e], y, acc[i][v]);
+                }
+            }
+            if (DUMP) {
+                const int n = n0 + col;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int m = m0 + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
+                    if (m < M && n < N) {
+                        int32_t* sp = sums + ((int64_t)m * N + n) * (2 * nsb) + 2 * s;
+                        sp[0] = ai[v];
+                        sp[1] = amin[v];
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // the region is rewritten by the next superblock's loads
+    }
+
+    // ---- fixed-order reduction of the 8 partial tiles through LDS ----
+    __syncthreads();  // every wave is done with its activation region
+    float* part = reinterpret_cast<float*>(smem);  // [wave][i][v][64]
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) part[((wave * 2 + i) * 16 + v) * 64 + lane] = acc[i][v];
+    __syncthreads();
+    // wave w (< 2) reduces m-tile i = w; the other waves are done
+    if (wave < 2) {
+        const int i = wave;
+        const int n = n0 + col;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            float y = part[((0 * 2 + i) * 16 + v) * 64 + lane];
+            for (int w = 1; w < kWaves; ++w) y += part[((w * 2 + i) * 16 + v) * 64 + lane];
+            const int m = m0 + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
+            if (m < M && n < N) Y[(int64_t)m * y_stride + n] = y;
+        }
+    }
+}
+
+hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+    if (w_row_bytes % 16 || N > (1 << 30) || M > (1 << 30) || K > (1 << 30)) return hipErrorNotSupported;
+    // the per-superblock scale DMA reads 64 scales at [s][m0 .. m0 + 63]: m_ld must cover the
+    // last m-tile (it is M rounded up to 128)
+    if (act.m_ld < ((M + kMT - 1) / kMT) * kMT) return hipErrorNotSupported;
+    const int nsb = (int)(K / 256);
+    dim3 grid((unsigned)((N + kNT - 1) / kNT), (unsigned)((M + kMT - 1) / kMT));
+    const size_t lds = (size_t)kWaves * kRegion;
+    auto fn = block_sums ? batch_q4k_kernel<true> : batch_q4k_kernel<false>;
+    hipLaunchKernelGGL(fn, grid, dim3(64 * kWaves), lds, st, (const uint8_t*)W, w_row_bytes, (int)N, nsb, act.qs,
+                       act.d, act.m_ld, (int)M, Y, y_stride, block_sums);
+    return hipGetLastError();
+}
+
+}  // namespace dcq

@@ -47,6 +47,11 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
 hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                                int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
 
+// Q4_K batched decode (M <= 128): 8-wave workgroups per 32 weight rows x 64 activation
+// rows, K split over the waves; hipErrorNotSupported when the shape is outside it.
+hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+
 // Int8-MFMA tiles for any M.
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                       int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);

@@ -491,6 +491,10 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
         const hipError_t e = launch_prefill_q8_0(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st);
         if (e != hipErrorNotSupported) return e;
     }
+    if (wtype == kTypeQ4_K && M <= 128) {
+        const hipError_t e = launch_batch_q4k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     MmqShape s;
     // Large M: 4 waves along n, 64 x 256 workgroup tiles. Small M: 4 waves split K,
     // so N/32 workgroups still fill the chip.
