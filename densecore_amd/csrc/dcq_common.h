@@ -138,6 +138,13 @@ __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));
     return v;
 }
+__device__ __forceinline__ int row16_or(int v) {
+    v |= dpp_mov<0xB1>(v);
+    v |= dpp_mov<0x4E>(v);
+    v |= dpp_mov<0x141>(v);
+    v |= dpp_mov<0x140>(v);
+    return v;
+}
 __device__ __forceinline__ int row16_min(int v) {
     v = min(v, dpp_mov<0xB1>(v));
     v = min(v, dpp_mov<0x4E>(v));
@@ -146,43 +153,71 @@ __device__ __forceinline__ int row16_min(int v) {
     return v;
 }
 
+// Pack the low bytes of four dwords (b0 lowest) into one dword.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
+    const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // b0.byte0 | b1.byte0 << 8
+    const uint32_t hi = __builtin_amdgcn_perm(b3, b2, 0x04000c0cu);  // b2.byte0 << 16 | b3.byte0 << 24
+    return lo | hi;
+}
+
 // One Q8_K superblock (quantize_row_q8_K_ref semantics) quantized by the 16 lanes of a
 // DPP row; lane g (= lane % 16) holds elements 16g .. 16g+15 in x[16]. Returns the lane's
 // 16 quantized bytes (4 dwords), the sum of its 16-element group (bsums[g]) and d.
 //   max = first element of largest |x| (strict '>' scan); iscale = -127/max;
 //   q = min(127, round-half-even(iscale*x)); d = 1/iscale; an all-zero block is all zero.
-// max |x| and the first index holding it do not depend on the reduction order, so the
-// bytes equal the sequential scan's.
+// Exactness notes:
+//   - max |x| and the first index holding it do not depend on the reduction order. Only
+//     the sign of that element matters (max = +-amax); it is decided by whether +amax /
+//     -amax occur in the block, and by the exact first-index scan when both occur.
+//   - |iscale*x| <= 127 (up to one rounding), so round-half-even(iscale*x) lies in
+//     [-127, 127] and the min(127, .) never binds. The rounding is ggml's nearest_int:
+//     u = fl(iscale*x) + 1.5*2^23 rounds to an integer (half even) and its bit pattern is
+//     0x4B400000 + q, so q's two's-complement byte is u's low byte and the 16-element sum
+//     is sum(bits(u)) - 16*0x4B400000.
 __device__ __forceinline__ void quantize_q8k_row16(const float (&x)[16], int g, uint32_t (&packed)[4], int& bsum,
                                                    float& dval) {
-    float best = -1.0f;
-    int bkey = 0;  // (index << 1) | sign of this lane's first maximum
+#pragma clang fp contract(off)
+    float amax_l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) amax_l = fmaxf(amax_l, fabsf(x[j]));
+    const float amax = row16_max(amax_l);
+    // does +amax / -amax occur in this lane? (row-wide OR below)
+    int has_pos = 0, has_neg = 0;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        const float a = fabsf(x[j]);
-        if (a > best) {
-            best = a;
-            bkey = ((16 * g + j) << 1) | (int)(__float_as_uint(x[j]) >> 31);
-        }
+        has_pos |= (x[j] == amax);
+        has_neg |= (x[j] == -amax);
     }
-    const float amax = row16_max(best);
-    // the smallest index holding the maximum wins
-    const int key = (best == amax) ? bkey : 0x7FFFFFFF;
-    const int win = row16_min(key);
-    const float maxv = (win & 1) ? -amax : amax;
+    const int flags = row16_or(has_pos | (has_neg << 1));
+    float maxv = (flags & 2) ? -amax : amax;
+    if (flags == 3) {
+        // both signs hold the maximum: the first index decides (exact scan, rare)
+        int key = 0x7FFFFFFF;
+#pragma unroll
+        for (int j = 15; j >= 0; --j)
+            key = (fabsf(x[j]) == amax) ? (((16 * g + j) << 1) | (int)(__float_as_uint(x[j]) >> 31)) : key;
+        key = row16_min(key);
+        maxv = (key & 1) ? -amax : amax;
+    }
     bsum = 0;
     dval = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) packed[i] = 0u;
     if (amax != 0.0f) {
         const float iscale = -127.f / maxv;
+        uint32_t u[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            int qv = (int)__builtin_rintf(iscale * x[j]);
-            qv = qv < 127 ? qv : 127;
-            bsum += qv;
-            packed[j >> 2] |= ((uint32_t)qv & 0xFFu) << (8 * (j & 3));
+            // two roundings, as ggml: fl(iscale*x), then + 1.5*2^23 (contraction is off here)
+            const float t = iscale * x[j];
+            u[j] = __float_as_uint(t + 12582912.0f);
         }
+        uint32_t sum = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sum += u[j];
+        bsum = (int)(sum - 16u * 0x4B400000u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) packed[i] = pack_low_bytes(u[4 * i], u[4 * i + 1], u[4 * i + 2], u[4 * i + 3]);
         dval = 1.0f / iscale;
     }
 }

@@ -37,7 +37,6 @@ namespace dcq {
 
 namespace {
 
-constexpr int kWG = 256;
 
 struct ActLds {
     int8_t* qs;   // [MT][K]
@@ -180,14 +179,14 @@ struct FmtQ6K {
 // Staging passes for the largest K a (P, NS) shape covers (nsb <= P*NS):
 // FUSE: (superblock, m) pairs, 16 per workgroup pass (one per 16-lane DPP row);
 // else: 16-byte chunks of the planar activation per thread.
-__host__ __device__ constexpr int stage_chunks(int P, int NS, int MT, bool fuse) {
-    return fuse ? (MT * P * NS + 15) / 16 : (MT * P * NS * 256 / 16 + kWG - 1) / kWG;
+__host__ __device__ constexpr int stage_chunks(int P, int NS, int MT, bool fuse, int NW) {
+    return fuse ? (MT * P * NS + 4 * NW - 1) / (4 * NW) : (MT * P * NS * 256 / 16 + 64 * NW - 1) / (64 * NW);
 }
 
 // FUSE: X is fp32 [M][x_stride], quantized in the workgroup; else planar Q8_K
 // (xqs, xd, xbs, m_ld). M <= MT activation rows; LDS holds MT rows, rows >= M unused.
-template <class Fmt, int P, int MT, int NS, bool FUSE, bool DUMP, int QC = stage_chunks(P, NS, MT, FUSE)>
-__global__ void __launch_bounds__(kWG) decode_kq_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+template <class Fmt, int P, int MT, int NS, bool FUSE, bool DUMP, int NW = 4, int QC = stage_chunks(P, NS, MT, FUSE, NW)>
+__global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                          int64_t n0, int64_t n1, int nsb,
                                                          const float* __restrict__ X, int64_t x_stride,
                                                          const int8_t* __restrict__ xqs, const float* __restrict__ xd,
@@ -210,7 +209,7 @@ __global__ void __launch_bounds__(kWG) decode_kq_kernel(const uint8_t* __restric
         const int g = tid & 15;
 #pragma unroll
         for (int i = 0; i < QC; ++i) {
-            int pr = (tid >> 4) + 16 * i;
+            int pr = (tid >> 4) + 4 * NW * i;
             pr = pr < last_pair ? pr : last_pair;
             const int s = pr / MT, m = pr % MT;  // MT is a power of two
             const float4* xp = reinterpret_cast<const float4*>(X + (int64_t)(m < M ? m : M - 1) * x_stride + 256 * s + 16 * g);
@@ -222,7 +221,7 @@ __global__ void __launch_bounds__(kWG) decode_kq_kernel(const uint8_t* __restric
         const int q_last = M * K / 16 - 1, b_last = M * K / 128 - 1;
 #pragma unroll
         for (int i = 0; i < QC; ++i) {
-            const int cc = tid + i * kWG;
+            const int cc = tid + i * 64 * NW;
             sq[i] = ld16(xqs + 16 * (int64_t)(cc < q_last ? cc : q_last));
             sb16[i] = ld16(xbs + 8 * (int64_t)(cc < b_last ? cc : b_last));
             const int cd = cc < last_pair ? cc : last_pair;
@@ -235,7 +234,7 @@ __global__ void __launch_bounds__(kWG) decode_kq_kernel(const uint8_t* __restric
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- 2. every weight load of this lane ----
-    const int64_t row = n0 + ((int64_t)blockIdx.x * 4 + wave) * RPW + lane / L;
+    const int64_t row = n0 + ((int64_t)blockIdx.x * NW + wave) * RPW + lane / L;
     const bool row_ok = row < n1;
     const uint8_t* wrow = W + (row_ok ? row : n1 - 1) * w_row_bytes;
     const int q = lane % L, p = q >> 2, c = q & 3;  // superblock p of the step, quarter c
@@ -252,7 +251,7 @@ __global__ void __launch_bounds__(kWG) decode_kq_kernel(const uint8_t* __restric
         const int g = tid & 15;
 #pragma unroll
         for (int i = 0; i < QC; ++i) {
-            int pr = (tid >> 4) + 16 * i;
+            int pr = (tid >> 4) + 4 * NW * i;
             pr = pr < last_pair ? pr : last_pair;
             const int s = pr / MT, m = pr % MT;
             float x[16];
@@ -278,7 +277,7 @@ __global__ void __launch_bounds__(kWG) decode_kq_kernel(const uint8_t* __restric
         const int q_last = M * K / 16 - 1, b_last = M * K / 128 - 1;
 #pragma unroll
         for (int i = 0; i < QC; ++i) {
-            const int cc = tid + i * kWG;
+            const int cc = tid + i * 64 * NW;
             *reinterpret_cast<uint4*>(act.qs + 16 * (cc < q_last ? cc : q_last)) = sq[i];
             *reinterpret_cast<uint4*>(act.bs + 8 * (cc < b_last ? cc : b_last)) = sb16[i];
             act.d[cc < last_pair ? cc : last_pair] = sd[i];
@@ -340,9 +339,17 @@ struct Shape {
 constexpr Shape kShapes[] = {{8, 1}, {4, 3}, {2, 5}, {16, 1}, {4, 5}, {8, 3}, {16, 2}, {8, 5}, {8, 6}, {16, 4}};
 constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
 
+// waves per workgroup (measured on config 2, fused: 2 waves 6.8 us, 4 waves 6.1 us, 8 waves
+// 7.05 us — 8-wave workgroups quantize the activation once per 32 weight rows instead of
+// 16 but are fewer and longer-lived)
+template <bool FUSE, int MT>
+constexpr int waves_of() {
+    return 4;
+}
+
 template <class Fmt, int I, int MT, bool FUSE, bool DUMP>
 DecodeFn fn_of() {
-    return decode_kq_kernel<Fmt, kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP>;
+    return decode_kq_kernel<Fmt, kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP, waves_of<FUSE, MT>()>;
 }
 
 template <class Fmt, int I, bool FUSE, bool DUMP>
@@ -411,24 +418,26 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, int64_t w_row_bytes, i
     const int idx = choose_shape(nsb);
     if (idx < 0) return hipErrorNotSupported;
     const int P = kShapes[idx].P;
-    const int rows_per_block = 4 * (64 / (4 * P));
-    const unsigned grid = (unsigned)((n1 - n0 + rows_per_block - 1) / rows_per_block);
     const int64_t per_row_sums = (wtype == kTypeQ4_K ? 2 : 1) * (K / 256);
     // validate every M tile before launching anything
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         if (act_lds_bytes_q8k(mt, K) > 64 * 1024) return hipErrorNotSupported;
-        if (stage_chunks(P, kShapes[idx].NS, mt, fuse) > 16) return hipErrorNotSupported;
+        const int nw = 4;
+        if (stage_chunks(P, kShapes[idx].NS, mt, fuse, nw) > 16) return hipErrorNotSupported;
     }
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         const size_t lds = act_lds_bytes_q8k(mt, K);
+        const int nw = 4;
+        const int rows_per_block = nw * (64 / (4 * P));
+        const unsigned grid = (unsigned)((n1 - n0 + rows_per_block - 1) / rows_per_block);
         DecodeFn fn = wtype == kTypeQ4_K ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, idx, mt)
                                          : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, idx, mt);
         // rows beyond mc in an MT tile stage the last real activation row and are never stored
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(kWG), lds, st, (const uint8_t*)W, w_row_bytes, n0, n1, nsb,
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), lds, st, (const uint8_t*)W, w_row_bytes, n0, n1, nsb,
                            fuse ? X + m0 * x_stride : nullptr, x_stride, fuse ? nullptr : act->qs + m0 * K,
                            fuse ? nullptr : act->d + m0, fuse ? nullptr : act->bs + m0 * (K / 16),
                            fuse ? 0 : act->m_ld, (int)mc, Y + m0 * y_stride, y_stride,

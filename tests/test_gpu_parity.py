@@ -58,6 +58,27 @@ def test_quantize_rows_bit_exact(O, dev, vdt, M, K):
     assert np.array_equal(got, want)
 
 
+def test_quantize_q8_K_ties_bit_exact(O, dev):
+    """Q8_K's scale comes from the FIRST element of largest |x|: blocks whose maximum |x| is held
+    by both signs (first occurrence negative, or positive, in different lanes of the 16-lane
+    group and in the same lane), a single maximum, an all-zero block and exact .5 products."""
+    K = 256 * 8
+    x = synth.normal(4 * K, 4242).reshape(4, K) * np.float32(0.5)
+    blk = lambda r, b: x[r, 256 * b:256 * (b + 1)]
+    blk(0, 0)[[37, 200]] = [-3.0, 3.0]       # negative first, different lanes
+    blk(0, 1)[[5, 250]] = [3.0, -3.0]        # positive first
+    blk(0, 2)[[16, 17]] = [-3.0, 3.0]        # same lane
+    blk(0, 3)[[255, 0]] = [-3.0, 3.0]        # last element negative, first positive
+    blk(1, 0)[:] = 0.0                       # all zero
+    blk(1, 1)[:] = 0.0
+    blk(1, 1)[77] = -1.0                     # single non-zero
+    blk(1, 2)[:] = np.float32(1.0)           # all equal
+    blk(2, 0)[[3, 4, 5]] = [-127.0, 63.5, -0.5]  # iscale = 1: exact .5 ties round half even
+    blk(2, 1)[[3, 4, 5]] = [127.0, 62.5, 1.5]
+    got = to_host(dc.quantize_rows(Q8_K, to_dev(x, dev)))
+    assert np.array_equal(got, O.quantize_rows(Q8_K, x))
+
+
 def test_quantize_rows_strided_input(O, dev):
     import torch
     x = synth.normal(4 * 1024, 91).reshape(4, 1024)
