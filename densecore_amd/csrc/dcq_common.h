@@ -153,6 +153,21 @@ __device__ __forceinline__ int row16_min(int v) {
     return v;
 }
 
+// Sum over aligned groups of L lanes (L a power of two <= 64); every lane of a group gets
+// the group's sum. Inside a 16-lane row by DPP (quad swaps, half-row mirror, row mirror:
+// each step adds a partner holding the same partial sum set), then across rows by
+// ds_bpermute. Partners add the same two values, so all lanes of a group agree bitwise.
+template <int L>
+__device__ __forceinline__ float lanes_sum(float v) {
+    if (L >= 2) v += __int_as_float(dpp_mov<0xB1>(__float_as_int(v)));
+    if (L >= 4) v += __int_as_float(dpp_mov<0x4E>(__float_as_int(v)));
+    if (L >= 8) v += __int_as_float(dpp_mov<0x141>(__float_as_int(v)));
+    if (L >= 16) v += __int_as_float(dpp_mov<0x140>(__float_as_int(v)));
+    if (L >= 32) v += __shfl_xor(v, 16, 64);
+    if (L >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 // Pack the low bytes of four dwords (b0 lowest) into one dword.
 __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
     const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // b0.byte0 | b1.byte0 << 8

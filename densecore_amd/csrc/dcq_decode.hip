@@ -312,12 +312,7 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
     }
     // ---- 5. reduce the L lanes of each row ----
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi) {
-        float v = acc[mi];
-#pragma unroll
-        for (int o = L >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        acc[mi] = v;
-    }
+    for (int mi = 0; mi < MT; ++mi) acc[mi] = lanes_sum<L>(acc[mi]);
     if (q == 0 && row_ok) {
 #pragma unroll
         for (int mi = 0; mi < MT; ++mi)
@@ -459,6 +454,8 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
                                int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                hipStream_t st) {
     if (env_int("DCQ_NO_FUSE", 0)) return hipErrorNotSupported;
+    if (wtype == kTypeQ8_0)
+        return launch_decode_fused_q8_0(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st);
     if (wtype != kTypeQ4_K && !(wtype == kTypeQ6_K && env_int("DCQ_Q6K_DECODE", 0))) return hipErrorNotSupported;
     return launch_kq(wtype, true, W, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums, N, st);
 }

@@ -1,0 +1,288 @@
+// dcq_decode_q8.hip — decode GEMV (M <= 8 per launch) for Q8_0 weights with the
+// activation's Q8_0 quantization fused in (one launch per decode step, no workspace).
+//
+// Replaces cb_gemv_custom's quantize-once-then-vec_dot-per-row (core/src/inference.cpp:
+// 887-923) for Q8_0 weights (vec_dot_type Q8_0, core/src/inference.cpp:970-984) and ggml's
+// CPU MUL_MAT at small M (core/src/inference.cpp:1063; executed at core/src/worker.cpp:544).
+//
+// Launch shape. A workgroup of NW waves owns NW * 64/G weight rows; G lanes stream a row,
+// lane g holding the block pairs u = g + G*t, t < NS (68 bytes: two 34-byte blocks, dword
+// aligned because K % 64 == 0 and the row stride is a multiple of 4). Every weight load of
+// a lane is issued right after the activation loads, before any arithmetic.
+//
+// Activation. Each workgroup quantizes the M fp32 rows into LDS: 8 lanes per 32-element
+// block, 4 floats per lane, the block's max |x| over the 8 lanes by DPP. The arithmetic is
+// the standalone quantizer's (ggml-cpu x86 quantize_row_q8_0): d = amax/127 stored as fp16,
+// id = amax ? 127/amax : 0, q = round-half-even(fl(x*id)) — the rounding done by adding
+// 1.5*2^23 (exact for |x*id| <= 2^22; here |x*id| <= 127), so bytes and scales are
+// bit-identical to dcq_quantize_rows.
+// LDS: qs int8 [MT][K], then dA fp32 [MT][K/32] (the fp16 scale widened).
+//
+// Dot. Per block b, I_b = sum_k qw*qa exactly (8 v_dot4, int32), and
+//   y += I_b * (dW_b * dA_b)          (vec_dot_q8_0_q8_0's per-block form)
+// two blocks per lane per step; the G lanes of a row are reduced once at the end.
+#include "dcq_common.h"
+#include "dcq_kernels.h"
+
+#include <stdlib.h>
+
+namespace dcq {
+
+namespace {
+
+// max over the 8 lanes 8k .. 8k+7: quad swaps, then the half-row mirror
+__device__ __forceinline__ float row8_max(float v) {
+    v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));
+    v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));
+    return v;
+}
+
+constexpr int kMaxStagePasses = 8;  // float4 registers of activation per thread
+
+// (block, activation row) items staged per workgroup pass: 8 lanes each
+__host__ __device__ constexpr int q8_stage_passes(int G, int NS, int MT, int NW) {
+    return (MT * 2 * G * NS + 8 * NW - 1) / (8 * NW);
+}
+
+int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
+}
+
+}  // namespace
+
+template <int G, int NS, int MT, int NW, bool DUMP, int QC = q8_stage_passes(G, NS, MT, NW)>
+__global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+                                                           int64_t N, int K, const float* __restrict__ X,
+                                                           int64_t x_stride, int M, float* __restrict__ Y,
+                                                           int64_t y_stride, int32_t* __restrict__ sums,
+                                                           int64_t sums_n_stride) {
+    if constexpr (QC <= kMaxStagePasses) {
+        extern __shared__ __align__(16) uint8_t smem[];
+        constexpr int RPW = 64 / G;  // rows per wave
+        const int nb = K / 32, U = K / 64;
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        int8_t* act_qs = reinterpret_cast<int8_t*>(smem);
+        float* act_d = reinterpret_cast<float*>(smem + (size_t)MT * K);
+        const int last_item = nb * MT - 1;
+
+        // ---- 1. activation loads, issued first ----
+        float4 xv[QC];
+#pragma unroll
+        for (int i = 0; i < QC; ++i) {
+            int it = (tid >> 3) + 8 * NW * i;
+            it = it < last_item ? it : last_item;
+            const int b = it / MT, m = it % MT;  // MT is a power of two
+            xv[i] = *reinterpret_cast<const float4*>(X + (int64_t)(m < M ? m : M - 1) * x_stride + 32 * b +
+                                                     4 * (tid & 7));
+        }
+        // loads retire in order: the staging below then waits for the activation only
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- 2. every weight load of this lane ----
+        const int64_t row = ((int64_t)blockIdx.x * NW + wave) * RPW + lane / G;
+        const bool row_ok = row < N;
+        const uint8_t* wrow = W + (row_ok ? row : N - 1) * w_row_bytes;
+        const int g = lane % G;
+        uint32_t raw[NS][17];
+#pragma clang loop unroll(full)
+        for (int t = 0; t < NS; ++t) {
+            int u = g + G * t;
+            u = u < U ? u : U - 1;
+            const uint8_t* p = wrow + (int64_t)u * 68;
+            const U32x4 a = ld4(p), b = ld4(p + 16), c = ld4(p + 32), d = ld4(p + 48);
+            raw[t][0] = a.x; raw[t][1] = a.y; raw[t][2] = a.z; raw[t][3] = a.w;
+            raw[t][4] = b.x; raw[t][5] = b.y; raw[t][6] = b.z; raw[t][7] = b.w;
+            raw[t][8] = c.x; raw[t][9] = c.y; raw[t][10] = c.z; raw[t][11] = c.w;
+            raw[t][12] = d.x; raw[t][13] = d.y; raw[t][14] = d.z; raw[t][15] = d.w;
+            raw[t][16] = ld1(p + 64);
+        }
+        // keep the quantizer's first use of the activation (and its wait) behind the weight loads
+        __builtin_amdgcn_sched_barrier(0);
+
+        // ---- 3. quantize the activation into LDS ----
+        {
+#pragma clang fp contract(off)
+#pragma unroll
+            for (int i = 0; i < QC; ++i) {
+                int it = (tid >> 3) + 8 * NW * i;
+                it = it < last_item ? it : last_item;
+                const int b = it / MT, m = it % MT;
+                const float4 v = xv[i];
+                const float amax =
+                    row8_max(fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+                const float dA = half_bits_to_float(float_to_half_bits(amax / 127.f));
+                const float id = amax != 0.0f ? 127.f / amax : 0.0f;
+                // |x*id| <= 127: fl(x*id) + 1.5*2^23 is the half-even integer in the low byte
+                const uint32_t u0 = __float_as_uint(v.x * id + 12582912.0f);
+                const uint32_t u1 = __float_as_uint(v.y * id + 12582912.0f);
+                const uint32_t u2 = __float_as_uint(v.z * id + 12582912.0f);
+                const uint32_t u3 = __float_as_uint(v.w * id + 12582912.0f);
+                // items past the end rewrite the last item with the values it already holds
+                *reinterpret_cast<uint32_t*>(act_qs + m * K + 32 * b + 4 * (tid & 7)) = pack_low_bytes(u0, u1, u2, u3);
+                if ((tid & 7) == 0) act_d[m * nb + b] = dA;
+            }
+        }
+        __syncthreads();
+
+        // ---- 4. exact block sums, one fp32 update per block ----
+        float acc[MT];
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
+#pragma clang loop unroll(full)
+        for (int t = 0; t < NS; ++t) {
+            const int u_raw = g + G * t;
+            const bool valid = u_raw < U;
+            const int u = valid ? u_raw : U - 1;
+            const uint32_t* w = raw[t];
+            const float dW0 = half_bits_to_float(w[0] & 0xFFFFu), dW1 = half_bits_to_float(w[8] >> 16);
+            // all MT rows, also those >= M (never stored): a guard would let the compiler merge
+            // the unrolled steps into one select-fed block
+#pragma unroll
+            for (int mi = 0; mi < MT; ++mi) {
+                const int8_t* aq = act_qs + mi * K + 64 * u;
+                const uint4 a0 = *reinterpret_cast<const uint4*>(aq);
+                const uint4 a1 = *reinterpret_cast<const uint4*>(aq + 16);
+                const uint4 a2 = *reinterpret_cast<const uint4*>(aq + 32);
+                const uint4 a3 = *reinterpret_cast<const uint4*>(aq + 48);
+                const float2 dA = *reinterpret_cast<const float2*>(act_d + mi * nb + 2 * u);
+                int i0 = sdot4((int)align_bytes(w[1], w[0], 2), (int)a0.x, 0);
+                i0 = sdot4((int)align_bytes(w[2], w[1], 2), (int)a0.y, i0);
+                i0 = sdot4((int)align_bytes(w[3], w[2], 2), (int)a0.z, i0);
+                i0 = sdot4((int)align_bytes(w[4], w[3], 2), (int)a0.w, i0);
+                i0 = sdot4((int)align_bytes(w[5], w[4], 2), (int)a1.x, i0);
+                i0 = sdot4((int)align_bytes(w[6], w[5], 2), (int)a1.y, i0);
+                i0 = sdot4((int)align_bytes(w[7], w[6], 2), (int)a1.z, i0);
+                i0 = sdot4((int)align_bytes(w[8], w[7], 2), (int)a1.w, i0);
+                int i1 = sdot4((int)w[9], (int)a2.x, 0);
+                i1 = sdot4((int)w[10], (int)a2.y, i1);
+                i1 = sdot4((int)w[11], (int)a2.z, i1);
+                i1 = sdot4((int)w[12], (int)a2.w, i1);
+                i1 = sdot4((int)w[13], (int)a3.x, i1);
+                i1 = sdot4((int)w[14], (int)a3.y, i1);
+                i1 = sdot4((int)w[15], (int)a3.z, i1);
+                i1 = sdot4((int)w[16], (int)a3.w, i1);
+                if (DUMP && valid && row_ok && mi < M) {
+                    int32_t* srow = sums + ((int64_t)mi * sums_n_stride + row) * nb;
+                    atomicAdd(srow + 2 * u, i0);
+                    atomicAdd(srow + 2 * u + 1, i1);
+                }
+                const float v = fmaf((float)i1, dW1 * dA.y, (float)i0 * (dW0 * dA.x));
+                acc[mi] = valid ? acc[mi] + v : acc[mi];
+            }
+        }
+        // ---- 5. reduce the G lanes of each row ----
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) acc[mi] = lanes_sum<G>(acc[mi]);
+        if (g == 0 && row_ok) {
+#pragma unroll
+            for (int mi = 0; mi < MT; ++mi)
+                if (mi < M) Y[(int64_t)mi * y_stride + row] = acc[mi];
+        }
+    }
+}
+
+namespace {
+
+using DecodeQ8Fn = void (*)(const uint8_t*, int64_t, int64_t, int, const float*, int64_t, int, float*, int64_t,
+                            int32_t*, int64_t);
+
+// (G lanes per row, NS pairs per lane): a row of U = K/64 pairs needs G*NS >= U
+struct Q8Shape {
+    int G, NS;
+};
+constexpr Q8Shape kQ8Shapes[] = {{16, 1}, {8, 2}, {32, 1}, {16, 2}, {64, 1}, {32, 2}, {16, 4}, {64, 2}, {32, 4}, {64, 4}};
+constexpr int kNumQ8Shapes = sizeof(kQ8Shapes) / sizeof(kQ8Shapes[0]);
+static_assert(kNumQ8Shapes == 10, "pick_q8_shape covers every shape");
+
+#ifndef DCQ_Q8_NW
+#define DCQ_Q8_NW 4
+#endif
+constexpr int kQ8Waves = DCQ_Q8_NW;
+
+template <int I, int MT, bool DUMP>
+DecodeQ8Fn q8_fn() {
+    return decode_q8_0_kernel<kQ8Shapes[I].G, kQ8Shapes[I].NS, MT, kQ8Waves, DUMP>;
+}
+template <int I, bool DUMP>
+DecodeQ8Fn q8_pick_mt(int mt) {
+    switch (mt) {
+        case 1: return q8_fn<I, 1, DUMP>();
+        case 2: return q8_fn<I, 2, DUMP>();
+        case 4: return q8_fn<I, 4, DUMP>();
+        default: return q8_fn<I, 8, DUMP>();
+    }
+}
+template <bool DUMP>
+DecodeQ8Fn q8_pick_shape(int idx, int mt) {
+    switch (idx) {
+        case 0: return q8_pick_mt<0, DUMP>(mt);
+        case 1: return q8_pick_mt<1, DUMP>(mt);
+        case 2: return q8_pick_mt<2, DUMP>(mt);
+        case 3: return q8_pick_mt<3, DUMP>(mt);
+        case 4: return q8_pick_mt<4, DUMP>(mt);
+        case 5: return q8_pick_mt<5, DUMP>(mt);
+        case 6: return q8_pick_mt<6, DUMP>(mt);
+        case 7: return q8_pick_mt<7, DUMP>(mt);
+        case 8: return q8_pick_mt<8, DUMP>(mt);
+        default: return q8_pick_mt<9, DUMP>(mt);
+    }
+}
+
+// fewest steps whose idle pair slots stay within a quarter; then any shape that fits.
+// DCQ_Q8_SHAPE=<index> forces one (tuning).
+int choose_q8_shape(int U) {
+    const int forced = env_int("DCQ_Q8_SHAPE", -1);
+    if (forced >= 0 && forced < kNumQ8Shapes && kQ8Shapes[forced].G * kQ8Shapes[forced].NS >= U) return forced;
+    int best = -1;
+    for (int pass = 0; pass < 2 && best < 0; ++pass) {
+        int best_ns = 1 << 30, best_waste = 1 << 30;
+        for (int i = 0; i < kNumQ8Shapes; ++i) {
+            const int cap = kQ8Shapes[i].G * kQ8Shapes[i].NS;
+            if (cap < U) continue;
+            const int waste = cap - U;
+            if (pass == 0 && 4 * waste > cap) continue;
+            if (kQ8Shapes[i].NS < best_ns || (kQ8Shapes[i].NS == best_ns && waste < best_waste)) {
+                best = i;
+                best_ns = kQ8Shapes[i].NS;
+                best_waste = waste;
+            }
+        }
+    }
+    return best;
+}
+
+}  // namespace
+
+hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
+                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                                    hipStream_t st) {
+    if (K % 64 != 0 || w_row_bytes % 4 != 0 || x_stride % 4 != 0) return hipErrorNotSupported;
+    const int U = (int)(K / 64);
+    const int idx = choose_q8_shape(U);
+    if (idx < 0) return hipErrorNotSupported;
+    const int G = kQ8Shapes[idx].G, NS = kQ8Shapes[idx].NS;
+    // validate every M tile before launching anything
+    for (int64_t m0 = 0; m0 < M; m0 += 8) {
+        const int64_t mc = M - m0 < 8 ? M - m0 : 8;
+        const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
+        if (q8_stage_passes(G, NS, mt, kQ8Waves) > kMaxStagePasses) return hipErrorNotSupported;
+        if ((size_t)mt * K * 9 / 8 > 64 * 1024) return hipErrorNotSupported;
+    }
+    const int rows_per_block = kQ8Waves * (64 / G);
+    const unsigned grid = (unsigned)((N + rows_per_block - 1) / rows_per_block);
+    const int64_t per_row_sums = K / 32;
+    for (int64_t m0 = 0; m0 < M; m0 += 8) {
+        const int64_t mc = M - m0 < 8 ? M - m0 : 8;
+        const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
+        const size_t lds = (size_t)mt * K * 9 / 8;
+        DecodeQ8Fn fn = block_sums ? q8_pick_shape<true>(idx, mt) : q8_pick_shape<false>(idx, mt);
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kQ8Waves), lds, st, (const uint8_t*)W, w_row_bytes, N, (int)K,
+                           X + m0 * x_stride, x_stride, (int)mc, Y + m0 * y_stride, y_stride,
+                           block_sums ? block_sums + m0 * N * per_row_sums : nullptr, N);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace dcq

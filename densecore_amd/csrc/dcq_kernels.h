@@ -42,6 +42,12 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
                                int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                hipStream_t st);
 
+// Q8_0 decode with the Q8_0 activation quantization fused in (K % 64 == 0, row stride a
+// multiple of 4 bytes, M*K*9/8 bytes of LDS per 8-row tile); hipErrorNotSupported otherwise.
+hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
+                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                                    hipStream_t st);
+
 // Q8_0 prefill: LDS-staged 128 x 128 int8-MFMA tiles (K % 128 == 0, w_row_bytes % 4 == 0);
 // hipErrorNotSupported otherwise (nothing launched).
 hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,

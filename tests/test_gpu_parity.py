@@ -114,6 +114,48 @@ def test_mul_mat_parity(O, dev, wt, M, N, K, path):
     O.assert_close(to_host(y2), y_ref, l1, RTOL, what="production kernel")
 
 
+def _with_quantizer_ties(x, vdt):
+    """Blocks whose scaled values hit exact .5 ties, an all-zero block and a single non-zero one."""
+    K = x.shape[1]
+    bs = 32 if vdt == Q8_0 else 256
+    x[0, :bs] = np.float32(0.25) * (np.arange(bs, dtype=np.float32) - bs / 2)
+    x[0, 0] = 127.0 if vdt == Q8_0 else -127.0  # scale 1: the .5 values are ties
+    x[0, 1:6] = [0.5, 1.5, -2.5, 62.5, -0.5]
+    if K >= 3 * bs:
+        x[-1, bs:2 * bs] = 0.0
+        x[-1, 2 * bs:3 * bs] = 0.0
+        x[-1, 2 * bs + 7] = -3.0
+    return x
+
+
+# Shapes for the decode kernels that quantize the activation in the workgroup (M <= 8):
+# Q8_0 lanes-per-row / pairs-per-lane shapes {16,1} (K 1024), {32,1} (2048), {64,1} (4096,
+# and 3072 with idle lanes), {64,2} (8192); M tiles 1, 2, 4 and 8 rows; N not a multiple of
+# the rows per workgroup. Q4_K for comparison on the same inputs.
+FUSED = [(Q8_0, 1, 96, 1024), (Q8_0, 8, 50, 1024), (Q8_0, 5, 37, 512), (Q8_0, 2, 41, 4096),
+         (Q8_0, 1, 29, 3072), (Q8_0, 1, 70, 8192), (Q8_0, 3, 33, 2048), (Q4_K, 1, 45, 2560),
+         (Q4_K, 7, 21, 1024)]
+
+
+@pytest.mark.parametrize("wt,M,N,K", FUSED)
+def test_decode_fused_quantization(O, dev, wt, M, N, K):
+    """The fused decode path (dcq_mul_mat_ex without workspace at M <= 8): block sums bit-exact
+    (so the in-workgroup activation bytes and scales equal the standalone quantizer's) and
+    outputs within tolerance, including exact rounding ties."""
+    import torch
+    wq, x = make_inputs(O, wt, M, N, K, seed=31 + M + K, outliers=1)
+    x = _with_quantizer_ties(x, O.vec_dot_type(wt))
+    y_ref, l1 = O.mul_mat(wt, wq, x)
+    per = dc.block_sums_per_row(wt, K)
+    sums = torch.zeros((M, N, per), dtype=torch.int32, device=dev)
+    y = dc.mul_mat_ex(wt, to_dev(wq, dev), N, K, to_dev(x, dev), path=dc.PATH_GEMV, block_sums=sums)
+    O.assert_close(to_host(y), y_ref, l1, RTOL, what=f"fused type {wt} M{M} N{N} K{K}")
+    want = O.block_sums_matrix(wt, K, wq, O.quantize_rows(O.vec_dot_type(wt), x))
+    assert np.array_equal(to_host(sums), want)
+    y2 = dc.mul_mat_ex(wt, to_dev(wq, dev), N, K, to_dev(x, dev), path=dc.PATH_GEMV)
+    O.assert_close(to_host(y2), y_ref, l1, RTOL, what="fused production kernel")
+
+
 def test_mul_mat_padded_strides_and_workspace(O, dev):
     """Row strides larger than the data (ggml nb[1] > row size) and a caller workspace."""
     import torch
