@@ -1,0 +1,299 @@
+// dcq_decode_q6.hip — decode GEMV (M <= 8 per launch) for Q6_K weights, rows staged in LDS.
+//
+// Replaces the per-row vec_dot_q6_K_q8_K loop of cb_gemv_custom (core/src/inference.cpp:
+// 896-923) and ggml's CPU MUL_MAT at small M (core/src/inference.cpp:1794-1797, executed at
+// core/src/worker.cpp:544) for Q6_K weights. HBM-bound: each weight byte is read once.
+//
+// Why LDS. A Q6_K superblock is 210 bytes, so every other superblock of a row starts two
+// bytes off a dword, and the pieces a lane needs (ql, qh, scales, d) lie 64..208 bytes
+// apart: loading them straight into lanes spreads each wave instruction over many cache
+// lines. Here each wave copies one weight row into LDS with direct-to-LDS loads (no
+// registers held in flight): 16-byte loads (global_load_lds_dwordx4, 1 KB per wave
+// instruction) over the row's 16-byte aligned interior, one dword load instruction each
+// for the unaligned head and tail (global_load_lds_dword, 256 B, written over the same
+// bytes the 16-byte loads write — equal values). The row's LDS image is placed so that
+// 16-byte aligned global addresses land on 16-byte aligned LDS addresses. The planar Q8_K
+// activation (qs, bsums, d) is staged once per workgroup, shared by its waves.
+//
+// Steps. Loads retire in order, so a wave computes superblocks 16k .. 16k+15 as soon as
+// the loads holding their bytes have landed (s_waitcnt vmcnt on the count issued after
+// them) while the rest of its row is still streaming.
+//
+// Dot. Lane = unit (superblock s, quarter c = (h, lh)): elements l in [16lh, 16lh+16) of
+// half h for the four quarters t: ql low/high nibbles, 2 qh bits, q = (nibble | qh << 4) - 32
+// with the -32 taken through the 16-element bsums:
+//   iS = sum_t sc_t * (sum q6*q8 - 32 * bsum_t)                     (exact int32)
+//   y += (d * dA) * iS                          (vec_dot_q6_K_q8_K's per-superblock form)
+// Pieces are read from the dword at or below them and re-aligned with v_alignbyte; the
+// 6-bit values are assembled with one v_bfi_b32 each from the nibble and the qh bit pair.
+#include "dcq_common.h"
+#include "dcq_kernels.h"
+
+#include <stdlib.h>
+
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 in the clobber list (see dma4)
+
+namespace dcq {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Direct-to-LDS loads: lane l writes base + 4*l (dword) or base + 16*l (dwordx4), base
+// wave-uniform in M0. Inline asm: the builtin form waits for every earlier LDS-direct load
+// before the next. The compiler does not count these loads; the kernel issues no other
+// global loads and waits with explicit s_waitcnt. M0 has no other use in the kernel.
+__device__ __forceinline__ void dma4(const void* g, const void* lds_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+// global address 16-byte aligned, base 16-byte aligned
+__device__ __forceinline__ void dma16(const void* g, const void* lds_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt fields at their maxima: no wait on them)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+// s_waitcnt vmcnt(n) for a wave-uniform n in [LO, HI]: binary search over the immediates
+template <int LO, int HI>
+__device__ __forceinline__ void wait_vmcnt_rt(int n) {
+    if constexpr (LO == HI) {
+        wait_vmcnt<LO>();
+    } else {
+        constexpr int MID = (LO + HI) / 2;
+        if (n <= MID)
+            wait_vmcnt_rt<LO, MID>(n);
+        else
+            wait_vmcnt_rt<MID + 1, HI>(n);
+    }
+}
+
+// (a & m) | (b & ~m) as one v_bfi_b32 (the compiler otherwise re-derives the masks)
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+    return r;
+}
+
+// 16 bytes at a 2-byte aligned LDS address p: five dwords from the dword at or below p
+// (the fifth may lie past the piece: LDS rows are padded), shifted by (p & 2) bytes.
+__device__ __forceinline__ void lds16_a2(const uint8_t* p, uint32_t (&out)[4]) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 2u;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - sh);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[4];
+    out[0] = align_bytes(w1, w0, sh);
+    out[1] = align_bytes(w2, w1, sh);
+    out[2] = align_bytes(w3, w2, sh);
+    out[3] = align_bytes(w4, w3, sh);
+}
+__device__ __forceinline__ void lds8_a2(const uint8_t* p, uint32_t (&out)[2]) {
+    const uint32_t sh = (uint32_t)(uintptr_t)p & 2u;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p - sh);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
+    out[0] = align_bytes(w1, w0, sh);
+    out[1] = align_bytes(w2, w1, sh);
+}
+
+int env_int(const char* name, int dflt) {
+    const char* s = getenv(name);
+    return (s && *s) ? atoi(s) : dflt;
+}
+
+constexpr int kWaves = 4;      // weight rows per workgroup (one per wave)
+constexpr int kSbStep = 16;    // superblocks per step: 4 lanes each, one wave
+constexpr int kMaxNsb = 64;    // K <= 16384: the scales gather is one dword instruction
+constexpr size_t kMaxLds = 160 * 1024;
+
+// LDS carve-up, every region a whole number of its DMA instructions (lanes past a region's
+// end write duplicates into its padding). Activation (shared): qs [MT][q_ld] (1 KB pieces),
+// bsums [MT][b_ld bytes] (1 KB pieces), d [MT][64] floats; then one row image per wave.
+struct Q6Lds {
+    int q_ld, b_ld, pitch;
+    size_t act_bytes, total;
+    __host__ __device__ Q6Lds(int nsb, int MT) {
+        q_ld = (int)round_up(256 * nsb, 1024);
+        b_ld = (int)round_up(32 * nsb, 1024);
+        // image at 16 - head (head < 16): 16 + 16-byte interior (1 KB pieces) + the tail dwords
+        pitch = (int)round_up(16 + round_up(210 * nsb, 1024) + 256, 256);
+        act_bytes = (size_t)MT * (q_ld + b_ld + 256);
+        total = act_bytes + (size_t)kWaves * pitch;
+    }
+};
+
+}  // namespace
+
+template <int MT, bool DUMP>
+__global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
+    const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
+    const int8_t* __restrict__ xqs, const float* __restrict__ xd, const int16_t* __restrict__ xbs, int64_t m_ld,
+    int M, float* __restrict__ Y, int64_t y_stride, int32_t* __restrict__ sums, int64_t sums_n_stride) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const Q6Lds L(nsb, MT);
+    const int K = 256 * nsb;
+    const int row_bytes = 210 * nsb, row_dw = row_bytes / 4;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int8_t* aq = reinterpret_cast<int8_t*>(smem);
+    int8_t* abb = reinterpret_cast<int8_t*>(smem + (size_t)MT * L.q_ld);
+    float* ad = reinterpret_cast<float*>(smem + (size_t)MT * (L.q_ld + L.b_ld));
+    uint8_t* lw = smem + L.act_bytes + (size_t)wave * L.pitch;
+    const int64_t row = n0 + (int64_t)blockIdx.x * kWaves + wave;
+    const bool row_ok = row < n1;
+
+    // ---- 1. activation share: qs and bsums in 1 KB pieces, the scales gathered ----
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+        const int m = mi < M ? mi : M - 1;
+        const int8_t* qsrc = xqs + (int64_t)m * K;
+        for (int part = wave; part * 1024 < K; part += kWaves) {
+            const int c = 64 * part + lane, c_last = K / 16 - 1;
+            dma16(qsrc + 16 * (c < c_last ? c : c_last), aq + mi * L.q_ld + 1024 * part);
+        }
+        const int8_t* bsrc = reinterpret_cast<const int8_t*>(xbs + (int64_t)m * (K / 16));
+        for (int part = wave; part * 1024 < K / 8; part += kWaves) {
+            const int c = 64 * part + lane, c_last = K / 128 - 1;
+            dma16(bsrc + 16 * (c < c_last ? c : c_last), abb + mi * L.b_ld + 1024 * part);
+        }
+        if (wave == mi % kWaves) dma4(xd + (int64_t)(lane < nsb ? lane : nsb - 1) * m_ld + m, ad + 64 * mi);
+    }
+
+    // ---- 2. this wave's row: head dwords, 16-byte interior, tail dwords ----
+    // row byte b sits at img + b; img + head is 16-byte aligned like src + head
+    const uint8_t* src = W + (row_ok ? row : n1 - 1) * w_row_bytes;
+    const int head = (int)((16u - ((uint32_t)(uintptr_t)src & 15u)) & 15u);
+    uint8_t* img = lw + 16 - head;
+    const int nfull = (row_bytes - head) / 16;  // whole 16-byte chunks after the head
+    const int nx4 = (nfull + 63) / 64;
+    dma4(src + 4 * (lane < row_dw ? lane : row_dw - 1), img);
+    for (int j = 0; j < nx4; ++j) {
+        const int c = 64 * j + lane;
+        dma16(src + head + 16 * (c < nfull ? c : nfull - 1), lw + 16 + 1024 * j);
+    }
+    const int tail0 = row_dw > 64 ? row_dw - 64 : 0;
+    dma4(src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), img + 4 * tail0);
+    const int issued = nx4 + 2;
+    wait_vmcnt_rt<0, 63>(issued);  // the activation share (issued before the row) is in
+    __syncthreads();
+
+    // ---- 3. steps of 16 superblocks, each computed once its bytes are in ----
+    float acc[MT];
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
+    const int c4 = lane & 3, h = c4 >> 1, lh = c4 & 1;
+    const int nsteps = (nsb + kSbStep - 1) / kSbStep;
+    for (int k = 0; k < nsteps; ++k) {
+        // loads holding row bytes < 210*16*(k+1): the head and the 16-byte pieces up to that
+        // byte; the last step also needs the tail
+        const int endb = 3360 * (k + 1) < row_bytes ? 3360 * (k + 1) : row_bytes;
+        const int need = (endb - head + 1023) / 1024;
+        const int done = k == nsteps - 1 ? issued : 1 + (need < nx4 ? need : nx4);
+        wait_vmcnt_rt<0, 63>(issued - done);
+        const int s_raw = kSbStep * k + (lane >> 2);
+        const bool valid = s_raw < nsb;
+        const int s = valid ? s_raw : nsb - 1;
+        const uint8_t* sb = img + 210 * s;
+        uint32_t qa[4], qb[4], qh[4], scw[2];
+        lds16_a2(sb + 64 * h + 16 * lh, qa);
+        lds16_a2(sb + 64 * h + 32 + 16 * lh, qb);
+        lds16_a2(sb + 128 + 32 * h + 16 * lh, qh);
+        lds8_a2(sb + 192 + 8 * h, scw);
+        const float dW = half_bits_to_float(*reinterpret_cast<const uint16_t*>(sb + 208));
+        // scales of groups 8h + 2t + lh: bytes lh + 2t of the half's eight
+        const uint32_t ssh = (uint32_t)lh * 8u;
+        const int sc[4] = {(int)(int8_t)(scw[0] >> ssh), (int)(int8_t)(scw[0] >> (16 + ssh)),
+                           (int)(int8_t)(scw[1] >> ssh), (int)(int8_t)(scw[1] >> (16 + ssh))};
+        // 6-bit values of the four quarters t for each dword i (4 elements):
+        //   t = 0: ql_a low nibble | qh bits 0-1 << 4     t = 2: ql_a high nibble | qh bits 4-5
+        //   t = 1: ql_b low nibble | qh bits 2-3 << 2     t = 3: ql_b high nibble | qh bits 6-7 >> 2
+        uint32_t q6[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t m = 0x0F0F0F0Fu;
+            const uint32_t ev = qh[i] & 0x33333333u, od = qh[i] & 0xCCCCCCCCu;
+            q6[0][i] = bfi(m, qa[i], ev << 4);
+            q6[1][i] = bfi(m, qb[i], od << 2);
+            q6[2][i] = bfi(m, qa[i] >> 4, ev);
+            q6[3][i] = bfi(m, qb[i] >> 4, od >> 2);
+        }
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi) {
+            const int8_t* ap = aq + mi * L.q_ld + 256 * s + 128 * h + 16 * lh;
+            // bsums of groups 8h + 2t + lh, t = 0..3: every other int16 of [16s + 8h, +8)
+            const uint4 bq = *reinterpret_cast<const uint4*>(abb + mi * L.b_ld + 32 * s + 16 * h);
+            const uint32_t bsh = (uint32_t)lh * 16u;
+            const int bs[4] = {(int)(int16_t)(bq.x >> bsh), (int)(int16_t)(bq.y >> bsh), (int)(int16_t)(bq.z >> bsh),
+                               (int)(int16_t)(bq.w >> bsh)};
+            int iS = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint4 av = *reinterpret_cast<const uint4*>(ap + 32 * t);
+                int I = sdot4((int)q6[t][0], (int)av.x, 0);
+                I = sdot4((int)q6[t][1], (int)av.y, I);
+                I = sdot4((int)q6[t][2], (int)av.z, I);
+                I = sdot4((int)q6[t][3], (int)av.w, I);
+                iS += __mul24(sc[t], I - 32 * bs[t]);  // |sc| < 128, |I - 32 bs| < 2^18
+            }
+            if (DUMP && valid && row_ok && mi < M)
+                atomicAdd(sums + ((int64_t)mi * sums_n_stride + (row - n0)) * nsb + s, iS);
+            const float v = (dW * ad[64 * mi + s]) * (float)iS;
+            acc[mi] = valid ? acc[mi] + v : acc[mi];
+        }
+    }
+
+    // ---- 4. reduce the row over the wave ----
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+        const float v = lanes_sum<64>(acc[mi]);
+        if (lane == 0 && row_ok && mi < M) Y[(int64_t)mi * y_stride + (row - n0)] = v;
+    }
+}
+
+namespace {
+
+using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, const int16_t*,
+                      int64_t, int, float*, int64_t, int32_t*, int64_t);
+
+template <bool DUMP>
+Q6Fn q6_pick(int mt) {
+    switch (mt) {
+        case 1: return decode_q6k_lds_kernel<1, DUMP>;
+        case 2: return decode_q6k_lds_kernel<2, DUMP>;
+        case 4: return decode_q6k_lds_kernel<4, DUMP>;
+        default: return decode_q6k_lds_kernel<8, DUMP>;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
+                                 const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                                 int64_t sums_n_stride, hipStream_t st) {
+    const int nsb = (int)(K / 256);
+    // dword-granular head/tail loads: the row's bytes and its stride must be whole dwords;
+    // the weight base is 16-byte aligned (checked by the C ABI)
+    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb) return hipErrorNotSupported;
+    if (env_int("DCQ_Q6K_LDS_OFF", 0)) return hipErrorNotSupported;
+    for (int64_t m0 = 0; m0 < M; m0 += 8) {
+        const int64_t mc = M - m0 < 8 ? M - m0 : 8;
+        const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
+        if (Q6Lds(nsb, mt).total > kMaxLds) return hipErrorNotSupported;
+    }
+    const unsigned grid = (unsigned)((n1 - n0 + kWaves - 1) / kWaves);
+    for (int64_t m0 = 0; m0 < M; m0 += 8) {
+        const int64_t mc = M - m0 < 8 ? M - m0 : 8;
+        const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
+        Q6Fn fn = block_sums ? q6_pick<true>(mt) : q6_pick<false>(mt);
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), Q6Lds(nsb, mt).total, st, (const uint8_t*)W, w_row_bytes,
+                           n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.bs + m0 * (K / 16), act.m_ld, (int)mc,
+                           Y + m0 * y_stride, y_stride, block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr,
+                           sums_n_stride);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace dcq

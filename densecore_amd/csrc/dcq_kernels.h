@@ -36,6 +36,12 @@ hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64
                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                             int64_t sums_n_stride, hipStream_t st);
 
+// Q6_K decode with the weight rows staged in LDS by direct-to-LDS loads (K/256 even,
+// w_row_bytes % 4 == 0); hipErrorNotSupported otherwise (nothing launched).
+hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
+                                 const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                                 int64_t sums_n_stride, hipStream_t st);
+
 // Decode with the activation quantization fused in (X fp32, no workspace): one launch per
 // 8 rows of M. hipErrorNotSupported: the caller quantizes and uses launch_gemv.
 hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,

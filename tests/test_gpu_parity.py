@@ -94,6 +94,7 @@ CASES = [
     (Q8_0, 130, 257, 256),
     (Q4_K, 1, 97, 2560), (Q4_K, 2, 64, 256), (Q4_K, 5, 40, 512), (Q4_K, 64, 96, 2048), (Q4_K, 70, 33, 768),
     (Q6_K, 1, 50, 9728), (Q6_K, 1, 3, 256), (Q6_K, 8, 64, 512), (Q6_K, 33, 65, 1024), (Q6_K, 3, 17, 768),
+    (Q6_K, 2, 9, 16384), (Q6_K, 1, 5, 16896),
 ]
 
 
@@ -156,10 +157,11 @@ def test_decode_fused_quantization(O, dev, wt, M, N, K):
     O.assert_close(to_host(y2), y_ref, l1, RTOL, what="fused production kernel")
 
 
-def test_mul_mat_padded_strides_and_workspace(O, dev):
+@pytest.mark.parametrize("wt,M", [(Q4_K, 9), (Q6_K, 3), (Q8_0, 2)])
+def test_mul_mat_padded_strides_and_workspace(O, dev, wt, M):
     """Row strides larger than the data (ggml nb[1] > row size) and a caller workspace."""
     import torch
-    wt, M, N, K = Q4_K, 9, 45, 512
+    N, K = 45, 512
     wq, x = make_inputs(O, wt, M, N, K, seed=5)
     rs = dc.row_size(wt, K)
     wpad = np.zeros((N, rs + 64), np.uint8)
