@@ -19,7 +19,8 @@
 //     m_j * S_j); the 6-bit scale is applied to the exact I_j with v_mad_i32_i24;
 //   - per superblock: acc += dA * (d * sum_j sc_j I_j - dmin * sum_j m_j S_j)
 //     (vec_dot_q4_K_q8_K's per-superblock form).
-// The 8 partial tiles are summed in wave order through LDS at the end (deterministic).
+// The 8 partial tiles are summed in wave order through LDS at the end (deterministic), each
+// wave summing an eighth of the tile.
 #include "dcq_common.h"
 #include "dcq_kernels.h"
 
@@ -111,6 +112,21 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
         const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
         const uint32_t mnw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
         const float d = half_bits_to_float(hdr.x & 0xFFFFu), dmin = half_bits_to_float(hdr.x >> 16);
+        // weight operands of the 8 sub-blocks, shared by both m-tiles: nibbles, 6-bit scale and
+        // min (the mins operand, every byte m_j, is rebuilt per use: it would hold 32 registers)
+        v4i bv[8];
+        int sc[8], mn[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint4 q = qw[j >> 1];
+            const uint32_t sh = (j & 1) ? 4u : 0u;
+            bv[j].x = (int)((q.x >> sh) & 0x0F0F0F0Fu);
+            bv[j].y = (int)((q.y >> sh) & 0x0F0F0F0Fu);
+            bv[j].z = (int)((q.z >> sh) & 0x0F0F0F0Fu);
+            bv[j].w = (int)((q.w >> sh) & 0x0F0F0F0Fu);
+            sc[j] = (int)((scw[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+            mn[j] = (int)(((mnw[j >> 2] >> (8 * (j & 3))) & 0xFFu) * 0x01010101u);
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             v16i ai, amin;
@@ -121,26 +137,17 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const uint4 q = qw[j >> 1];
-                const uint32_t sh = (j & 1) ? 4u : 0u;
-                v4i bv;
-                bv.x = (int)((q.x >> sh) & 0x0F0F0F0Fu);
-                bv.y = (int)((q.y >> sh) & 0x0F0F0F0Fu);
-                bv.z = (int)((q.z >> sh) & 0x0F0F0F0Fu);
-                bv.w = (int)((q.w >> sh) & 0x0F0F0F0Fu);
-                const int sc = (int)((scw[j >> 2] >> (8 * (j & 3))) & 0xFFu);
-                const uint32_t mb = ((mnw[j >> 2] >> (8 * (j & 3))) & 0xFFu) * 0x01010101u;
-                v4i bm;
-                bm.x = bm.y = bm.z = bm.w = (int)mb;
                 // activation fragment: rows 32i + col, k = 32j + 16hl .. +16 (logical slot 2j + hl)
                 const v4i av = *reinterpret_cast<const v4i*>(a_lds + aswz(32 * i + col, 2 * j + hl));
                 v16i zero;
 #pragma unroll
                 for (int v = 0; v < 16; ++v) zero[v] = 0;
-                const v16i I = mfma32(av, bv, zero);
+                v4i bm;
+                bm.x = bm.y = bm.z = bm.w = mn[j];
+                const v16i I = mfma32(av, bv[j], zero);
                 amin = mfma32(av, bm, amin);
 #pragma unroll
-                for (int v = 0; v < 16; ++v) ai[v] = __mul24(sc, I[v]) + ai[v];
+                for (int v = 0; v < 16; ++v) ai[v] = __mul24(sc[j], I[v]) + ai[v];
             }
             // lane owns weight row n = n0 + col and activation rows m_v = 32i + 8(v/4) + 4hl + v%4
 #pragma unroll
@@ -178,14 +185,18 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
 #pragma unroll
         for (int v = 0; v < 16; ++v) part[((wave * 2 + i) * 16 + v) * 64 + lane] = acc[i][v];
     __syncthreads();
-    // wave w (< 2) reduces m-tile i = w; the other waves are done
-    if (wave < 2) {
-        const int i = wave;
+    // every wave sums 4 of the 32 (m-tile, value) pairs over the 8 partial tiles, in wave order
+    {
         const int n = n0 + col;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            float y = part[((0 * 2 + i) * 16 + v) * 64 + lane];
-            for (int w = 1; w < kWaves; ++w) y += part[((w * 2 + i) * 16 + v) * 64 + lane];
+        for (int k = 0; k < 4; ++k) {
+            const int pv = wave * 4 + k, i = pv >> 4, v = pv & 15;
+            float p8[kWaves];
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) p8[w] = part[((w * 2 + i) * 16 + v) * 64 + lane];
+            float y = p8[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) y += p8[w];
             const int m = m0 + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
             if (m < M && n < N) Y[(int64_t)m * y_stride + n] = y;
         }
