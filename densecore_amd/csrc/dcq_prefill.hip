@@ -105,26 +105,20 @@ __device__ __forceinline__ void block_step(const Stage& S, int kb, const Frag& f
     for (int j = 0; j < 2; ++j) cw[j] = -f.dw[j] * kMagicF;  // exact: 11-bit significand times 3*2^22
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        float da[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 v = *reinterpret_cast<const float4*>(&S.da[kb][wm + 32 * i + 8 * q + 4 * hl]);
-            da[4 * q] = v.x;
-            da[4 * q + 1] = v.y;
-            da[4 * q + 2] = v.z;
-            da[4 * q + 3] = v.w;
-        }
         const v16i D0 = mfma32(f.a[i], f.b[0], cmagic);
         const v16i D1 = mfma32(f.a[i], f.b[1], cmagic);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const float t = fmaf(__int_as_float(D0[v]), f.dw[0], cw[0]);
-            acc[i][0][v] = fmaf(t, da[v], acc[i][0][v]);
-        }
+        for (int q = 0; q < 4; ++q) {
+            const float4 v4 = *reinterpret_cast<const float4*>(&S.da[kb][wm + 32 * i + 8 * q + 4 * hl]);
+            const float da4[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const float t = fmaf(__int_as_float(D1[v]), f.dw[1], cw[1]);
-            acc[i][1][v] = fmaf(t, da[v], acc[i][1][v]);
+            for (int e = 0; e < 4; ++e) {
+                const int v = 4 * q + e;
+                const float t0 = fmaf(__int_as_float(D0[v]), f.dw[0], cw[0]);
+                acc[i][0][v] = fmaf(t0, da4[e], acc[i][0][v]);
+                const float t1 = fmaf(__int_as_float(D1[v]), f.dw[1], cw[1]);
+                acc[i][1][v] = fmaf(t1, da4[e], acc[i][1][v]);
+            }
         }
         if (DUMP) {
 #pragma unroll
@@ -173,13 +167,10 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
     // fills tile rows 8*(4w+i) .. +8, lane l the 16-byte slot (l % 8) of row 8*(4w+i) + l/8,
     // which holds logical slot (l % 8) ^ (row % 8)
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const int8_t* a_src[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = 8 * (4 * wave_u + i) + (lane >> 3);
-        const int slot = (lane & 7) ^ (row & 7);
-        a_src[i] = xqs + (int64_t)min(m0 + row, M - 1) * K + 16 * slot;
-    }
+    // instruction i: rows 8*(4w + i) + lane/8 share the slot pattern; one base row pointer,
+    // the other rows at +8*K per instruction (rows past M clamp to M - 1)
+    const int a_row0 = 8 * (4 * wave_u) + (lane >> 3);
+    const int a_slot = (lane & 7) ^ (a_row0 & 7);
     // activation scales: waves 0 and 1, one 1 KB instruction each: lane l of wave w holds
     // block (64w + l) / 32, rows 4 * ((64w + l) % 32) .. +4
     const int dc = 64 * (wave_u & 1) + lane;
@@ -192,7 +183,8 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
 #define DCQ_ISSUE(s_, S_)                                                                      \
     do {                                                                                       \
         _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                                       \
-            dma16(a_src[i_] + (s_) * kKS, (S_).a + 1024 * (4 * wave_u + i_));                  \
+            dma16(xqs + (int64_t)min(m0 + a_row0 + 8 * i_, M - 1) * K + 16 * a_slot + (s_) * kKS, \
+                  (S_).a + 1024 * (4 * wave_u + i_));                                          \
         if (wave_u < 2) dma16(da_src + (int64_t)(s_) * kKB * m_ld, &(S_).da[0][0] + 256 * wave_u); \
         const uint8_t* wp_ = w_src + (int64_t)(s_) * (kKB * 34);                               \
         _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_) {                                     \
