@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--replays", type=int, default=3)
+    ap.add_argument("--no-extras", action="store_true", help="skip the gate/up pair measurement")
     ap.add_argument("--profile", action="store_true", help="eager steps + a calibration copy, for rocprofv3 --pmc")
     return ap.parse_args()
 
@@ -210,6 +211,46 @@ def bench_config(cfg, args, dev):
     return out
 
 
+def bench_gate_up(cfg, args, dev):
+    """The SwiGLU gate/up pair at a config's shape (two weights of the same type and shape
+    sharing X): one dcq_ffn_gate_up call against two dcq_mul_mat calls (the reference's two
+    ggml_mul_mat nodes, without its separate silu and mul). Weight GB/s counts both matrices."""
+    import torch
+    import densecore_amd as dc
+    wq, x, _ = make_config_inputs(cfg, dev)
+    rb = dc.row_size(cfg.wtype, cfg.K)
+    wbytes = cfg.N * rb
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    bg = torch.empty((copies, cfg.N, rb), dtype=torch.uint8, device=dev)
+    bu = torch.empty((copies, cfg.N, rb), dtype=torch.uint8, device=dev)
+    for r in range(copies):
+        bg[r].copy_(wq)
+        bu[r].copy_(wq.roll(1, 0))  # a different matrix of the same statistics
+    ws = torch.empty(max(dc.ffn_gate_up_workspace_size(cfg.wtype, cfg.M, cfg.N, cfg.K),
+                         dc.mul_mat_workspace_size(cfg.wtype, cfg.M, cfg.K)), dtype=torch.uint8, device=dev)
+    y = torch.empty((cfg.M, cfg.N), dtype=torch.float32, device=dev)
+    u = torch.empty_like(y)
+    torch.cuda.synchronize()
+
+    def fused(i):
+        dc.ffn_gate_up(cfg.wtype, bg[i % copies], bu[i % copies], cfg.N, cfg.K, x, y=y, workspace=ws,
+                       stream=torch.cuda.current_stream().cuda_stream)
+
+    def separate(i):
+        s = torch.cuda.current_stream().cuda_stream
+        dc.mul_mat(cfg.wtype, bg[i % copies], cfg.N, cfg.K, x, y=y, workspace=ws, stream=s)
+        dc.mul_mat(cfg.wtype, bu[i % copies], cfg.N, cfg.K, x, y=u, workspace=ws, stream=s)
+
+    f_ms, f_k = time_graph(fused, args.steps, args.warmup, args.replays)
+    s_ms, s_k = time_graph(separate, args.steps, args.warmup, args.replays)
+    del bg, bu, ws, y, u, x, wq
+    torch.cuda.empty_cache()
+    return {"shape": f"config {cfg.index}: {dc.TYPE_NAMES[cfg.wtype]} M={cfg.M} N={cfg.N} K={cfg.K}, two weights",
+            "fused_us": f_ms * 1e3, "fused_kernels": f_k, "separate_us": s_ms * 1e3, "separate_kernels": s_k,
+            "fused_weight_GBps": 2 * wbytes / (f_ms * 1e-3) / 1e9,
+            "separate_weight_GBps": 2 * wbytes / (s_ms * 1e-3) / 1e9}
+
+
 def profile_config(cfg, args, dev):
     """Eager steps of one config (counter collection needs plain dispatches)."""
     import torch
@@ -296,6 +337,12 @@ def main():
             print(f"# config {c.index} {c.name}: step {r['step_us']:.2f} us ({r['kernels_per_step']} kernels), "
                   f"dominant kernel {r['dominant_us']:.2f} us, roofline {r['roofline']['achieved']:.1f} "
                   f"{r['roofline']['unit']} ({100 * r['roofline']['frac']:.1f} %)", file=sys.stderr, flush=True)
+    extras = {}
+    if HEADLINE in wanted and not args.no_extras:
+        extras["ffn_gate_up"] = bench_gate_up(dc.by_index(HEADLINE), args, dev)
+        g = extras["ffn_gate_up"]
+        print(f"# gate/up pair at config {HEADLINE}: fused {g['fused_us']:.2f} us ({g['fused_kernels']} kernels), "
+              f"two mul_mat calls {g['separate_us']:.2f} us", file=sys.stderr, flush=True)
     head = next((r for r in results if r["config"] == HEADLINE), results[0])
     hcfg = dc.by_index(head["config"])
     line = {
@@ -319,6 +366,7 @@ def main():
         "roofline": head["roofline"],
         "device": props.name, "gcn_arch": getattr(props, "gcnArchName", ""), "host": platform.node(),
         "configs": results,
+        "extras": extras,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(hcfg, args.cpu_seconds, args.cpu_threads)

@@ -14,7 +14,7 @@ SYMBOLS = [
     "dcq_version", "dcq_status_string", "dcq_block_size", "dcq_type_size", "dcq_row_size", "dcq_vec_dot_type",
     "dcq_supports_mul_mat", "dcq_quantize_rows", "dcq_mul_mat_workspace_size", "dcq_mul_mat", "dcq_mul_mat_ex",
     "dcq_block_sums_per_row", "dcq_dot_rows", "dcq_quantize_weights", "dcq_dequantize_rows",
-    "dcq_quantize_src1", "dcq_mul_mat_q",
+    "dcq_quantize_src1", "dcq_mul_mat_q", "dcq_ffn_gate_up_workspace_size", "dcq_ffn_gate_up",
 ]
 
 PATH_AUTO, PATH_GEMV, PATH_MMQ = 0, 1, 2
@@ -59,6 +59,8 @@ def lib():
             "dcq_dequantize_rows": (i32, [i32, vp, i64, i64, sz, vp, vp]),
             "dcq_quantize_src1": (i32, [i32, vp, i64, i64, sz, vp, sz, vp]),
             "dcq_mul_mat_q": (i32, [i32, vp, i64, i64, sz, vp, sz, i64, vp, sz, i32, vp]),
+            "dcq_ffn_gate_up_workspace_size": (sz, [i32, i64, i64, i64]),
+            "dcq_ffn_gate_up": (i32, [i32, vp, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp, sz, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -156,6 +158,24 @@ def mul_mat(wt, wq, n, k, x, y=None, workspace=None, w_row_bytes=None, stream=No
     _check("dcq_mul_mat", lib().dcq_mul_mat(
         wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace), ws_bytes,
         _stream(stream)))
+    return y
+
+
+def ffn_gate_up_workspace_size(wt, m, n, k):
+    return lib().dcq_ffn_gate_up_workspace_size(wt, m, n, k)
+
+
+def ffn_gate_up(wt, wg, wu, n, k, x, y=None, workspace=None, w_row_bytes=None, stream=None):
+    """Y[M, N] = silu(Wg x) * (Wu x): the SwiGLU gate/up pair with one activation quantization."""
+    import torch
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("dcq_ffn_gate_up", lib().dcq_ffn_gate_up(
+        wt, _ptr(wg), _ptr(wu), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace),
+        ws_bytes, _stream(stream)))
     return y
 
 

@@ -217,6 +217,58 @@ int dcq_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_byt
                           workspace_bytes, DCQ_PATH_AUTO, nullptr, stream);
 }
 
+size_t dcq_ffn_gate_up_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
+    const size_t a = dcq_mul_mat_workspace_size(wtype, M, K);
+    if (!a || N <= 0) return 0;
+    return a + (size_t)round_up(M * N * 4, 256);
+}
+
+int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_t K, size_t w_row_bytes,
+                    const float* X, int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = validate_mul_mat(wtype, Wg, N, K, w_row_bytes, X, M, x_stride_bytes, Y, y_stride_bytes);
+    if (rc) return rc;
+    if (!Wu) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(Wu, 16)) return DCQ_ERR_MISALIGNED;
+    const size_t need = dcq_ffn_gate_up_workspace_size(wtype, M, N, K);
+    if (workspace) {
+        if (workspace_bytes < need) return DCQ_ERR_WORKSPACE;
+        if (!aligned(workspace, 256)) return DCQ_ERR_MISALIGNED;
+    }
+    rc = check_device();
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
+    if (M <= 8) {
+        // one launch: both weight rows per lane group, the activation quantized in the workgroup
+        hipError_t e = launch_decode_fused_glu(wtype, Wg, Wu, (int64_t)w_row_bytes, N, K, X,
+                                               (int64_t)(x_stride_bytes / 4), M, Y, y_stride, st);
+        if (e != hipErrorNotSupported) return hip_status(e);
+    }
+    void* ws = workspace;
+    if (!ws) {
+        if (hipMallocAsync(&ws, need, st) != hipSuccess) return DCQ_ERR_HIP;
+    }
+    const int vdt = dcq_vec_dot_type(wtype);
+    PlanarBuffers pb;
+    const size_t act_bytes = planar_bytes(vdt, M, K, &pb, ws);
+    float* U = reinterpret_cast<float*>(static_cast<char*>(ws) + act_bytes);  // [M][N]
+    hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
+    const bool use_gemv = M <= 8;
+    if (e == hipSuccess)
+        e = use_gemv ? launch_gemv(wtype, Wg, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
+                     : launch_mmq(wtype, Wg, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st);
+    if (e == hipSuccess)
+        e = use_gemv ? launch_gemv(wtype, Wu, (int64_t)w_row_bytes, 0, N, K, pb, M, U, N, nullptr, N, st)
+                     : launch_mmq(wtype, Wu, (int64_t)w_row_bytes, N, K, pb, M, U, N, nullptr, st);
+    if (e == hipSuccess) e = launch_silu_mul(Y, y_stride, U, N, M, N, st);
+    if (!workspace) {
+        hipError_t e2 = hipFreeAsync(ws, st);
+        if (e == hipSuccess) e = e2;
+    }
+    return hip_status(e);
+}
+
 int dcq_quantize_src1(int wtype, const float* X, int64_t M, int64_t K, size_t x_stride_bytes, void* workspace,
                       size_t workspace_bytes, void* stream) {
     if (!is_weight_type(wtype)) return DCQ_ERR_UNSUPPORTED;

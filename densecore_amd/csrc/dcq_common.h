@@ -168,6 +168,10 @@ __device__ __forceinline__ float lanes_sum(float v) {
     return v;
 }
 
+// SiLU of the SwiGLU gate, g / (1 + e^-g) (ggml_silu's definition). expf is within a few ulp,
+// far inside the fp32 tolerance of the dot products it multiplies.
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
 // Pack the low bytes of four dwords (b0 lowest) into one dword.
 __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2, uint32_t b3) {
     const uint32_t lo = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);  // b0.byte0 | b1.byte0 << 8

@@ -33,6 +33,8 @@
 
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace dcq {
 
 namespace {
@@ -185,8 +187,12 @@ __host__ __device__ constexpr int stage_chunks(int P, int NS, int MT, bool fuse,
 
 // FUSE: X is fp32 [M][x_stride], quantized in the workgroup; else planar Q8_K
 // (xqs, xd, xbs, m_ld). M <= MT activation rows; LDS holds MT rows, rows >= M unused.
-template <class Fmt, int P, int MT, int NS, bool FUSE, bool DUMP, int NW = 4, int QC = stage_chunks(P, NS, MT, FUSE, NW)>
-__global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+// GLU: a second weight matrix W2 of the same shape shares the activation; the output is
+// silu(W x) * (W2 x) (the SwiGLU gate and up projections).
+template <class Fmt, int P, int MT, int NS, bool FUSE, bool DUMP, bool GLU = false, int NW = 4,
+          int QC = stage_chunks(P, NS, MT, FUSE, NW)>
+__global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __restrict__ W,
+                                                         const uint8_t* __restrict__ W2, int64_t w_row_bytes,
                                                          int64_t n0, int64_t n1, int nsb,
                                                          const float* __restrict__ X, int64_t x_stride,
                                                          const int8_t* __restrict__ xqs, const float* __restrict__ xd,
@@ -238,12 +244,21 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
     const bool row_ok = row < n1;
     const uint8_t* wrow = W + (row_ok ? row : n1 - 1) * w_row_bytes;
     const int q = lane % L, p = q >> 2, c = q & 3;  // superblock p of the step, quarter c
-    typename Fmt::Raw raw[NS];
+    typename Fmt::Raw raw[NS], raw2[GLU ? NS : 1];
 #pragma clang loop unroll(full)
     for (int t = 0; t < NS; ++t) {
         int s = t * P + p;
         s = s < nsb ? s : nsb - 1;
         Fmt::load(wrow + s * Fmt::kBytes, c, raw[t]);
+    }
+    if constexpr (GLU) {
+        const uint8_t* wrow2 = W2 + (row_ok ? row : n1 - 1) * w_row_bytes;
+#pragma clang loop unroll(full)
+        for (int t = 0; t < NS; ++t) {
+            int s = t * P + p;
+            s = s < nsb ? s : nsb - 1;
+            Fmt::load(wrow2 + s * Fmt::kBytes, c, raw2[t]);
+        }
     }
 
     // ---- 3. activation into LDS ----
@@ -286,9 +301,9 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
     __syncthreads();
 
     // ---- 4. per step: exact integer sums, one fp32 update per superblock ----
-    float acc[MT];
+    float acc[MT], acc2[MT];
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
+    for (int mi = 0; mi < MT; ++mi) acc[mi] = acc2[mi] = 0.0f;
     // fully unrolled: raw[t] must stay in registers (a rolled loop indexes it dynamically)
 #pragma clang loop unroll(full)
     for (int t = 0; t < NS; ++t) {
@@ -308,11 +323,18 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
                 for (int k = 0; k < Fmt::kSumsPerSb; ++k) atomicAdd(srow + Fmt::kSumsPerSb * s + k, ints[k]);
             }
             acc[mi] = valid ? acc[mi] + v : acc[mi];
+            if constexpr (GLU) {
+                const float v2 = Fmt::dot(raw2[t], act, mi, s, c, K, MT, nsb, ints);
+                acc2[mi] = valid ? acc2[mi] + v2 : acc2[mi];
+            }
         }
     }
     // ---- 5. reduce the L lanes of each row ----
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi) acc[mi] = lanes_sum<L>(acc[mi]);
+    for (int mi = 0; mi < MT; ++mi) {
+        acc[mi] = lanes_sum<L>(acc[mi]);
+        if constexpr (GLU) acc[mi] = silu(acc[mi]) * lanes_sum<L>(acc2[mi]);
+    }
     if (q == 0 && row_ok) {
 #pragma unroll
         for (int mi = 0; mi < MT; ++mi)
@@ -323,8 +345,9 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
 // ------------------------------------------------------------------ dispatch
 namespace {
 
-using DecodeFn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const float*, int64_t, const int8_t*,
-                          const float*, const int16_t*, int64_t, int, float*, int64_t, int32_t*, int64_t);
+using DecodeFn = void (*)(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, int, const float*, int64_t,
+                          const int8_t*, const float*, const int16_t*, int64_t, int, float*, int64_t, int32_t*,
+                          int64_t);
 
 // Launch shapes (P superblocks of a row per step, NS steps): a row of nsb <= P*NS
 // superblocks. Other K fall back to the generic kernel.
@@ -342,39 +365,43 @@ constexpr int waves_of() {
     return 4;
 }
 
-template <class Fmt, int I, int MT, bool FUSE, bool DUMP>
+template <class Fmt, int I, int MT, bool FUSE, bool DUMP, bool GLU>
 DecodeFn fn_of() {
-    return decode_kq_kernel<Fmt, kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP, waves_of<FUSE, MT>()>;
+    return decode_kq_kernel<Fmt, kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP, GLU, waves_of<FUSE, MT>()>;
 }
 
-template <class Fmt, int I, bool FUSE, bool DUMP>
+template <class Fmt, int I, bool FUSE, bool DUMP, bool GLU>
 DecodeFn pick_mt(int mt) {
     switch (mt) {
-        case 1: return fn_of<Fmt, I, 1, FUSE, DUMP>();
-        case 2: return fn_of<Fmt, I, 2, FUSE, DUMP>();
-        case 4: return fn_of<Fmt, I, 4, FUSE, DUMP>();
-        default: return fn_of<Fmt, I, 8, FUSE, DUMP>();
+        case 1: return fn_of<Fmt, I, 1, FUSE, DUMP, GLU>();
+        case 2: return fn_of<Fmt, I, 2, FUSE, DUMP, GLU>();
+        case 4: return fn_of<Fmt, I, 4, FUSE, DUMP, GLU>();
+        default: return fn_of<Fmt, I, 8, FUSE, DUMP, GLU>();
     }
 }
 
-template <class Fmt, bool FUSE, bool DUMP>
+template <class Fmt, bool FUSE, bool DUMP, bool GLU = false>
 DecodeFn pick_shape(int idx, int mt) {
     switch (idx) {
-        case 0: return pick_mt<Fmt, 0, FUSE, DUMP>(mt);
-        case 1: return pick_mt<Fmt, 1, FUSE, DUMP>(mt);
-        case 2: return pick_mt<Fmt, 2, FUSE, DUMP>(mt);
-        case 3: return pick_mt<Fmt, 3, FUSE, DUMP>(mt);
-        case 4: return pick_mt<Fmt, 4, FUSE, DUMP>(mt);
-        case 5: return pick_mt<Fmt, 5, FUSE, DUMP>(mt);
-        case 6: return pick_mt<Fmt, 6, FUSE, DUMP>(mt);
-        case 7: return pick_mt<Fmt, 7, FUSE, DUMP>(mt);
-        case 8: return pick_mt<Fmt, 8, FUSE, DUMP>(mt);
-        default: return pick_mt<Fmt, 9, FUSE, DUMP>(mt);
+        case 0: return pick_mt<Fmt, 0, FUSE, DUMP, GLU>(mt);
+        case 1: return pick_mt<Fmt, 1, FUSE, DUMP, GLU>(mt);
+        case 2: return pick_mt<Fmt, 2, FUSE, DUMP, GLU>(mt);
+        case 3: return pick_mt<Fmt, 3, FUSE, DUMP, GLU>(mt);
+        case 4: return pick_mt<Fmt, 4, FUSE, DUMP, GLU>(mt);
+        case 5: return pick_mt<Fmt, 5, FUSE, DUMP, GLU>(mt);
+        case 6: return pick_mt<Fmt, 6, FUSE, DUMP, GLU>(mt);
+        case 7: return pick_mt<Fmt, 7, FUSE, DUMP, GLU>(mt);
+        case 8: return pick_mt<Fmt, 8, FUSE, DUMP, GLU>(mt);
+        default: return pick_mt<Fmt, 9, FUSE, DUMP, GLU>(mt);
     }
 }
 
+// the gate/up pair (GLU) is built for Q4_K with the fused activation only
 template <class Fmt>
-DecodeFn pick_fn(bool fuse, bool dump, int idx, int mt) {
+DecodeFn pick_fn(bool fuse, bool dump, bool glu, int idx, int mt) {
+    if constexpr (std::is_same<Fmt, FmtQ4K>::value) {
+        if (glu) return pick_shape<Fmt, true, false, true>(idx, mt);
+    }
     return fuse ? (dump ? pick_shape<Fmt, true, true>(idx, mt) : pick_shape<Fmt, true, false>(idx, mt))
                 : (dump ? pick_shape<Fmt, false, true>(idx, mt) : pick_shape<Fmt, false, false>(idx, mt));
 }
@@ -404,11 +431,14 @@ int choose_shape(int nsb) {
     return best;
 }
 
-hipError_t launch_kq(int wtype, bool fuse, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
-                     const float* X, int64_t x_stride, const PlanarBuffers* act, int64_t M, float* Y,
+// W2 != nullptr: the gate/up pair (Q4_K, fused activation, no block sums): Y = silu(W x) * (W2 x)
+hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_t w_row_bytes, int64_t n0, int64_t n1,
+                     int64_t K, const float* X, int64_t x_stride, const PlanarBuffers* act, int64_t M, float* Y,
                      int64_t y_stride, int32_t* block_sums, int64_t sums_n_stride, hipStream_t st) {
     const int nsb = (int)(K / 256);
     if (wtype != kTypeQ4_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
+    const bool glu = W2 != nullptr;
+    if (glu && (wtype != kTypeQ4_K || !fuse || block_sums)) return hipErrorNotSupported;
     if (wtype == kTypeQ4_K ? (w_row_bytes % 16 != 0) : (w_row_bytes % 2 != 0)) return hipErrorNotSupported;
     const int idx = choose_shape(nsb);
     if (idx < 0) return hipErrorNotSupported;
@@ -429,10 +459,11 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, int64_t w_row_bytes, i
         const int nw = 4;
         const int rows_per_block = nw * (64 / (4 * P));
         const unsigned grid = (unsigned)((n1 - n0 + rows_per_block - 1) / rows_per_block);
-        DecodeFn fn = wtype == kTypeQ4_K ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, idx, mt)
-                                         : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, idx, mt);
+        DecodeFn fn = wtype == kTypeQ4_K ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, glu, idx, mt)
+                                         : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, false, idx, mt);
         // rows beyond mc in an MT tile stage the last real activation row and are never stored
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), lds, st, (const uint8_t*)W, w_row_bytes, n0, n1, nsb,
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), lds, st, (const uint8_t*)W, (const uint8_t*)W2, w_row_bytes,
+                           n0, n1, nsb,
                            fuse ? X + m0 * x_stride : nullptr, x_stride, fuse ? nullptr : act->qs + m0 * K,
                            fuse ? nullptr : act->d + m0, fuse ? nullptr : act->bs + m0 * (K / 16),
                            fuse ? 0 : act->m_ld, (int)mc, Y + m0 * y_stride, y_stride,
@@ -446,7 +477,7 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, int64_t w_row_bytes, i
 hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                             int64_t sums_n_stride, hipStream_t st) {
-    return launch_kq(wtype, false, W, w_row_bytes, n0, n1, K, nullptr, 0, &act, M, Y, y_stride, block_sums,
+    return launch_kq(wtype, false, W, nullptr, w_row_bytes, n0, n1, K, nullptr, 0, &act, M, Y, y_stride, block_sums,
                      sums_n_stride, st);
 }
 
@@ -457,7 +488,18 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
     if (wtype == kTypeQ8_0)
         return launch_decode_fused_q8_0(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st);
     if (wtype != kTypeQ4_K && !(wtype == kTypeQ6_K && env_int("DCQ_Q6K_DECODE", 0))) return hipErrorNotSupported;
-    return launch_kq(wtype, true, W, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums, N, st);
+    return launch_kq(wtype, true, W, nullptr, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums,
+                     N, st);
+}
+
+hipError_t launch_decode_fused_glu(int wtype, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
+                                   const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
+                                   hipStream_t st) {
+    if (env_int("DCQ_NO_FUSE", 0)) return hipErrorNotSupported;
+    if (wtype == kTypeQ8_0)
+        return launch_decode_fused_q8_0_glu(Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, st);
+    if (wtype != kTypeQ4_K) return hipErrorNotSupported;
+    return launch_kq(wtype, true, Wg, Wu, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, nullptr, N, st);
 }
 
 }  // namespace dcq

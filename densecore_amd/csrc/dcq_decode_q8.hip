@@ -38,6 +38,38 @@ __device__ __forceinline__ float row8_max(float v) {
     return v;
 }
 
+// 68 bytes (two 34-byte blocks) at a dword aligned address into 17 dwords
+__device__ __forceinline__ void load_pair(const uint8_t* p, uint32_t (&r)[17]) {
+    const U32x4 a = ld4(p), b = ld4(p + 16), c = ld4(p + 32), d = ld4(p + 48);
+    r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+    r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+    r[8] = c.x; r[9] = c.y; r[10] = c.z; r[11] = c.w;
+    r[12] = d.x; r[13] = d.y; r[14] = d.z; r[15] = d.w;
+    r[16] = ld1(p + 64);
+}
+
+// exact int32 sums of a block pair (w: 17 dwords, block 0's bytes start at byte 2, block 1's at
+// byte 36) against 64 activation bytes
+__device__ __forceinline__ void pair_sums(const uint32_t* w, uint4 a0, uint4 a1, uint4 a2, uint4 a3, int& i0,
+                                          int& i1) {
+    i0 = sdot4((int)align_bytes(w[1], w[0], 2), (int)a0.x, 0);
+    i0 = sdot4((int)align_bytes(w[2], w[1], 2), (int)a0.y, i0);
+    i0 = sdot4((int)align_bytes(w[3], w[2], 2), (int)a0.z, i0);
+    i0 = sdot4((int)align_bytes(w[4], w[3], 2), (int)a0.w, i0);
+    i0 = sdot4((int)align_bytes(w[5], w[4], 2), (int)a1.x, i0);
+    i0 = sdot4((int)align_bytes(w[6], w[5], 2), (int)a1.y, i0);
+    i0 = sdot4((int)align_bytes(w[7], w[6], 2), (int)a1.z, i0);
+    i0 = sdot4((int)align_bytes(w[8], w[7], 2), (int)a1.w, i0);
+    i1 = sdot4((int)w[9], (int)a2.x, 0);
+    i1 = sdot4((int)w[10], (int)a2.y, i1);
+    i1 = sdot4((int)w[11], (int)a2.z, i1);
+    i1 = sdot4((int)w[12], (int)a2.w, i1);
+    i1 = sdot4((int)w[13], (int)a3.x, i1);
+    i1 = sdot4((int)w[14], (int)a3.y, i1);
+    i1 = sdot4((int)w[15], (int)a3.z, i1);
+    i1 = sdot4((int)w[16], (int)a3.w, i1);
+}
+
 constexpr int kMaxStagePasses = 8;  // float4 registers of activation per thread
 
 // (block, activation row) items staged per workgroup pass: 8 lanes each
@@ -52,8 +84,10 @@ int env_int(const char* name, int dflt) {
 
 }  // namespace
 
-template <int G, int NS, int MT, int NW, bool DUMP, int QC = q8_stage_passes(G, NS, MT, NW)>
-__global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+// GLU: a second weight matrix W2 shares the activation; the output is silu(W x) * (W2 x).
+template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, int QC = q8_stage_passes(G, NS, MT, NW)>
+__global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __restrict__ W,
+                                                           const uint8_t* __restrict__ W2, int64_t w_row_bytes,
                                                            int64_t N, int K, const float* __restrict__ X,
                                                            int64_t x_stride, int M, float* __restrict__ Y,
                                                            int64_t y_stride, int32_t* __restrict__ sums,
@@ -85,18 +119,21 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __r
         const bool row_ok = row < N;
         const uint8_t* wrow = W + (row_ok ? row : N - 1) * w_row_bytes;
         const int g = lane % G;
-        uint32_t raw[NS][17];
+        uint32_t raw[NS][17], raw2[GLU ? NS : 1][17];
 #pragma clang loop unroll(full)
         for (int t = 0; t < NS; ++t) {
             int u = g + G * t;
             u = u < U ? u : U - 1;
-            const uint8_t* p = wrow + (int64_t)u * 68;
-            const U32x4 a = ld4(p), b = ld4(p + 16), c = ld4(p + 32), d = ld4(p + 48);
-            raw[t][0] = a.x; raw[t][1] = a.y; raw[t][2] = a.z; raw[t][3] = a.w;
-            raw[t][4] = b.x; raw[t][5] = b.y; raw[t][6] = b.z; raw[t][7] = b.w;
-            raw[t][8] = c.x; raw[t][9] = c.y; raw[t][10] = c.z; raw[t][11] = c.w;
-            raw[t][12] = d.x; raw[t][13] = d.y; raw[t][14] = d.z; raw[t][15] = d.w;
-            raw[t][16] = ld1(p + 64);
+            load_pair(wrow + (int64_t)u * 68, raw[t]);
+        }
+        if constexpr (GLU) {
+            const uint8_t* wrow2 = W2 + (row_ok ? row : N - 1) * w_row_bytes;
+#pragma clang loop unroll(full)
+            for (int t = 0; t < NS; ++t) {
+                int u = g + G * t;
+                u = u < U ? u : U - 1;
+                load_pair(wrow2 + (int64_t)u * 68, raw2[t]);
+            }
         }
         // keep the quantizer's first use of the activation (and its wait) behind the weight loads
         __builtin_amdgcn_sched_barrier(0);
@@ -127,9 +164,9 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __r
         __syncthreads();
 
         // ---- 4. exact block sums, one fp32 update per block ----
-        float acc[MT];
+        float acc[MT], acc2[MT];
 #pragma unroll
-        for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
+        for (int mi = 0; mi < MT; ++mi) acc[mi] = acc2[mi] = 0.0f;
 #pragma clang loop unroll(full)
         for (int t = 0; t < NS; ++t) {
             const int u_raw = g + G * t;
@@ -147,22 +184,8 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __r
                 const uint4 a2 = *reinterpret_cast<const uint4*>(aq + 32);
                 const uint4 a3 = *reinterpret_cast<const uint4*>(aq + 48);
                 const float2 dA = *reinterpret_cast<const float2*>(act_d + mi * nb + 2 * u);
-                int i0 = sdot4((int)align_bytes(w[1], w[0], 2), (int)a0.x, 0);
-                i0 = sdot4((int)align_bytes(w[2], w[1], 2), (int)a0.y, i0);
-                i0 = sdot4((int)align_bytes(w[3], w[2], 2), (int)a0.z, i0);
-                i0 = sdot4((int)align_bytes(w[4], w[3], 2), (int)a0.w, i0);
-                i0 = sdot4((int)align_bytes(w[5], w[4], 2), (int)a1.x, i0);
-                i0 = sdot4((int)align_bytes(w[6], w[5], 2), (int)a1.y, i0);
-                i0 = sdot4((int)align_bytes(w[7], w[6], 2), (int)a1.z, i0);
-                i0 = sdot4((int)align_bytes(w[8], w[7], 2), (int)a1.w, i0);
-                int i1 = sdot4((int)w[9], (int)a2.x, 0);
-                i1 = sdot4((int)w[10], (int)a2.y, i1);
-                i1 = sdot4((int)w[11], (int)a2.z, i1);
-                i1 = sdot4((int)w[12], (int)a2.w, i1);
-                i1 = sdot4((int)w[13], (int)a3.x, i1);
-                i1 = sdot4((int)w[14], (int)a3.y, i1);
-                i1 = sdot4((int)w[15], (int)a3.z, i1);
-                i1 = sdot4((int)w[16], (int)a3.w, i1);
+                int i0, i1;
+                pair_sums(w, a0, a1, a2, a3, i0, i1);
                 if (DUMP && valid && row_ok && mi < M) {
                     int32_t* srow = sums + ((int64_t)mi * sums_n_stride + row) * nb;
                     atomicAdd(srow + 2 * u, i0);
@@ -170,11 +193,22 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __r
                 }
                 const float v = fmaf((float)i1, dW1 * dA.y, (float)i0 * (dW0 * dA.x));
                 acc[mi] = valid ? acc[mi] + v : acc[mi];
+                if constexpr (GLU) {
+                    const uint32_t* w2 = raw2[t];
+                    const float eW0 = half_bits_to_float(w2[0] & 0xFFFFu), eW1 = half_bits_to_float(w2[8] >> 16);
+                    int j0, j1;
+                    pair_sums(w2, a0, a1, a2, a3, j0, j1);
+                    const float v2 = fmaf((float)j1, eW1 * dA.y, (float)j0 * (eW0 * dA.x));
+                    acc2[mi] = valid ? acc2[mi] + v2 : acc2[mi];
+                }
             }
         }
         // ---- 5. reduce the G lanes of each row ----
 #pragma unroll
-        for (int mi = 0; mi < MT; ++mi) acc[mi] = lanes_sum<G>(acc[mi]);
+        for (int mi = 0; mi < MT; ++mi) {
+            acc[mi] = lanes_sum<G>(acc[mi]);
+            if constexpr (GLU) acc[mi] = silu(acc[mi]) * lanes_sum<G>(acc2[mi]);
+        }
         if (g == 0 && row_ok) {
 #pragma unroll
             for (int mi = 0; mi < MT; ++mi)
@@ -185,8 +219,8 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __r
 
 namespace {
 
-using DecodeQ8Fn = void (*)(const uint8_t*, int64_t, int64_t, int, const float*, int64_t, int, float*, int64_t,
-                            int32_t*, int64_t);
+using DecodeQ8Fn = void (*)(const uint8_t*, const uint8_t*, int64_t, int64_t, int, const float*, int64_t, int,
+                            float*, int64_t, int32_t*, int64_t);
 
 // (G lanes per row, NS pairs per lane): a row of U = K/64 pairs needs G*NS >= U
 struct Q8Shape {
@@ -201,32 +235,32 @@ static_assert(kNumQ8Shapes == 10, "pick_q8_shape covers every shape");
 #endif
 constexpr int kQ8Waves = DCQ_Q8_NW;
 
-template <int I, int MT, bool DUMP>
+template <int I, int MT, bool DUMP, bool GLU>
 DecodeQ8Fn q8_fn() {
-    return decode_q8_0_kernel<kQ8Shapes[I].G, kQ8Shapes[I].NS, MT, kQ8Waves, DUMP>;
+    return decode_q8_0_kernel<kQ8Shapes[I].G, kQ8Shapes[I].NS, MT, kQ8Waves, DUMP, GLU>;
 }
-template <int I, bool DUMP>
+template <int I, bool DUMP, bool GLU>
 DecodeQ8Fn q8_pick_mt(int mt) {
     switch (mt) {
-        case 1: return q8_fn<I, 1, DUMP>();
-        case 2: return q8_fn<I, 2, DUMP>();
-        case 4: return q8_fn<I, 4, DUMP>();
-        default: return q8_fn<I, 8, DUMP>();
+        case 1: return q8_fn<I, 1, DUMP, GLU>();
+        case 2: return q8_fn<I, 2, DUMP, GLU>();
+        case 4: return q8_fn<I, 4, DUMP, GLU>();
+        default: return q8_fn<I, 8, DUMP, GLU>();
     }
 }
-template <bool DUMP>
+template <bool DUMP, bool GLU = false>
 DecodeQ8Fn q8_pick_shape(int idx, int mt) {
     switch (idx) {
-        case 0: return q8_pick_mt<0, DUMP>(mt);
-        case 1: return q8_pick_mt<1, DUMP>(mt);
-        case 2: return q8_pick_mt<2, DUMP>(mt);
-        case 3: return q8_pick_mt<3, DUMP>(mt);
-        case 4: return q8_pick_mt<4, DUMP>(mt);
-        case 5: return q8_pick_mt<5, DUMP>(mt);
-        case 6: return q8_pick_mt<6, DUMP>(mt);
-        case 7: return q8_pick_mt<7, DUMP>(mt);
-        case 8: return q8_pick_mt<8, DUMP>(mt);
-        default: return q8_pick_mt<9, DUMP>(mt);
+        case 0: return q8_pick_mt<0, DUMP, GLU>(mt);
+        case 1: return q8_pick_mt<1, DUMP, GLU>(mt);
+        case 2: return q8_pick_mt<2, DUMP, GLU>(mt);
+        case 3: return q8_pick_mt<3, DUMP, GLU>(mt);
+        case 4: return q8_pick_mt<4, DUMP, GLU>(mt);
+        case 5: return q8_pick_mt<5, DUMP, GLU>(mt);
+        case 6: return q8_pick_mt<6, DUMP, GLU>(mt);
+        case 7: return q8_pick_mt<7, DUMP, GLU>(mt);
+        case 8: return q8_pick_mt<8, DUMP, GLU>(mt);
+        default: return q8_pick_mt<9, DUMP, GLU>(mt);
     }
 }
 
@@ -255,10 +289,13 @@ int choose_q8_shape(int U) {
 
 }  // namespace
 
-hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
-                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                    hipStream_t st) {
+namespace {
+
+// W2 != nullptr: the gate/up pair (no block sums), Y = silu(W x) * (W2 x)
+hipError_t launch_q8(const void* W, const void* W2, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
+                     int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
     if (K % 64 != 0 || w_row_bytes % 4 != 0 || x_stride % 4 != 0) return hipErrorNotSupported;
+    if (W2 && block_sums) return hipErrorNotSupported;
     const int U = (int)(K / 64);
     const int idx = choose_q8_shape(U);
     if (idx < 0) return hipErrorNotSupported;
@@ -277,12 +314,27 @@ hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t 
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         const size_t lds = (size_t)mt * K * 9 / 8;
-        DecodeQ8Fn fn = block_sums ? q8_pick_shape<true>(idx, mt) : q8_pick_shape<false>(idx, mt);
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kQ8Waves), lds, st, (const uint8_t*)W, w_row_bytes, N, (int)K,
-                           X + m0 * x_stride, x_stride, (int)mc, Y + m0 * y_stride, y_stride,
+        DecodeQ8Fn fn = W2 ? q8_pick_shape<false, true>(idx, mt)
+                           : (block_sums ? q8_pick_shape<true>(idx, mt) : q8_pick_shape<false>(idx, mt));
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kQ8Waves), lds, st, (const uint8_t*)W, (const uint8_t*)W2,
+                           w_row_bytes, N, (int)K, X + m0 * x_stride, x_stride, (int)mc, Y + m0 * y_stride, y_stride,
                            block_sums ? block_sums + m0 * N * per_row_sums : nullptr, N);
     }
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
+                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                                    hipStream_t st) {
+    return launch_q8(W, nullptr, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st);
+}
+
+hipError_t launch_decode_fused_q8_0_glu(const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
+                                        const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
+                                        hipStream_t st) {
+    return launch_q8(Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, nullptr, st);
 }
 
 }  // namespace dcq

@@ -36,6 +36,18 @@ hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64
                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                             int64_t sums_n_stride, hipStream_t st);
 
+// SwiGLU gate/up pair at M <= 8 with the activation quantization fused in (Q4_K, Q8_0):
+// Y = silu(Wg x) * (Wu x); hipErrorNotSupported when the fused kernels do not cover the shape.
+hipError_t launch_decode_fused_glu(int wtype, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
+                                   const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
+                                   hipStream_t st);
+hipError_t launch_decode_fused_q8_0_glu(const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
+                                        const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
+                                        hipStream_t st);
+// Y[m][n] = silu(Y[m][n]) * U[m][n] (the SwiGLU product after two separate projections)
+hipError_t launch_silu_mul(float* Y, int64_t y_stride, const float* U, int64_t u_stride, int64_t M, int64_t N,
+                           hipStream_t st);
+
 // Q6_K decode with the weight rows staged in LDS by direct-to-LDS loads (K/256 even,
 // w_row_bytes % 4 == 0); hipErrorNotSupported otherwise (nothing launched).
 hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,

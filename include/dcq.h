@@ -129,6 +129,19 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
                   const void* workspace, size_t workspace_bytes, int64_t M, float* Y,
                   size_t y_stride_bytes, int path, void* stream);
 
+/* ---- the SwiGLU gate/up pair ----
+ * Y[m][n] = silu(sum_k Wg[n][k] x[m][k]) * (sum_k Wu[n][k] x[m][k]), silu(g) = g / (1 + e^-g):
+ * the reference FFN's w1 = mul_mat(W1, x), w3 = mul_mat(W3, x), ggml_mul(ggml_silu(w1), w3)
+ * (core/src/inference.cpp:1794-1796) in one call. Both weights share wtype, shape and row
+ * stride, and X's quantization. At M <= 8 (Q4_K, Q8_0) one fused kernel streams both weight
+ * rows; otherwise X is quantized once, both projections run, then the product.
+ * Requirements as dcq_mul_mat's, for both weights. workspace may be NULL; otherwise it must hold
+ * dcq_ffn_gate_up_workspace_size(wtype, M, N, K) bytes, 256-byte aligned. */
+size_t dcq_ffn_gate_up_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
+int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_t K, size_t w_row_bytes,
+                    const float* X, int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- row-range dot with pre-quantized input ----
  * ComputeDotProductBatch (core/src/simd_ops.cpp:140-197): Y[r - n0] = vec_dot(K, W row r, Xq)
  * for r in [n0, n1); Xq is ONE row already quantized to the vec_dot_type (ggml layout, as

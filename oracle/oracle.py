@@ -198,6 +198,39 @@ def mul_mat(wt, wq, x, variant=Q8_0_X86, nthreads=0, want_l1=True):
     return (y, l1) if want_l1 else y
 
 
+def silu(g):
+    """ggml_silu, the SwiGLU gate nonlinearity g / (1 + e^-g), in float64 (ggml's definition;
+    reference call ggml_silu at core/src/inference.cpp:1796)."""
+    g = np.asarray(g, dtype=np.float64)
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g))
+
+
+def ffn_gate_up(wt, wg, wu, x, variant=Q8_0_X86, nthreads=0):
+    """The reference FFN's gate/up pair and product (core/src/inference.cpp:1794-1796):
+    w1 = mul_mat(W1, x), w3 = mul_mat(W3, x), y = silu(w1) * w3, both projections on the same
+    quantized x. Returns y (float64) and (g, l1_g, u, l1_u) for the tolerance."""
+    g, l1g = mul_mat(wt, wg, x, variant, nthreads)
+    u, l1u = mul_mat(wt, wu, x, variant, nthreads)
+    return silu(g) * u.astype(np.float64), (g, l1g, u, l1u)
+
+
+def assert_close_gate_up(y, y_ref, parts, rtol=1e-4, what=""):
+    """Tolerance of silu(g) * u when g and u each carry the mul_mat bound
+    |dg| <= rtol * max(|g|, L1_g) (same for u): |dy| <= 1.1 |dg| (|u| + |du|) + |silu(g)| |du|
+    (|silu'| < 1.1 everywhere)."""
+    g, l1g, u, l1u = (np.asarray(a, dtype=np.float64) for a in parts)
+    dg = rtol * np.maximum(np.abs(g), l1g)
+    du = rtol * np.maximum(np.abs(u), l1u)
+    bound = 1.1 * dg * (np.abs(u) + du) + np.abs(silu(g)) * du + 1e-30
+    err = np.abs(np.asarray(y, dtype=np.float64) - y_ref)
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err / bound), err.shape)
+        raise AssertionError(f"{what}: {int(bad.sum())} of {err.size} outside the bound; worst at {i}: "
+                             f"got {y[i]} want {y_ref[i]} bound {bound[i]}")
+
+
 def assert_close(y, y_ref, l1, rtol=1e-4, what=""):
     """The output tolerance: |y - y_ref| <= rtol * max(|y_ref|, L1), elementwise.
 

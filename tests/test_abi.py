@@ -106,6 +106,29 @@ def test_dot_rows_and_quantize_validation():
     assert L.dcq_dequantize_rows(2, 0x1000, 1, 256, 64, 0x2000, None) == UNSUPPORTED
 
 
+def test_ffn_gate_up_workspace_and_validation():
+    """The gate/up pair: workspace = the activation's + an fp32 [M][N] buffer; argument errors
+    (the second weight included) come back before any device call."""
+    L = dc.lib()
+    assert dc.ffn_gate_up_workspace_size(12, 64, 100, 2048) == dc.mul_mat_workspace_size(12, 64, 2048) + 25600
+    assert dc.ffn_gate_up_workspace_size(12, 1, 1, 2048) == dc.mul_mat_workspace_size(12, 1, 2048) + 256
+    assert dc.ffn_gate_up_workspace_size(12, 1, 16, 100) == 0
+    assert dc.ffn_gate_up_workspace_size(12, 1, 0, 256) == 0
+
+    def ffn(wt=12, Wg=0x1000, Wu=0x5000, N=16, K=256, M=1, ws=None, wsb=0):
+        return L.dcq_ffn_gate_up(wt, Wg, Wu, N, K, dc.row_size(wt, K), 0x2000, M, K * 4, 0x3000, N * 4, ws, wsb,
+                                 None)
+    assert ffn(wt=2) == UNSUPPORTED
+    assert ffn(Wg=None) == INVALID
+    assert ffn(Wu=None) == INVALID
+    assert ffn(Wu=0x5004) == MISALIGNED
+    assert ffn(K=100) == BAD_SHAPE
+    assert ffn(ws=0x4000, wsb=16) == WORKSPACE
+    import torch
+    if not torch.cuda.is_available():
+        assert ffn() == NO_DEVICE
+
+
 def test_binding_raises_on_error():
     with pytest.raises(dc.DcqError):
         dc._lib._check("dcq_mul_mat", MISALIGNED)

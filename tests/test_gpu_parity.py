@@ -157,6 +157,28 @@ def test_decode_fused_quantization(O, dev, wt, M, N, K):
     O.assert_close(to_host(y2), y_ref, l1, RTOL, what="fused production kernel")
 
 
+# SwiGLU gate/up pair: the fused kernels (Q4_K, Q8_0 at M <= 8, shapes of both launch families)
+# and the general path (Q6_K; M > 8: the batched and prefill kernels plus the product kernel)
+GATE_UP = [(Q4_K, 1, 97, 2560), (Q4_K, 5, 40, 1024), (Q8_0, 1, 96, 1024), (Q8_0, 3, 41, 2048),
+           (Q6_K, 1, 50, 1024), (Q6_K, 3, 17, 768), (Q4_K, 33, 64, 512), (Q8_0, 40, 100, 512)]
+
+
+@pytest.mark.parametrize("wt,M,N,K", GATE_UP)
+def test_ffn_gate_up(O, dev, wt, M, N, K):
+    """dcq_ffn_gate_up = silu(Wg x) * (Wu x) against the oracle's pair of mul_mats and float64
+    silu, within the propagated mul_mat tolerance; with and without a caller workspace."""
+    import torch
+    wg, x = make_inputs(O, wt, M, N, K, seed=61 + M + K, outliers=1)
+    wu, _ = make_inputs(O, wt, M, N, K, seed=62 + M + K)
+    y_ref, parts = O.ffn_gate_up(wt, wg, wu, x)
+    wgd, wud, xd = to_dev(wg, dev), to_dev(wu, dev), to_dev(x, dev)
+    y = dc.ffn_gate_up(wt, wgd, wud, N, K, xd)
+    O.assert_close_gate_up(to_host(y), y_ref, parts, RTOL, what=f"gate/up type {wt} M{M} N{N} K{K}")
+    ws = torch.empty(dc.ffn_gate_up_workspace_size(wt, M, N, K), dtype=torch.uint8, device=dev)
+    y2 = dc.ffn_gate_up(wt, wgd, wud, N, K, xd, workspace=ws)
+    O.assert_close_gate_up(to_host(y2), y_ref, parts, RTOL, what="gate/up with workspace")
+
+
 @pytest.mark.parametrize("wt,M", [(Q4_K, 9), (Q6_K, 3), (Q8_0, 2)])
 def test_mul_mat_padded_strides_and_workspace(O, dev, wt, M):
     """Row strides larger than the data (ggml nb[1] > row size) and a caller workspace."""

@@ -289,3 +289,34 @@ def test_mul_mat_rows_and_dot_rows(O):
             assert l1[m, r] == np.float32(O.vec_dot_l1(Q6_K, k, wq[r], xq[m]))
     part = O.dot_rows(Q6_K, wq, xq[1], k, 5, 17)
     assert np.array_equal(part, y[1, 5:17])
+
+
+# ---------------------------------------------------------------- SwiGLU gate (ggml_silu)
+def test_silu_against_scipy_and_identities(O):
+    """silu(g) = g * sigmoid(g): against scipy's expit (an independent implementation); the
+    identity silu(g) - silu(-g) = g (catches a sign or a missing factor g); silu(0) = 0; the
+    asymptotes g (g >> 0) and 0 (g << 0) without overflow warnings escaping."""
+    from scipy.special import expit
+    g = np.concatenate([np.linspace(-30, 30, 601), [-1e4, -800.0, 0.0, 800.0, 1e4]])
+    s = O.silu(g)
+    np.testing.assert_allclose(s, g * expit(g), rtol=1e-13, atol=1e-300)
+    np.testing.assert_allclose(O.silu(g) - O.silu(-g), g, rtol=1e-12, atol=1e-12)
+    assert O.silu(0.0) == 0.0
+    assert O.silu(1e4) == 1e4 and O.silu(-1e4) == 0.0
+    # the derivative bound the gate/up tolerance relies on: |silu'| < 1.1
+    h = 1e-6
+    d = (O.silu(g[:601] + h) - O.silu(g[:601] - h)) / (2 * h)
+    assert np.max(np.abs(d)) < 1.1
+
+
+def test_ffn_gate_up_tolerance_catches_a_swapped_pair(O):
+    """The gate/up check must fail when gate and up are swapped (silu(u) * g != silu(g) * u)."""
+    k, n = 256, 8
+    wg = O.quantize_matrix(Q4_K, synth.normal(n * k, 51, 0.0, 0.02).reshape(n, k))
+    wu = O.quantize_matrix(Q4_K, synth.normal(n * k, 52, 0.0, 0.02).reshape(n, k))
+    x = synth.normal(2 * k, 53).reshape(2, k)
+    y, parts = O.ffn_gate_up(Q4_K, wg, wu, x)
+    O.assert_close_gate_up(y.astype(np.float32), y, parts, what="self")
+    swapped, _ = O.ffn_gate_up(Q4_K, wu, wg, x)
+    with pytest.raises(AssertionError):
+        O.assert_close_gate_up(swapped.astype(np.float32), y, parts, what="swapped")
