@@ -251,6 +251,36 @@ def bench_gate_up(cfg, args, dev):
             "separate_weight_GBps": 2 * wbytes / (s_ms * 1e-3) / 1e9}
 
 
+def bench_gguf_load(args, dev, mib=512):
+    """GGUF ingest: a file of Q4_K tensors (mib MiB, in the page cache after it is written) loaded
+    tensor by tensor into HBM with dcq_gguf_load_tensor; host-to-device GB/s (PCIe bound)."""
+    import tempfile
+    import torch
+    import densecore_amd as dc
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from gguf_writer import write_gguf
+    rb = dc.row_size(dc.TYPE_Q4_K, 4096)
+    rows = (mib << 20) // (8 * rb)
+    rng = np.random.default_rng(5)
+    payload = rng.integers(0, 256, size=rows * rb, dtype=np.uint8).tobytes()
+    tensors = [(f"blk.{i}.ffn_up.weight", dc.TYPE_Q4_K, [4096, rows], payload) for i in range(8)]
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "bench.gguf")
+        write_gguf(path, [], tensors)
+        dst = torch.empty(len(payload), dtype=torch.uint8, device=dev)
+        with dc.GGUF(path) as g:
+            g.load(0, dst=dst)  # warm
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(len(tensors)):
+                g.load(i, dst=dst)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+    total = len(payload) * len(tensors)
+    return {"bytes": total, "tensors": len(tensors), "seconds": dt, "GBps": total / dt / 1e9,
+            "note": "file in the page cache; read into two pinned 32 MB chunks, each copied while the next is read"}
+
+
 def profile_config(cfg, args, dev):
     """Eager steps of one config (counter collection needs plain dispatches)."""
     import torch
@@ -343,6 +373,10 @@ def main():
         g = extras["ffn_gate_up"]
         print(f"# gate/up pair at config {HEADLINE}: fused {g['fused_us']:.2f} us ({g['fused_kernels']} kernels), "
               f"two mul_mat calls {g['separate_us']:.2f} us", file=sys.stderr, flush=True)
+    if not args.no_extras:
+        extras["gguf_load"] = bench_gguf_load(args, dev)
+        print(f"# GGUF ingest: {extras['gguf_load']['GBps']:.1f} GB/s host-to-HBM over "
+              f"{extras['gguf_load']['bytes'] >> 20} MiB", file=sys.stderr, flush=True)
     head = next((r for r in results if r["config"] == HEADLINE), results[0])
     hcfg = dc.by_index(head["config"])
     line = {

@@ -15,6 +15,8 @@ SYMBOLS = [
     "dcq_supports_mul_mat", "dcq_quantize_rows", "dcq_mul_mat_workspace_size", "dcq_mul_mat", "dcq_mul_mat_ex",
     "dcq_block_sums_per_row", "dcq_dot_rows", "dcq_quantize_weights", "dcq_dequantize_rows",
     "dcq_quantize_src1", "dcq_mul_mat_q", "dcq_ffn_gate_up_workspace_size", "dcq_ffn_gate_up",
+    "dcq_gguf_open", "dcq_gguf_close", "dcq_gguf_tensor_count", "dcq_gguf_find_tensor", "dcq_gguf_tensor_info",
+    "dcq_gguf_get_int", "dcq_gguf_get_str", "dcq_gguf_load_tensor",
 ]
 
 PATH_AUTO, PATH_GEMV, PATH_MMQ = 0, 1, 2
@@ -61,6 +63,16 @@ def lib():
             "dcq_mul_mat_q": (i32, [i32, vp, i64, i64, sz, vp, sz, i64, vp, sz, i32, vp]),
             "dcq_ffn_gate_up_workspace_size": (sz, [i32, i64, i64, i64]),
             "dcq_ffn_gate_up": (i32, [i32, vp, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp, sz, vp]),
+            "dcq_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+            "dcq_gguf_close": (None, [vp]),
+            "dcq_gguf_tensor_count": (i64, [vp]),
+            "dcq_gguf_find_tensor": (i64, [vp, ctypes.c_char_p]),
+            "dcq_gguf_tensor_info": (i32, [vp, i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(i32),
+                                           ctypes.POINTER(i32), ctypes.POINTER(i64), ctypes.POINTER(ctypes.c_uint64),
+                                           ctypes.POINTER(ctypes.c_uint64)]),
+            "dcq_gguf_get_int": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(i64)]),
+            "dcq_gguf_get_str": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]),
+            "dcq_gguf_load_tensor": (i32, [vp, i64, vp, sz, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -177,6 +189,69 @@ def ffn_gate_up(wt, wg, wu, n, k, x, y=None, workspace=None, w_row_bytes=None, s
         wt, _ptr(wg), _ptr(wu), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace),
         ws_bytes, _stream(stream)))
     return y
+
+
+class GGUF:
+    """A GGUF weight file (dcq_gguf_*): tensor table and metadata parsed on the host, tensors
+    streamed into device memory in the block layout dcq_mul_mat takes."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        _check("dcq_gguf_open", lib().dcq_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().dcq_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self):
+        return lib().dcq_gguf_tensor_count(self._h)
+
+    def find(self, name):
+        return lib().dcq_gguf_find_tensor(self._h, name.encode())
+
+    def info(self, i):
+        name, typ, nd = ctypes.c_char_p(), ctypes.c_int(), ctypes.c_int()
+        ne = (ctypes.c_int64 * 4)()
+        off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+        _check("dcq_gguf_tensor_info", lib().dcq_gguf_tensor_info(
+            self._h, i, ctypes.byref(name), ctypes.byref(typ), ctypes.byref(nd), ne, ctypes.byref(off),
+            ctypes.byref(nb)))
+        return {"name": name.value.decode(), "type": typ.value, "ne": list(ne[:nd.value]),
+                "file_offset": off.value, "nbytes": nb.value}
+
+    def get_int(self, key):
+        v = ctypes.c_int64()
+        _check("dcq_gguf_get_int", lib().dcq_gguf_get_int(self._h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def get_str(self, key):
+        v = ctypes.c_char_p()
+        _check("dcq_gguf_get_str", lib().dcq_gguf_get_str(self._h, key.encode(), ctypes.byref(v)))
+        return v.value.decode()
+
+    def load(self, i, dst=None, device="cuda:0", stream=None):
+        """The tensor's bytes as a uint8 device tensor (rows packed: [ne[1]*..., row bytes])."""
+        import torch
+        meta = self.info(i)
+        if dst is None:
+            dst = torch.empty(meta["nbytes"], dtype=torch.uint8, device=device)
+        _check("dcq_gguf_load_tensor", lib().dcq_gguf_load_tensor(
+            self._h, i, _ptr(dst), dst.numel() * dst.element_size(), _stream(stream)))
+        return dst
 
 
 def dot_rows(wt, wq, xq_row, k, n0, n1, y=None, w_row_bytes=None, stream=None):

@@ -91,6 +91,9 @@ const char* dcq_status_string(int s) {
         case DCQ_ERR_WORKSPACE: return "workspace too small";
         case DCQ_ERR_HIP: return "HIP runtime error";
         case DCQ_ERR_NO_DEVICE: return "no gfx950 device";
+        case DCQ_ERR_FORMAT: return "malformed GGUF file";
+        case DCQ_ERR_IO: return "file could not be opened or read";
+        case DCQ_ERR_NOT_FOUND: return "key not found";
         default: return "unknown status";
     }
 }

@@ -57,6 +57,9 @@ extern "C" {
 #define DCQ_ERR_WORKSPACE (-5)       /* workspace smaller than dcq_mul_mat_workspace_size */
 #define DCQ_ERR_HIP (-6)             /* a HIP runtime call failed */
 #define DCQ_ERR_NO_DEVICE (-7)       /* no usable gfx950 device */
+#define DCQ_ERR_FORMAT (-8)          /* malformed GGUF file */
+#define DCQ_ERR_IO (-9)              /* file could not be opened or read */
+#define DCQ_ERR_NOT_FOUND (-10)      /* GGUF metadata key not present */
 
 /* kernel path selection for dcq_mul_mat_ex */
 #define DCQ_PATH_AUTO 0
@@ -160,6 +163,35 @@ int dcq_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* 
  * Y[r][k] = value of element k of row r; N rows of K elements, Y rows packed. */
 int dcq_dequantize_rows(int type, const void* Wq, int64_t N, int64_t K, size_t w_row_bytes, float* Y,
                         void* stream);
+
+/* ---- GGUF weight ingest ----
+ * The reference reads a model with ggml's gguf_init_from_file (no_alloc = false: every tensor's
+ * bytes into host ggml buffers, core/src/model_loader.cpp:96-130), reads metadata with
+ * gguf_find_key / gguf_get_val_* and maps tensors by name with ggml_get_tensor
+ * (core/src/model_loader.cpp:294-402). Here the file is parsed on the host (GGUF v2/v3; every
+ * count and length checked against the file size) and each tensor's bytes are streamed into
+ * device memory the caller owns, in the block layout dcq_mul_mat takes (the tensor's ne[0] is K,
+ * ne[1] is N, rows packed: w_row_bytes = dcq_row_size(type, K)). Real Q4_K_M files mix Q4_K,
+ * Q6_K and F32 tensors; every ggml type with a fixed block size is accepted by the parser.
+ *   dcq_gguf_open: DCQ_ERR_IO (open/read), DCQ_ERR_FORMAT (malformed), DCQ_ERR_UNSUPPORTED (a
+ *     tensor type without a fixed block size).
+ *   dcq_gguf_tensor_info: file_offset is the absolute byte offset of the tensor's data.
+ *   dcq_gguf_get_int: any integer or bool value; dcq_gguf_get_str: string values (the pointer
+ *     lives until dcq_gguf_close); DCQ_ERR_NOT_FOUND when the key is absent.
+ *   dcq_gguf_load_tensor: copies nbytes to dst (device memory of at least nbytes) on `stream`
+ *     through two pinned host chunks of up to 32 MB, which the handle's first load allocates and
+ *     dcq_gguf_close frees; returns when the copy is complete. Loads on one handle share those
+ *     chunks, so calls on one handle from several threads must not overlap. */
+typedef struct dcq_gguf dcq_gguf;
+int dcq_gguf_open(const char* path, dcq_gguf** out);
+void dcq_gguf_close(dcq_gguf* g);
+int64_t dcq_gguf_tensor_count(const dcq_gguf* g);
+int64_t dcq_gguf_find_tensor(const dcq_gguf* g, const char* name);
+int dcq_gguf_tensor_info(const dcq_gguf* g, int64_t i, const char** name, int* type, int* n_dims,
+                         int64_t ne[4], uint64_t* file_offset, uint64_t* nbytes);
+int dcq_gguf_get_int(const dcq_gguf* g, const char* key, int64_t* out);
+int dcq_gguf_get_str(const dcq_gguf* g, const char* key, const char** out);
+int dcq_gguf_load_tensor(const dcq_gguf* g, int64_t i, void* dst, size_t dst_bytes, void* stream);
 
 #ifdef __cplusplus
 }

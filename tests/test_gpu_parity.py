@@ -289,3 +289,35 @@ def test_quantize_src1_then_mul_mat_q(O, dev, wt, M, N, K, path):
         y = dc.mul_mat_q(wt, to_dev(wq, dev), N, K, ws, M, path=path)
         y_ref, l1 = O.mul_mat(wt, wq, x)
         O.assert_close(to_host(y), y_ref, l1, RTOL, what=f"split type {wt} M{M} path {path}")
+
+
+# ---------------------------------------------------------------- GGUF ingest to HBM
+def test_gguf_load_to_device_and_mul_mat(O, dev, tmp_path):
+    """Tensors of a Q4_K_M-style file (Q4_K, Q6_K, Q8_0, F32) streamed into device memory
+    byte-exact, including one larger than a 32 MB transfer chunk, and a loaded weight used by
+    dcq_mul_mat directly (rows packed in the file as dcq_mul_mat reads them)."""
+    import torch
+    from gguf_writer import T_STR, write_gguf
+    shapes = [("blk.0.ffn_up.weight", Q4_K, 96, 2560), ("blk.0.ffn_down.weight", Q6_K, 40, 1024),
+              ("blk.0.attn_q.weight", Q8_0, 33, 512)]
+    tensors, weights = [], {}
+    for i, (name, wt, n, k) in enumerate(shapes):
+        wq = O.quantize_matrix(wt, synth.normal(n * k, 700 + i, 0.0, 0.02).reshape(n, k))
+        weights[name] = (wt, n, k, wq)
+        tensors.append((name, wt, [k, n], wq.tobytes()))
+    big = np.frombuffer(synth.normal(9 * 2 ** 20, 777).tobytes(), dtype=np.uint8)  # 36 MiB of F32
+    tensors.append(("token_embd.weight", 0, [len(big) // 4], big.tobytes()))
+    path = tmp_path / "model.gguf"
+    write_gguf(path, [("general.architecture", T_STR, "qwen3")], tensors, alignment=32)
+    with dc.GGUF(path) as g:
+        assert g.get_str("general.architecture") == "qwen3"
+        for name, t, ne, data in tensors:
+            i = g.find(name)
+            d = g.load(i, device=dev)
+            assert np.array_equal(to_host(d), np.frombuffer(data, dtype=np.uint8)), name
+        for name, (wt, n, k, wq) in weights.items():
+            w_dev = g.load(g.find(name), device=dev).view(n, -1)
+            x = synth.normal(3 * k, 800).reshape(3, k)
+            y = dc.mul_mat(wt, w_dev, n, k, to_dev(x, dev))
+            y_ref, l1 = O.mul_mat(wt, wq, x)
+            O.assert_close(to_host(y), y_ref, l1, RTOL, what=f"mul_mat on loaded {name}")
