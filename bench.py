@@ -251,6 +251,51 @@ def bench_gate_up(cfg, args, dev):
             "separate_weight_GBps": 2 * wbytes / (s_ms * 1e-3) / 1e9}
 
 
+def bench_kv_attention(args, dev, ct, n_tokens=1, n_past=4095, n_layer=36, n_head=32, n_head_kv=8, hd=128):
+    """Attention of one layer over DenseCore's paged KV cache (dcq_kv_attention) at Qwen3-4B's
+    heads (32 query, 8 KV, head_dim 128). Each step attends the next of n_layer layers, so the
+    arenas (K and V of every layer, more than the 256 MB MALL) stream from HBM. Bytes per step:
+    the K and V history of that layer plus the query, current rows and output."""
+    import torch
+    import densecore_amd as dc
+    n_pos = n_past + n_tokens
+    n_blocks = (n_pos + 15) // 16
+    cache = dc.PagedKVCache(ct, n_blocks, n_layer, n_head_kv, hd, device=dev)
+    table = torch.arange(n_blocks, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    row = n_head_kv * hd
+    if n_past:
+        hist = torch.randn((n_past, row), generator=g, device=dev)
+        for layer in range(n_layer):
+            cache.write("k", layer, table, 0, hist)
+            cache.write("v", layer, table, 0, hist.roll(1, 1))
+    q = torch.randn((n_tokens, n_head * hd), generator=g, device=dev)
+    kc = torch.randn((n_tokens, row), generator=g, device=dev)
+    vc = torch.randn((n_tokens, row), generator=g, device=dev)
+    out = torch.empty_like(q)
+    need = dc.kv_attention_workspace_size(n_head, n_head_kv, hd, n_tokens, n_past)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        cache.attention(i % n_layer, table, q, kc, vc, n_past, 1.0 / hd ** 0.5, out=out, workspace=ws,
+                        stream=torch.cuda.current_stream().cuda_stream)
+
+    ms, kern = time_graph(step, args.steps, args.warmup, args.replays)
+    hist_bytes = 2 * n_past * cache.slot_bytes
+    io_bytes = 4 * (2 * q.numel() + kc.numel() + vc.numel())
+    pairs = n_tokens * n_past + n_tokens * (n_tokens + 1) // 2  # (query, visible key) pairs
+    flops = 4 * pairs * n_head * hd
+    del cache, ws
+    torch.cuda.empty_cache()
+    names = {dc.TYPE_F32: "F32", dc.TYPE_F16: "F16", dc.TYPE_Q8_0: "Q8_0"}
+    return {"shape": f"{names[ct]} cache, {n_head}/{n_head_kv} heads x {hd}, n_tokens={n_tokens}, "
+                     f"n_past={n_past}, {n_layer} layers rotated",
+            "us": ms * 1e3, "kernels": kern, "bytes": hist_bytes + io_bytes,
+            "GBps": (hist_bytes + io_bytes) / (ms * 1e-3) / 1e9, "TFLOPs": flops / (ms * 1e-3) / 1e12}
+
+
 def bench_gguf_load(args, dev, mib=512):
     """GGUF ingest: a file of Q4_K tensors (mib MiB, in the page cache after it is written) loaded
     tensor by tensor into HBM with dcq_gguf_load_tensor; host-to-device GB/s (PCIe bound)."""
@@ -374,6 +419,12 @@ def main():
         print(f"# gate/up pair at config {HEADLINE}: fused {g['fused_us']:.2f} us ({g['fused_kernels']} kernels), "
               f"two mul_mat calls {g['separate_us']:.2f} us", file=sys.stderr, flush=True)
     if not args.no_extras:
+        for name, kw in (("kv_attention_decode_q8_0", dict(ct=dc.TYPE_Q8_0)),
+                         ("kv_attention_decode_f16", dict(ct=dc.TYPE_F16)),
+                         ("kv_attention_prefill_q8_0", dict(ct=dc.TYPE_Q8_0, n_tokens=2048, n_past=0, n_layer=2))):
+            e = extras[name] = bench_kv_attention(args, dev, **kw)
+            print(f"# {name}: {e['us']:.2f} us ({e['kernels']} kernels), {e['GBps']:.0f} GB/s, "
+                  f"{e['TFLOPs']:.2f} TFLOP/s", file=sys.stderr, flush=True)
         extras["gguf_load"] = bench_gguf_load(args, dev)
         print(f"# GGUF ingest: {extras['gguf_load']['GBps']:.1f} GB/s host-to-HBM over "
               f"{extras['gguf_load']['bytes'] >> 20} MiB", file=sys.stderr, flush=True)

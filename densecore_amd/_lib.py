@@ -17,7 +17,10 @@ SYMBOLS = [
     "dcq_quantize_src1", "dcq_mul_mat_q", "dcq_ffn_gate_up_workspace_size", "dcq_ffn_gate_up",
     "dcq_gguf_open", "dcq_gguf_close", "dcq_gguf_tensor_count", "dcq_gguf_find_tensor", "dcq_gguf_tensor_info",
     "dcq_gguf_get_int", "dcq_gguf_get_str", "dcq_gguf_load_tensor",
+    "dcq_kv_slot_bytes", "dcq_kv_write", "dcq_kv_gather", "dcq_kv_attention_workspace_size", "dcq_kv_attention",
 ]
+
+KV_BLOCK_SIZE = 16
 
 PATH_AUTO, PATH_GEMV, PATH_MMQ = 0, 1, 2
 
@@ -73,6 +76,12 @@ def lib():
             "dcq_gguf_get_int": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(i64)]),
             "dcq_gguf_get_str": (i32, [vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]),
             "dcq_gguf_load_tensor": (i32, [vp, i64, vp, sz, vp]),
+            "dcq_kv_slot_bytes": (sz, [i32, i64]),
+            "dcq_kv_write": (i32, [i32, vp, i64, i32, i32, i64, vp, i64, i64, vp, sz, i64, vp]),
+            "dcq_kv_gather": (i32, [i32, vp, i64, i32, i32, i64, vp, i64, i64, vp, sz, i64, vp, sz, vp]),
+            "dcq_kv_attention_workspace_size": (sz, [i32, i32, i32, i64, i64]),
+            "dcq_kv_attention": (i32, [i32, vp, vp, i64, i32, i32, vp, i64, i32, i32, i32, vp, sz, vp, vp, sz,
+                                       i64, i64, ctypes.c_float, vp, sz, vp, sz, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -301,3 +310,72 @@ def mul_mat_q(wt, wq, n, k, workspace, m, y=None, path=PATH_AUTO, w_row_bytes=No
     _check("dcq_mul_mat_q", lib().dcq_mul_mat_q(wt, _ptr(wq), n, k, wrb, _ptr(workspace), workspace.numel(), m,
                                                 _ptr(y), y.stride(0) * 4, path, _stream(stream)))
     return y
+
+
+# ---------------------------------------------------------------- paged KV cache
+def kv_slot_bytes(cache_type, row_elems):
+    return int(lib().dcq_kv_slot_bytes(cache_type, row_elems))
+
+
+class PagedKVCache:
+    """K and V arenas of DenseCore's paged KV cache in device memory (layout of the reference's
+    PagedKVCache, core/src/kv_cache.cpp:341-409): n_blocks blocks of 16 token slots per layer,
+    each slot one token's row of n_head_kv * head_dim values in cache_type (F32, F16, Q8_0).
+    Block tables are int32 device tensors mapping position // 16 to an arena block."""
+
+    def __init__(self, cache_type, n_blocks, n_layer, n_head_kv, head_dim, device="cuda"):
+        import torch
+        self.cache_type, self.n_blocks, self.n_layer = cache_type, n_blocks, n_layer
+        self.n_head_kv, self.head_dim = n_head_kv, head_dim
+        self.row_elems = n_head_kv * head_dim
+        self.slot_bytes = kv_slot_bytes(cache_type, self.row_elems)
+        if self.slot_bytes == 0:
+            raise DcqError("dcq_kv_slot_bytes", -2)
+        nbytes = n_blocks * n_layer * KV_BLOCK_SIZE * self.slot_bytes
+        self.k = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        self.v = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+    def _arena(self, which):
+        return self.k if which == "k" else self.v
+
+    def write(self, which, layer, table, pos0, rows, stream=None):
+        """WriteKSlot / WriteVSlot for rows [N, row_elems] at positions pos0 .. pos0 + N - 1."""
+        _check("dcq_kv_write", lib().dcq_kv_write(
+            self.cache_type, _ptr(self._arena(which)), self.n_blocks, self.n_layer, layer, self.row_elems,
+            _ptr(table), table.numel(), pos0, _ptr(rows), rows.stride(0) * 4 if rows.dim() == 2 else 0,
+            rows.shape[0], _stream(stream)))
+
+    def gather(self, which, layer, table, n_past, cur, out=None, stream=None):
+        """[n_past + N, row_elems] fp32: history from the cache, then cur (cb_kv_update_and_gather)."""
+        import torch
+        n = cur.shape[0]
+        if out is None:
+            out = torch.empty((n_past + n, self.row_elems), dtype=torch.float32, device=cur.device)
+        _check("dcq_kv_gather", lib().dcq_kv_gather(
+            self.cache_type, _ptr(self._arena(which)), self.n_blocks, self.n_layer, layer, self.row_elems,
+            _ptr(table), table.numel() if table is not None else 0, n_past, _ptr(cur), cur.stride(0) * 4, n,
+            _ptr(out), out.stride(0) * 4, _stream(stream)))
+        return out
+
+    def attention(self, layer, table, q, k_cur, v_cur, n_past, scale, out=None, workspace=None, stream=None):
+        """q [N, n_head * head_dim] fp32 -> out [N, n_head * head_dim]: causal attention of the N
+        batch tokens (positions n_past ..) over the cached history and their own k_cur / v_cur rows."""
+        import torch
+        n = q.shape[0]
+        n_head = q.shape[1] // self.head_dim
+        if out is None:
+            out = torch.empty((n, n_head * self.head_dim), dtype=torch.float32, device=q.device)
+        need = kv_attention_workspace_size(n_head, self.n_head_kv, self.head_dim, n, n_past)
+        if workspace is None and need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        _check("dcq_kv_attention", lib().dcq_kv_attention(
+            self.cache_type, _ptr(self.k), _ptr(self.v), self.n_blocks, self.n_layer, layer, _ptr(table),
+            table.numel() if table is not None else 0, n_head, self.n_head_kv, self.head_dim, _ptr(q),
+            q.stride(0) * 4, _ptr(k_cur), _ptr(v_cur), k_cur.stride(0) * 4, n, n_past, scale, _ptr(out),
+            out.stride(0) * 4, _ptr(workspace), ws_bytes, _stream(stream)))
+        return out
+
+
+def kv_attention_workspace_size(n_head, n_head_kv, head_dim, n_tokens, n_past):
+    return int(lib().dcq_kv_attention_workspace_size(n_head, n_head_kv, head_dim, n_tokens, n_past))

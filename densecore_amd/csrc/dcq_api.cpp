@@ -75,6 +75,18 @@ int validate_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_ro
     return DCQ_OK;
 }
 
+bool is_cache_type(int t) { return t == kTypeQ8_0 || t == kTypeF16 || t == kTypeF32; }
+
+// Shared checks of the arena arguments (no device calls).
+int validate_arena(int ct, const void* arena, int64_t n_blocks, int n_layer, int layer, int64_t row_elems) {
+    if (!is_cache_type(ct)) return DCQ_ERR_UNSUPPORTED;
+    if (!arena) return DCQ_ERR_INVALID_ARG;
+    if (n_blocks <= 0 || n_blocks > INT32_MAX || n_layer <= 0 || layer < 0 || layer >= n_layer) return DCQ_ERR_BAD_SHAPE;
+    if (row_elems <= 0 || row_elems % 32 || row_elems > ((int64_t)1 << 24)) return DCQ_ERR_BAD_SHAPE;
+    if (!aligned(arena, 16)) return DCQ_ERR_MISALIGNED;
+    return DCQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -360,6 +372,93 @@ int dcq_dequantize_rows(int type, const void* Wq, int64_t N, int64_t K, size_t w
     int rc = check_device();
     if (rc) return rc;
     return hip_status(launch_dequantize(type, Wq, N, K, (int64_t)w_row_bytes, Y, (hipStream_t)stream));
+}
+
+size_t dcq_kv_slot_bytes(int cache_type, int64_t row_elems) {
+    if (!is_cache_type(cache_type) || row_elems <= 0 || row_elems % 32) return 0;
+    return dcq_row_size(cache_type, row_elems);
+}
+
+int dcq_kv_write(int cache_type, void* arena, int64_t n_blocks, int n_layer, int layer, int64_t row_elems,
+                 const int32_t* block_table, int64_t n_table, int64_t pos0, const float* src,
+                 size_t src_stride_bytes, int64_t n_tokens, void* stream) {
+    int rc = validate_arena(cache_type, arena, n_blocks, n_layer, layer, row_elems);
+    if (rc) return rc;
+    if (n_tokens < 0 || pos0 < 0 || n_tokens > INT32_MAX || pos0 + n_tokens > INT32_MAX) return DCQ_ERR_BAD_SHAPE;
+    if (n_tokens == 0) return DCQ_OK;
+    if (!block_table || !src) return DCQ_ERR_INVALID_ARG;
+    if ((pos0 + n_tokens - 1) / DCQ_KV_BLOCK_SIZE >= n_table) return DCQ_ERR_INVALID_ARG;
+    if (src_stride_bytes < (size_t)row_elems * 4) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(src, 16) || src_stride_bytes % 16 || !aligned(block_table, 4)) return DCQ_ERR_MISALIGNED;
+    if ((rc = check_device())) return rc;
+    return hip_status(launch_kv_write(cache_type, arena, (int)n_blocks, n_layer, layer, row_elems,
+                                      (int64_t)dcq_kv_slot_bytes(cache_type, row_elems), block_table, (int)pos0, src,
+                                      (int64_t)(src_stride_bytes / 4), (int)n_tokens, (hipStream_t)stream));
+}
+
+int dcq_kv_gather(int cache_type, const void* arena, int64_t n_blocks, int n_layer, int layer, int64_t row_elems,
+                  const int32_t* block_table, int64_t n_table, int64_t n_past, const float* cur,
+                  size_t cur_stride_bytes, int64_t n_tokens, float* dst, size_t dst_stride_bytes, void* stream) {
+    int rc = validate_arena(cache_type, arena, n_blocks, n_layer, layer, row_elems);
+    if (rc) return rc;
+    if (n_tokens < 0 || n_past < 0 || n_table < 0 || n_past + n_tokens > INT32_MAX) return DCQ_ERR_BAD_SHAPE;
+    if (n_past + n_tokens == 0) return DCQ_OK;
+    if (!dst || (n_tokens > 0 && !cur) || (n_past > 0 && n_table > 0 && !block_table)) return DCQ_ERR_INVALID_ARG;
+    if (dst_stride_bytes < (size_t)row_elems * 4 || (n_tokens > 0 && cur_stride_bytes < (size_t)row_elems * 4))
+        return DCQ_ERR_INVALID_ARG;
+    if (!aligned(dst, 16) || dst_stride_bytes % 16 || !aligned(block_table, 4)) return DCQ_ERR_MISALIGNED;
+    if (n_tokens > 0 && (!aligned(cur, 16) || cur_stride_bytes % 16)) return DCQ_ERR_MISALIGNED;
+    if ((rc = check_device())) return rc;
+    const int nt = n_table > INT32_MAX ? INT32_MAX : (int)n_table;
+    return hip_status(launch_kv_gather(cache_type, arena, (int)n_blocks, n_layer, layer, row_elems,
+                                       (int64_t)dcq_kv_slot_bytes(cache_type, row_elems), block_table, nt,
+                                       (int)n_past, cur, (int64_t)(cur_stride_bytes / 4), (int)n_tokens, dst,
+                                       (int64_t)(dst_stride_bytes / 4), (hipStream_t)stream));
+}
+
+static int validate_attention_shape(int n_head, int n_head_kv, int head_dim, int64_t n_tokens, int64_t n_past) {
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return DCQ_ERR_UNSUPPORTED;
+    if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv || n_head > 4096) return DCQ_ERR_BAD_SHAPE;
+    if (n_tokens <= 0 || n_tokens > 65535 || n_past < 0 || n_past > ((int64_t)1 << 24)) return DCQ_ERR_BAD_SHAPE;
+    return DCQ_OK;
+}
+
+size_t dcq_kv_attention_workspace_size(int n_head, int n_head_kv, int head_dim, int64_t n_tokens, int64_t n_past) {
+    if (validate_attention_shape(n_head, n_head_kv, head_dim, n_tokens, n_past)) return 0;
+    return attn_workspace_bytes(head_dim, n_head, n_head_kv, (int)n_tokens, (int)n_past);
+}
+
+int dcq_kv_attention(int cache_type, const void* k_arena, const void* v_arena, int64_t n_blocks, int n_layer,
+                     int layer, const int32_t* block_table, int64_t n_table, int n_head, int n_head_kv,
+                     int head_dim, const float* q, size_t q_stride_bytes, const float* k_cur, const float* v_cur,
+                     size_t kv_stride_bytes, int64_t n_tokens, int64_t n_past, float scale, float* out,
+                     size_t out_stride_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+    const int64_t row_elems = (int64_t)n_head_kv * head_dim;
+    int rc = validate_attention_shape(n_head, n_head_kv, head_dim, n_tokens, n_past);
+    if (rc) return rc;
+    if ((rc = validate_arena(cache_type, k_arena, n_blocks, n_layer, layer, row_elems))) return rc;
+    if ((rc = validate_arena(cache_type, v_arena, n_blocks, n_layer, layer, row_elems))) return rc;
+    if (!q || !k_cur || !v_cur || !out || (n_past > 0 && n_table > 0 && !block_table) || n_table < 0)
+        return DCQ_ERR_INVALID_ARG;
+    if (!(scale == scale) || scale == INFINITY || scale == -INFINITY) return DCQ_ERR_INVALID_ARG;
+    const size_t q_row = (size_t)n_head * head_dim * 4, kv_row = (size_t)row_elems * 4;
+    if (q_stride_bytes < q_row || kv_stride_bytes < kv_row || out_stride_bytes < q_row) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(q, 16) || !aligned(k_cur, 16) || !aligned(v_cur, 16) || !aligned(out, 4) ||
+        !aligned(block_table, 4))
+        return DCQ_ERR_MISALIGNED;
+    if (q_stride_bytes % 16 || kv_stride_bytes % 16 || out_stride_bytes % 4) return DCQ_ERR_MISALIGNED;
+    const size_t need = attn_workspace_bytes(head_dim, n_head, n_head_kv, (int)n_tokens, (int)n_past);
+    if (need) {
+        if (!workspace || workspace_bytes < need) return DCQ_ERR_WORKSPACE;
+        if (!aligned(workspace, 256)) return DCQ_ERR_MISALIGNED;
+    }
+    if ((rc = check_device())) return rc;
+    const int nt = n_table > INT32_MAX ? INT32_MAX : (int)n_table;
+    return hip_status(launch_kv_attention(
+        cache_type, k_arena, v_arena, (int)n_blocks, n_layer, layer, (int64_t)dcq_kv_slot_bytes(cache_type, row_elems),
+        block_table, nt, n_head, n_head_kv, head_dim, q, (int64_t)(q_stride_bytes / 4), k_cur, v_cur,
+        (int64_t)(kv_stride_bytes / 4), (int)n_tokens, (int)n_past, scale, out, (int64_t)(out_stride_bytes / 4),
+        workspace, workspace_bytes, (hipStream_t)stream));
 }
 
 }  // extern "C"

@@ -80,6 +80,23 @@ hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                       int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
 
+// Paged KV cache (arena layout of the reference's PagedKVCache; row_elems % 32 == 0, pointers
+// and strides 16-byte aligned, checked by the caller).
+hipError_t launch_kv_write(int ct, void* arena, int n_blocks, int n_layer, int layer, int64_t row_elems, int64_t sb,
+                           const int32_t* table, int pos0, const float* src, int64_t src_stride, int n_tokens,
+                           hipStream_t st);
+hipError_t launch_kv_gather(int ct, const void* arena, int n_blocks, int n_layer, int layer, int64_t row_elems,
+                            int64_t sb, const int32_t* table, int n_table, int n_past, const float* cur,
+                            int64_t cur_stride, int n_tokens, float* dst, int64_t dst_stride, hipStream_t st);
+// Attention over the arena (head_dim 64/128/256); workspace from attn_workspace_bytes (0 when
+// the keys are not split). hipErrorNotSupported for another head_dim or cache type.
+size_t attn_workspace_bytes(int hd, int n_head, int n_head_kv, int n_tokens, int n_past);
+hipError_t launch_kv_attention(int ct, const void* k_arena, const void* v_arena, int n_blocks, int n_layer, int layer,
+                               int64_t sb, const int32_t* table, int n_table, int n_head, int n_head_kv, int hd,
+                               const float* q, int64_t q_stride, const float* k_cur, const float* v_cur,
+                               int64_t kv_stride, int n_tokens, int n_past, float scale, float* out,
+                               int64_t out_stride, void* ws, size_t ws_bytes, hipStream_t st);
+
 hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, hipStream_t st);
 hipError_t launch_dequantize(int type, const void* Wq, int64_t N, int64_t K, int64_t w_row_bytes, float* Y,
                              hipStream_t st);

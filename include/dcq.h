@@ -193,6 +193,55 @@ int dcq_gguf_get_int(const dcq_gguf* g, const char* key, int64_t* out);
 int dcq_gguf_get_str(const dcq_gguf* g, const char* key, const char** out);
 int dcq_gguf_load_tensor(const dcq_gguf* g, int64_t i, void* dst, size_t dst_bytes, void* stream);
 
+/* ---- Paged KV cache: F32 / F16 / Q8_0 slots, and the attention that reads them ----
+ * Arena layout, as the reference's PagedKVCache (core/src/kv_cache.cpp:341-409,
+ * core/include/kv_cache.h:17): 16 token slots per block; slot (block, layer, s) at byte
+ * ((block * n_layer + layer) * 16 + s) * dcq_kv_slot_bytes(type, row_elems), where a slot holds
+ * one token's row of row_elems = n_head_kv * head_dim values, KV head h at h * head_dim.
+ * n_blocks is the number of blocks the arena holds (its size is n_blocks * n_layer * 16 *
+ * slot_bytes). block_table maps a sequence's logical block (position / 16) to an arena block;
+ * it lives in device memory. Types: DCQ_TYPE_F32, DCQ_TYPE_F16, DCQ_TYPE_Q8_0; row_elems a
+ * multiple of 32; arena, src, cur, dst, q, k_cur, v_cur 16-byte aligned with strides a multiple
+ * of 16 bytes (out: 4). */
+#define DCQ_KV_BLOCK_SIZE 16
+
+/* bytes of one slot: PagedKVCache::GetBytesPerSlot (core/src/kv_cache.cpp:341-347); 0 when the
+ * type is not a cache type or row_elems is not a multiple of 32. */
+size_t dcq_kv_slot_bytes(int cache_type, int64_t row_elems);
+
+/* Write n_tokens rows (positions pos0 .. pos0 + n_tokens - 1 of one sequence) into their slots:
+ * PagedKVCache::WriteKSlot / WriteVSlot (core/src/kv_cache.cpp:565-598) as called per token by
+ * cb_kv_update_and_gather (core/src/inference.cpp:711-745). Q8_0 is ggml_quantize_chunk's
+ * quantize_row_q8_0_ref, F16 is round-to-nearest-even; bit-exact. A table entry outside
+ * [0, n_blocks) is skipped, as the reference skips a null slot. The table must cover every
+ * position written (DCQ_ERR_INVALID_ARG otherwise; the reference skips those tokens). */
+int dcq_kv_write(int cache_type, void* arena, int64_t n_blocks, int n_layer, int layer, int64_t row_elems,
+                 const int32_t* block_table, int64_t n_table, int64_t pos0, const float* src,
+                 size_t src_stride_bytes, int64_t n_tokens, void* stream);
+
+/* dst[n_past + n_tokens][row_elems] fp32: positions 0 .. n_past - 1 read from the arena, then the
+ * n_tokens rows of cur as given, as cb_kv_update_and_gather leaves K_all / V_all
+ * (core/src/inference.cpp:748-784; ReadKSlot at core/src/kv_cache.cpp:600-629). Positions whose
+ * block is missing from the table, or outside [0, n_blocks), read as zeros. */
+int dcq_kv_gather(int cache_type, const void* arena, int64_t n_blocks, int n_layer, int layer, int64_t row_elems,
+                  const int32_t* block_table, int64_t n_table, int64_t n_past, const float* cur,
+                  size_t cur_stride_bytes, int64_t n_tokens, float* dst, size_t dst_stride_bytes, void* stream);
+
+/* The attention of one layer over the cache: the reference's standard path
+ * (core/src/inference.cpp:1577-1746) on the K_all / V_all of dcq_kv_gather, fused: query
+ * token i (position n_past + i) of q[n_tokens][n_head][head_dim] attends keys 0 .. n_past + i,
+ * history from the arenas and the batch's own rows from k_cur / v_cur[n_tokens][n_head_kv]
+ * [head_dim] in fp32; query head h uses KV head h / (n_head / n_head_kv);
+ * out[i][h][:] = softmax_t(scale * q . k_t) . v_t, written as [n_tokens][n_head][head_dim].
+ * head_dim 64, 128 or 256; n_head a multiple of n_head_kv; n_tokens <= 65535. The workspace
+ * holds per-split partial results (dcq_kv_attention_workspace_size; 0 needs none). */
+size_t dcq_kv_attention_workspace_size(int n_head, int n_head_kv, int head_dim, int64_t n_tokens, int64_t n_past);
+int dcq_kv_attention(int cache_type, const void* k_arena, const void* v_arena, int64_t n_blocks, int n_layer,
+                     int layer, const int32_t* block_table, int64_t n_table, int n_head, int n_head_kv,
+                     int head_dim, const float* q, size_t q_stride_bytes, const float* k_cur, const float* v_cur,
+                     size_t kv_stride_bytes, int64_t n_tokens, int64_t n_past, float scale, float* out,
+                     size_t out_stride_bytes, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

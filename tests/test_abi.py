@@ -132,3 +132,49 @@ def test_ffn_gate_up_workspace_and_validation():
 def test_binding_raises_on_error():
     with pytest.raises(dc.DcqError):
         dc._lib._check("dcq_mul_mat", MISALIGNED)
+
+
+def test_kv_slot_bytes_and_workspace():
+    assert dc.kv_slot_bytes(8, 1024) == 1088 and dc.kv_slot_bytes(1, 1024) == 2048
+    assert dc.kv_slot_bytes(0, 1024) == 4096
+    assert dc.kv_slot_bytes(12, 1024) == 0 and dc.kv_slot_bytes(8, 1000) == 0
+    # decode at a long context splits the keys (a workspace); a large prefill does not
+    assert dc.kv_attention_workspace_size(32, 8, 128, 1, 4095) > 0
+    assert dc.kv_attention_workspace_size(32, 8, 128, 2048, 0) == 0
+    assert dc.kv_attention_workspace_size(32, 8, 96, 1, 100) == 0  # unsupported head_dim
+
+
+def test_kv_validation_before_any_device_call():
+    L = dc.lib()
+
+    def write(ct=8, arena=0x1000, n_blocks=4, n_layer=2, layer=1, row=256, table=0x2000, n_table=4, pos0=0,
+              src=0x3000, stride=1024, n=3):
+        return L.dcq_kv_write(ct, arena, n_blocks, n_layer, layer, row, table, n_table, pos0, src, stride, n, None)
+    assert write(ct=12) == UNSUPPORTED
+    assert write(arena=None) == INVALID
+    assert write(layer=2) == BAD_SHAPE
+    assert write(row=100) == BAD_SHAPE
+    assert write(pos0=62, n=3) == INVALID   # position 64 needs a 5th table entry
+    assert write(stride=512) == INVALID
+    assert write(src=0x3004) == MISALIGNED
+    assert write(n=0) == OK                 # nothing to write
+
+    def attn(ct=8, hd=128, n_head=32, n_kv=8, n=1, n_past=10, q=0x1000, qs=None, ws=0x100000, wsb=1 << 30,
+             scale=0.1):
+        qs = qs if qs is not None else n_head * hd * 4
+        return L.dcq_kv_attention(ct, 0x10000, 0x20000, 4, 1, 0, 0x2000, 4, n_head, n_kv, hd, q, qs, 0x3000,
+                                  0x4000, n_kv * hd * 4, n, n_past, scale, 0x5000, n_head * hd * 4, ws, wsb, None)
+    assert attn(hd=96) == UNSUPPORTED
+    assert attn(ct=14) == UNSUPPORTED
+    assert attn(n_kv=5) == BAD_SHAPE
+    assert attn(n=0) == BAD_SHAPE
+    assert attn(q=None) == INVALID
+    assert attn(qs=100) == INVALID
+    assert attn(q=0x1008) == MISALIGNED
+    assert attn(scale=float("nan")) == INVALID
+    assert attn(n_past=4095, ws=None, wsb=0) == WORKSPACE   # the split decode needs its workspace
+    assert attn(ws=0x100010) == MISALIGNED
+    import torch
+    if not torch.cuda.is_available():
+        assert attn() == NO_DEVICE
+        assert write() == NO_DEVICE
