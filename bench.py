@@ -293,7 +293,12 @@ def bench_kv_attention(args, dev, ct, n_tokens=1, n_past=4095, n_layer=36, n_hea
     return {"shape": f"{names[ct]} cache, {n_head}/{n_head_kv} heads x {hd}, n_tokens={n_tokens}, "
                      f"n_past={n_past}, {n_layer} layers rotated",
             "us": ms * 1e3, "kernels": kern, "bytes": hist_bytes + io_bytes,
-            "GBps": (hist_bytes + io_bytes) / (ms * 1e-3) / 1e9, "TFLOPs": flops / (ms * 1e-3) / 1e12}
+            "GBps": (hist_bytes + io_bytes) / (ms * 1e-3) / 1e9, "TFLOPs": flops / (ms * 1e-3) / 1e12,
+            # decode streams the history (HBM-bound); a long prefill is fp32 arithmetic on the VALU
+            "roofline": ({"bound": "hbm", "peak": 8000.0, "unit": "GB/s",
+                          "frac": (hist_bytes + io_bytes) / (ms * 1e-3) / 1e9 / 8000.0} if n_tokens == 1 else
+                         {"bound": "fp32", "peak": 157.3, "unit": "TFLOP/s",
+                          "frac": flops / (ms * 1e-3) / 1e12 / 157.3})}
 
 
 def bench_gguf_load(args, dev, mib=512):
