@@ -365,13 +365,18 @@ constexpr int waves_of() {
     return 4;
 }
 
-template <class Fmt, int I, int MT, bool FUSE, bool DUMP, bool GLU>
+template <class Fmt, int I, int MT, bool FUSE, bool DUMP, bool GLU, int NW = waves_of<FUSE, MT>()>
 DecodeFn fn_of() {
-    return decode_kq_kernel<Fmt, kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP, GLU, waves_of<FUSE, MT>()>;
+    return decode_kq_kernel<Fmt, kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP, GLU, NW>;
 }
 
+// the fused single-row decode (the common decode step) also comes in 5-wave workgroups: rows
+// per workgroup then spread the matrix over the CUs more evenly for some N (see choose_waves)
 template <class Fmt, int I, bool FUSE, bool DUMP, bool GLU>
-DecodeFn pick_mt(int mt) {
+DecodeFn pick_mt(int mt, int nw) {
+    if constexpr (FUSE && !DUMP) {
+        if (mt == 1 && nw == 5) return fn_of<Fmt, I, 1, FUSE, DUMP, GLU, 5>();
+    }
     switch (mt) {
         case 1: return fn_of<Fmt, I, 1, FUSE, DUMP, GLU>();
         case 2: return fn_of<Fmt, I, 2, FUSE, DUMP, GLU>();
@@ -381,29 +386,29 @@ DecodeFn pick_mt(int mt) {
 }
 
 template <class Fmt, bool FUSE, bool DUMP, bool GLU = false>
-DecodeFn pick_shape(int idx, int mt) {
+DecodeFn pick_shape(int idx, int mt, int nw) {
     switch (idx) {
-        case 0: return pick_mt<Fmt, 0, FUSE, DUMP, GLU>(mt);
-        case 1: return pick_mt<Fmt, 1, FUSE, DUMP, GLU>(mt);
-        case 2: return pick_mt<Fmt, 2, FUSE, DUMP, GLU>(mt);
-        case 3: return pick_mt<Fmt, 3, FUSE, DUMP, GLU>(mt);
-        case 4: return pick_mt<Fmt, 4, FUSE, DUMP, GLU>(mt);
-        case 5: return pick_mt<Fmt, 5, FUSE, DUMP, GLU>(mt);
-        case 6: return pick_mt<Fmt, 6, FUSE, DUMP, GLU>(mt);
-        case 7: return pick_mt<Fmt, 7, FUSE, DUMP, GLU>(mt);
-        case 8: return pick_mt<Fmt, 8, FUSE, DUMP, GLU>(mt);
-        default: return pick_mt<Fmt, 9, FUSE, DUMP, GLU>(mt);
+        case 0: return pick_mt<Fmt, 0, FUSE, DUMP, GLU>(mt, nw);
+        case 1: return pick_mt<Fmt, 1, FUSE, DUMP, GLU>(mt, nw);
+        case 2: return pick_mt<Fmt, 2, FUSE, DUMP, GLU>(mt, nw);
+        case 3: return pick_mt<Fmt, 3, FUSE, DUMP, GLU>(mt, nw);
+        case 4: return pick_mt<Fmt, 4, FUSE, DUMP, GLU>(mt, nw);
+        case 5: return pick_mt<Fmt, 5, FUSE, DUMP, GLU>(mt, nw);
+        case 6: return pick_mt<Fmt, 6, FUSE, DUMP, GLU>(mt, nw);
+        case 7: return pick_mt<Fmt, 7, FUSE, DUMP, GLU>(mt, nw);
+        case 8: return pick_mt<Fmt, 8, FUSE, DUMP, GLU>(mt, nw);
+        default: return pick_mt<Fmt, 9, FUSE, DUMP, GLU>(mt, nw);
     }
 }
 
 // the gate/up pair (GLU) is built for Q4_K with the fused activation only
 template <class Fmt>
-DecodeFn pick_fn(bool fuse, bool dump, bool glu, int idx, int mt) {
+DecodeFn pick_fn(bool fuse, bool dump, bool glu, int idx, int mt, int nw) {
     if constexpr (std::is_same<Fmt, FmtQ4K>::value) {
-        if (glu) return pick_shape<Fmt, true, false, true>(idx, mt);
+        if (glu) return pick_shape<Fmt, true, false, true>(idx, mt, nw);
     }
-    return fuse ? (dump ? pick_shape<Fmt, true, true>(idx, mt) : pick_shape<Fmt, true, false>(idx, mt))
-                : (dump ? pick_shape<Fmt, false, true>(idx, mt) : pick_shape<Fmt, false, false>(idx, mt));
+    return fuse ? (dump ? pick_shape<Fmt, true, true>(idx, mt, nw) : pick_shape<Fmt, true, false>(idx, mt, nw))
+                : (dump ? pick_shape<Fmt, false, true>(idx, mt, nw) : pick_shape<Fmt, false, false>(idx, mt, nw));
 }
 static_assert(kNumShapes == 10, "pick_shape covers every shape");
 
@@ -431,6 +436,48 @@ int choose_shape(int nsb) {
     return best;
 }
 
+// Launch shape and waves per workgroup for the fused single-row decode. A decode GEMV streams
+// each row once, and its time follows the most rows any one CU has to read (measured on
+// MI355X at K = 2560: 32 rows per CU 4.7 us, 40 rows 5.7 us, 48 rows 6.0 us, one workgroup per
+// CU beating two at the same row count). Among the shapes that leave at most a quarter of their
+// superblock slots idle, and 4- or 5-wave workgroups, take the fewest rows on the busiest CU,
+// then the fewest workgroups per CU. Other variants keep choose_shape with 4 waves.
+struct Launch {
+    int idx, nw;
+};
+int cu_count() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        hipDeviceProp_t p;
+        cus[dev] = hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+    }
+    return cus[dev];
+}
+Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
+    const int forced = env_int("DCQ_Q4K_SHAPE", -1);
+    if (forced >= 0) return {choose_shape(nsb), 4};
+    const int cus = cu_count();
+    Launch best{choose_shape(nsb), 4};
+    int64_t best_rows = INT64_MAX, best_per_cu = INT64_MAX;
+    for (int i = 0; i < kNumShapes; ++i) {
+        const int cap = kShapes[i].P * kShapes[i].NS;
+        if (cap < nsb || 4 * (cap - nsb) > cap) continue;
+        for (int nw = 4; nw <= (nw5_ok ? 5 : 4); ++nw) {
+            const int64_t rpw = nw * (64 / (4 * kShapes[i].P));
+            const int64_t wgs = (rows + rpw - 1) / rpw, per_cu = (wgs + cus - 1) / cus;
+            const int64_t busiest = per_cu * rpw;
+            if (busiest < best_rows || (busiest == best_rows && per_cu < best_per_cu)) {
+                best = {i, nw};
+                best_rows = busiest;
+                best_per_cu = per_cu;
+            }
+        }
+    }
+    return best;
+}
+
 // W2 != nullptr: the gate/up pair (Q4_K, fused activation, no block sums): Y = silu(W x) * (W2 x)
 hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_t w_row_bytes, int64_t n0, int64_t n1,
                      int64_t K, const float* X, int64_t x_stride, const PlanarBuffers* act, int64_t M, float* Y,
@@ -440,7 +487,10 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
     const bool glu = W2 != nullptr;
     if (glu && (wtype != kTypeQ4_K || !fuse || block_sums)) return hipErrorNotSupported;
     if (wtype == kTypeQ4_K ? (w_row_bytes % 16 != 0) : (w_row_bytes % 2 != 0)) return hipErrorNotSupported;
-    const int idx = choose_shape(nsb);
+    // the 5-wave variants exist for the fused, sum-free single-row decode only
+    const bool single = fuse && !block_sums && M == 1;
+    const Launch ln = single ? choose_launch(nsb, n1 - n0, true) : Launch{choose_shape(nsb), 4};
+    const int idx = ln.idx;
     if (idx < 0) return hipErrorNotSupported;
     const int P = kShapes[idx].P;
     const int64_t per_row_sums = (wtype == kTypeQ4_K ? 2 : 1) * (K / 256);
@@ -449,18 +499,17 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         if (act_lds_bytes_q8k(mt, K) > 64 * 1024) return hipErrorNotSupported;
-        const int nw = 4;
-        if (stage_chunks(P, kShapes[idx].NS, mt, fuse, nw) > 16) return hipErrorNotSupported;
+        if (stage_chunks(P, kShapes[idx].NS, mt, fuse, ln.nw) > 16) return hipErrorNotSupported;
     }
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         const size_t lds = act_lds_bytes_q8k(mt, K);
-        const int nw = 4;
+        const int nw = ln.nw;
         const int rows_per_block = nw * (64 / (4 * P));
         const unsigned grid = (unsigned)((n1 - n0 + rows_per_block - 1) / rows_per_block);
-        DecodeFn fn = wtype == kTypeQ4_K ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, glu, idx, mt)
-                                         : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, false, idx, mt);
+        DecodeFn fn = wtype == kTypeQ4_K ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, glu, idx, mt, nw)
+                                         : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, false, idx, mt, nw);
         // rows beyond mc in an MT tile stage the last real activation row and are never stored
         hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), lds, st, (const uint8_t*)W, (const uint8_t*)W2, w_row_bytes,
                            n0, n1, nsb,

@@ -93,6 +93,8 @@ CASES = [
     (Q8_0, 1, 96, 1024), (Q8_0, 3, 70, 2048), (Q8_0, 1, 33, 96), (Q8_0, 2, 40, 160), (Q8_0, 40, 100, 512),
     (Q8_0, 130, 257, 256),
     (Q4_K, 1, 97, 2560), (Q4_K, 2, 64, 256), (Q4_K, 5, 40, 512), (Q4_K, 64, 96, 2048), (Q4_K, 70, 33, 768),
+    # single-row decode at full width: 5-wave workgroups (rows spread evenly over the CUs)
+    (Q4_K, 1, 9728, 2560), (Q4_K, 1, 2570, 4096), (Q4_K, 1, 2561, 9728),
     (Q6_K, 1, 50, 9728), (Q6_K, 1, 3, 256), (Q6_K, 8, 64, 512), (Q6_K, 33, 65, 1024), (Q6_K, 3, 17, 768),
     (Q6_K, 2, 9, 16384), (Q6_K, 1, 5, 16896),
 ]
@@ -159,7 +161,7 @@ def test_decode_fused_quantization(O, dev, wt, M, N, K):
 
 # SwiGLU gate/up pair: the fused kernels (Q4_K, Q8_0 at M <= 8, shapes of both launch families)
 # and the general path (Q6_K; M > 8: the batched and prefill kernels plus the product kernel)
-GATE_UP = [(Q4_K, 1, 97, 2560), (Q4_K, 5, 40, 1024), (Q8_0, 1, 96, 1024), (Q8_0, 3, 41, 2048),
+GATE_UP = [(Q4_K, 1, 97, 2560), (Q4_K, 1, 9728, 2560), (Q4_K, 5, 40, 1024), (Q8_0, 1, 96, 1024), (Q8_0, 3, 41, 2048),
            (Q6_K, 1, 50, 1024), (Q6_K, 3, 17, 768), (Q4_K, 33, 64, 512), (Q8_0, 40, 100, 512)]
 
 
