@@ -536,7 +536,9 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
     if (env_int("DCQ_NO_FUSE", 0)) return hipErrorNotSupported;
     if (wtype == kTypeQ8_0)
         return launch_decode_fused_q8_0(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st);
-    if (wtype != kTypeQ4_K && !(wtype == kTypeQ6_K && env_int("DCQ_Q6K_DECODE", 0))) return hipErrorNotSupported;
+    if (wtype == kTypeQ6_K && !env_int("DCQ_Q6K_DECODE", 0))
+        return launch_decode_fused_q6k(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st);
+    if (wtype != kTypeQ4_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
     return launch_kq(wtype, true, W, nullptr, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums,
                      N, st);
 }

@@ -104,7 +104,7 @@ int env_int(const char* name, int dflt) {
     return (s && *s) ? atoi(s) : dflt;
 }
 
-constexpr int kWaves = 4;      // weight rows per workgroup (one per wave)
+// weight rows per workgroup: one per wave (kWaves, 4 at every launch)
 constexpr int kSbStep = 16;    // superblocks per step: 4 lanes each, one wave
 constexpr int kMaxNsb = 64;    // K <= 16384: the scales gather is one dword instruction
 constexpr size_t kMaxLds = 160 * 1024;
@@ -115,25 +115,31 @@ constexpr size_t kMaxLds = 160 * 1024;
 struct Q6Lds {
     int q_ld, b_ld, pitch;
     size_t act_bytes, total;
-    __host__ __device__ Q6Lds(int nsb, int MT) {
+    __host__ __device__ Q6Lds(int nsb, int MT, int nw) {
         q_ld = (int)round_up(256 * nsb, 1024);
         b_ld = (int)round_up(32 * nsb, 1024);
         // image at 16 - head (head < 16): 16 + 16-byte interior (1 KB pieces) + the tail dwords
         pitch = (int)round_up(16 + round_up(210 * nsb, 1024) + 256, 256);
         act_bytes = (size_t)MT * (q_ld + b_ld + 256);
-        total = act_bytes + (size_t)kWaves * pitch;
+        total = act_bytes + (size_t)nw * pitch;
     }
 };
 
 }  // namespace
 
-template <int MT, bool DUMP>
+// FUSE: X is fp32 [M][x_stride] and the workgroup quantizes it to Q8_K in LDS (the same wave
+// quantizer as the fused Q4_K decode: bit-identical bytes), saving the separate quantize
+// launch. Its loads are issued after the row's direct-to-LDS loads: loads retire in order, so
+// the wait the compiler places before the quantizer (it does not count the inline-asm loads)
+// lands when the whole row is in as well. QC passes of 16 (superblock, row) pairs.
+template <int MT, bool DUMP, bool FUSE = false, int QC = 1, int kWaves = 4>
 __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
     const int8_t* __restrict__ xqs, const float* __restrict__ xd, const int16_t* __restrict__ xbs, int64_t m_ld,
+    const float* __restrict__ X, int64_t x_stride,
     int M, float* __restrict__ Y, int64_t y_stride, int32_t* __restrict__ sums, int64_t sums_n_stride) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const Q6Lds L(nsb, MT);
+    const Q6Lds L(nsb, MT, kWaves);
     const int K = 256 * nsb;
     const int row_bytes = 210 * nsb, row_dw = row_bytes / 4;
     const int lane = threadIdx.x & 63;
@@ -147,7 +153,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
 
     // ---- 1. activation share: qs and bsums in 1 KB pieces, the scales gathered ----
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi) {
+    for (int mi = 0; mi < (FUSE ? 0 : MT); ++mi) {
         const int m = mi < M ? mi : M - 1;
         const int8_t* qsrc = xqs + (int64_t)m * K;
         for (int part = wave; part * 1024 < K; part += kWaves) {
@@ -177,7 +183,44 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     const int tail0 = row_dw > 64 ? row_dw - 64 : 0;
     dma4(src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), img + 4 * tail0);
     const int issued = nx4 + 2;
-    wait_vmcnt_rt<0, 63>(issued);  // the activation share (issued before the row) is in
+    if constexpr (FUSE) {
+        // the activation: QC passes of 16 (superblock, row) pairs, one per 16-lane group
+        const int tid = threadIdx.x, g = tid & 15, last_pair = nsb * MT - 1;
+        float4 xv[QC][4];
+#pragma unroll
+        for (int i = 0; i < QC; ++i) {
+            int pr = (tid >> 4) + 4 * kWaves * i;
+            pr = pr < last_pair ? pr : last_pair;
+            const int s = pr / MT, m = pr % MT;  // MT is a power of two
+            const float4* xp =
+                reinterpret_cast<const float4*>(X + (int64_t)(m < M ? m : M - 1) * x_stride + 256 * s + 16 * g);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xv[i][j] = xp[j];
+        }
+#pragma unroll
+        for (int i = 0; i < QC; ++i) {
+            int pr = (tid >> 4) + 4 * kWaves * i;
+            pr = pr < last_pair ? pr : last_pair;
+            const int s = pr / MT, m = pr % MT;
+            float x[16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                x[4 * j] = xv[i][j].x, x[4 * j + 1] = xv[i][j].y;
+                x[4 * j + 2] = xv[i][j].z, x[4 * j + 3] = xv[i][j].w;
+            }
+            uint32_t packed[4];
+            int bsum;
+            float dval;
+            quantize_q8k_row16(x, g, packed, bsum, dval);
+            *reinterpret_cast<uint4*>(aq + m * L.q_ld + 256 * s + 16 * g) =
+                make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            reinterpret_cast<int16_t*>(abb + m * L.b_ld)[16 * s + g] = (int16_t)bsum;
+            if (g == 0) ad[64 * m + s] = dval;
+        }
+        wait_vmcnt<0>();  // every load of the row is in as well (they were issued first)
+    } else {
+        wait_vmcnt_rt<0, 63>(issued);  // the activation share (issued before the row) is in
+    }
     __syncthreads();
 
     // ---- 3. steps of 16 superblocks, each computed once its bytes are in ----
@@ -256,7 +299,23 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
 namespace {
 
 using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, const int16_t*,
-                      int64_t, int, float*, int64_t, int32_t*, int64_t);
+                      int64_t, const float*, int64_t, int, float*, int64_t, int32_t*, int64_t);
+
+// fused activation: M <= 2 rows, nsb <= 16: at most 2 staging passes
+constexpr int kFuseMaxQc = 2;
+template <int MT, bool DUMP, int QC>
+Q6Fn q6_fused_qc(int qc) {
+    if constexpr (QC > kFuseMaxQc) {
+        return nullptr;
+    } else {
+        if (qc == QC) return decode_q6k_lds_kernel<MT, DUMP, true, QC>;
+        return q6_fused_qc<MT, DUMP, QC + 1>(qc);
+    }
+}
+template <bool DUMP>
+Q6Fn q6_pick_fused(int mt, int qc) {
+    return mt == 1 ? q6_fused_qc<1, DUMP, 1>(qc) : mt == 2 ? q6_fused_qc<2, DUMP, 1>(qc) : nullptr;
+}
 
 template <bool DUMP>
 Q6Fn q6_pick(int mt) {
@@ -281,18 +340,40 @@ hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0,
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
-        if (Q6Lds(nsb, mt).total > kMaxLds) return hipErrorNotSupported;
+        if (Q6Lds(nsb, mt, 4).total > kMaxLds) return hipErrorNotSupported;
     }
-    const unsigned grid = (unsigned)((n1 - n0 + kWaves - 1) / kWaves);
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
+        const int nw = 4;  // 5-wave workgroups (rows spread more evenly) measured no faster here
+        const unsigned grid = (unsigned)((n1 - n0 + nw - 1) / nw);
         Q6Fn fn = block_sums ? q6_pick<true>(mt) : q6_pick<false>(mt);
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), Q6Lds(nsb, mt).total, st, (const uint8_t*)W, w_row_bytes,
-                           n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.bs + m0 * (K / 16), act.m_ld, (int)mc,
-                           Y + m0 * y_stride, y_stride, block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr,
-                           sums_n_stride);
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), Q6Lds(nsb, mt, nw).total, st, (const uint8_t*)W, w_row_bytes,
+                           n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.bs + m0 * (K / 16), act.m_ld,
+                           (const float*)nullptr, (int64_t)0, (int)mc, Y + m0 * y_stride, y_stride,
+                           block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr, sums_n_stride);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
+                                   int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                                   hipStream_t st) {
+    const int nsb = (int)(K / 256);
+    // measured: fusing wins up to K = 4096 (e.g. 2560 x 4096: 5.9 vs 7.2 us) and loses at
+    // K = 9728 (11.6 vs 10.3 us), where every workgroup re-reads and re-quantizes 39 KB of X
+    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > 16 || M > 2) return hipErrorNotSupported;
+    if (env_int("DCQ_Q6K_LDS_OFF", 0) || env_int("DCQ_Q6K_NO_FUSE", 0)) return hipErrorNotSupported;
+    constexpr int kWaves = 4;
+    const int mt = M == 1 ? 1 : 2;
+    const int qc = (nsb * mt + 4 * kWaves - 1) / (4 * kWaves);
+    if (Q6Lds(nsb, mt, kWaves).total > kMaxLds) return hipErrorNotSupported;
+    Q6Fn fn = block_sums ? q6_pick_fused<true>(mt, qc) : q6_pick_fused<false>(mt, qc);
+    if (!fn) return hipErrorNotSupported;
+    const unsigned grid = (unsigned)((N + kWaves - 1) / kWaves);
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), Q6Lds(nsb, mt, kWaves).total, st, (const uint8_t*)W,
+                       w_row_bytes, (int64_t)0, N, nsb, (const int8_t*)nullptr, (const float*)nullptr, (const int16_t*)nullptr,
+                       (int64_t)0, X, x_stride, (int)M, Y, y_stride, block_sums, N);
     return hipGetLastError();
 }
 

@@ -50,6 +50,11 @@ hipError_t launch_silu_mul(float* Y, int64_t y_stride, const float* U, int64_t u
 
 // Q6_K decode with the weight rows staged in LDS by direct-to-LDS loads (K/256 even,
 // w_row_bytes % 4 == 0); hipErrorNotSupported otherwise (nothing launched).
+// Q6_K decode with the Q8_K activation quantization fused in (M <= 2, K % 512 == 0,
+// K <= 16384, row stride a multiple of 4 bytes); hipErrorNotSupported otherwise.
+hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
+                                   int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                                   hipStream_t st);
 hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                                  const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                  int64_t sums_n_stride, hipStream_t st);

@@ -97,6 +97,8 @@ CASES = [
     (Q4_K, 1, 9728, 2560), (Q4_K, 1, 2570, 4096), (Q4_K, 1, 2561, 9728),
     (Q6_K, 1, 50, 9728), (Q6_K, 1, 3, 256), (Q6_K, 8, 64, 512), (Q6_K, 33, 65, 1024), (Q6_K, 3, 17, 768),
     (Q6_K, 2, 9, 16384), (Q6_K, 1, 5, 16896),
+    # Q6_K decode with the activation quantized in the workgroup (M <= 2, K <= 4096)
+    (Q6_K, 1, 1000, 2560), (Q6_K, 2, 70, 4096),
 ]
 
 
