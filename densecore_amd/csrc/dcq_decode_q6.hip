@@ -53,6 +53,16 @@ __device__ __forceinline__ void dma16(const void* g, const void* lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
 
+// A 16-byte global load the compiler does not track, for loads that must sit in the same
+// in-order queue as the direct-to-LDS loads above: its value may be read only after an explicit
+// wait that covers it, followed by a sched_barrier (the compiler takes the result as ready).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 gload16_untracked(const void* g) {
+    u32x4 r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(g) : "memory");
+    return r;
+}
+
 // s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt fields at their maxima: no wait on them)
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -129,9 +139,9 @@ struct Q6Lds {
 
 // FUSE: X is fp32 [M][x_stride] and the workgroup quantizes it to Q8_K in LDS (the same wave
 // quantizer as the fused Q4_K decode: bit-identical bytes), saving the separate quantize
-// launch. Its loads are issued after the row's direct-to-LDS loads: loads retire in order, so
-// the wait the compiler places before the quantizer (it does not count the inline-asm loads)
-// lands when the whole row is in as well. QC passes of 16 (superblock, row) pairs.
+// launch. Its loads are untracked inline-asm loads issued before the row's direct-to-LDS
+// loads: loads retire in order, so an explicit wait for all but the row's loads covers them,
+// and the quantizer runs while the row streams. QC passes of 16 (superblock, row) pairs.
 template <int MT, bool DUMP, bool FUSE = false, int QC = 1, int kWaves = 4>
 __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
@@ -168,6 +178,21 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
         if (wave == mi % kWaves) dma4(xd + (int64_t)(lane < nsb ? lane : nsb - 1) * m_ld + m, ad + 64 * mi);
     }
 
+    // ---- 1b. fused: the fp32 activation, issued ahead of the row so that it lands first ----
+    [[maybe_unused]] u32x4 xr[FUSE ? QC : 1][4];
+    if constexpr (FUSE) {
+        const int g = threadIdx.x & 15, last_pair = nsb * MT - 1;
+#pragma unroll
+        for (int i = 0; i < QC; ++i) {
+            int pr = (threadIdx.x >> 4) + 4 * kWaves * i;
+            pr = pr < last_pair ? pr : last_pair;
+            const int s = pr / MT, m = pr % MT;  // MT is a power of two
+            const float* xp = X + (int64_t)(m < M ? m : M - 1) * x_stride + 256 * s + 16 * g;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xr[i][j] = gload16_untracked(xp + 4 * j);
+        }
+    }
+
     // ---- 2. this wave's row: head dwords, 16-byte interior, tail dwords ----
     // row byte b sits at img + b; img + head is 16-byte aligned like src + head
     const uint8_t* src = W + (row_ok ? row : n1 - 1) * w_row_bytes;
@@ -184,19 +209,11 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     dma4(src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), img + 4 * tail0);
     const int issued = nx4 + 2;
     if constexpr (FUSE) {
-        // the activation: QC passes of 16 (superblock, row) pairs, one per 16-lane group
+        // quantize the activation (QC passes of 16 (superblock, row) pairs, one per 16-lane
+        // group) while the row streams: wait for the activation loads only (issued before it)
+        wait_vmcnt_rt<0, 63>(issued);
+        __builtin_amdgcn_sched_barrier(0);
         const int tid = threadIdx.x, g = tid & 15, last_pair = nsb * MT - 1;
-        float4 xv[QC][4];
-#pragma unroll
-        for (int i = 0; i < QC; ++i) {
-            int pr = (tid >> 4) + 4 * kWaves * i;
-            pr = pr < last_pair ? pr : last_pair;
-            const int s = pr / MT, m = pr % MT;  // MT is a power of two
-            const float4* xp =
-                reinterpret_cast<const float4*>(X + (int64_t)(m < M ? m : M - 1) * x_stride + 256 * s + 16 * g);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) xv[i][j] = xp[j];
-        }
 #pragma unroll
         for (int i = 0; i < QC; ++i) {
             int pr = (tid >> 4) + 4 * kWaves * i;
@@ -205,8 +222,8 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
             float x[16];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                x[4 * j] = xv[i][j].x, x[4 * j + 1] = xv[i][j].y;
-                x[4 * j + 2] = xv[i][j].z, x[4 * j + 3] = xv[i][j].w;
+                x[4 * j] = __uint_as_float(xr[i][j].x), x[4 * j + 1] = __uint_as_float(xr[i][j].y);
+                x[4 * j + 2] = __uint_as_float(xr[i][j].z), x[4 * j + 3] = __uint_as_float(xr[i][j].w);
             }
             uint32_t packed[4];
             int bsum;
@@ -217,7 +234,6 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
             reinterpret_cast<int16_t*>(abb + m * L.b_ld)[16 * s + g] = (int16_t)bsum;
             if (g == 0) ad[64 * m + s] = dval;
         }
-        wait_vmcnt<0>();  // every load of the row is in as well (they were issued first)
     } else {
         wait_vmcnt_rt<0, 63>(issued);  // the activation share (issued before the row) is in
     }
@@ -301,8 +317,8 @@ namespace {
 using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, const int16_t*,
                       int64_t, const float*, int64_t, int, float*, int64_t, int32_t*, int64_t);
 
-// fused activation: M <= 2 rows, nsb <= 16: at most 2 staging passes
-constexpr int kFuseMaxQc = 2;
+// fused activation: M <= 2 rows, nsb <= 64: at most 8 staging passes
+constexpr int kFuseMaxQc = 8;
 template <int MT, bool DUMP, int QC>
 Q6Fn q6_fused_qc(int qc) {
     if constexpr (QC > kFuseMaxQc) {
@@ -360,9 +376,12 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                    hipStream_t st) {
     const int nsb = (int)(K / 256);
-    // measured: fusing wins up to K = 4096 (e.g. 2560 x 4096: 5.9 vs 7.2 us) and loses at
-    // K = 9728 (11.6 vs 10.3 us), where every workgroup re-reads and re-quantizes 39 KB of X
-    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > 16 || M > 2) return hipErrorNotSupported;
+    // measured (M = 1): fusing wins up to K = 4096 (2560 x 4096: 5.7 vs 7.2 us; 1024 x 2560: 3.8
+    // vs 5.8 us) and loses at K = 9728 (11.6 vs 10.3 us), where each of the 640 workgroups
+    // re-reads and re-quantizes 39 KB of X; DCQ_Q6K_FUSE_MAX_NSB overrides the limit (tuning)
+    const int fuse_max_nsb = env_int("DCQ_Q6K_FUSE_MAX_NSB", 16);
+    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || nsb > fuse_max_nsb || M > 2)
+        return hipErrorNotSupported;
     if (env_int("DCQ_Q6K_LDS_OFF", 0) || env_int("DCQ_Q6K_NO_FUSE", 0)) return hipErrorNotSupported;
     constexpr int kWaves = 4;
     const int mt = M == 1 ? 1 : 2;
