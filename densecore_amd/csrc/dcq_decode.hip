@@ -441,7 +441,9 @@ int choose_shape(int nsb) {
 // MI355X at K = 2560: 32 rows per CU 4.7 us, 40 rows 5.7 us, 48 rows 6.0 us, one workgroup per
 // CU beating two at the same row count). Among the shapes that leave at most a quarter of their
 // superblock slots idle, and 4- or 5-wave workgroups, take the fewest rows on the busiest CU,
-// then the fewest workgroups per CU. Other variants keep choose_shape with 4 waves.
+// then the fewest workgroups per CU. Other variants keep choose_shape with 4 waves. (8- and
+// 10-wave workgroups of 4-row waves, more waves for the same rows, measured slower: 6.3-7.0 us
+// against 5.7 us at N = 9728; bytes in flight per lane matter more than waves per CU.)
 struct Launch {
     int idx, nw;
 };
@@ -457,7 +459,7 @@ int cu_count() {
 }
 Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
     const int forced = env_int("DCQ_Q4K_SHAPE", -1);
-    if (forced >= 0) return {choose_shape(nsb), 4};
+    if (forced >= 0) return {choose_shape(nsb), env_int("DCQ_Q4K_NW", 4) == 5 ? 5 : 4};
     const int cus = cu_count();
     Launch best{choose_shape(nsb), 4};
     int64_t best_rows = INT64_MAX, best_per_cu = INT64_MAX;
