@@ -251,6 +251,47 @@ def bench_gate_up(cfg, args, dev):
             "separate_weight_GBps": 2 * wbytes / (s_ms * 1e-3) / 1e9}
 
 
+def bench_qkv(args, dev, K=2560, parts=(4096, 1024, 1024), wtype=None):
+    """The Q/K/V projections of one Qwen3-4B layer at decode (M = 1, Q4_K), which share X
+    (core/src/inference.cpp:1128-1130): three dcq_mul_mat calls against one call over the three
+    weights loaded back to back (same type and K, so one row stride). Weight GB/s counts all three."""
+    import torch
+    import densecore_amd as dc
+    wtype = dc.TYPE_Q4_K if wtype is None else wtype
+    rb = dc.row_size(wtype, K)
+    n_all = sum(parts)
+    w = torch.randn((n_all, K), device=dev) * 0.02
+    wq = dc.quantize_weights(wtype, w)
+    del w
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / (n_all * rb))))
+    big = torch.empty((copies, n_all, rb), dtype=torch.uint8, device=dev)
+    for r in range(copies):
+        big[r].copy_(wq)
+    x = torch.randn((1, K), device=dev)
+    y = torch.empty((1, n_all), dtype=torch.float32, device=dev)
+    ys = [torch.empty((1, n), dtype=torch.float32, device=dev) for n in parts]
+    ws = torch.empty(max(dc.mul_mat_workspace_size(wtype, 1, K), 256), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+
+    def separate(i):
+        s, r0 = torch.cuda.current_stream().cuda_stream, 0
+        for n, yy in zip(parts, ys):
+            dc.mul_mat(wtype, big[i % copies][r0:r0 + n], n, K, x, y=yy, workspace=ws, stream=s)
+            r0 += n
+
+    def fused(i):
+        dc.mul_mat(wtype, big[i % copies], n_all, K, x, y=y, workspace=ws,
+                   stream=torch.cuda.current_stream().cuda_stream)
+
+    s_ms, s_k = time_graph(separate, args.steps, args.warmup, args.replays)
+    f_ms, f_k = time_graph(fused, args.steps, args.warmup, args.replays)
+    del big, wq
+    torch.cuda.empty_cache()
+    return {"shape": f"Q4_K q/k/v {list(parts)} x K={K}, M=1", "separate_us": s_ms * 1e3, "separate_kernels": s_k,
+            "one_call_us": f_ms * 1e3, "one_call_kernels": f_k,
+            "one_call_weight_GBps": n_all * rb / (f_ms * 1e-3) / 1e9}
+
+
 def bench_kv_attention(args, dev, ct, n_tokens=1, n_past=4095, n_layer=36, n_head=32, n_head_kv=8, hd=128):
     """Attention of one layer over DenseCore's paged KV cache (dcq_kv_attention) at Qwen3-4B's
     heads (32 query, 8 KV, head_dim 128). Each step attends the next of n_layer layers, so the
@@ -424,6 +465,9 @@ def main():
         print(f"# gate/up pair at config {HEADLINE}: fused {g['fused_us']:.2f} us ({g['fused_kernels']} kernels), "
               f"two mul_mat calls {g['separate_us']:.2f} us", file=sys.stderr, flush=True)
     if not args.no_extras:
+        q = extras["qkv_projections"] = bench_qkv(args, dev)
+        print(f"# q/k/v projections: three calls {q['separate_us']:.2f} us, one call over the concatenated "
+              f"weights {q['one_call_us']:.2f} us", file=sys.stderr, flush=True)
         for name, kw in (("kv_attention_decode_q8_0", dict(ct=dc.TYPE_Q8_0)),
                          ("kv_attention_decode_f16", dict(ct=dc.TYPE_F16)),
                          ("kv_attention_prefill_q8_0", dict(ct=dc.TYPE_Q8_0, n_tokens=2048, n_past=0, n_layer=2))):

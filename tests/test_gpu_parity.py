@@ -325,3 +325,39 @@ def test_gguf_load_to_device_and_mul_mat(O, dev, tmp_path):
             y = dc.mul_mat(wt, w_dev, n, k, to_dev(x, dev))
             y_ref, l1 = O.mul_mat(wt, wq, x)
             O.assert_close(to_host(y), y_ref, l1, RTOL, what=f"mul_mat on loaded {name}")
+
+
+# ---------------------------------------------------------------- projections sharing X (Q/K/V)
+@pytest.mark.parametrize("wt", [Q4_K, Q8_0])
+def test_concatenated_projections_one_call(O, dev, tmp_path, wt):
+    """The Q/K/V projections (core/src/inference.cpp:1128-1130) share X. Loaded back to back into
+    one device buffer (same type and K, so the same row bytes), one dcq_mul_mat over the
+    concatenated rows gives [Q | K | V] per activation row: each slice against the oracle's
+    separate product. Loaded through the GGUF reader, as an integration would."""
+    import torch
+    from gguf_writer import write_gguf
+    K = 2560 if wt == Q4_K else 1024
+    parts = [("blk.0.attn_q.weight", 512), ("blk.0.attn_k.weight", 128), ("blk.0.attn_v.weight", 128)]
+    wqs, tensors = [], []
+    for i, (name, n) in enumerate(parts):
+        wq = O.quantize_matrix(wt, synth.normal(n * K, 900 + i, 0.0, 0.02).reshape(n, K))
+        wqs.append(wq)
+        tensors.append((name, wt, [K, n], wq.tobytes()))
+    path = tmp_path / "qkv.gguf"
+    write_gguf(path, [], tensors)
+    rb = dc.row_size(wt, K)
+    n_all = sum(n for _, n in parts)
+    buf = torch.empty((n_all, rb), dtype=torch.uint8, device=dev)
+    with dc.GGUF(path) as g:
+        r0 = 0
+        for name, n in parts:
+            g.load(g.find(name), dst=buf[r0:r0 + n])
+            r0 += n
+    for M in (1, 3):
+        x = synth.normal(M * K, 950 + M).reshape(M, K)
+        y = to_host(dc.mul_mat(wt, buf, n_all, K, to_dev(x, dev)))
+        r0 = 0
+        for (name, n), wq in zip(parts, wqs):
+            y_ref, l1 = O.mul_mat(wt, wq, x)
+            O.assert_close(y[:, r0:r0 + n], y_ref, l1, RTOL, what=f"{name} slice, M={M}")
+            r0 += n
