@@ -292,6 +292,43 @@ def bench_qkv(args, dev, K=2560, parts=(4096, 1024, 1024), wtype=None):
             "one_call_weight_GBps": n_all * rb / (f_ms * 1e-3) / 1e9}
 
 
+def bench_residual(args, dev, wtype, N=2560, K=9728):
+    """The FFN down projection of Qwen3-4B at decode with its residual connection
+    (core/src/inference.cpp:1799-1800): dcq_mul_mat followed by torch's add, against one
+    dcq_mul_mat_add call with the residual in place (R is Y)."""
+    import torch
+    import densecore_amd as dc
+    rb = dc.row_size(wtype, K)
+    w = torch.randn((N, K), device=dev) * 0.02
+    wq = dc.quantize_weights(wtype, w)
+    del w
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / (N * rb))))
+    big = torch.empty((copies, N, rb), dtype=torch.uint8, device=dev)
+    for r in range(copies):
+        big[r].copy_(wq)
+    x = torch.randn((1, K), device=dev)
+    resid = torch.randn((1, N), device=dev)
+    y = torch.empty((1, N), dtype=torch.float32, device=dev)
+    ws = torch.empty(max(dc.mul_mat_add_workspace_size(wtype, 1, N, K), 256), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+
+    def separate(i):
+        dc.mul_mat(wtype, big[i % copies], N, K, x, y=y, workspace=ws, stream=torch.cuda.current_stream().cuda_stream)
+        resid.add_(y)
+
+    def fused(i):
+        dc.mul_mat_add(wtype, big[i % copies], N, K, x, resid, y=resid, workspace=ws,
+                       stream=torch.cuda.current_stream().cuda_stream)
+
+    s_ms, s_k = time_graph(separate, args.steps, args.warmup, args.replays)
+    f_ms, f_k = time_graph(fused, args.steps, args.warmup, args.replays)
+    del big, wq
+    torch.cuda.empty_cache()
+    return {"shape": f"{dc.TYPE_NAMES[wtype]} ffn_down {N} x K={K}, M=1, residual in place",
+            "mul_mat_then_add_us": s_ms * 1e3, "mul_mat_then_add_kernels": s_k,
+            "mul_mat_add_us": f_ms * 1e3, "mul_mat_add_kernels": f_k}
+
+
 def bench_kv_attention(args, dev, ct, n_tokens=1, n_past=4095, n_layer=36, n_head=32, n_head_kv=8, hd=128):
     """Attention of one layer over DenseCore's paged KV cache (dcq_kv_attention) at Qwen3-4B's
     heads (32 query, 8 KV, head_dim 128). Each step attends the next of n_layer layers, so the
@@ -468,6 +505,11 @@ def main():
         q = extras["qkv_projections"] = bench_qkv(args, dev)
         print(f"# q/k/v projections: three calls {q['separate_us']:.2f} us, one call over the concatenated "
               f"weights {q['one_call_us']:.2f} us", file=sys.stderr, flush=True)
+        for wt in (dc.TYPE_Q6_K, dc.TYPE_Q4_K):
+            e = extras[f"ffn_down_residual_{dc.TYPE_NAMES[wt].lower()}"] = bench_residual(args, dev, wt)
+            print(f"# {e['shape']}: mul_mat + add {e['mul_mat_then_add_us']:.2f} us "
+                  f"({e['mul_mat_then_add_kernels']} kernels), mul_mat_add {e['mul_mat_add_us']:.2f} us "
+                  f"({e['mul_mat_add_kernels']} kernels)", file=sys.stderr, flush=True)
         for name, kw in (("kv_attention_decode_q8_0", dict(ct=dc.TYPE_Q8_0)),
                          ("kv_attention_decode_f16", dict(ct=dc.TYPE_F16)),
                          ("kv_attention_prefill_q8_0", dict(ct=dc.TYPE_Q8_0, n_tokens=2048, n_past=0, n_layer=2))):

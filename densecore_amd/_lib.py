@@ -14,7 +14,8 @@ SYMBOLS = [
     "dcq_version", "dcq_status_string", "dcq_block_size", "dcq_type_size", "dcq_row_size", "dcq_vec_dot_type",
     "dcq_supports_mul_mat", "dcq_quantize_rows", "dcq_mul_mat_workspace_size", "dcq_mul_mat", "dcq_mul_mat_ex",
     "dcq_block_sums_per_row", "dcq_dot_rows", "dcq_quantize_weights", "dcq_dequantize_rows",
-    "dcq_quantize_src1", "dcq_mul_mat_q", "dcq_ffn_gate_up_workspace_size", "dcq_ffn_gate_up",
+    "dcq_quantize_src1", "dcq_mul_mat_q", "dcq_mul_mat_add_workspace_size", "dcq_mul_mat_add",
+    "dcq_ffn_gate_up_workspace_size", "dcq_ffn_gate_up",
     "dcq_gguf_open", "dcq_gguf_close", "dcq_gguf_tensor_count", "dcq_gguf_find_tensor", "dcq_gguf_tensor_info",
     "dcq_gguf_get_int", "dcq_gguf_get_str", "dcq_gguf_load_tensor",
     "dcq_kv_slot_bytes", "dcq_kv_write", "dcq_kv_gather", "dcq_kv_attention_workspace_size", "dcq_kv_attention",
@@ -64,6 +65,8 @@ def lib():
             "dcq_dequantize_rows": (i32, [i32, vp, i64, i64, sz, vp, vp]),
             "dcq_quantize_src1": (i32, [i32, vp, i64, i64, sz, vp, sz, vp]),
             "dcq_mul_mat_q": (i32, [i32, vp, i64, i64, sz, vp, sz, i64, vp, sz, i32, vp]),
+            "dcq_mul_mat_add_workspace_size": (sz, [i32, i64, i64, i64]),
+            "dcq_mul_mat_add": (i32, [i32, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp, sz, vp, sz, vp]),
             "dcq_ffn_gate_up_workspace_size": (sz, [i32, i64, i64, i64]),
             "dcq_ffn_gate_up": (i32, [i32, vp, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp, sz, vp]),
             "dcq_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
@@ -179,6 +182,26 @@ def mul_mat(wt, wq, n, k, x, y=None, workspace=None, w_row_bytes=None, stream=No
     _check("dcq_mul_mat", lib().dcq_mul_mat(
         wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace), ws_bytes,
         _stream(stream)))
+    return y
+
+
+def mul_mat_add_workspace_size(wt, m, n, k):
+    return lib().dcq_mul_mat_add_workspace_size(wt, m, n, k)
+
+
+def mul_mat_add(wt, wq, n, k, x, r, y=None, workspace=None, w_row_bytes=None, stream=None):
+    """Y[M, N] = W x + R: a projection and its residual (R [M, N], may be y itself) or bias (R [N],
+    broadcast over the rows)."""
+    import torch
+    m = x.shape[0]
+    if y is None:
+        y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    r_stride = 0 if r.dim() == 1 else r.stride(0) * 4
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check("dcq_mul_mat_add", lib().dcq_mul_mat_add(
+        wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(r), r_stride, _ptr(y), y.stride(0) * 4,
+        _ptr(workspace), ws_bytes, _stream(stream)))
     return y
 
 

@@ -232,6 +232,74 @@ int dcq_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_byt
                           workspace_bytes, DCQ_PATH_AUTO, nullptr, stream);
 }
 
+size_t dcq_mul_mat_add_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
+    const size_t a = dcq_mul_mat_workspace_size(wtype, M, K);
+    if (!a || N <= 0) return 0;
+    return a + (size_t)round_up(M * N * 4, 256);
+}
+
+int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X, int64_t M,
+                    size_t x_stride_bytes, const float* R, size_t r_stride_bytes, float* Y, size_t y_stride_bytes,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = validate_mul_mat(wtype, W, N, K, w_row_bytes, X, M, x_stride_bytes, Y, y_stride_bytes);
+    if (rc) return rc;
+    if (!R) return DCQ_ERR_INVALID_ARG;
+    if (r_stride_bytes != 0 && r_stride_bytes < (size_t)N * 4) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(R, 4) || r_stride_bytes % 4) return DCQ_ERR_MISALIGNED;
+    // R is either Y itself (same stride: each element is read, then written, by one lane) or
+    // disjoint from Y's extent
+    const bool in_place = (const void*)R == (const void*)Y;
+    if (in_place && r_stride_bytes != y_stride_bytes) return DCQ_ERR_INVALID_ARG;
+    if (!in_place) {
+        const uintptr_t y0 = (uintptr_t)Y, y1 = y0 + (size_t)(M - 1) * y_stride_bytes + (size_t)N * 4;
+        const uintptr_t r0 = (uintptr_t)R, r1 = r0 + (size_t)(M - 1) * r_stride_bytes + (size_t)N * 4;
+        if (r0 < y1 && y0 < r1) return DCQ_ERR_INVALID_ARG;
+    }
+    const size_t need = dcq_mul_mat_add_workspace_size(wtype, M, N, K);
+    if (workspace) {
+        if (workspace_bytes < need) return DCQ_ERR_WORKSPACE;
+        if (!aligned(workspace, 256)) return DCQ_ERR_MISALIGNED;
+    }
+    rc = check_device();
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t y_stride = (int64_t)(y_stride_bytes / 4), r_stride = (int64_t)(r_stride_bytes / 4);
+    if (M <= 8) {
+        // decode: the add is the fused kernel's store epilogue
+        hipError_t e = launch_decode_fused(wtype, W, (int64_t)w_row_bytes, N, K, X, (int64_t)(x_stride_bytes / 4), M,
+                                           Y, y_stride, nullptr, st, R, r_stride);
+        if (e != hipErrorNotSupported) return hip_status(e);
+    }
+    void* ws = workspace;
+    if (!ws) {
+        if (hipMallocAsync(&ws, need, st) != hipSuccess) return DCQ_ERR_HIP;
+    }
+    const int vdt = dcq_vec_dot_type(wtype);
+    PlanarBuffers pb;
+    const size_t act_bytes = planar_bytes(vdt, M, K, &pb, ws);
+    // the product goes to Y when R is elsewhere, else to a workspace temporary [M][N]
+    float* T = in_place ? reinterpret_cast<float*>(static_cast<char*>(ws) + act_bytes) : Y;
+    const int64_t t_stride = in_place ? N : y_stride;
+    hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
+    bool added = false;
+    if (e == hipSuccess && M <= 8) {
+        // the LDS-staged decode kernels add R in their store
+        e = launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st, R, r_stride);
+        added = e != hipErrorNotSupported;
+        if (!added) e = hipSuccess;
+    }
+    if (e == hipSuccess && !added) {
+        e = M <= 8 ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, T, t_stride, nullptr, N, st)
+                   : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, T, t_stride, nullptr, st);
+        if (e == hipSuccess) e = launch_add_rows(Y, y_stride, T, t_stride, R, r_stride, M, N, st);
+    }
+    if (!workspace) {
+        hipError_t e2 = hipFreeAsync(ws, st);
+        if (e == hipSuccess) e = e2;
+    }
+    return hip_status(e);
+}
+
 size_t dcq_ffn_gate_up_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {
     const size_t a = dcq_mul_mat_workspace_size(wtype, M, K);
     if (!a || N <= 0) return 0;

@@ -197,8 +197,9 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
                                                          const float* __restrict__ X, int64_t x_stride,
                                                          const int8_t* __restrict__ xqs, const float* __restrict__ xd,
                                                          const int16_t* __restrict__ xbs, int64_t m_ld, int M,
-                                                         float* __restrict__ Y, int64_t y_stride,
-                                                         int32_t* __restrict__ sums, int64_t sums_n_stride) {
+                                                         float* Y, int64_t y_stride,  // R may alias Y
+                                                         int32_t* __restrict__ sums, int64_t sums_n_stride,
+                                                         const float* R, int64_t r_stride) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int L = 4 * P;     // lanes per row
     constexpr int RPW = 64 / L;  // rows per wave
@@ -338,7 +339,8 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
     if (q == 0 && row_ok) {
 #pragma unroll
         for (int mi = 0; mi < MT; ++mi)
-            if (mi < M) Y[(int64_t)mi * y_stride + (row - n0)] = acc[mi];
+            if (mi < M)  // R (optional, may alias Y): Y = W x + R, the residual or bias add
+                Y[(int64_t)mi * y_stride + (row - n0)] = R ? acc[mi] + R[(int64_t)mi * r_stride + (row - n0)] : acc[mi];
     }
 }
 
@@ -347,7 +349,7 @@ namespace {
 
 using DecodeFn = void (*)(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, int, const float*, int64_t,
                           const int8_t*, const float*, const int16_t*, int64_t, int, float*, int64_t, int32_t*,
-                          int64_t);
+                          int64_t, const float*, int64_t);
 
 // Launch shapes (P superblocks of a row per step, NS steps): a row of nsb <= P*NS
 // superblocks. Other K fall back to the generic kernel.
@@ -483,7 +485,8 @@ Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
 // W2 != nullptr: the gate/up pair (Q4_K, fused activation, no block sums): Y = silu(W x) * (W2 x)
 hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_t w_row_bytes, int64_t n0, int64_t n1,
                      int64_t K, const float* X, int64_t x_stride, const PlanarBuffers* act, int64_t M, float* Y,
-                     int64_t y_stride, int32_t* block_sums, int64_t sums_n_stride, hipStream_t st) {
+                     int64_t y_stride, int32_t* block_sums, int64_t sums_n_stride, hipStream_t st,
+                     const float* R = nullptr, int64_t r_stride = 0) {
     const int nsb = (int)(K / 256);
     if (wtype != kTypeQ4_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
     const bool glu = W2 != nullptr;
@@ -519,7 +522,8 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
                            fuse ? X + m0 * x_stride : nullptr, x_stride, fuse ? nullptr : act->qs + m0 * K,
                            fuse ? nullptr : act->d + m0, fuse ? nullptr : act->bs + m0 * (K / 16),
                            fuse ? 0 : act->m_ld, (int)mc, Y + m0 * y_stride, y_stride,
-                           block_sums ? block_sums + m0 * sums_n_stride * per_row_sums : nullptr, sums_n_stride);
+                           block_sums ? block_sums + m0 * sums_n_stride * per_row_sums : nullptr, sums_n_stride,
+                           R ? R + m0 * r_stride : nullptr, r_stride);
     }
     return hipGetLastError();
 }
@@ -528,22 +532,24 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
 
 hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                            int64_t sums_n_stride, hipStream_t st) {
+                            int64_t sums_n_stride, hipStream_t st, const float* R, int64_t r_stride) {
     return launch_kq(wtype, false, W, nullptr, w_row_bytes, n0, n1, K, nullptr, 0, &act, M, Y, y_stride, block_sums,
-                     sums_n_stride, st);
+                     sums_n_stride, st, R, r_stride);
 }
 
 hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
                                int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                               hipStream_t st) {
+                               hipStream_t st, const float* R, int64_t r_stride) {
     if (env_int("DCQ_NO_FUSE", 0)) return hipErrorNotSupported;
     if (wtype == kTypeQ8_0)
-        return launch_decode_fused_q8_0(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st);
+        return launch_decode_fused_q8_0(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R,
+                                        r_stride);
     if (wtype == kTypeQ6_K && !env_int("DCQ_Q6K_DECODE", 0))
-        return launch_decode_fused_q6k(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st);
+        return launch_decode_fused_q6k(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R,
+                                       r_stride);
     if (wtype != kTypeQ4_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
     return launch_kq(wtype, true, W, nullptr, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums,
-                     N, st);
+                     N, st, R, r_stride);
 }
 
 hipError_t launch_decode_fused_glu(int wtype, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,

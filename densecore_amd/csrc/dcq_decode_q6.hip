@@ -147,7 +147,8 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
     const int8_t* __restrict__ xqs, const float* __restrict__ xd, const int16_t* __restrict__ xbs, int64_t m_ld,
     const float* __restrict__ X, int64_t x_stride,
-    int M, float* __restrict__ Y, int64_t y_stride, int32_t* __restrict__ sums, int64_t sums_n_stride) {
+    int M, float* Y, int64_t y_stride, int32_t* __restrict__ sums, int64_t sums_n_stride,
+    const float* R, int64_t r_stride) {
     extern __shared__ __align__(16) uint8_t smem[];
     const Q6Lds L(nsb, MT, kWaves);
     const int K = 256 * nsb;
@@ -308,14 +309,16 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi) {
         const float v = lanes_sum<64>(acc[mi]);
-        if (lane == 0 && row_ok && mi < M) Y[(int64_t)mi * y_stride + (row - n0)] = v;
+        if (lane == 0 && row_ok && mi < M)  // R (optional, may alias Y): Y = W x + R
+            Y[(int64_t)mi * y_stride + (row - n0)] = R ? v + R[(int64_t)mi * r_stride + (row - n0)] : v;
     }
 }
 
 namespace {
 
 using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, const int16_t*,
-                      int64_t, const float*, int64_t, int, float*, int64_t, int32_t*, int64_t);
+                      int64_t, const float*, int64_t, int, float*, int64_t, int32_t*, int64_t, const float*,
+                      int64_t);
 
 // fused activation: M <= 2 rows, nsb <= 64: at most 8 staging passes
 constexpr int kFuseMaxQc = 8;
@@ -347,7 +350,7 @@ Q6Fn q6_pick(int mt) {
 
 hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                                  const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                 int64_t sums_n_stride, hipStream_t st) {
+                                 int64_t sums_n_stride, hipStream_t st, const float* R, int64_t r_stride) {
     const int nsb = (int)(K / 256);
     // dword-granular head/tail loads: the row's bytes and its stride must be whole dwords;
     // the weight base is 16-byte aligned (checked by the C ABI)
@@ -367,14 +370,15 @@ hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0,
         hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), Q6Lds(nsb, mt, nw).total, st, (const uint8_t*)W, w_row_bytes,
                            n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.bs + m0 * (K / 16), act.m_ld,
                            (const float*)nullptr, (int64_t)0, (int)mc, Y + m0 * y_stride, y_stride,
-                           block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr, sums_n_stride);
+                           block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr, sums_n_stride,
+                           R ? R + m0 * r_stride : nullptr, r_stride);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                   hipStream_t st) {
+                                   hipStream_t st, const float* R, int64_t r_stride) {
     const int nsb = (int)(K / 256);
     // measured (M = 1): fusing wins up to K = 4096 (2560 x 4096: 5.7 vs 7.2 us; 1024 x 2560: 3.8
     // vs 5.8 us) and loses at K = 9728 (11.6 vs 10.3 us), where each of the 640 workgroups
@@ -392,7 +396,7 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
     const unsigned grid = (unsigned)((N + kWaves - 1) / kWaves);
     hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), Q6Lds(nsb, mt, kWaves).total, st, (const uint8_t*)W,
                        w_row_bytes, (int64_t)0, N, nsb, (const int8_t*)nullptr, (const float*)nullptr, (const int16_t*)nullptr,
-                       (int64_t)0, X, x_stride, (int)M, Y, y_stride, block_sums, N);
+                       (int64_t)0, X, x_stride, (int)M, Y, y_stride, block_sums, N, R, r_stride);
     return hipGetLastError();
 }
 

@@ -89,9 +89,9 @@ template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, int QC = q
 __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __restrict__ W,
                                                            const uint8_t* __restrict__ W2, int64_t w_row_bytes,
                                                            int64_t N, int K, const float* __restrict__ X,
-                                                           int64_t x_stride, int M, float* __restrict__ Y,
+                                                           int64_t x_stride, int M, float* Y,  // R may alias Y
                                                            int64_t y_stride, int32_t* __restrict__ sums,
-                                                           int64_t sums_n_stride) {
+                                                           int64_t sums_n_stride, const float* R, int64_t r_stride) {
     if constexpr (QC <= kMaxStagePasses) {
         extern __shared__ __align__(16) uint8_t smem[];
         constexpr int RPW = 64 / G;  // rows per wave
@@ -212,7 +212,8 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __r
         if (g == 0 && row_ok) {
 #pragma unroll
             for (int mi = 0; mi < MT; ++mi)
-                if (mi < M) Y[(int64_t)mi * y_stride + row] = acc[mi];
+                if (mi < M)  // R (optional, may alias Y): Y = W x + R
+                    Y[(int64_t)mi * y_stride + row] = R ? acc[mi] + R[(int64_t)mi * r_stride + row] : acc[mi];
         }
     }
 }
@@ -220,7 +221,7 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __r
 namespace {
 
 using DecodeQ8Fn = void (*)(const uint8_t*, const uint8_t*, int64_t, int64_t, int, const float*, int64_t, int,
-                            float*, int64_t, int32_t*, int64_t);
+                            float*, int64_t, int32_t*, int64_t, const float*, int64_t);
 
 // (G lanes per row, NS pairs per lane): a row of U = K/64 pairs needs G*NS >= U
 struct Q8Shape {
@@ -293,7 +294,8 @@ namespace {
 
 // W2 != nullptr: the gate/up pair (no block sums), Y = silu(W x) * (W2 x)
 hipError_t launch_q8(const void* W, const void* W2, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
-                     int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+                     int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                     const float* R = nullptr, int64_t r_stride = 0) {
     if (K % 64 != 0 || w_row_bytes % 4 != 0 || x_stride % 4 != 0) return hipErrorNotSupported;
     if (W2 && block_sums) return hipErrorNotSupported;
     const int U = (int)(K / 64);
@@ -318,7 +320,8 @@ hipError_t launch_q8(const void* W, const void* W2, int64_t w_row_bytes, int64_t
                            : (block_sums ? q8_pick_shape<true>(idx, mt) : q8_pick_shape<false>(idx, mt));
         hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kQ8Waves), lds, st, (const uint8_t*)W, (const uint8_t*)W2,
                            w_row_bytes, N, (int)K, X + m0 * x_stride, x_stride, (int)mc, Y + m0 * y_stride, y_stride,
-                           block_sums ? block_sums + m0 * N * per_row_sums : nullptr, N);
+                           block_sums ? block_sums + m0 * N * per_row_sums : nullptr, N,
+                           R ? R + m0 * r_stride : nullptr, r_stride);
     }
     return hipGetLastError();
 }
@@ -327,8 +330,8 @@ hipError_t launch_q8(const void* W, const void* W2, int64_t w_row_bytes, int64_t
 
 hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
                                     int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                    hipStream_t st) {
-    return launch_q8(W, nullptr, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st);
+                                    hipStream_t st, const float* R, int64_t r_stride) {
+    return launch_q8(W, nullptr, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R, r_stride);
 }
 
 hipError_t launch_decode_fused_q8_0_glu(const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,

@@ -341,7 +341,7 @@ static int env_int(const char* name, int dflt) {
 
 hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                        const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                       int64_t sums_n_stride, hipStream_t st) {
+                       int64_t sums_n_stride, hipStream_t st, const float* R, int64_t r_stride) {
     // Q6_K: weight rows staged through LDS by coalesced direct-to-LDS loads (its 2-byte aligned
     // superblocks make lane-direct loads scatter: 4x the L1 accesses of the staged form);
     // DCQ_Q6K_DECODE=1 selects the lane-direct four-lanes-per-superblock kernel instead
@@ -349,12 +349,13 @@ hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0
         hipError_t e = hipErrorNotSupported;
         if (wtype == kTypeQ4_K || (wtype == kTypeQ6_K && env_int("DCQ_Q6K_DECODE", 0)))
             e = launch_decode_kq(wtype, W, w_row_bytes, n0, n1, K, act, M, Y, y_stride, block_sums, sums_n_stride,
-                                 st);
+                                 st, R, r_stride);
         else if (wtype == kTypeQ6_K)
             e = launch_decode_q6k_lds(W, w_row_bytes, n0, n1, K, act, M, Y, y_stride, block_sums, sums_n_stride,
-                                      st);
+                                      st, R, r_stride);
         if (e != hipErrorNotSupported) return e;
     }
+    if (R) return hipErrorNotSupported;  // the generic kernels have no add in their store
     int f;
     if (wtype == kTypeQ8_0)
         f = (K % 64 == 0 && w_row_bytes % 4 == 0) ? kQ8_0Pair : kQ8_0Single;

@@ -26,15 +26,18 @@ hipError_t launch_unpack_ggml_rows(int vdt, const void* in, int64_t in_row_bytes
 
 // Decode GEMV / small-M: wave-per-row-group int8 dot products.
 // Y[m*y_stride + n] for m < M, n in [n0, n1); block_sums optional (atomics, pre-zeroed).
+// R (optional, indexed like Y, may be Y itself): Y = W x + R, added in the store of the
+// LDS-staged Q4_K / Q6_K kernels; with R given and neither covering the shape, nothing is
+// launched and the result is hipErrorNotSupported.
 hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                        const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                       int64_t sums_n_stride, hipStream_t st);
+                       int64_t sums_n_stride, hipStream_t st, const float* R = nullptr, int64_t r_stride = 0);
 
 // LDS-staged decode kernels (M <= 8 per launch, tiled by 8). hipErrorNotSupported means the
 // shape is outside what they cover and nothing was launched.
 hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                            int64_t sums_n_stride, hipStream_t st);
+                            int64_t sums_n_stride, hipStream_t st, const float* R = nullptr, int64_t r_stride = 0);
 
 // SwiGLU gate/up pair at M <= 8 with the activation quantization fused in (Q4_K, Q8_0):
 // Y = silu(Wg x) * (Wu x); hipErrorNotSupported when the fused kernels do not cover the shape.
@@ -47,6 +50,8 @@ hipError_t launch_decode_fused_q8_0_glu(const void* Wg, const void* Wu, int64_t 
 // Y[m][n] = silu(Y[m][n]) * U[m][n] (the SwiGLU product after two separate projections)
 hipError_t launch_silu_mul(float* Y, int64_t y_stride, const float* U, int64_t u_stride, int64_t M, int64_t N,
                            hipStream_t st);
+hipError_t launch_add_rows(float* Y, int64_t y_stride, const float* T, int64_t t_stride, const float* R,
+                           int64_t r_stride, int64_t M, int64_t N, hipStream_t st);
 
 // Q6_K decode with the weight rows staged in LDS by direct-to-LDS loads (K/256 even,
 // w_row_bytes % 4 == 0); hipErrorNotSupported otherwise (nothing launched).
@@ -54,22 +59,26 @@ hipError_t launch_silu_mul(float* Y, int64_t y_stride, const float* U, int64_t u
 // K <= 16384, row stride a multiple of 4 bytes); hipErrorNotSupported otherwise.
 hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                   hipStream_t st);
+                                   hipStream_t st, const float* R = nullptr,
+                                   int64_t r_stride = 0);
 hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                                  const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                 int64_t sums_n_stride, hipStream_t st);
+                                 int64_t sums_n_stride, hipStream_t st, const float* R = nullptr,
+                                 int64_t r_stride = 0);
 
 // Decode with the activation quantization fused in (X fp32, no workspace): one launch per
 // 8 rows of M. hipErrorNotSupported: the caller quantizes and uses launch_gemv.
 hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
                                int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                               hipStream_t st);
+                               hipStream_t st, const float* R = nullptr,
+                                   int64_t r_stride = 0);
 
 // Q8_0 decode with the Q8_0 activation quantization fused in (K % 64 == 0, row stride a
 // multiple of 4 bytes, M*K*9/8 bytes of LDS per 8-row tile); hipErrorNotSupported otherwise.
 hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
                                     int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                    hipStream_t st);
+                                    hipStream_t st, const float* R = nullptr,
+                                   int64_t r_stride = 0);
 
 // Q8_0 prefill: LDS-staged 128 x 128 int8-MFMA tiles (K % 128 == 0, w_row_bytes % 4 == 0);
 // hipErrorNotSupported otherwise (nothing launched).

@@ -132,6 +132,24 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
                   const void* workspace, size_t workspace_bytes, int64_t M, float* Y,
                   size_t y_stride_bytes, int path, void* stream);
 
+/* ---- a projection and its residual or bias ----
+ * Y[m][n] = (sum_k W[n][k] x[m][k]) + R[m][n], one fp32 add per element after dcq_mul_mat's
+ * product: the reference's residual connections cur = ggml_add(mul_mat(wo, .), inpL) and
+ * ggml_add(mul_mat(w2, .), inpFF) (core/src/inference.cpp:1763-1764, 1799-1800), and the
+ * projection biases bq/bk/bv/bo (core/src/inference.cpp:1133-1151, 1760-1761). Y equals
+ * dcq_mul_mat's output plus R bit for bit. r_stride_bytes 0 broadcasts one bias row of N
+ * floats; otherwise it is >= N*4. R may be Y itself (r_stride_bytes == y_stride_bytes: the
+ * in-place residual) or must not overlap Y. R 4-byte aligned, strides multiples of 4; the rest
+ * as dcq_mul_mat. At M <= 8 the add is the fused decode kernel's store; otherwise the product
+ * goes to Y (or, when R is Y, a workspace temporary) and one add kernel follows. workspace may
+ * be NULL; otherwise it must hold dcq_mul_mat_add_workspace_size(wtype, M, N, K) bytes,
+ * 256-byte aligned. */
+size_t dcq_mul_mat_add_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
+int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes,
+                    const float* X, int64_t M, size_t x_stride_bytes, const float* R,
+                    size_t r_stride_bytes, float* Y, size_t y_stride_bytes, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 /* ---- the SwiGLU gate/up pair ----
  * Y[m][n] = silu(sum_k Wg[n][k] x[m][k]) * (sum_k Wu[n][k] x[m][k]), silu(g) = g / (1 + e^-g):
  * the reference FFN's w1 = mul_mat(W1, x), w3 = mul_mat(W3, x), ggml_mul(ggml_silu(w1), w3)

@@ -129,6 +129,32 @@ def test_ffn_gate_up_workspace_and_validation():
         assert ffn() == NO_DEVICE
 
 
+def test_mul_mat_add_workspace_and_validation():
+    """Projection + residual/bias: R is Y itself (same stride) or disjoint from Y's extent;
+    a zero R stride broadcasts a bias row. Errors come back before any device call."""
+    L = dc.lib()
+    assert dc.mul_mat_add_workspace_size(8, 64, 100, 1024) == dc.mul_mat_workspace_size(8, 64, 1024) + 25600
+    assert dc.mul_mat_add_workspace_size(12, 1, 16, 100) == 0
+
+    def mma(R=0x8000, rs=64, Y=0x3000, ys=64, M=2, N=16, K=256, ws=None, wsb=0):
+        return L.dcq_mul_mat_add(12, 0x1000, N, K, dc.row_size(12, K), 0x2000, M, K * 4, R, rs, Y, ys, ws, wsb,
+                                 None)
+    assert mma(R=None) == INVALID
+    assert mma(rs=32) == INVALID                 # a residual row shorter than N
+    assert mma(R=0x8002) == MISALIGNED
+    assert mma(rs=66) == MISALIGNED
+    assert mma(R=0x3000, rs=128) == INVALID      # R is Y with another stride
+    assert mma(R=0x3040 - 4, rs=64) == INVALID   # R starts inside Y
+    assert mma(R=0x3000 - 64, rs=64) == INVALID  # R's second row overlaps Y's first
+    assert mma(R=0x3000 - 64, rs=0) != INVALID   # one bias row just below Y
+    assert mma(ws=0x4000, wsb=16) == WORKSPACE
+    import torch
+    if not torch.cuda.is_available():
+        assert mma() == NO_DEVICE
+        assert mma(R=0x3000, rs=64) == NO_DEVICE  # in place
+        assert mma(rs=0) == NO_DEVICE             # bias broadcast
+
+
 def test_binding_raises_on_error():
     with pytest.raises(dc.DcqError):
         dc._lib._check("dcq_mul_mat", MISALIGNED)

@@ -70,6 +70,20 @@ def test_gate_up_graph_replays(dev):
                                           stream=torch.cuda.current_stream().cuda_stream), [y])
 
 
+@pytest.mark.parametrize("wt,M,N,K", [(Q4_K, 1, 2560, 9728), (Q6_K, 1, 2560, 9728), (Q8_0, 64, 256, 1024)])
+def test_mul_mat_add_graph_replays(dev, wt, M, N, K):
+    """Projection + residual in a graph: the fused store epilogue and the add kernel after."""
+    import torch
+    w = torch.from_numpy(synth.normal(N * K, 14, 0.0, 0.02).reshape(N, K)).to(dev)
+    wq = dc.quantize_weights(wt, w)
+    x = torch.from_numpy(synth.normal(M * K, 15).reshape(M, K)).to(dev)
+    r = torch.from_numpy(synth.normal(M * N, 16).reshape(M, N)).to(dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ws = torch.empty(dc.mul_mat_add_workspace_size(wt, M, N, K), dtype=torch.uint8, device=dev)
+    _replays_match(lambda: dc.mul_mat_add(wt, wq, N, K, x, r, y=y, workspace=ws,
+                                          stream=torch.cuda.current_stream().cuda_stream), [y])
+
+
 @pytest.mark.parametrize("ct,n,n_past", [(Q8_0, 1, 4095), (1, 1, 1000), (Q8_0, 9, 300)])
 def test_kv_attention_and_write_graph_replays(dev, ct, n, n_past):
     """Decode (key splits + combine) and a small prefill; the write is captured too (it writes

@@ -361,3 +361,54 @@ def test_concatenated_projections_one_call(O, dev, tmp_path, wt):
             y_ref, l1 = O.mul_mat(wt, wq, x)
             O.assert_close(y[:, r0:r0 + n], y_ref, l1, RTOL, what=f"{name} slice, M={M}")
             r0 += n
+
+
+# ---------------------------------------------------------------- projection + residual / bias
+# The shapes cover every kernel family the add rides on: the fused Q4_K (5-wave and 4-wave
+# launches, several rows), Q8_0 and Q6_K decode kernels (add in the store), the Q6_K decode that
+# quantizes first (K > 4096) and the batched / prefill MFMA kernels (add kernel after).
+MUL_MAT_ADD = [(Q4_K, 1, 2560, 9728), (Q4_K, 1, 97, 2560), (Q4_K, 5, 40, 1024), (Q8_0, 1, 1024, 2048),
+               (Q8_0, 3, 41, 2048), (Q6_K, 1, 1024, 2560), (Q6_K, 1, 2560, 9728), (Q6_K, 2, 70, 4096),
+               (Q4_K, 64, 96, 512), (Q8_0, 130, 64, 1024), (Q6_K, 9, 33, 512)]
+
+
+@pytest.mark.parametrize("mode", ["residual", "in_place", "bias"])
+@pytest.mark.parametrize("wt,M,N,K", MUL_MAT_ADD)
+def test_mul_mat_add(O, dev, wt, M, N, K, mode):
+    """dcq_mul_mat_add = the same call's dcq_mul_mat output + R, one float32 add per element,
+    bit for bit (the reference's ggml_add on the projection); the product itself within the
+    oracle's tolerance. R is a separate [M, N] residual, Y itself, or a broadcast [N] bias."""
+    import torch
+    wq, x = make_inputs(O, wt, M, N, K, seed=71 + M + N, outliers=1)
+    r = synth.normal((1 if mode == "bias" else M) * N, 72 + M, 0.0, 3.0).reshape(-1, N)
+    wd, xd = to_dev(wq, dev), to_dev(x, dev)
+    y_mm = to_host(dc.mul_mat(wt, wd, N, K, xd))
+    y_ref, l1 = O.mul_mat(wt, wq, x)
+    O.assert_close(y_mm, y_ref, l1, RTOL, what=f"product type {wt} M{M} N{N} K{K}")
+    want = (y_mm + r).astype(np.float32)  # float32 + float32, rounded once
+    for ws in (None, torch.empty(dc.mul_mat_add_workspace_size(wt, M, N, K), dtype=torch.uint8, device=dev)):
+        if mode == "in_place":
+            y = to_dev(r, dev)
+            dc.mul_mat_add(wt, wd, N, K, xd, y, y=y, workspace=ws)
+        elif mode == "bias":
+            y = dc.mul_mat_add(wt, wd, N, K, xd, to_dev(r[0], dev), workspace=ws)
+        else:
+            y = dc.mul_mat_add(wt, wd, N, K, xd, to_dev(r, dev), workspace=ws)
+        got = to_host(y)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+            f"{mode} type {wt} M{M} N{N} K{K} workspace={ws is not None}"
+
+
+def test_mul_mat_add_strided_residual(O, dev):
+    """Residual and output rows inside wider buffers: nothing written past each output row."""
+    import torch
+    wt, M, N, K = Q4_K, 3, 45, 512
+    wq, x = make_inputs(O, wt, M, N, K, seed=80)
+    wd, xd = to_dev(wq, dev), to_dev(x, dev)
+    y_mm = to_host(dc.mul_mat(wt, wd, N, K, xd))
+    rbig = synth.normal(M * (N + 7), 81).reshape(M, N + 7)
+    ybig = torch.full((M, N + 3), -7.0, dtype=torch.float32, device=dev)
+    dc.mul_mat_add(wt, wd, N, K, xd, to_dev(rbig, dev)[:, :N], y=ybig[:, :N])
+    yb = to_host(ybig)
+    assert np.array_equal(yb[:, :N], (y_mm + rbig[:, :N]).astype(np.float32))
+    assert np.all(yb[:, N:] == -7.0)
