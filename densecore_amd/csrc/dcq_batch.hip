@@ -14,9 +14,11 @@
 //     only this wave reads the region), 16-byte slots XOR-swizzled by row % 16;
 //   - loads its weight fragments (row = lane % 32, 16 nibble bytes per 32-element
 //     sub-block half, plus the 16-byte header) into registers;
-//   - runs v_mfma_i32_32x32x32_i8 per 32-element sub-block j: I_j (weight nibbles) and
-//     the mins term (a weight operand whose bytes all equal m_j, so the MFMA yields
-//     m_j * S_j); the 6-bit scale is applied to the exact I_j with v_mad_i32_i24;
+//   - runs v_mfma_i32_32x32x32_i8 per 32-element sub-block j, accumulating over the
+//     superblock's eight: sum_j sc_j I_j as two MFMAs on the nibbles pre-multiplied by the
+//     two halves of the 6-bit scale (sc = 8 sc_hi + sc_lo, each product <= 105 fits int8),
+//     and the mins term (a weight operand whose bytes all equal m_j, so the MFMA yields
+//     m_j * S_j);
 //   - per superblock: acc += dA * (d * sum_j sc_j I_j - dmin * sum_j m_j S_j)
 //     (vec_dot_q4_K_q8_K's per-superblock form).
 // The 8 partial tiles are summed in wave order through LDS at the end (deterministic), each
@@ -32,6 +34,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int kWaves = 8;
@@ -112,43 +115,53 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
         const uint32_t scw[2] = {s0 & 0x3F3F3F3Fu, (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u)};
         const uint32_t mnw[2] = {s1 & 0x3F3F3F3Fu, ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u)};
         const float d = half_bits_to_float(hdr.x & 0xFFFFu), dmin = half_bits_to_float(hdr.x >> 16);
-        // weight operands of the 8 sub-blocks, shared by both m-tiles: nibbles, 6-bit scale and
-        // min (the mins operand, every byte m_j, is rebuilt per use: it would hold 32 registers)
-        v4i bv[8];
-        int sc[8], mn[8];
+        // weight operands of the 8 sub-blocks, shared by both m-tiles. The 6-bit scale is split
+        // as sc = 8 sc_hi + sc_lo (both <= 7), so sc_hi * q and sc_lo * q (<= 105) are int8
+        // operands and sum_j sc_j I_j = 8 sum_j I_j(sc_hi q) + sum_j I_j(sc_lo q) accumulates
+        // inside the MFMA over all eight sub-blocks. The products are formed per byte by a
+        // packed 16-bit multiply (no byte carries into the next: 15 * 7 < 256). The mins operand
+        // (every byte m_j) is rebuilt per use: it would hold 32 registers.
+        v4i bhi[8], blo[8];
+        int mn[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const uint4 q = qw[j >> 1];
             const uint32_t sh = (j & 1) ? 4u : 0u;
-            bv[j].x = (int)((q.x >> sh) & 0x0F0F0F0Fu);
-            bv[j].y = (int)((q.y >> sh) & 0x0F0F0F0Fu);
-            bv[j].z = (int)((q.z >> sh) & 0x0F0F0F0Fu);
-            bv[j].w = (int)((q.w >> sh) & 0x0F0F0F0Fu);
-            sc[j] = (int)((scw[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+            const int sc = (int)((scw[j >> 2] >> (8 * (j & 3))) & 0xFFu);
+            const u16x2 s_hi = {(uint16_t)(sc >> 3), (uint16_t)(sc >> 3)};
+            const u16x2 s_lo = {(uint16_t)(sc & 7), (uint16_t)(sc & 7)};
+            const uint32_t nib[4] = {(q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu, (q.z >> sh) & 0x0F0F0F0Fu,
+                                     (q.w >> sh) & 0x0F0F0F0Fu};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const u16x2 b = __builtin_bit_cast(u16x2, nib[e]);
+                bhi[j][e] = __builtin_bit_cast(int, (u16x2)(b * s_hi));
+                blo[j][e] = __builtin_bit_cast(int, (u16x2)(b * s_lo));
+            }
             mn[j] = (int)(((mnw[j >> 2] >> (8 * (j & 3))) & 0xFFu) * 0x01010101u);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            v16i ai, amin;
+            v16i ahi, alo, amin;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                ai[v] = 0;
+                ahi[v] = 0;
+                alo[v] = 0;
                 amin[v] = 0;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 // activation fragment: rows 32i + col, k = 32j + 16hl .. +16 (logical slot 2j + hl)
                 const v4i av = *reinterpret_cast<const v4i*>(a_lds + aswz(32 * i + col, 2 * j + hl));
-                v16i zero;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) zero[v] = 0;
                 v4i bm;
                 bm.x = bm.y = bm.z = bm.w = mn[j];
-                const v16i I = mfma32(av, bv[j], zero);
+                ahi = mfma32(av, bhi[j], ahi);
+                alo = mfma32(av, blo[j], alo);
                 amin = mfma32(av, bm, amin);
-#pragma unroll
-                for (int v = 0; v < 16; ++v) ai[v] = __mul24(sc[j], I[v]) + ai[v];
             }
+            v16i ai;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) ai[v] = (ahi[v] << 3) + alo[v];
             // lane owns weight row n = n0 + col and activation rows m_v = 32i + 8(v/4) + 4hl + v%4
 #pragma unroll
             for (int q = 0; q < 4; ++q) {

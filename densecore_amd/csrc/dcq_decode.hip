@@ -352,6 +352,18 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
 }
 
 // ------------------------------------------------------------------ dispatch
+// compute units of the current device, cached per device (idempotent writes)
+int cu_count() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        hipDeviceProp_t p;
+        cus[dev] = hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+    }
+    return cus[dev];
+}
+
 namespace {
 
 using DecodeFn = void (*)(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, int, const float*, int64_t,
@@ -456,16 +468,6 @@ int choose_shape(int nsb) {
 struct Launch {
     int idx, nw;
 };
-int cu_count() {
-    static int cus[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
-        hipDeviceProp_t p;
-        cus[dev] = hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
-    }
-    return cus[dev];
-}
 Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
     const int forced = env_int("DCQ_Q4K_SHAPE", -1);
     if (forced >= 0) return {choose_shape(nsb), env_int("DCQ_Q4K_NW", 4) == 5 ? 5 : 4};

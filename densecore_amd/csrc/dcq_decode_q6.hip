@@ -320,20 +320,30 @@ using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8
                       int64_t, const float*, int64_t, int, float*, int64_t, int32_t*, int64_t, const float*,
                       int64_t);
 
-// fused activation: M <= 2 rows, nsb <= 64: at most 8 staging passes
-constexpr int kFuseMaxQc = 8;
-template <int MT, bool DUMP, int QC>
+// fused activation: M <= 2 rows, nsb <= 64: at most 8 staging passes of 16 (superblock, row)
+// pairs per wave with 4 waves, 4 with 8..12 waves
+template <int MT, bool DUMP, int NW, int QC>
 Q6Fn q6_fused_qc(int qc) {
-    if constexpr (QC > kFuseMaxQc) {
+    if constexpr (QC > 32 / NW) {
         return nullptr;
     } else {
-        if (qc == QC) return decode_q6k_lds_kernel<MT, DUMP, true, QC>;
-        return q6_fused_qc<MT, DUMP, QC + 1>(qc);
+        if (qc == QC) return decode_q6k_lds_kernel<MT, DUMP, true, QC, NW>;
+        return q6_fused_qc<MT, DUMP, NW, QC + 1>(qc);
     }
 }
+template <bool DUMP, int NW>
+Q6Fn q6_fused_nw(int mt, int qc) {
+    return mt == 1 ? q6_fused_qc<1, DUMP, NW, 1>(qc) : mt == 2 ? q6_fused_qc<2, DUMP, NW, 1>(qc) : nullptr;
+}
 template <bool DUMP>
-Q6Fn q6_pick_fused(int mt, int qc) {
-    return mt == 1 ? q6_fused_qc<1, DUMP, 1>(qc) : mt == 2 ? q6_fused_qc<2, DUMP, 1>(qc) : nullptr;
+Q6Fn q6_pick_fused(int mt, int qc, int nw) {
+    switch (nw) {
+        case 4: return q6_fused_nw<DUMP, 4>(mt, qc);
+        case 8: return q6_fused_nw<DUMP, 8>(mt, qc);
+        case 10: return q6_fused_nw<DUMP, 10>(mt, qc);
+        case 12: return q6_fused_nw<DUMP, 12>(mt, qc);
+        default: return nullptr;
+    }
 }
 
 template <bool DUMP>
@@ -380,18 +390,27 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                    hipStream_t st, const float* R, int64_t r_stride) {
     const int nsb = (int)(K / 256);
-    // measured (M = 1): fusing wins up to K = 4096 (2560 x 4096: 5.7 vs 7.2 us; 1024 x 2560: 3.8
-    // vs 5.8 us) and loses at K = 9728 (11.6 vs 10.3 us), where each of the 640 workgroups
-    // re-reads and re-quantizes 39 KB of X; DCQ_Q6K_FUSE_MAX_NSB overrides the limit (tuning)
-    const int fuse_max_nsb = env_int("DCQ_Q6K_FUSE_MAX_NSB", 16);
-    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || nsb > fuse_max_nsb || M > 2)
-        return hipErrorNotSupported;
+    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || M > 2) return hipErrorNotSupported;
     if (env_int("DCQ_Q6K_LDS_OFF", 0) || env_int("DCQ_Q6K_NO_FUSE", 0)) return hipErrorNotSupported;
-    constexpr int kWaves = 4;
+    // Workgroup width (one row per wave). Up to K = 4096, 4 waves (measured at M = 1 against
+    // quantize + decode: 2560 x 4096 5.7 vs 7.2 us; 1024 x 2560 3.8 vs 5.8 us). Beyond, every
+    // workgroup re-reads and re-quantizes the whole activation (39 KB at K = 9728: 4-wave
+    // workgroups 12.3 us against 10.5 us unfused), so a workgroup takes all rows of its CU
+    // instead, 8 to 12 waves, one workgroup per CU (2560 x 9728: 10 waves 9.3 us, 12 waves
+    // 9.5 us). Outside 8..12 rows per CU the separate quantize kernel stays.
+    int nw = 4;
+    if (nsb > 16) {
+        const int cus = cu_count();
+        const int64_t per_cu = (N + cus - 1) / cus;
+        if (per_cu < 8 || per_cu > 12) return hipErrorNotSupported;
+        nw = per_cu <= 8 ? 8 : per_cu <= 10 ? 10 : 12;
+    }
+    nw = env_int("DCQ_Q6K_FUSE_NW", nw);  // tuning override: 4, 8, 10 or 12
+    const int kWaves = nw;
     const int mt = M == 1 ? 1 : 2;
     const int qc = (nsb * mt + 4 * kWaves - 1) / (4 * kWaves);
     if (Q6Lds(nsb, mt, kWaves).total > kMaxLds) return hipErrorNotSupported;
-    Q6Fn fn = block_sums ? q6_pick_fused<true>(mt, qc) : q6_pick_fused<false>(mt, qc);
+    Q6Fn fn = block_sums ? q6_pick_fused<true>(mt, qc, kWaves) : q6_pick_fused<false>(mt, qc, kWaves);
     if (!fn) return hipErrorNotSupported;
     const unsigned grid = (unsigned)((N + kWaves - 1) / kWaves);
     hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), Q6Lds(nsb, mt, kWaves).total, st, (const uint8_t*)W,

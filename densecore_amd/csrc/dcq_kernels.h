@@ -29,6 +29,9 @@ hipError_t launch_unpack_ggml_rows(int vdt, const void* in, int64_t in_row_bytes
 // R (optional, indexed like Y, may be Y itself): Y = W x + R, added in the store of the
 // LDS-staged Q4_K / Q6_K kernels; with R given and neither covering the shape, nothing is
 // launched and the result is hipErrorNotSupported.
+// compute units of the current device (cached per device)
+int cu_count();
+
 hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                        const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                        int64_t sums_n_stride, hipStream_t st, const float* R = nullptr, int64_t r_stride = 0);
