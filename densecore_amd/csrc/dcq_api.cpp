@@ -5,7 +5,9 @@
 // stream-ordered on the caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <array>
 #include <mutex>
+#include <stdlib.h>
 #include <string.h>
 
 #include "../../include/dcq.h"
@@ -28,6 +30,28 @@ size_t planar_bytes(int vdt, int64_t M, int64_t K, PlanarBuffers* pb, void* base
         pb->m_ld = m_ld;
     }
     return qs_b + d_b + bs_b;
+}
+
+int knob(Knob k) {
+    struct Entry {
+        const char* name;
+        int dflt;
+    };
+    static const Entry kEntries[(int)Knob::kCount] = {
+        {"DCQ_Q4K_SHAPE", -1}, {"DCQ_Q4K_NW", 4},      {"DCQ_NO_FUSE", 0},      {"DCQ_Q6K_DECODE", 0},
+        {"DCQ_Q6K_LDS_OFF", 0}, {"DCQ_Q6K_NO_FUSE", 0}, {"DCQ_Q6K_FUSE_NW", -1}, {"DCQ_Q8_SHAPE", -1},
+        {"DCQ_GEMV_GENERIC", 0}, {"DCQ_GEMV_LG", -1},
+    };
+    // read once (thread-safe static initialisation), not per call: getenv walks the environment
+    static const std::array<int, (int)Knob::kCount> values = [] {
+        std::array<int, (int)Knob::kCount> v{};
+        for (int i = 0; i < (int)Knob::kCount; ++i) {
+            const char* s = getenv(kEntries[i].name);
+            v[i] = (s && *s) ? atoi(s) : kEntries[i].dflt;
+        }
+        return v;
+    }();
+    return values[(int)k];
 }
 
 }  // namespace dcq

@@ -59,10 +59,6 @@ size_t act_lds_bytes_q8k(int MT, int64_t K) {
     return (size_t)MT * K + (size_t)MT * (K / 8) + (size_t)MT * (K / 256) * 4;
 }
 
-int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
 
 }  // namespace
 
@@ -437,7 +433,7 @@ static_assert(kNumShapes == 10, "pick_shape covers every shape");
 // whose idle superblock slots stay within a quarter of the slots; DCQ_Q4K_SHAPE=<index>
 // forces one (tuning).
 int choose_shape(int nsb) {
-    const int forced = env_int("DCQ_Q4K_SHAPE", -1);
+    const int forced = knob(Knob::Q4KShape);
     if (forced >= 0 && forced < kNumShapes && kShapes[forced].P * kShapes[forced].NS >= nsb) return forced;
     int best = -1;
     for (int pass = 0; pass < 2 && best < 0; ++pass) {
@@ -469,8 +465,8 @@ struct Launch {
     int idx, nw;
 };
 Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
-    const int forced = env_int("DCQ_Q4K_SHAPE", -1);
-    if (forced >= 0) return {choose_shape(nsb), env_int("DCQ_Q4K_NW", 4) == 5 ? 5 : 4};
+    const int forced = knob(Knob::Q4KShape);
+    if (forced >= 0) return {choose_shape(nsb), knob(Knob::Q4KWaves) == 5 ? 5 : 4};
     const int cus = cu_count();
     Launch best{choose_shape(nsb), 4};
     int64_t best_rows = INT64_MAX, best_per_cu = INT64_MAX;
@@ -549,11 +545,11 @@ hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64
 hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
                                int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                hipStream_t st, const float* R, int64_t r_stride) {
-    if (env_int("DCQ_NO_FUSE", 0)) return hipErrorNotSupported;
+    if (knob(Knob::NoFuse)) return hipErrorNotSupported;
     if (wtype == kTypeQ8_0)
         return launch_decode_fused_q8_0(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R,
                                         r_stride);
-    if (wtype == kTypeQ6_K && !env_int("DCQ_Q6K_DECODE", 0))
+    if (wtype == kTypeQ6_K && !knob(Knob::Q6KDecode))
         return launch_decode_fused_q6k(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R,
                                        r_stride);
     if (wtype != kTypeQ4_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
@@ -564,7 +560,7 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
 hipError_t launch_decode_fused_glu(int wtype, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
                                    const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
                                    hipStream_t st) {
-    if (env_int("DCQ_NO_FUSE", 0)) return hipErrorNotSupported;
+    if (knob(Knob::NoFuse)) return hipErrorNotSupported;
     if (wtype == kTypeQ8_0)
         return launch_decode_fused_q8_0_glu(Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, st);
     if (wtype != kTypeQ4_K) return hipErrorNotSupported;

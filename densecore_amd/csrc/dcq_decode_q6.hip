@@ -109,10 +109,6 @@ __device__ __forceinline__ void lds8_a2(const uint8_t* p, uint32_t (&out)[2]) {
     out[1] = align_bytes(w2, w1, sh);
 }
 
-int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
 
 // weight rows per workgroup: one per wave (kWaves, 4 at every launch)
 constexpr int kSbStep = 16;    // superblocks per step: 4 lanes each, one wave
@@ -379,7 +375,7 @@ hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0,
     // dword-granular head/tail loads: the row's bytes and its stride must be whole dwords;
     // the weight base is 16-byte aligned (checked by the C ABI)
     if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb) return hipErrorNotSupported;
-    if (env_int("DCQ_Q6K_LDS_OFF", 0)) return hipErrorNotSupported;
+    if (knob(Knob::Q6KLdsOff)) return hipErrorNotSupported;
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
@@ -405,7 +401,7 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
                                    hipStream_t st, const float* R, int64_t r_stride) {
     const int nsb = (int)(K / 256);
     if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || M > 2) return hipErrorNotSupported;
-    if (env_int("DCQ_Q6K_LDS_OFF", 0) || env_int("DCQ_Q6K_NO_FUSE", 0)) return hipErrorNotSupported;
+    if (knob(Knob::Q6KLdsOff) || knob(Knob::Q6KNoFuse)) return hipErrorNotSupported;
     // Workgroup width (one row per wave). Up to K = 4096, 4 waves (measured at M = 1 against
     // quantize + decode: 2560 x 4096 5.7 vs 7.2 us; 1024 x 2560 3.8 vs 5.8 us). Beyond, every
     // workgroup re-reads and re-quantizes the whole activation (39 KB at K = 9728: 4-wave
@@ -419,7 +415,7 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
         if (per_cu < 8 || per_cu > 12) return hipErrorNotSupported;
         nw = per_cu <= 8 ? 8 : per_cu <= 10 ? 10 : 12;
     }
-    nw = env_int("DCQ_Q6K_FUSE_NW", nw);  // tuning override: 4, 8, 10 or 12
+    if (knob(Knob::Q6KFuseWaves) > 0) nw = knob(Knob::Q6KFuseWaves);  // tuning override: 4, 8, 10 or 12
     const int kWaves = nw;
     const int mt = M == 1 ? 1 : 2;
     const int qc = (nsb * mt + 4 * kWaves - 1) / (4 * kWaves);

@@ -77,10 +77,6 @@ __host__ __device__ constexpr int q8_stage_passes(int G, int NS, int MT, int NW)
     return (MT * 2 * G * NS + 8 * NW - 1) / (8 * NW);
 }
 
-int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
 
 }  // namespace
 
@@ -268,7 +264,7 @@ DecodeQ8Fn q8_pick_shape(int idx, int mt) {
 // fewest steps whose idle pair slots stay within a quarter; then any shape that fits.
 // DCQ_Q8_SHAPE=<index> forces one (tuning).
 int choose_q8_shape(int U) {
-    const int forced = env_int("DCQ_Q8_SHAPE", -1);
+    const int forced = knob(Knob::Q8Shape);
     if (forced >= 0 && forced < kNumQ8Shapes && kQ8Shapes[forced].G * kQ8Shapes[forced].NS >= U) return forced;
     int best = -1;
     for (int pass = 0; pass < 2 && best < 0; ++pass) {

@@ -334,10 +334,6 @@ static GemvFn pick_fmt(int f, int mt, int upl) {
     }
 }
 
-static int env_int(const char* name, int dflt) {
-    const char* s = getenv(name);
-    return (s && *s) ? atoi(s) : dflt;
-}
 
 hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                        const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
@@ -345,9 +341,9 @@ hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0
     // Q6_K: weight rows staged through LDS by coalesced direct-to-LDS loads (its 2-byte aligned
     // superblocks make lane-direct loads scatter: 4x the L1 accesses of the staged form);
     // DCQ_Q6K_DECODE=1 selects the lane-direct four-lanes-per-superblock kernel instead
-    if (env_int("DCQ_GEMV_GENERIC", 0) == 0) {
+    if (knob(Knob::GemvGeneric) == 0) {
         hipError_t e = hipErrorNotSupported;
-        if (wtype == kTypeQ4_K || (wtype == kTypeQ6_K && env_int("DCQ_Q6K_DECODE", 0)))
+        if (wtype == kTypeQ4_K || (wtype == kTypeQ6_K && knob(Knob::Q6KDecode)))
             e = launch_decode_kq(wtype, W, w_row_bytes, n0, n1, K, act, M, Y, y_stride, block_sums, sums_n_stride,
                                  st, R, r_stride);
         else if (wtype == kTypeQ6_K)
@@ -367,7 +363,7 @@ hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0
     // lanes per row: smallest power of two covering the row's units (capped at a wave)
     int lg = 0;
     while ((1 << lg) < U && lg < 6) ++lg;
-    lg = env_int("DCQ_GEMV_LG", lg);
+    if (knob(Knob::GemvLanes) >= 0) lg = knob(Knob::GemvLanes);
     const int G = 1 << lg;
     const int64_t rows = n1 - n0;
     const int64_t rows_per_block = 4 * (64 / G);

@@ -32,6 +32,23 @@ hipError_t launch_unpack_ggml_rows(int vdt, const void* in, int64_t in_row_bytes
 // compute units of the current device (cached per device)
 int cu_count();
 
+// Tuning overrides for measurements, read from the environment once per process (the
+// defaults are the measured choices; -1 or 0 means "not set" as listed in dcq_api.cpp).
+enum class Knob {
+    Q4KShape,     // DCQ_Q4K_SHAPE: force a decode shape index (-1: launch rule)
+    Q4KWaves,     // DCQ_Q4K_NW: 5 for 5-wave workgroups with a forced shape (default 4)
+    NoFuse,       // DCQ_NO_FUSE: 1 disables the fused-activation decode kernels
+    Q6KDecode,    // DCQ_Q6K_DECODE: 1 selects the lane-direct Q6_K decode kernel
+    Q6KLdsOff,    // DCQ_Q6K_LDS_OFF: 1 disables the LDS-staged Q6_K kernels
+    Q6KNoFuse,    // DCQ_Q6K_NO_FUSE: 1 disables the fused Q6_K decode
+    Q6KFuseWaves, // DCQ_Q6K_FUSE_NW: force the fused Q6_K workgroup width (4, 8, 10, 12)
+    Q8Shape,      // DCQ_Q8_SHAPE: force a Q8_0 decode shape index (-1: launch rule)
+    GemvGeneric,  // DCQ_GEMV_GENERIC: 1 forces the generic GEMV kernel
+    GemvLanes,    // DCQ_GEMV_LG: log2 lanes per row of the generic GEMV (-1: rule)
+    kCount
+};
+int knob(Knob k);
+
 hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                        const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                        int64_t sums_n_stride, hipStream_t st, const float* R = nullptr, int64_t r_stride = 0);
