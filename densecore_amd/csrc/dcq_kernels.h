@@ -45,6 +45,7 @@ enum class Knob {
     Q8Shape,      // DCQ_Q8_SHAPE: force a Q8_0 decode shape index (-1: launch rule)
     GemvGeneric,  // DCQ_GEMV_GENERIC: 1 forces the generic GEMV kernel
     GemvLanes,    // DCQ_GEMV_LG: log2 lanes per row of the generic GEMV (-1: rule)
+    AttnNoMfma,   // DCQ_ATTN_NO_MFMA: 1 keeps prompts on the VALU attention kernel
     kCount
 };
 int knob(Knob k);

@@ -605,6 +605,209 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restri
     }
 }
 
+// ---------------------------------------------------------------- prompt attention on fp32 MFMA
+// For prompts (head_dim 64 or 128, query-head groups that divide into fours): a workgroup is 4
+// waves = 4 query heads of one KV head over the same 32 query tokens; it walks the keys its
+// tile sees in blocks of 32 with the online softmax in base 2 of the VALU kernel above.
+//   Per block the workgroup stages K ([key][dim]) and V transposed ([dim][key]) in LDS as fp32
+//   (Q8_0 / F16 slots decoded, the batch's own rows copied), shared by its four heads.
+//   S^T = K Q^T (keys x queries) by v_mfma_f32_32x32x2f32 over head_dim in HD/2 steps: in step
+//   s lane l supplies key l%32 and query l%32 at dim HD/2 * (l/32) + s. In the 32x32 result
+//   lane l holds S^T[8(i/4) + 4(l/32) + i%4][l%32], i = 0..15: sixteen keys of ONE query row,
+//   so the row's max and sum are the lane's own plus one exchange with the other half-wave.
+//   O^T += V^T P^T (dims x queries) in 32-dim tiles and 16 steps over the block's keys: step s
+//   takes key 8(s/4) + 4(l/32) + s%4, which is the lane's own P value i = s, so P needs no
+//   transpose and the rescale of O^T by the row's alpha is lane-local.
+// The products are fp32 and the sums fp32 (in the MFMA's order), as in the VALU kernel.
+typedef float v16f __attribute__((ext_vector_type(16)));
+constexpr int kAttnMfmaMinTokens = 64;
+
+template <int HD>
+struct __align__(16) MfmaAttnSmem {
+    static constexpr int KP = HD + 4;  // K row pitch (floats), keeps rows 16-byte aligned
+    static constexpr int VP = 36;      // V^T row pitch: 32 keys + 4
+    float k[32][KP];
+    float vt[HD][VP];
+};
+
+// E consecutive elements e0 .. e0+E-1 of a head's piece (E = 8 or 16: inside one Q8_0 block)
+template <int CT, int E>
+__device__ __forceinline__ void load_head_elems(const uint8_t* head, int e0, float (&out)[E]) {
+    if constexpr (CT == kTypeQ8_0) {
+        const uint8_t* b = head + (e0 / 32) * 34;
+        const float d = half_bits_to_float(ldu16(b));
+        const uint8_t* qs = b + 2 + (e0 % 32);  // 2-byte aligned
+        uint32_t w[E / 4];
+        if constexpr (E == 16) {
+            ld16_a2(qs, w);
+        } else {
+#pragma unroll
+            for (int j = 0; j < E / 4; ++j) w[j] = ldu16(qs + 4 * j) | (ldu16(qs + 4 * j + 2) << 16);
+        }
+#pragma unroll
+        for (int j = 0; j < E; ++j) out[j] = d * (float)(int32_t)__builtin_amdgcn_sbfe(w[j / 4], 8 * (j % 4), 8);
+    } else if constexpr (CT == kTypeF16) {
+#pragma unroll
+        for (int j = 0; j < E / 8; ++j) {
+            const uint4 h = ld16(head + 2 * e0 + 16 * j);
+            const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                out[8 * j + 2 * k] = half_bits_to_float(hw[k] & 0xFFFF);
+                out[8 * j + 2 * k + 1] = half_bits_to_float(hw[k] >> 16);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < E / 4; ++j) {
+            const float4 f = *reinterpret_cast<const float4*>(head + 4 * e0 + 16 * j);
+            out[4 * j] = f.x, out[4 * j + 1] = f.y, out[4 * j + 2] = f.z, out[4 * j + 3] = f.w;
+        }
+    }
+}
+
+template <int CT, int HD>
+__global__ void __launch_bounds__(256, 2) attn_mfma_kernel(AttnArgs a) {
+    constexpr int E = HD / 8;     // elements per staging thread
+    constexpr int HALF = HD / 2;  // steps of the score product
+    constexpr int NT = HD / 32;   // 32-dim tiles of the output
+    __shared__ MfmaAttnSmem<HD> sm;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int p = lane >> 5, c32 = lane & 31;
+    const int rep = a.n_head / a.n_head_kv, quads = rep / 4;
+    const int n_qt = (a.n_tokens + 31) / 32;
+    const int per_tile = a.n_head_kv * quads;
+    const int id = blockIdx.x;
+    const int qt = n_qt - 1 - id / per_tile;  // the tiles that see the most keys go first
+    const int grp = id % per_tile;
+    const int h_kv = grp / quads;
+    const int h = h_kv * rep + (grp % quads) * 4 + wave;
+    const int i0 = qt * 32;
+    const int iq = i0 + c32;  // this lane's query token
+    const bool q_ok = iq < a.n_tokens;
+    const int64_t hb = head_bytes<CT>(HD);
+
+    // the lane's query row at dims HALF*p .. HALF*p + HALF - 1, pre-scaled to base-2 scores
+    float qr[HALF];
+    {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + (int64_t)(q_ok ? iq : 0) * a.q_stride +
+                                                           (int64_t)h * HD + HALF * p);
+#pragma unroll
+        for (int j = 0; j < HALF / 4; ++j) {
+            const float4 v = qp[j];
+            qr[4 * j] = q_ok ? v.x * a.scale_log2e : 0.0f;
+            qr[4 * j + 1] = q_ok ? v.y * a.scale_log2e : 0.0f;
+            qr[4 * j + 2] = q_ok ? v.z * a.scale_log2e : 0.0f;
+            qr[4 * j + 3] = q_ok ? v.w * a.scale_log2e : 0.0f;
+        }
+    }
+    v16f o[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[t][v] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // keys 0 .. n_past + last token are visible to some row of the tile
+    const int last_tok = min(i0 + 31, a.n_tokens - 1);
+    const int nblk = (a.n_past + last_tok + 1 + 31) / 32;
+    const int skey = tid & 31, se0 = E * (tid >> 5);  // staging: one key, E elements
+    for (int bi = 0; bi < nblk; ++bi) {
+        const int kb = 32 * bi;
+        // ---- stage the block's K and V^T: history slots (missing blocks read as zeros), the
+        // batch's own fp32 rows, zeros past the last key
+        {
+            const int kk = kb + skey;
+            float kv[E], vv[E];
+#pragma unroll
+            for (int j = 0; j < E; ++j) kv[j] = vv[j] = 0.0f;
+            if (kk < a.n_past) {
+                const int lb = kk / kKvBlock;
+                const int blk = lb < a.n_table ? a.table[lb] : -1;
+                if (blk >= 0 && blk < a.n_blocks) {
+                    const int64_t off = (((int64_t)blk * a.n_layer + a.layer) * kKvBlock + kk % kKvBlock) * a.sb +
+                                        (int64_t)h_kv * hb;
+                    load_head_elems<CT, E>(a.k_arena + off, se0, kv);
+                    load_head_elems<CT, E>(a.v_arena + off, se0, vv);
+                }
+            } else if (kk < a.n_past + a.n_tokens) {
+                const int64_t off = ((int64_t)(kk - a.n_past) * a.kv_stride + (int64_t)h_kv * HD) * 4;
+                load_head_elems<kTypeF32, E>(reinterpret_cast<const uint8_t*>(a.k_cur) + off, se0, kv);
+                load_head_elems<kTypeF32, E>(reinterpret_cast<const uint8_t*>(a.v_cur) + off, se0, vv);
+            }
+#pragma unroll
+            for (int j = 0; j < E; j += 4)
+                *reinterpret_cast<float4*>(&sm.k[skey][se0 + j]) = make_float4(kv[j], kv[j + 1], kv[j + 2], kv[j + 3]);
+#pragma unroll
+            for (int j = 0; j < E; ++j) sm.vt[se0 + j][skey] = vv[j];
+        }
+        __syncthreads();
+
+        // ---- S^T = K Q^T
+        v16f sc;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sc[v] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < HALF / 16; ++c) {
+            float kr[16];
+            const float4* kp = reinterpret_cast<const float4*>(&sm.k[c32][HALF * p + 16 * c]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = kp[j];
+                kr[4 * j] = v.x, kr[4 * j + 1] = v.y, kr[4 * j + 2] = v.z, kr[4 * j + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[j], qr[16 * c + j], sc, 0, 0, 0);
+        }
+
+        // ---- causal mask and the online softmax of row iq
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kk = kb + 8 * (i >> 2) + 4 * p + (i & 3);
+            sc[i] = kk <= a.n_past + iq ? sc[i] : -INFINITY;
+            mx = fmaxf(mx, sc[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run - m_new);
+        float pv[16], ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            pv[i] = m_new == -INFINITY ? 0.0f : exp2f(sc[i] - m_new);
+            ls += pv[i];
+        }
+        ls += __shfl_xor(ls, 32, 64);
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+
+        // ---- O^T = alpha O^T + V^T P^T
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[t][v] *= alpha;
+            float vr[16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = *reinterpret_cast<const float4*>(&sm.vt[32 * t + c32][8 * j + 4 * p]);
+                vr[4 * j] = v.x, vr[4 * j + 1] = v.y, vr[4 * j + 2] = v.z, vr[4 * j + 3] = v.w;
+            }
+#pragma unroll
+            for (int st = 0; st < 16; ++st) o[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr[st], pv[st], o[t], 0, 0, 0);
+        }
+        __syncthreads();  // the next block overwrites the staging
+    }
+
+    // ---- the lane's query row: dims 32t + 8(v/4) + 4p + v%4 of O^T / l
+    if (q_ok) {
+        float* orow = a.out + (int64_t)iq * a.out_stride + (int64_t)h * HD;
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) orow[32 * t + 8 * (v >> 2) + 4 * p + (v & 3)] = o[t][v] / l_run;
+    }
+}
+
 // ---------------------------------------------------------------- launchers
 hipError_t launch_kv_write(int ct, void* arena, int n_blocks, int n_layer, int layer, int64_t row_elems, int64_t sb,
                            const int32_t* table, int pos0, const float* src, int64_t src_stride, int n_tokens,
@@ -658,7 +861,16 @@ static AttnPlan attn_plan(int hd, int n_head, int n_head_kv, int n_tokens, int n
     return p;
 }
 
+// Prompts take the MFMA kernel (no key splits, no workspace): head_dim 64 or 128, query-head
+// groups that divide into fours, and enough query tiles.
+static bool attn_use_mfma(int hd, int n_head, int n_head_kv, int n_tokens, int n_past) {
+    (void)n_past;
+    return (hd == 64 || hd == 128) && (n_head / n_head_kv) % 4 == 0 && n_tokens >= kAttnMfmaMinTokens &&
+           knob(Knob::AttnNoMfma) == 0;
+}
+
 size_t attn_workspace_bytes(int hd, int n_head, int n_head_kv, int n_tokens, int n_past) {
+    if (attn_use_mfma(hd, n_head, n_head_kv, n_tokens, n_past)) return 0;
     const AttnPlan p = attn_plan(hd, n_head, n_head_kv, n_tokens, n_past);
     if (p.splits <= 1) return 0;
     const size_t rows = (size_t)p.splits * n_tokens * n_head;
@@ -678,6 +890,7 @@ hipError_t launch_kv_attention(int ct, const void* k_arena, const void* v_arena,
                                const float* q, int64_t q_stride, const float* k_cur, const float* v_cur,
                                int64_t kv_stride, int n_tokens, int n_past, float scale, float* out,
                                int64_t out_stride, void* ws, size_t ws_bytes, hipStream_t st) {
+    const bool mfma = attn_use_mfma(hd, n_head, n_head_kv, n_tokens, n_past);
     const AttnPlan p = attn_plan(hd, n_head, n_head_kv, n_tokens, n_past);
     if (ws_bytes < attn_workspace_bytes(hd, n_head, n_head_kv, n_tokens, n_past)) return hipErrorInvalidValue;
     AttnArgs a{};
@@ -691,6 +904,23 @@ hipError_t launch_kv_attention(int ct, const void* k_arena, const void* v_arena,
     a.hpw = p.hpw, a.nq = p.nq, a.nch_hist = p.nch_hist, a.nch_total = p.nch_total, a.cps = p.cps;
     a.splits = p.splits, a.groups = p.groups;
     a.scale_log2e = scale * 1.4426950408889634f;
+    if (mfma) {
+        const int64_t wgs = (int64_t)((n_tokens + 31) / 32) * n_head / 4;
+        const dim3 grid((unsigned)wgs);
+#define DCQ_ATTN_MFMA_CASE(C, H)                                                  \
+    if (ct == C && hd == H) {                                                     \
+        hipLaunchKernelGGL((attn_mfma_kernel<C, H>), grid, dim3(256), 0, st, a); \
+    } else
+        DCQ_ATTN_MFMA_CASE(kTypeQ8_0, 128)
+        DCQ_ATTN_MFMA_CASE(kTypeQ8_0, 64)
+        DCQ_ATTN_MFMA_CASE(kTypeF16, 128)
+        DCQ_ATTN_MFMA_CASE(kTypeF16, 64)
+        DCQ_ATTN_MFMA_CASE(kTypeF32, 128)
+        DCQ_ATTN_MFMA_CASE(kTypeF32, 64)
+        return hipErrorNotSupported;
+#undef DCQ_ATTN_MFMA_CASE
+        return hipGetLastError();
+    }
     if (p.splits > 1) {
         const size_t rows = (size_t)p.splits * n_tokens * n_head;
         a.ws_o = static_cast<float*>(ws);

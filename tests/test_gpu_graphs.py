@@ -84,7 +84,7 @@ def test_mul_mat_add_graph_replays(dev, wt, M, N, K):
                                           stream=torch.cuda.current_stream().cuda_stream), [y])
 
 
-@pytest.mark.parametrize("ct,n,n_past", [(Q8_0, 1, 4095), (1, 1, 1000), (Q8_0, 9, 300)])
+@pytest.mark.parametrize("ct,n,n_past", [(Q8_0, 1, 4095), (1, 1, 1000), (Q8_0, 9, 300), (Q8_0, 64, 100)])
 def test_kv_attention_and_write_graph_replays(dev, ct, n, n_past):
     """Decode (key splits + combine) and a small prefill; the write is captured too (it writes
     the same bytes on every replay)."""

@@ -95,6 +95,14 @@ ATTN = [
     (F16, 5, 33, 16, 4, 64),
     (F32, 1, 200, 8, 2, 128),
     (F32, 17, 40, 4, 2, 256),
+    # prompts on the MFMA kernel (>= 64 tokens, query-head groups of 4k): two exact 32-token
+    # tiles; a ragged last tile over a history that is not a multiple of 32 keys; head_dim 64
+    # with 8 query heads per KV head; one KV head; a Qwen3-4B-sized prompt chunk
+    (Q8_0, 64, 0, 32, 8, 128),
+    (Q8_0, 100, 37, 8, 2, 128),
+    (F16, 96, 50, 16, 2, 64),
+    (F32, 70, 20, 4, 1, 128),
+    (Q8_0, 256, 300, 32, 8, 128),
 ]
 
 
@@ -129,10 +137,11 @@ def test_kv_attention(KV, dev, ct, n, n_past, n_head, n_kv, hd):
                               what=f"attention ct={ct} n={n} n_past={n_past} heads={n_head}/{n_kv} hd={hd}")
 
 
-def test_kv_attention_missing_blocks_read_as_zero_keys(KV, dev):
+@pytest.mark.parametrize("n", [2, 80])  # the VALU kernel with key splits; the MFMA prompt kernel
+def test_kv_attention_missing_blocks_read_as_zero_keys(KV, dev, n):
     """A history block absent from the table (-1, or past the table's end) is a zero K/V row,
     as in the reference's gathered K_all: score 0, value 0."""
-    ct, n, n_past, n_head, n_kv, hd, n_layer = Q8_0, 2, 90, 8, 2, 128, 1
+    ct, n_past, n_head, n_kv, hd, n_layer = Q8_0, 90, 8, 2, 128, 1
     row = n_kv * hd
     n_blocks = 8
     sb = KV.slot_bytes(ct, row)
