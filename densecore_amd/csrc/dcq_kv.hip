@@ -605,6 +605,33 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restri
     }
 }
 
+// Few splits over many rows (prompts): one thread per output element, the splits' loads issued
+// together (S <= 16), merged in split order like attn_combine_kernel's groups.
+template <int S>
+__global__ void __launch_bounds__(256) attn_combine_few_kernel(const float* __restrict__ ws_o,
+                                                               const float* __restrict__ ws_ml, int splits,
+                                                               int n_tokens, int n_head, int hd,
+                                                               float* __restrict__ out, int64_t out_stride) {
+    const int64_t rows = (int64_t)n_tokens * n_head;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * hd) return;
+    const int64_t row = idx / hd;
+    const int d = (int)(idx % hd);
+    float mv[S], lv[S], ov[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int64_t r = (int64_t)s * rows + row;
+        mv[s] = s < splits ? ws_ml[2 * r] : -INFINITY;
+        lv[s] = s < splits ? ws_ml[2 * r + 1] : 0.0f;
+        ov[s] = s < splits ? ws_o[r * hd + d] : 0.0f;
+    }
+    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) merge_online(m, l, acc, mv[s], lv[s], ov[s]);
+    const int i = (int)(row / n_head), h = (int)(row % n_head);
+    out[(int64_t)i * out_stride + (int64_t)h * hd + d] = acc / l;
+}
+
 // ---------------------------------------------------------------- prompt attention on fp32 MFMA
 // For prompts (head_dim 64 or 128, query-head groups that divide into fours): a workgroup is 4
 // waves = 4 query heads of one KV head over the same 32 query tokens; it walks the keys its
@@ -620,7 +647,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restri
 //   transpose and the rescale of O^T by the row's alpha is lane-local.
 // The products are fp32 and the sums fp32 (in the MFMA's order), as in the VALU kernel.
 typedef float v16f __attribute__((ext_vector_type(16)));
-constexpr int kAttnMfmaMinTokens = 64;
+constexpr int kAttnMfmaMinTokens = 32;
 
 template <int HD>
 struct __align__(16) MfmaAttnSmem {
@@ -678,8 +705,9 @@ __global__ void __launch_bounds__(256, 2) attn_mfma_kernel(AttnArgs a) {
     const int n_qt = (a.n_tokens + 31) / 32;
     const int per_tile = a.n_head_kv * quads;
     const int id = blockIdx.x;
-    const int qt = n_qt - 1 - id / per_tile;  // the tiles that see the most keys go first
     const int grp = id % per_tile;
+    const int split = (id / per_tile) % a.splits;
+    const int qt = n_qt - 1 - id / per_tile / a.splits;  // the tiles that see the most keys go first
     const int h_kv = grp / quads;
     const int h = h_kv * rep + (grp % quads) * 4 + wave;
     const int i0 = qt * 32;
@@ -708,11 +736,13 @@ __global__ void __launch_bounds__(256, 2) attn_mfma_kernel(AttnArgs a) {
         for (int v = 0; v < 16; ++v) o[t][v] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    // keys 0 .. n_past + last token are visible to some row of the tile
+    // keys 0 .. n_past + last token are visible to some row of the tile; with key splits this
+    // workgroup takes blocks [split * cps, split * cps + cps) of them (possibly none)
     const int last_tok = min(i0 + 31, a.n_tokens - 1);
     const int nblk = (a.n_past + last_tok + 1 + 31) / 32;
+    const int b_begin = split * a.cps, b_end = min(nblk, b_begin + a.cps);
     const int skey = tid & 31, se0 = E * (tid >> 5);  // staging: one key, E elements
-    for (int bi = 0; bi < nblk; ++bi) {
+    for (int bi = b_begin; bi < b_end; ++bi) {
         const int kb = 32 * bi;
         // ---- stage the block's K and V^T: history slots (missing blocks read as zeros), the
         // batch's own fp32 rows, zeros past the last key
@@ -798,13 +828,29 @@ __global__ void __launch_bounds__(256, 2) attn_mfma_kernel(AttnArgs a) {
         __syncthreads();  // the next block overwrites the staging
     }
 
-    // ---- the lane's query row: dims 32t + 8(v/4) + 4p + v%4 of O^T / l
+    // ---- the lane's query row: dims 32t + 8(v/4) + 4p + v%4 of O^T / l, or with key splits
+    // the unnormalised sums and (m, l) for the combine kernel (m = -inf, l = 0 if no key)
     if (q_ok) {
-        float* orow = a.out + (int64_t)iq * a.out_stride + (int64_t)h * HD;
+        if (a.splits == 1) {
+            float* orow = a.out + (int64_t)iq * a.out_stride + (int64_t)h * HD;
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
+            for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) orow[32 * t + 8 * (v >> 2) + 4 * p + (v & 3)] = o[t][v] / l_run;
+                for (int v = 0; v < 16; ++v) orow[32 * t + 8 * (v >> 2) + 4 * p + (v & 3)] = o[t][v] / l_run;
+        } else {
+            const int64_t row = ((int64_t)split * a.n_tokens + iq) * a.n_head + h;
+            float* orow = a.ws_o + row * HD;
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    *reinterpret_cast<float4*>(orow + 32 * t + 8 * j + 4 * p) =
+                        make_float4(o[t][4 * j], o[t][4 * j + 1], o[t][4 * j + 2], o[t][4 * j + 3]);
+            if (p == 0) {
+                a.ws_ml[2 * row] = m_run;
+                a.ws_ml[2 * row + 1] = l_run;
+            }
+        }
     }
 }
 
@@ -861,16 +907,38 @@ static AttnPlan attn_plan(int hd, int n_head, int n_head_kv, int n_tokens, int n
     return p;
 }
 
-// Prompts take the MFMA kernel (no key splits, no workspace): head_dim 64 or 128, query-head
-// groups that divide into fours, and enough query tiles.
-static bool attn_use_mfma(int hd, int n_head, int n_head_kv, int n_tokens, int n_past) {
-    (void)n_past;
+// Prompts take the MFMA kernel: head_dim 64 or 128, query-head groups that divide into fours,
+// at least kAttnMfmaMinTokens tokens.
+static bool attn_use_mfma(int hd, int n_head, int n_head_kv, int n_tokens) {
     return (hd == 64 || hd == 128) && (n_head / n_head_kv) % 4 == 0 && n_tokens >= kAttnMfmaMinTokens &&
            knob(Knob::AttnNoMfma) == 0;
 }
 
+// Key splits of the MFMA kernel: about 512 workgroups in flight (two per CU), at least 8 key
+// blocks of 32 per split (the last query tile's count) so the combine stays small.
+struct MfmaPlan {
+    int splits, bps;  // splits, key blocks per split
+};
+static MfmaPlan attn_mfma_plan(int n_head, int n_tokens, int n_past) {
+    const int64_t base = (int64_t)((n_tokens + 31) / 32) * (n_head / 4);
+    const int nblk_max = (n_past + n_tokens + 31) / 32;
+    int want = (int)((512 + base - 1) / base);
+    const int cap = (nblk_max + 7) / 8;
+    if (want > cap) want = cap;
+    if (want < 1) want = 1;
+    MfmaPlan m;
+    m.bps = (nblk_max + want - 1) / want;
+    m.splits = (nblk_max + m.bps - 1) / m.bps;
+    return m;
+}
+
 size_t attn_workspace_bytes(int hd, int n_head, int n_head_kv, int n_tokens, int n_past) {
-    if (attn_use_mfma(hd, n_head, n_head_kv, n_tokens, n_past)) return 0;
+    if (attn_use_mfma(hd, n_head, n_head_kv, n_tokens)) {
+        const MfmaPlan m = attn_mfma_plan(n_head, n_tokens, n_past);
+        if (m.splits <= 1) return 0;
+        const size_t rows = (size_t)m.splits * n_tokens * n_head;
+        return round_up((int64_t)(rows * hd * 4), 256) + round_up((int64_t)(rows * 2 * 4), 256);
+    }
     const AttnPlan p = attn_plan(hd, n_head, n_head_kv, n_tokens, n_past);
     if (p.splits <= 1) return 0;
     const size_t rows = (size_t)p.splits * n_tokens * n_head;
@@ -890,7 +958,7 @@ hipError_t launch_kv_attention(int ct, const void* k_arena, const void* v_arena,
                                const float* q, int64_t q_stride, const float* k_cur, const float* v_cur,
                                int64_t kv_stride, int n_tokens, int n_past, float scale, float* out,
                                int64_t out_stride, void* ws, size_t ws_bytes, hipStream_t st) {
-    const bool mfma = attn_use_mfma(hd, n_head, n_head_kv, n_tokens, n_past);
+    const bool mfma = attn_use_mfma(hd, n_head, n_head_kv, n_tokens);
     const AttnPlan p = attn_plan(hd, n_head, n_head_kv, n_tokens, n_past);
     if (ws_bytes < attn_workspace_bytes(hd, n_head, n_head_kv, n_tokens, n_past)) return hipErrorInvalidValue;
     AttnArgs a{};
@@ -905,7 +973,15 @@ hipError_t launch_kv_attention(int ct, const void* k_arena, const void* v_arena,
     a.splits = p.splits, a.groups = p.groups;
     a.scale_log2e = scale * 1.4426950408889634f;
     if (mfma) {
-        const int64_t wgs = (int64_t)((n_tokens + 31) / 32) * n_head / 4;
+        const MfmaPlan m = attn_mfma_plan(n_head, n_tokens, n_past);
+        a.splits = m.splits, a.cps = m.bps;
+        if (m.splits > 1) {
+            const size_t rows = (size_t)m.splits * n_tokens * n_head;
+            a.ws_o = static_cast<float*>(ws);
+            a.ws_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + round_up((int64_t)(rows * hd * 4), 256));
+        }
+        const int64_t wgs = (int64_t)((n_tokens + 31) / 32) * (n_head / 4) * m.splits;
+        if (wgs > INT32_MAX) return hipErrorInvalidValue;
         const dim3 grid((unsigned)wgs);
 #define DCQ_ATTN_MFMA_CASE(C, H)                                                  \
     if (ct == C && hd == H) {                                                     \
@@ -919,6 +995,19 @@ hipError_t launch_kv_attention(int ct, const void* k_arena, const void* v_arena,
         DCQ_ATTN_MFMA_CASE(kTypeF32, 64)
         return hipErrorNotSupported;
 #undef DCQ_ATTN_MFMA_CASE
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || m.splits <= 1) return e;
+        const int64_t elems = (int64_t)n_tokens * n_head * hd;
+        const dim3 cgrid((unsigned)((elems + 255) / 256));
+        if (m.splits <= 4)
+            hipLaunchKernelGGL(attn_combine_few_kernel<4>, cgrid, dim3(256), 0, st, a.ws_o, a.ws_ml, m.splits,
+                               n_tokens, n_head, hd, out, out_stride);
+        else if (m.splits <= 16)
+            hipLaunchKernelGGL(attn_combine_few_kernel<16>, cgrid, dim3(256), 0, st, a.ws_o, a.ws_ml, m.splits,
+                               n_tokens, n_head, hd, out, out_stride);
+        else
+            hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)(n_tokens * n_head), (unsigned)(hd / 32)),
+                               dim3(256), 0, st, a.ws_o, a.ws_ml, m.splits, n_tokens, n_head, hd, out, out_stride);
         return hipGetLastError();
     }
     if (p.splits > 1) {

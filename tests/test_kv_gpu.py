@@ -103,6 +103,9 @@ ATTN = [
     (F16, 96, 50, 16, 2, 64),
     (F32, 70, 20, 4, 1, 128),
     (Q8_0, 256, 300, 32, 8, 128),
+    # the MFMA kernel with its keys split over workgroups (few tokens over a long history)
+    (Q8_0, 32, 700, 8, 2, 128),
+    (F16, 40, 1000, 16, 4, 64),
 ]
 
 
