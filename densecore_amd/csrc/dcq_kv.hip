@@ -707,7 +707,11 @@ __global__ void __launch_bounds__(256, 2) attn_mfma_kernel(AttnArgs a) {
     const int id = blockIdx.x;
     const int grp = id % per_tile;
     const int split = (id / per_tile) % a.splits;
-    const int qt = n_qt - 1 - id / per_tile / a.splits;  // the tiles that see the most keys go first
+    // query tiles see 1, 2, ... key blocks: the first half of the launch order takes the largest
+    // tiles, descending, the second half the smallest, ascending, so that the two workgroups a
+    // CU receives (one from each half, in dispatch order) carry about the same keys together
+    const int rank = id / per_tile / a.splits, half = (n_qt + 1) / 2;
+    const int qt = rank < half ? n_qt - 1 - rank : rank - half;
     const int h_kv = grp / quads;
     const int h = h_kv * rep + (grp % quads) * 4 + wave;
     const int i0 = qt * 32;
