@@ -512,7 +512,8 @@ def main():
                   f"({e['mul_mat_add_kernels']} kernels)", file=sys.stderr, flush=True)
         for name, kw in (("kv_attention_decode_q8_0", dict(ct=dc.TYPE_Q8_0)),
                          ("kv_attention_decode_f16", dict(ct=dc.TYPE_F16)),
-                         ("kv_attention_prefill_q8_0", dict(ct=dc.TYPE_Q8_0, n_tokens=2048, n_past=0, n_layer=2))):
+                         ("kv_attention_prefill_q8_0", dict(ct=dc.TYPE_Q8_0, n_tokens=2048, n_past=0, n_layer=2)),
+                         ("kv_attention_chunk_q8_0", dict(ct=dc.TYPE_Q8_0, n_tokens=256, n_past=4096, n_layer=2))):
             e = extras[name] = bench_kv_attention(args, dev, **kw)
             print(f"# {name}: {e['us']:.2f} us ({e['kernels']} kernels), {e['GBps']:.0f} GB/s, "
                   f"{e['TFLOPs']:.2f} TFLOP/s", file=sys.stderr, flush=True)
