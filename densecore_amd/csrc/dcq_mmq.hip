@@ -26,6 +26,12 @@
 //   Q4_K: acc_i += sc_j * I_j (v_mad_i32_i24) per 32-sub-block; the mins term
 //     sum_j m_j * S_j runs on the MFMA against a weight operand whose bytes all
 //     equal m_j; per superblock acc += dA * (d * acc_i - dmin * acc_min).
+//     The 2 x 2-tile form (large M), VALU-bound that way, moves both onto the MFMA:
+//     sum_j sc_j I_j as two accumulations over the sub-blocks against the nibbles
+//     times sc_hi and sc_lo (sc = 8 sc_hi + sc_lo, each <= 7: every product fits
+//     int8), and sum_j m_j S_j from the activation's 16-element sums: S_j = 64 hi_j +
+//     lo_j (lo_j in [0, 63], hi_j in [-64, 63]) as int8 bytes against the bytes m_j,
+//     two MFMAs per tile per superblock instead of eight.
 //   Q6_K: acc_i += sc_g * I_g per 16-group (signed q - 32 operands); per
 //     superblock acc += dA * d * acc_i.
 #include "dcq_common.h"
@@ -35,6 +41,7 @@ namespace dcq {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kMagic = 0x4B400000;  // bit pattern of 12582912.0f = 1.5 * 2^23
 constexpr float kMagicF = 12582912.0f;
@@ -156,7 +163,7 @@ __global__ void __launch_bounds__(256) mmq_q8_0_kernel(const uint8_t* __restrict
                                                        int64_t K, const int8_t* __restrict__ xqs,
                                                        const float* __restrict__ xd, int64_t m_ld, int64_t M,
                                                        float* __restrict__ Y, int64_t y_stride,
-                                                       int32_t* __restrict__ sums) {
+                                                       int32_t* __restrict__ sums, const int16_t* __restrict__ xbs) {
     extern __shared__ float lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wn = wave % WN, wk = wave / WN;
@@ -239,7 +246,8 @@ __global__ void __launch_bounds__(256) mmq_q4_K_kernel(const uint8_t* __restrict
                                                        int64_t K, const int8_t* __restrict__ xqs,
                                                        const float* __restrict__ xd, int64_t m_ld, int64_t M,
                                                        float* __restrict__ Y, int64_t y_stride,
-                                                       int32_t* __restrict__ sums) {
+                                                       int32_t* __restrict__ sums, const int16_t* __restrict__ xbs) {
+    constexpr bool kSplit = TM == 2 && TN == 2;  // see the Q4_K notes at the top
     extern __shared__ float lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wn = wave % WN, wk = wave / WN;
@@ -296,39 +304,115 @@ __global__ void __launch_bounds__(256) mmq_q4_K_kernel(const uint8_t* __restrict
             scw[j][1] = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
             mnw[j][1] = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
         }
+        // 2 x 2 tiles: the mins' activation operand of each m-tile (lanes with hl = 0 carry
+        // k' 0..15: lo_0..lo_7, hi_0..hi_7 of the superblock's S_j; the others zeros)
+        [[maybe_unused]] v4i amop[TM];
+        if constexpr (kSplit) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                int64_t m = mbase + 32 * i + col;
+                m = m < M ? m : M - 1;
+                const uint4* bp = reinterpret_cast<const uint4*>(xbs + m * (K / 16) + 16 * (int64_t)s);
+                const uint4 b0 = bp[0], b1 = bp[1];
+                const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+                uint32_t lo[2] = {0u, 0u}, hi[2] = {0u, 0u};
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int S = (int)(int16_t)(bw[jj] & 0xFFFFu) + (int)(int16_t)(bw[jj] >> 16);
+                    lo[jj >> 2] |= (uint32_t)(S & 63) << (8 * (jj & 3));
+                    hi[jj >> 2] |= ((uint32_t)(S >> 6) & 0xFFu) << (8 * (jj & 3));
+                }
+                amop[i].x = hl ? 0 : (int)lo[0];
+                amop[i].y = hl ? 0 : (int)lo[1];
+                amop[i].z = hl ? 0 : (int)hi[0];
+                amop[i].w = hl ? 0 : (int)hi[1];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             v16i ai[TM], amin[TM];
+            if constexpr (kSplit) {
+                v16i ahi[TM], alo[TM];
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    ai[i][v] = 0;
-                    amin[i][v] = 0;
+                    for (int v = 0; v < 16; ++v) ahi[i][v] = alo[i][v] = 0;
+#pragma unroll
+                for (int sub = 0; sub < 8; ++sub) {
+                    const uint4 q = qw[j][sub >> 1];
+                    const uint32_t sh = (sub & 1) ? 4u : 0u;
+                    const int sc = (int)((scw[j][sub >> 2] >> (8 * (sub & 3))) & 0xFFu);
+                    const u16x2 s_hi = {(uint16_t)(sc >> 3), (uint16_t)(sc >> 3)};
+                    const u16x2 s_lo = {(uint16_t)(sc & 7), (uint16_t)(sc & 7)};
+                    const uint32_t nib[4] = {(q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu,
+                                             (q.z >> sh) & 0x0F0F0F0Fu, (q.w >> sh) & 0x0F0F0F0Fu};
+                    v4i bhi, blo;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const u16x2 b = __builtin_bit_cast(u16x2, nib[e]);
+                        bhi[e] = __builtin_bit_cast(int, (u16x2)(b * s_hi));
+                        blo[e] = __builtin_bit_cast(int, (u16x2)(b * s_lo));
+                    }
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const v4i av = as_v4i(qa[i][sub]);
+                        ahi[i] = mfma32(av, bhi, ahi[i]);
+                        alo[i] = mfma32(av, blo, alo[i]);
+                    }
                 }
-#pragma unroll
-            for (int sub = 0; sub < 8; ++sub) {
-                const uint4 q = qw[j][sub >> 1];
-                const uint32_t sh = (sub & 1) ? 4u : 0u;
-                v4i bv;
-                bv.x = (int)((q.x >> sh) & 0x0F0F0F0Fu);
-                bv.y = (int)((q.y >> sh) & 0x0F0F0F0Fu);
-                bv.z = (int)((q.z >> sh) & 0x0F0F0F0Fu);
-                bv.w = (int)((q.w >> sh) & 0x0F0F0F0Fu);
-                const int sc = (int)((scw[j][sub >> 2] >> (8 * (sub & 3))) & 0xFFu);
-                const uint32_t mb = ((mnw[j][sub >> 2] >> (8 * (sub & 3))) & 0xFFu) * 0x01010101u;
-                v4i bm;
-                bm.x = bm.y = bm.z = bm.w = (int)mb;
+                // the mins' weight operands: bytes m_0..m_7 against lo (k' 0..7), then hi (8..15)
+                v4i bml, bmh;
+                bml.x = hl ? 0 : (int)mnw[j][0];
+                bml.y = hl ? 0 : (int)mnw[j][1];
+                bml.z = bml.w = 0;
+                bmh.x = bmh.y = 0;
+                bmh.z = hl ? 0 : (int)mnw[j][0];
+                bmh.w = hl ? 0 : (int)mnw[j][1];
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
-                    const v4i av = as_v4i(qa[i][sub]);
                     v16i zero;
 #pragma unroll
                     for (int v = 0; v < 16; ++v) zero[v] = 0;
-                    const v16i I = mfma32(av, bv, zero);
-                    amin[i] = mfma32(av, bm, amin[i]);
+                    const v16i ml = mfma32(amop[i], bml, zero);
+                    const v16i mh = mfma32(amop[i], bmh, zero);
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) ai[i][v] = __mul24(sc, I[v]) + ai[i][v];
+                    for (int v = 0; v < 16; ++v) {
+                        ai[i][v] = (ahi[i][v] << 3) + alo[i][v];
+                        amin[i][v] = ml[v] + (mh[v] << 6);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        ai[i][v] = 0;
+                        amin[i][v] = 0;
+                    }
+#pragma unroll
+                for (int sub = 0; sub < 8; ++sub) {
+                    const uint4 q = qw[j][sub >> 1];
+                    const uint32_t sh = (sub & 1) ? 4u : 0u;
+                    v4i bv;
+                    bv.x = (int)((q.x >> sh) & 0x0F0F0F0Fu);
+                    bv.y = (int)((q.y >> sh) & 0x0F0F0F0Fu);
+                    bv.z = (int)((q.z >> sh) & 0x0F0F0F0Fu);
+                    bv.w = (int)((q.w >> sh) & 0x0F0F0F0Fu);
+                    const int sc = (int)((scw[j][sub >> 2] >> (8 * (sub & 3))) & 0xFFu);
+                    const uint32_t mb = ((mnw[j][sub >> 2] >> (8 * (sub & 3))) & 0xFFu) * 0x01010101u;
+                    v4i bm;
+                    bm.x = bm.y = bm.z = bm.w = (int)mb;
+#pragma unroll
+                    for (int i = 0; i < TM; ++i) {
+                        const v4i av = as_v4i(qa[i][sub]);
+                        v16i zero;
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) zero[v] = 0;
+                        const v16i I = mfma32(av, bv, zero);
+                        amin[i] = mfma32(av, bm, amin[i]);
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) ai[i][v] = __mul24(sc, I[v]) + ai[i][v];
+                    }
                 }
             }
             const float d = half_bits_to_float(hdr[j].x & 0xFFFFu), dmin = half_bits_to_float(hdr[j].x >> 16);
@@ -365,7 +449,7 @@ __global__ void __launch_bounds__(256) mmq_q6_K_kernel(const uint8_t* __restrict
                                                        int64_t K, const int8_t* __restrict__ xqs,
                                                        const float* __restrict__ xd, int64_t m_ld, int64_t M,
                                                        float* __restrict__ Y, int64_t y_stride,
-                                                       int32_t* __restrict__ sums) {
+                                                       int32_t* __restrict__ sums, const int16_t* __restrict__ xbs) {
     extern __shared__ float lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wn = wave % WN, wk = wave / WN;
@@ -464,7 +548,7 @@ __global__ void __launch_bounds__(256) mmq_q6_K_kernel(const uint8_t* __restrict
 
 // ============================================================== dispatch
 using MmqFn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, const int8_t*, const float*, int64_t, int64_t,
-                       float*, int64_t, int32_t*);
+                       float*, int64_t, int32_t*, const int16_t*);
 
 template <int TM, int TN, int WN, int WK, bool DUMP>
 static MmqFn pick_fmt(int wtype) {
@@ -512,7 +596,7 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
     const size_t lds = s.wk > 1 ? (size_t)s.tm * s.tn * 16 * 64 * 4 * (s.wk - 1) * s.wn : 0;
     MmqFn fn = block_sums ? pick<true>(wtype, s) : pick<false>(wtype, s);
     hipLaunchKernelGGL(fn, grid, dim3(256), lds, st, (const uint8_t*)W, w_row_bytes, N, K, act.qs, act.d, act.m_ld, M,
-                       Y, y_stride, block_sums);
+                       Y, y_stride, block_sums, act.bs);
     return hipGetLastError();
 }
 

@@ -868,23 +868,27 @@ double dcqo_vec_dot_l1(int wtype, int64_t k, const void* w, const void* xq) {
             s += fabs((double)dcqo_fp16_to_fp32(x[b].d) * dcqo_fp16_to_fp32(y[b].d) * ib[b]);
         free(ib);
     } else if (wtype == DCQO_TYPE_Q4_K) {
+        /* the terms vec_dot_q4_K_q8_K adds in fp32: the eight lane sums d * aux32[l] of each
+         * superblock (they can cancel to a much smaller superblock total) and the mins term */
         const blk_q4_K* x = (const blk_q4_K*)w;
         const blk_q8_K* y = (const blk_q8_K*)xq;
-        int32_t* ib = (int32_t*)malloc(sizeof(int32_t) * (size_t)(2 * k / QK_K));
-        dcqo_block_sums(wtype, k, w, xq, ib);
         for (int64_t b = 0; b < k / QK_K; ++b) {
-            s += fabs((double)dcqo_fp16_to_fp32(x[b].d) * y[b].d * ib[2 * b]);
-            s += fabs((double)dcqo_fp16_to_fp32(x[b].dmin) * y[b].d * ib[2 * b + 1]);
+            int32_t aux32[8], mins_sum;
+            q4k_superblock_ints(&x[b], &y[b], aux32, &mins_sum);
+            const double d = (double)dcqo_fp16_to_fp32(x[b].d) * y[b].d;
+            for (int l = 0; l < 8; ++l) s += fabs(d * aux32[l]);
+            s += fabs((double)dcqo_fp16_to_fp32(x[b].dmin) * y[b].d * mins_sum);
         }
-        free(ib);
     } else if (wtype == DCQO_TYPE_Q6_K) {
+        /* the eight lane sums d * aux32[l] of each superblock, as vec_dot_q6_K_q8_K adds them */
         const blk_q6_K* x = (const blk_q6_K*)w;
         const blk_q8_K* y = (const blk_q8_K*)xq;
-        int32_t* ib = (int32_t*)malloc(sizeof(int32_t) * (size_t)(k / QK_K));
-        dcqo_block_sums(wtype, k, w, xq, ib);
-        for (int64_t b = 0; b < k / QK_K; ++b)
-            s += fabs((double)dcqo_fp16_to_fp32(x[b].d) * y[b].d * ib[b]);
-        free(ib);
+        for (int64_t b = 0; b < k / QK_K; ++b) {
+            int32_t aux32[8];
+            q6k_superblock_ints(&x[b], &y[b], aux32);
+            const double d = (double)dcqo_fp16_to_fp32(x[b].d) * y[b].d;
+            for (int l = 0; l < 8; ++l) s += fabs(d * aux32[l]);
+        }
     }
     return s;
 }

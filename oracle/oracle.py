@@ -137,6 +137,9 @@ def vec_dot_f64(wt, k, w_row, xq_row):
 
 
 def vec_dot_l1(wt, k, w_row, xq_row):
+    """Sum of the magnitudes of the fp32 terms the reference's vec_dot adds: |d_b * I_b| per
+    Q8_0 block; for Q4_K / Q6_K the eight per-superblock lane sums |d * aux32[l]| (plus the
+    Q4_K mins term), which can cancel to a much smaller superblock total."""
     w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
     xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
     return float(lib().dcqo_vec_dot_l1(wt, k, _p(w_row), _p(xq_row)))
@@ -234,8 +237,9 @@ def assert_close_gate_up(y, y_ref, parts, rtol=1e-4, what=""):
 def assert_close(y, y_ref, l1, rtol=1e-4, what=""):
     """The output tolerance: |y - y_ref| <= rtol * max(|y_ref|, L1), elementwise.
 
-    L1 = sum over blocks of |scale_b * int_b| guards outputs whose blocks cancel:
-    their fp32 rounding error scales with L1, not with |y_ref|.
+    L1 = sum of the magnitudes of the fp32 terms of the reference's summation (vec_dot_l1)
+    guards outputs whose terms cancel: their fp32 rounding error scales with L1, not with
+    |y_ref|.
     """
     y = np.asarray(y, dtype=np.float64)
     y_ref = np.asarray(y_ref, dtype=np.float64)

@@ -2,8 +2,9 @@
 
 Bars: quantized activation bytes and per-block int32 sums
 bit-exact; fp32 outputs within |y - y_ref| <= 1e-4 * max(|y_ref|, L1), where L1
-is the sum over blocks of |scale_b * int_b| (the magnitude the fp32 rounding of
-both summation orders scales with).
+is the sum of the magnitudes of the fp32 terms the reference adds (|scale_b * int_b|
+per Q8_0 block; the eight per-superblock lane sums of Q4_K / Q6_K, plus the mins term):
+the magnitude the fp32 rounding of both summation orders scales with.
 """
 import numpy as np
 import pytest
@@ -416,3 +417,24 @@ def test_mul_mat_add_strided_residual(O, dev):
     yb = to_host(ybig)
     assert np.array_equal(yb[:, :N], (y_mm + rbig[:, :N]).astype(np.float32))
     assert np.all(yb[:, N:] == -7.0)
+
+
+@pytest.mark.parametrize("wt,M,N,K", [(Q4_K, 520, 16400, 256), (Q6_K, 520, 16400, 256), (Q8_0, 30, 16400, 256)])
+def test_mul_mat_large_tiles(O, dev, wt, M, N, K):
+    """Shapes that take the large-tile kernels (64 x 256 workgroup tiles for Q4_K / Q6_K at
+    >= 512 tiles; ragged M and N): the output against the oracle, and the exact per-block
+    integer sums on a corner of rows and columns (the oracle's sums are slow at full size)."""
+    import torch
+    wq, x = make_inputs(O, wt, M, N, K, seed=90 + wt, outliers=1)
+    y_ref, l1 = O.mul_mat(wt, wq, x)
+    per = dc.block_sums_per_row(wt, K)
+    sums = torch.zeros((M, N, per), dtype=torch.int32, device=dev)
+    y = dc.mul_mat_ex(wt, to_dev(wq, dev), N, K, to_dev(x, dev), path=dc.PATH_MMQ, block_sums=sums)
+    O.assert_close(to_host(y), y_ref, l1, RTOL, what=f"large tiles type {wt} M{M} N{N} K{K}")
+    rows = np.r_[0:8, M - 8:M]
+    cols = np.r_[0:64, N - 64:N]
+    want = O.block_sums_matrix(wt, K, wq[cols], O.quantize_rows(O.vec_dot_type(wt), x[rows]))
+    got = to_host(sums)[rows][:, cols]
+    assert np.array_equal(got, want)
+    y2 = dc.mul_mat(wt, to_dev(wq, dev), N, K, to_dev(x, dev))
+    O.assert_close(to_host(y2), y_ref, l1, RTOL, what="production kernel")
