@@ -138,6 +138,23 @@ __device__ __forceinline__ float row16_max(float v) {
     v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));
     return v;
 }
+// Two independent row maxima of NON-NEGATIVE floats, interleaved step by step. Their bit
+// patterns order like the values as signed integers (a -0.0 sorts below everything, and is
+// equal to +0.0 as a float), so the steps are integer maxima: no canonicalizing of the DPP
+// operand, and each move folds into the max as its DPP source.
+__device__ __forceinline__ void row16_max2_nonneg(float& a, float& b) {
+    int ia = __float_as_int(a), ib = __float_as_int(b);
+    ia = max(ia, __builtin_amdgcn_mov_dpp(ia, 0xB1, 0xF, 0xF, false));
+    ib = max(ib, __builtin_amdgcn_mov_dpp(ib, 0xB1, 0xF, 0xF, false));
+    ia = max(ia, __builtin_amdgcn_mov_dpp(ia, 0x4E, 0xF, 0xF, false));
+    ib = max(ib, __builtin_amdgcn_mov_dpp(ib, 0x4E, 0xF, 0xF, false));
+    ia = max(ia, __builtin_amdgcn_mov_dpp(ia, 0x141, 0xF, 0xF, false));
+    ib = max(ib, __builtin_amdgcn_mov_dpp(ib, 0x141, 0xF, 0xF, false));
+    ia = max(ia, __builtin_amdgcn_mov_dpp(ia, 0x140, 0xF, 0xF, false));
+    ib = max(ib, __builtin_amdgcn_mov_dpp(ib, 0x140, 0xF, 0xF, false));
+    a = __int_as_float(ia);
+    b = __int_as_float(ib);
+}
 __device__ __forceinline__ int row16_or(int v) {
     v |= dpp_mov<0xB1>(v);
     v |= dpp_mov<0x4E>(v);
@@ -196,18 +213,17 @@ __device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uin
 __device__ __forceinline__ void quantize_q8k_row16(const float (&x)[16], int g, uint32_t (&packed)[4], int& bsum,
                                                    float& dval) {
 #pragma clang fp contract(off)
-    float amax_l = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) amax_l = fmaxf(amax_l, fabsf(x[j]));
-    const float amax = row16_max(amax_l);
-    // does +amax / -amax occur in this lane? (row-wide OR below)
-    int has_pos = 0, has_neg = 0;
+    // max(0, x_j) and max(0, -x_j) over the lane, then over the row: amax = max |x_j|, and
+    // +amax (-amax) occurs in the row iff the first (second) of the two reaches it
+    float hi = 0.0f, nlo = 0.0f;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        has_pos |= (x[j] == amax);
-        has_neg |= (x[j] == -amax);
+        hi = fmaxf(hi, x[j]);
+        nlo = fmaxf(nlo, -x[j]);
     }
-    const int flags = row16_or(has_pos | (has_neg << 1));
+    row16_max2_nonneg(hi, nlo);
+    const float amax = fmaxf(hi, nlo);
+    const int flags = (hi == amax ? 1 : 0) | (nlo == amax ? 2 : 0);
     float maxv = (flags & 2) ? -amax : amax;
     if (flags == 3) {
         // both signs hold the maximum: the first index decides (exact scan, rare)
