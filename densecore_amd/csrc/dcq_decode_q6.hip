@@ -137,8 +137,9 @@ struct Q6Lds {
 // quantizer as the fused Q4_K decode: bit-identical bytes), saving the separate quantize
 // launch. Its loads are untracked inline-asm loads issued before the row's direct-to-LDS
 // loads: loads retire in order, so an explicit wait for all but the row's loads covers them,
-// and the quantizer runs while the row streams. QC passes of 16 (superblock, row) pairs.
-template <int MT, bool DUMP, bool FUSE = false, int QC = 1, int kWaves = 4>
+// and the quantizer runs while the row streams. The first SW waves stage the activation, QC
+// passes of 4 * SW (superblock, row) pairs; the other waves only stream their rows.
+template <int MT, bool DUMP, bool FUSE = false, int QC = 1, int kWaves = 4, int SW = kWaves>
 __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
     const int8_t* __restrict__ xqs, const float* __restrict__ xd, const int16_t* __restrict__ xbs, int64_t m_ld,
@@ -177,11 +178,13 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
 
     // ---- 1b. fused: the fp32 activation, issued ahead of the row so that it lands first ----
     [[maybe_unused]] u32x4 xr[FUSE ? QC : 1][4];
+    const bool stager = wave < SW;  // wave-uniform
     if constexpr (FUSE) {
         const int g = threadIdx.x & 15, last_pair = nsb * MT - 1;
 #pragma unroll
         for (int i = 0; i < QC; ++i) {
-            int pr = (threadIdx.x >> 4) + 4 * kWaves * i;
+            if (!stager) break;
+            int pr = (threadIdx.x >> 4) + 4 * SW * i;
             pr = pr < last_pair ? pr : last_pair;
             const int s = pr / MT, m = pr % MT;  // MT is a power of two
             const float* xp = X + (int64_t)(m < M ? m : M - 1) * x_stride + 256 * s + 16 * g;
@@ -201,25 +204,29 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     // out before the activation is waited for (fewer loads ahead of it), the rest once it is
     // quantized (measured at M = 1: 2560 x 9728 9.5 -> 8.7 us; with 4-wave workgroups rows of
     // three 1 KB pieces lose: 1024 x 2560 3.8 -> 4.2 us)
+    // Waves past the first SW stage nothing and issue the whole row at once. The staging
+    // waves are dispatched first, so their activation loads still lead the CU's queue (with
+    // every wave staging, the last-dispatched waves' activation landed about 1.1 us after
+    // the first's, and the barrier waited for them).
     constexpr bool split = FUSE && kWaves > 4;
-    const int n_early = split ? (2 * nx4) / 5 : nx4;
+    const int n_early = split && stager ? (2 * nx4) / 5 : nx4;
     dma4(src + 4 * (lane < row_dw ? lane : row_dw - 1), img);
     for (int j = 0; j < n_early; ++j) {
         const int c = 64 * j + lane;
         dma16(src + head + 16 * (c < nfull ? c : nfull - 1), lw + 16 + 1024 * j);
     }
     const int tail0 = row_dw > 64 ? row_dw - 64 : 0;
-    if constexpr (!split) dma4(src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), img + 4 * tail0);
+    if (!split || !stager) dma4(src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), img + 4 * tail0);
     const int issued = nx4 + 2;  // every row load, in issue order: head, pieces, tail
-    if constexpr (FUSE) {
-        // quantize the activation (QC passes of 16 (superblock, row) pairs, one per 16-lane
+    if (FUSE && stager) {
+        // quantize the activation (QC passes of 4 * SW (superblock, row) pairs, one per 16-lane
         // group) while the row streams: wait for the activation loads only (issued before it)
         wait_vmcnt_rt<0, 63>(split ? n_early + 1 : issued);
         __builtin_amdgcn_sched_barrier(0);
         const int tid = threadIdx.x, g = tid & 15, last_pair = nsb * MT - 1;
 #pragma unroll
         for (int i = 0; i < QC; ++i) {
-            int pr = (tid >> 4) + 4 * kWaves * i;
+            int pr = (tid >> 4) + 4 * SW * i;
             pr = pr < last_pair ? pr : last_pair;
             const int s = pr / MT, m = pr % MT;
             float x[16];
@@ -330,14 +337,17 @@ using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8
                       int64_t, const float*, int64_t, int, float*, int64_t, int32_t*, int64_t, const float*,
                       int64_t);
 
-// fused activation: M <= 2 rows, nsb <= 64: at most 8 staging passes of 16 (superblock, row)
-// pairs per wave with 4 waves, 4 with 8..12 waves
+// fused activation: M <= 2 rows, nsb <= 64. 4-wave workgroups: every wave stages, at most 8
+// passes of 16 (superblock, row) pairs. 8..12 waves: the first 4 waves stage, at most 4 passes
+// (nsb * M <= 64; 64 registers of activation per lane)
+constexpr int q6_stage_waves(int nw) { return nw > 4 ? 4 : nw; }
 template <int MT, bool DUMP, int NW, int QC>
 Q6Fn q6_fused_qc(int qc) {
-    if constexpr (QC > 32 / NW) {
+    constexpr int SW = q6_stage_waves(NW);
+    if constexpr (QC > (NW > 4 ? 4 : 8)) {
         return nullptr;
     } else {
-        if (qc == QC) return decode_q6k_lds_kernel<MT, DUMP, true, QC, NW>;
+        if (qc == QC) return decode_q6k_lds_kernel<MT, DUMP, true, QC, NW, SW>;
         return q6_fused_qc<MT, DUMP, NW, QC + 1>(qc);
     }
 }
@@ -418,7 +428,8 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
     if (knob(Knob::Q6KFuseWaves) > 0) nw = knob(Knob::Q6KFuseWaves);  // tuning override: 4, 8, 10 or 12
     const int kWaves = nw;
     const int mt = M == 1 ? 1 : 2;
-    const int qc = (nsb * mt + 4 * kWaves - 1) / (4 * kWaves);
+    const int sw = q6_stage_waves(kWaves);
+    const int qc = (nsb * mt + 4 * sw - 1) / (4 * sw);
     if (Q6Lds(nsb, mt, kWaves).total > kMaxLds) return hipErrorNotSupported;
     Q6Fn fn = block_sums ? q6_pick_fused<true>(mt, qc, kWaves) : q6_pick_fused<false>(mt, qc, kWaves);
     if (!fn) return hipErrorNotSupported;
