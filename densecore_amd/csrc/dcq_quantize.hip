@@ -156,17 +156,22 @@ __global__ void __launch_bounds__(256) unpack_q8_K_rows_kernel(const uint8_t* __
 }
 
 // ---- host launchers ----
+// Block size: 256 threads, or 64 when that leaves fewer workgroups than two per CU, so that
+// a small activation (a few rows) spreads over more CUs and L2 channels.
+static int quant_block(int64_t threads) { return threads < 2 * 256 * (int64_t)cu_count() ? 64 : 256; }
 hipError_t launch_quantize_ggml(int vdt, const float* X, int64_t x_stride, int64_t M, int64_t K, void* out,
                                 int64_t out_row_bytes, hipStream_t st) {
     if (vdt == kTypeQ8_0) {
         const int64_t threads = M * (K / QK8_0) * 4;
-        const int64_t grid = (threads + 255) / 256;
-        hipLaunchKernelGGL(quantize_q8_0_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
+        const int bs = quant_block(threads);
+        const int64_t grid = (threads + bs - 1) / bs;
+        hipLaunchKernelGGL(quantize_q8_0_kernel<false>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
                            (uint8_t*)out, out_row_bytes, (int8_t*)nullptr, (float*)nullptr, M);
     } else {
         const int64_t threads = M * (K / QK_K) * 16;
-        const int64_t grid = (threads + 255) / 256;
-        hipLaunchKernelGGL(quantize_q8_K_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
+        const int bs = quant_block(threads);
+        const int64_t grid = (threads + bs - 1) / bs;
+        hipLaunchKernelGGL(quantize_q8_K_kernel<false>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
                            (uint8_t*)out, out_row_bytes, (int8_t*)nullptr, (float*)nullptr, (int16_t*)nullptr, M);
     }
     return hipGetLastError();
@@ -176,13 +181,15 @@ hipError_t launch_quantize_planar(int vdt, const float* X, int64_t x_stride, int
                                   const PlanarBuffers& pb, hipStream_t st) {
     if (vdt == kTypeQ8_0) {
         const int64_t threads = pb.m_ld * (K / QK8_0) * 4;
-        const int64_t grid = (threads + 255) / 256;
-        hipLaunchKernelGGL(quantize_q8_0_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
+        const int bs = quant_block(threads);
+        const int64_t grid = (threads + bs - 1) / bs;
+        hipLaunchKernelGGL(quantize_q8_0_kernel<true>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
                            (uint8_t*)nullptr, (int64_t)0, pb.qs, pb.d, pb.m_ld);
     } else {
         const int64_t threads = pb.m_ld * (K / QK_K) * 16;
-        const int64_t grid = (threads + 255) / 256;
-        hipLaunchKernelGGL(quantize_q8_K_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
+        const int bs = quant_block(threads);
+        const int64_t grid = (threads + bs - 1) / bs;
+        hipLaunchKernelGGL(quantize_q8_K_kernel<true>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
                            (uint8_t*)nullptr, (int64_t)0, pb.qs, pb.d, pb.bs, pb.m_ld);
     }
     return hipGetLastError();
