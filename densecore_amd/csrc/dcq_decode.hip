@@ -34,6 +34,7 @@
 
 #include <stdlib.h>
 
+#include <atomic>
 #include <type_traits>
 
 namespace dcq {
@@ -361,16 +362,19 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
 }
 
 // ------------------------------------------------------------------ dispatch
-// compute units of the current device, cached per device (idempotent writes)
+// compute units of the current device, cached per device (threads that race on the first
+// call store the same value; atomics keep that well defined)
 int cu_count() {
-    static int cus[64] = {0};
+    static std::atomic<int> cus[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cus[dev]) {
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (!n) {
         hipDeviceProp_t p;
-        cus[dev] = hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+        n = hipGetDeviceProperties(&p, dev) == hipSuccess && p.multiProcessorCount > 0 ? p.multiProcessorCount : 256;
+        cus[dev].store(n, std::memory_order_relaxed);
     }
-    return cus[dev];
+    return n;
 }
 
 namespace {
