@@ -102,8 +102,11 @@ CASES = [
     (Q6_K, 1, 1000, 2560), (Q6_K, 2, 70, 4096),
     # fused Q4_K decode at the concatenated Q/K/V rows of Qwen3-4B and at twice the ffn width
     (Q4_K, 1, 6144, 2560), (Q4_K, 1, 12288, 2560),
-    # fused Q6_K beyond K = 4096: one 8..12-wave workgroup per CU (rows per CU 8, 10, 12; two rows)
+    # fused Q6_K beyond K = 4096: one 8..12-wave workgroup per CU (rows per CU 8, 10, 12), the
+    # activation staged by the first four waves in up to 4 passes; two rows at K = 9728 exceed
+    # the 4 passes and take the separate quantize
     (Q6_K, 1, 2048, 9728), (Q6_K, 2, 2560, 9728), (Q6_K, 1, 3000, 5120),
+    (Q6_K, 2, 2560, 8192), (Q6_K, 1, 2048, 12288),
 ]
 
 
