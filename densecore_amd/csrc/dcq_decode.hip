@@ -176,11 +176,17 @@ struct FmtQ6K {
     }
 };
 
+// Waves that stage the fused activation: at most four, one per SIMD. In wider workgroups the
+// last-dispatched waves would otherwise hold the barrier: their activation loads queue behind
+// the earlier waves' weight loads.
+__host__ __device__ constexpr int stage_waves(int NW) { return NW > 4 ? 4 : NW; }
+
 // Staging passes for the largest K a (P, NS) shape covers (nsb <= P*NS):
-// FUSE: (superblock, m) pairs, 16 per workgroup pass (one per 16-lane DPP row);
+// FUSE: (superblock, m) pairs, 4 per staging wave per pass (one per 16-lane DPP row);
 // else: 16-byte chunks of the planar activation per thread.
 __host__ __device__ constexpr int stage_chunks(int P, int NS, int MT, bool fuse, int NW) {
-    return fuse ? (MT * P * NS + 4 * NW - 1) / (4 * NW) : (MT * P * NS * 256 / 16 + 64 * NW - 1) / (64 * NW);
+    return fuse ? (MT * P * NS + 4 * stage_waves(NW) - 1) / (4 * stage_waves(NW))
+                : (MT * P * NS * 256 / 16 + 64 * NW - 1) / (64 * NW);
 }
 
 // FUSE: X is fp32 [M][x_stride], quantized in the workgroup; else planar Q8_K
@@ -207,6 +213,7 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
     const int last_pair = nsb * MT - 1;
 
     // ---- 1. activation loads, issued first ----
+    constexpr int SW = stage_waves(NW);  // waves >= SW load (clamped pairs) but never quantize
     float4 xv[FUSE ? QC : 1][4];
     uint4 sq[FUSE ? 1 : QC], sb16[FUSE ? 1 : QC];
     float sd[FUSE ? 1 : QC];
@@ -214,7 +221,7 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
         const int g = tid & 15;
 #pragma unroll
         for (int i = 0; i < QC; ++i) {
-            int pr = (tid >> 4) + 4 * NW * i;
+            int pr = (tid >> 4) + 4 * SW * i;
             pr = pr < last_pair ? pr : last_pair;
             const int s = pr / MT, m = pr % MT;  // MT is a power of two
             const float4* xp = reinterpret_cast<const float4*>(X + (int64_t)(m < M ? m : M - 1) * x_stride + 256 * s + 16 * g);
@@ -270,8 +277,8 @@ __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __res
             // a wave whose four pairs all lie past the last one would only rewrite the last
             // pair's bytes: it skips the quantizer (wave-uniform), which frees its SIMD for the
             // wave that shares it (K = 2560, 5 waves: 10 pairs in 20 slots; 5.13 -> 4.96 us)
-            if (4 * wave + 4 * NW * i > last_pair) continue;
-            int pr = (tid >> 4) + 4 * NW * i;
+            if (wave >= SW || 4 * wave + 4 * SW * i > last_pair) continue;
+            int pr = (tid >> 4) + 4 * SW * i;
             pr = pr < last_pair ? pr : last_pair;
             const int s = pr / MT, m = pr % MT;
             float x[16];
