@@ -144,10 +144,12 @@ def _with_quantizer_ties(x, vdt):
 # Shapes for the decode kernels that quantize the activation in the workgroup (M <= 8):
 # Q8_0 lanes-per-row / pairs-per-lane shapes {16,1} (K 1024), {32,1} (2048), {64,1} (4096,
 # and 3072 with idle lanes), {64,2} (8192); M tiles 1, 2, 4 and 8 rows; N not a multiple of
-# the rows per workgroup. Q4_K for comparison on the same inputs.
+# the rows per workgroup. Q4_K for comparison on the same inputs. Q6_K beyond K = 4096: the
+# 8..12-wave workgroups whose first four waves stage the activation (3 and 4 passes).
 FUSED = [(Q8_0, 1, 96, 1024), (Q8_0, 8, 50, 1024), (Q8_0, 5, 37, 512), (Q8_0, 2, 41, 4096),
          (Q8_0, 1, 29, 3072), (Q8_0, 1, 70, 8192), (Q8_0, 3, 33, 2048), (Q4_K, 1, 45, 2560),
-         (Q4_K, 7, 21, 1024)]
+         (Q4_K, 7, 21, 1024), (Q4_K, 1, 2560, 9728),
+         (Q6_K, 1, 2560, 9728), (Q6_K, 2, 2560, 8192), (Q6_K, 1, 3000, 5120)]
 
 
 @pytest.mark.parametrize("wt,M,N,K", FUSED)
