@@ -605,31 +605,51 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restri
     }
 }
 
-// Few splits over many rows (prompts): one thread per output element, the splits' loads issued
-// together (S <= 16), merged in split order like attn_combine_kernel's groups.
+// Few splits over many rows (prompts): one thread per 4 consecutive output elements (head_dim a
+// multiple of 4: the MFMA kernel's 64 and 128), the splits' loads issued together (S <= 16).
+// Two passes over the splits: the row maximum, then the weighted sums, so a thread evaluates
+// S powers of two for its 4 elements (the sequential merge took 2 S per element).
 template <int S>
 __global__ void __launch_bounds__(256) attn_combine_few_kernel(const float* __restrict__ ws_o,
                                                                const float* __restrict__ ws_ml, int splits,
                                                                int n_tokens, int n_head, int hd,
                                                                float* __restrict__ out, int64_t out_stride) {
     const int64_t rows = (int64_t)n_tokens * n_head;
+    const int q4 = hd / 4;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= rows * hd) return;
-    const int64_t row = idx / hd;
-    const int d = (int)(idx % hd);
-    float mv[S], lv[S], ov[S];
+    if (idx >= rows * q4) return;
+    const int64_t row = idx / q4;
+    const int d = (int)(idx % q4) * 4;
+    float mv[S], lv[S];
+    float4 ov[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int64_t r = (int64_t)s * rows + row;
         mv[s] = s < splits ? ws_ml[2 * r] : -INFINITY;
         lv[s] = s < splits ? ws_ml[2 * r + 1] : 0.0f;
-        ov[s] = s < splits ? ws_o[r * hd + d] : 0.0f;
+        ov[s] = s < splits ? *reinterpret_cast<const float4*>(ws_o + r * hd + d) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    float m = -INFINITY, l = 0.0f, acc = 0.0f;
+    float m = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < S; ++s) merge_online(m, l, acc, mv[s], lv[s], ov[s]);
+    for (int s = 0; s < S; ++s) m = fmaxf(m, mv[s]);  // finite: every row sees at least one key
+    float l = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const float c = mv[s] == -INFINITY ? 0.0f : exp2f(mv[s] - m);  // a split without keys adds 0
+        l = fmaf(lv[s], c, l);
+        acc.x = fmaf(ov[s].x, c, acc.x);
+        acc.y = fmaf(ov[s].y, c, acc.y);
+        acc.z = fmaf(ov[s].z, c, acc.z);
+        acc.w = fmaf(ov[s].w, c, acc.w);
+    }
+    const float inv = 1.0f / l;
     const int i = (int)(row / n_head), h = (int)(row % n_head);
-    out[(int64_t)i * out_stride + (int64_t)h * hd + d] = acc / l;
+    float* o = out + (int64_t)i * out_stride + (int64_t)h * hd + d;
+    o[0] = acc.x * inv;
+    o[1] = acc.y * inv;
+    o[2] = acc.z * inv;
+    o[3] = acc.w * inv;
 }
 
 // ---------------------------------------------------------------- prompt attention on fp32 MFMA
@@ -1001,10 +1021,13 @@ hipError_t launch_kv_attention(int ct, const void* k_arena, const void* v_arena,
 #undef DCQ_ATTN_MFMA_CASE
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || m.splits <= 1) return e;
-        const int64_t elems = (int64_t)n_tokens * n_head * hd;
-        const dim3 cgrid((unsigned)((elems + 255) / 256));
+        const int64_t quads = (int64_t)n_tokens * n_head * (hd / 4);  // one thread per 4 elements
+        const dim3 cgrid((unsigned)((quads + 255) / 256));
         if (m.splits <= 4)
             hipLaunchKernelGGL(attn_combine_few_kernel<4>, cgrid, dim3(256), 0, st, a.ws_o, a.ws_ml, m.splits,
+                               n_tokens, n_head, hd, out, out_stride);
+        else if (m.splits <= 8)
+            hipLaunchKernelGGL(attn_combine_few_kernel<8>, cgrid, dim3(256), 0, st, a.ws_o, a.ws_ml, m.splits,
                                n_tokens, n_head, hd, out, out_stride);
         else if (m.splits <= 16)
             hipLaunchKernelGGL(attn_combine_few_kernel<16>, cgrid, dim3(256), 0, st, a.ws_o, a.ws_ml, m.splits,
