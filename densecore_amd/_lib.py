@@ -15,7 +15,7 @@ SYMBOLS = [
     "dcq_supports_mul_mat", "dcq_quantize_rows", "dcq_mul_mat_workspace_size", "dcq_mul_mat", "dcq_mul_mat_ex",
     "dcq_block_sums_per_row", "dcq_dot_rows", "dcq_quantize_weights", "dcq_dequantize_rows",
     "dcq_quantize_src1", "dcq_mul_mat_q", "dcq_mul_mat_add_workspace_size", "dcq_mul_mat_add",
-    "dcq_ffn_gate_up_workspace_size", "dcq_ffn_gate_up",
+    "dcq_ffn_gate_up_workspace_size", "dcq_ffn_gate_up", "dcq_mul_mat_noalloc",
     "dcq_gguf_open", "dcq_gguf_close", "dcq_gguf_tensor_count", "dcq_gguf_find_tensor", "dcq_gguf_tensor_info",
     "dcq_gguf_get_int", "dcq_gguf_get_str", "dcq_gguf_load_tensor",
     "dcq_kv_slot_bytes", "dcq_kv_write", "dcq_kv_gather", "dcq_kv_attention_workspace_size", "dcq_kv_attention",
@@ -69,6 +69,7 @@ def lib():
             "dcq_mul_mat_add": (i32, [i32, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp, sz, vp, sz, vp]),
             "dcq_ffn_gate_up_workspace_size": (sz, [i32, i64, i64, i64]),
             "dcq_ffn_gate_up": (i32, [i32, vp, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp, sz, vp]),
+            "dcq_mul_mat_noalloc": (i32, [i32, vp, i64, i64, sz, vp, i64, sz, vp, sz, vp]),
             "dcq_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
             "dcq_gguf_close": (None, [vp]),
             "dcq_gguf_tensor_count": (i64, [vp]),
@@ -182,6 +183,19 @@ def mul_mat(wt, wq, n, k, x, y=None, workspace=None, w_row_bytes=None, stream=No
     _check("dcq_mul_mat", lib().dcq_mul_mat(
         wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace), ws_bytes,
         _stream(stream)))
+    return y
+
+
+NOALLOC_SCRATCH_BYTES = 8 << 20  # DCQ_NOALLOC_SCRATCH_BYTES
+
+
+def mul_mat_noalloc(wt, wq, n, k, x, y, w_row_bytes=None, stream=None):
+    """dcq_mul_mat_noalloc: dcq_mul_mat with the library's static device scratch as workspace
+    (no allocation on the library side; y must be given)."""
+    m = x.shape[0]
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    _check("dcq_mul_mat_noalloc", lib().dcq_mul_mat_noalloc(
+        wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _stream(stream)))
     return y
 
 
@@ -402,3 +416,4 @@ class PagedKVCache:
 
 def kv_attention_workspace_size(n_head, n_head_kv, head_dim, n_tokens, n_past):
     return int(lib().dcq_kv_attention_workspace_size(n_head, n_head_kv, head_dim, n_tokens, n_past))
+

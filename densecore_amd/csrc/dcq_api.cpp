@@ -130,6 +130,7 @@ const char* dcq_status_string(int s) {
         case DCQ_ERR_FORMAT: return "malformed GGUF file";
         case DCQ_ERR_IO: return "file could not be opened or read";
         case DCQ_ERR_NOT_FOUND: return "key not found";
+        case DCQ_ERR_SCRATCH_LIMIT: return "product needs more than the no-alloc scratch (DCQ_NOALLOC_SCRATCH_BYTES)";
         default: return "unknown status";
     }
 }
@@ -254,6 +255,21 @@ int dcq_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_byt
                 void* stream) {
     return dcq_mul_mat_ex(wtype, W, N, K, w_row_bytes, X, M, x_stride_bytes, Y, y_stride_bytes, workspace,
                           workspace_bytes, DCQ_PATH_AUTO, nullptr, stream);
+}
+
+int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X,
+                        int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes, void* stream) {
+    int rc = validate_mul_mat(wtype, W, N, K, w_row_bytes, X, M, x_stride_bytes, Y, y_stride_bytes);
+    if (rc) return rc;
+    if (planar_bytes(dcq_vec_dot_type(wtype), M, K, nullptr, nullptr) > DCQ_NOALLOC_SCRATCH_BYTES)
+        return DCQ_ERR_SCRATCH_LIMIT;
+    if ((rc = check_device())) return rc;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    if ((rc = noalloc_scratch(&ws, &ws_bytes))) return rc;
+    // a non-null workspace: dcq_mul_mat_ex allocates nothing
+    return dcq_mul_mat_ex(wtype, W, N, K, w_row_bytes, X, M, x_stride_bytes, Y, y_stride_bytes, ws, ws_bytes,
+                          DCQ_PATH_AUTO, nullptr, stream);
 }
 
 size_t dcq_mul_mat_add_workspace_size(int wtype, int64_t M, int64_t N, int64_t K) {

@@ -132,6 +132,10 @@ hipError_t launch_kv_attention(int ct, const void* k_arena, const void* v_arena,
                                int64_t kv_stride, int n_tokens, int n_past, float scale, float* out,
                                int64_t out_stride, void* ws, size_t ws_bytes, hipStream_t st);
 
+// The current device's copy of the no-alloc scratch array (dcq_noalloc.hip): its device address,
+// looked up on the device's first call, and its size. DCQ_OK, or DCQ_ERR_* if the lookup fails.
+int noalloc_scratch(void** ptr, size_t* bytes);
+
 hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, hipStream_t st);
 hipError_t launch_dequantize(int type, const void* Wq, int64_t N, int64_t K, int64_t w_row_bytes, float* Y,
                              hipStream_t st);

@@ -60,6 +60,7 @@ extern "C" {
 #define DCQ_ERR_FORMAT (-8)          /* malformed GGUF file */
 #define DCQ_ERR_IO (-9)              /* file could not be opened or read */
 #define DCQ_ERR_NOT_FOUND (-10)      /* GGUF metadata key not present */
+#define DCQ_ERR_SCRATCH_LIMIT (-11)  /* needs more than DCQ_NOALLOC_SCRATCH_BYTES (dcq_mul_mat_noalloc) */
 
 /* kernel path selection for dcq_mul_mat_ex */
 #define DCQ_PATH_AUTO 0
@@ -131,6 +132,20 @@ int dcq_quantize_src1(int wtype, const float* X, int64_t M, int64_t K, size_t x_
 int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes,
                   const void* workspace, size_t workspace_bytes, int64_t M, float* Y,
                   size_t y_stride_bytes, int path, void* stream);
+
+/* ---- the operator without allocation ----
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * stream capture, serving loops or harnesses that forbid hipMalloc). Same arguments, result and
+ * kernels as dcq_mul_mat with workspace = NULL, except that the workspace is a static device
+ * array of DCQ_NOALLOC_SCRATCH_BYTES (8 MiB) that the library holds on each GPU it runs on until
+ * the process ends, instead of stream-ordered scratch. No hipMalloc, hipFree or other
+ * allocating call is made. A product whose dcq_mul_mat_workspace_size(wtype, M, K) exceeds the
+ * array returns DCQ_ERR_SCRATCH_LIMIT before any device work (M*K up to about 7.4 M elements).
+ * Every call on one GPU shares that GPU's array: calls on one stream are ordered, but calls that
+ * overlap on one GPU (different streams, or host threads without ordering) race on it. */
+#define DCQ_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
+int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X,
+                        int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes, void* stream);
 
 /* ---- a projection and its residual or bias ----
  * Y[m][n] = (sum_k W[n][k] x[m][k]) + R[m][n], one fp32 add per element after dcq_mul_mat's

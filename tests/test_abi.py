@@ -17,7 +17,8 @@ OK, INVALID, UNSUPPORTED, BAD_SHAPE, MISALIGNED, WORKSPACE, HIP, NO_DEVICE = 0, 
 
 
 def declared_symbols():
-    text = open(os.path.join(ROOT, "include", "dcq.h")).read()
+    inc = os.path.join(ROOT, "include")
+    text = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc)) if f.endswith(".h"))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(dcq_[a-z0-9_]+)\s*\(", text)))
 
@@ -84,6 +85,29 @@ def test_mul_mat_validation_order():
     assert _mm(path=7) == INVALID
     assert _mm(ws=0x4000, wsb=16) == WORKSPACE
     assert _mm(ws=0x4010, wsb=1 << 20) == MISALIGNED
+
+
+def test_noalloc_validation_and_limit():
+    """dcq_mul_mat_noalloc validates like dcq_mul_mat, and refuses a product whose activation
+    workspace exceeds the static scratch (DCQ_ERR_SCRATCH_LIMIT), all before any device call."""
+    L = dc.lib()
+    SCRATCH_LIMIT = -11
+
+    def na(wt=8, W=0x1000, N=16, K=1024, M=1, X=0x2000, Y=0x3000):
+        return L.dcq_mul_mat_noalloc(wt, W, N, K, dc.row_size(wt, K), X, M, K * 4, Y, N * 4, None)
+    assert na(wt=2) == UNSUPPORTED
+    assert na(W=None) == INVALID
+    assert na(K=100) == BAD_SHAPE
+    assert na(X=0x2004) == MISALIGNED
+    big_m = dc.NOALLOC_SCRATCH_BYTES // 1024 + 1
+    assert dc.mul_mat_workspace_size(8, big_m, 1024) > dc.NOALLOC_SCRATCH_BYTES
+    assert na(M=big_m) == SCRATCH_LIMIT
+    assert "scratch" in dc._lib.status_string(SCRATCH_LIMIT)
+    # config 5 (M = 2048, K = 2048, Q8_0) fits
+    assert dc.mul_mat_workspace_size(8, 2048, 2048) <= dc.NOALLOC_SCRATCH_BYTES
+    import torch
+    if not torch.cuda.is_available():
+        assert na(M=2048, K=2048) == NO_DEVICE
 
 
 def test_well_formed_call_without_gpu_fails_loudly():
