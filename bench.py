@@ -12,9 +12,11 @@ Printed: one JSON line. `value` is the headline configuration's (BASELINE config
 Q4_K GEMV, M = 1) weight GB/s over whole steps. `roofline` is for the dominant kernel
 of that step: the whole step when it is one kernel (decode with fused activation
 quantization), else the mul_mat kernel timed alone on pre-quantized activations.
-Every configuration is listed under "configs". The CPU baseline is the oracle's
-restatement of the reference CPU path (quantize once, row-partitioned vec_dot,
-threaded), timed on this host on a bounded sample.
+Every configuration is listed under "configs", each decode config with the measured
+pure-read time of its weight bytes (the ceiling any weight-streaming kernel can reach at
+that size) beside the 8 TB/s peak. The CPU baseline (configs 2 and 5) is a SIMD
+restatement of the reference CPU path (quantize once, row-partitioned AVX2 / AVX-512
+VNNI vec_dots, one pinned worker per physical core), timed on this host.
 
 --profile runs the same steps eagerly (no graph) followed by a device-to-device copy
 of known size, for rocprofv3 counter passes (the copy calibrates FETCH_SIZE /
@@ -45,12 +47,22 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--configs", default="1,2,3,4,5")
     ap.add_argument("--rotate-mb", type=int, default=1024, help="total bytes of W copies cycled through")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=5.0, help="CPU baseline: time budget per config")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--replays", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true", help="skip the gate/up pair measurement")
     ap.add_argument("--profile", action="store_true", help="eager steps + a calibration copy, for rocprofv3 --pmc")
+    ap.add_argument("--profile-read", action="store_true",
+                    help="eager pure-read launches at each config's weight size, for rocprofv3 --kernel-trace")
+    ap.add_argument("--no-read-ceiling", action="store_true", help="skip the pure-read ceiling sweep")
+    ap.add_argument("--no-clocks", action="store_true", help="skip sampling the GPU clocks under load")
+    ap.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
+                    help="print profiles/counters.txt lines from rocprofv3 --pmc counter_collection.csv files "
+                         "of --profile runs (no GPU needed)")
+    ap.add_argument("--summarize-read", metavar="CSV",
+                    help="print profiles/read_ceiling.txt lines from the rocprofv3 kernel_trace.csv of a "
+                         "--profile-read run made with the same --configs/--steps/--warmup (no GPU needed)")
     return ap.parse_args()
 
 
@@ -95,10 +107,14 @@ def _graph_kernel_nodes(g):
         return None
 
 
-def time_graph(fn_steps, steps, warmup, replays):
-    """Capture `steps` calls into one graph and replay it; return (mean ms per step, kernels per step).
+def time_graph(fn_steps, steps, warmup, replays, min_event_ms=1.0):
+    """Capture `steps` calls into one graph and replay it; return (mean ms per step, kernels per
+    step, graph replays per timed event).
 
-    The events are recorded on the stream the graph replays on (the kernels' stream)."""
+    Each timed event pair brackets k back-to-back replays, k chosen so that it spans at least
+    min_event_ms of GPU work whatever `steps` is (the fixed cost of one graph launch is then
+    spread over k * steps steps). The events are recorded on the stream the graph replays on
+    (the kernels' stream)."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -115,21 +131,24 @@ def time_graph(fn_steps, steps, warmup, replays):
             fn_steps(i)
     torch.cuda.synchronize()
     kernels = _graph_kernel_nodes(g)
-    g.replay()  # warm replay
-    torch.cuda.synchronize()
-    times = []
-    for _ in range(replays):
+
+    def timed(k):
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         with torch.cuda.stream(s):
             e0.record(s)
-            g.replay()
+            for _ in range(k):
+                g.replay()
             e1.record(s)
         torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1) / steps)
+        return e0.elapsed_time(e1)
+
+    timed(1)  # warm replay
+    k = max(1, int(np.ceil(min_event_ms / max(timed(1), 1e-3))))
+    times = [timed(k) / (k * steps) for _ in range(replays)]
     del g
-    return float(np.median(times)), (kernels / steps if kernels is not None else None)
+    return float(np.median(times)), (kernels / steps if kernels is not None else None), k
 
 
 def load_traffic(cfg_index):
@@ -151,6 +170,98 @@ def load_traffic(cfg_index):
                 except (KeyError, ValueError):
                     return None
     return None
+
+
+def load_counters(cfg_index):
+    """The dominant kernel's utilisation counters from the committed PMC summary
+    (profiles/counters.txt, written by --summarize-pmc from rocprofv3 --pmc runs of --profile),
+    or None."""
+    path = os.path.join(ROOT, "profiles", "counters.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("#") or not line.strip():
+                continue
+            kv = dict(tok.split("=", 1) for tok in line.split() if "=" in tok)
+            if kv.get("config") == str(cfg_index):
+                out = {}
+                for k, v in kv.items():
+                    try:
+                        out[k] = float(v)
+                    except ValueError:
+                        out[k] = v
+                out.pop("config", None)
+                out["source"] = "profiles/counters.txt"
+                return out
+    return None
+
+
+READ_VARIANTS = [(u, g) for u in (1, 2, 4, 8, 16) for g in (0, 1024, 2048)]
+
+
+def read_ceiling(big, wbytes, copies, args):
+    """The fastest pure read of wbytes over the same rotated copies the operator reads
+    (dcq_probe_stream_read, include/dcq_probe.h), over a sweep of loads per lane and workgroup
+    caps: the best any kernel that must stream the weights once can do at this size."""
+    import torch
+    import densecore_amd as dc
+    sink = torch.zeros(64, dtype=torch.int32, device=big.device)
+    best = None
+    for u, g in READ_VARIANTS:
+        def rd(i, u=u, g=g):
+            dc.probe_stream_read(big[i % copies], wbytes, u, g, sink, stream=torch.cuda.current_stream().cuda_stream)
+        ms, _, _ = time_graph(rd, args.steps, min(args.warmup, 5), args.replays)
+        if best is None or ms < best[0]:
+            best = (ms, u, g)
+    ms, u, g = best
+    return {"us": ms * 1e3, "GBps": wbytes / (ms * 1e-3) / 1e9, "frac_of_peak": wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "best_variant": f"{u} x 16-byte loads per lane, " + (f"at most {g} workgroups" if g else "one pass"),
+            "variants": len(READ_VARIANTS)}
+
+
+def sample_clocks_under_load(fn_steps, steps, seconds=5.0):
+    """GPU clocks (amd-smi metric -c) sampled while a graph of `steps` calls of fn_steps replays
+    back to back; None if amd-smi is unavailable. Returns the mean GFX clock over the XCDs and
+    the memory clock, in MHz."""
+    import re
+    import subprocess
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(steps):
+            fn_steps(i)
+    torch.cuda.synchronize()
+
+    def replay():
+        with torch.cuda.stream(s):
+            for _ in range(4):
+                g.replay()
+    try:
+        proc = subprocess.Popen(["amd-smi", "metric", "-c", "-g", "0"], stdout=subprocess.PIPE,
+                                stderr=subprocess.DEVNULL, text=True)
+    except OSError:
+        return None
+    t_end = time.time() + seconds
+    while proc.poll() is None and time.time() < t_end:
+        replay()
+        torch.cuda.synchronize()
+    try:
+        out, _ = proc.communicate(timeout=max(1.0, t_end - time.time() + 1.0))
+    except subprocess.TimeoutExpired:
+        proc.kill()
+        return None
+    sections = re.findall(r"^\s*(GFX_\d+|MEM_\d+|UCLK_\d+|FCLK_\d+|SOCCLK_\d+):\s*\n\s*CLK:\s*([\d.]+)\s*MHz", out, re.M)
+    gfx = [float(v) for k, v in sections if k.startswith("GFX")]
+    mem = [float(v) for k, v in sections if k.startswith(("MEM", "UCLK"))]
+    del g
+    if not gfx:
+        return None
+    return {"gfx_mhz_mean": float(np.mean(gfx)), "gfx_mhz_min": min(gfx), "gfx_mhz_max": max(gfx),
+            "mem_mhz": mem[0] if mem else None, "how": "amd-smi metric -c while the config's step graph replays"}
 
 
 def bench_config(cfg, args, dev):
@@ -175,14 +286,14 @@ def bench_config(cfg, args, dev):
         dc.mul_mat_q(cfg.wtype, big[i % copies], cfg.N, cfg.K, ws, cfg.M, y=y,
                      stream=torch.cuda.current_stream().cuda_stream)
 
-    step_ms, step_kernels = time_graph(step, args.steps, args.warmup, args.replays)
+    step_ms, step_kernels, k_step = time_graph(step, args.steps, args.warmup, args.replays)
     if step_kernels == 1:
         # the whole step is one kernel (decode with the activation quantization fused in)
         dom_ms, dom = step_ms, "decode kernel with fused activation quantization (the whole step)"
     else:
         dc.quantize_src1(cfg.wtype, x, ws)
         torch.cuda.synchronize()
-        dom_ms, _ = time_graph(kernel_only, args.steps, args.warmup, args.replays)
+        dom_ms, _, _ = time_graph(kernel_only, args.steps, args.warmup, args.replays)
         dom = "mul_mat kernel on pre-quantized activations (dcq_mul_mat_q)"
 
     ops = 2.0 * cfg.M * cfg.N * cfg.K
@@ -195,17 +306,27 @@ def bench_config(cfg, args, dev):
         "boundary_GBps_step": boundary / (step_ms * 1e-3) / 1e9,
         "TOPS_step": ops / (step_ms * 1e-3) / 1e12, "digests": digests,
     }
+    out["replays_per_timed_event"] = k_step
     traffic = load_traffic(cfg.index)
+    counters = load_counters(cfg.index)
     if cfg.bound == "hbm":
         achieved = wbytes / (dom_ms * 1e-3) / 1e9
         out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                            "algorithmic_bytes_per_launch": wbytes}
+        if not args.no_read_ceiling:
+            # the measured pure-read time of the same bytes: what any weight-streaming kernel can reach
+            c = out["read_ceiling"] = read_ceiling(big, wbytes, copies, args)
+            out["roofline"]["frac_of_read_ceiling"] = c["us"] / (dom_ms * 1e3)
     else:
         achieved = ops / (dom_ms * 1e-3) / 1e12
         out["roofline"] = {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                            "frac": achieved / INT8_PEAK_TOPS, "traffic": traffic,
                            "algorithmic_ops_per_launch": ops}
+    if counters is not None:
+        out["roofline"]["counters"] = counters
+    if cfg.index in (HEADLINE, 5) and not args.no_clocks:
+        out["clocks"] = sample_clocks_under_load(step, args.steps)
     del big, ws, y, x, wq
     torch.cuda.empty_cache()
     return out
@@ -241,8 +362,8 @@ def bench_gate_up(cfg, args, dev):
         dc.mul_mat(cfg.wtype, bg[i % copies], cfg.N, cfg.K, x, y=y, workspace=ws, stream=s)
         dc.mul_mat(cfg.wtype, bu[i % copies], cfg.N, cfg.K, x, y=u, workspace=ws, stream=s)
 
-    f_ms, f_k = time_graph(fused, args.steps, args.warmup, args.replays)
-    s_ms, s_k = time_graph(separate, args.steps, args.warmup, args.replays)
+    f_ms, f_k, _ = time_graph(fused, args.steps, args.warmup, args.replays)
+    s_ms, s_k, _ = time_graph(separate, args.steps, args.warmup, args.replays)
     del bg, bu, ws, y, u, x, wq
     torch.cuda.empty_cache()
     return {"shape": f"config {cfg.index}: {dc.TYPE_NAMES[cfg.wtype]} M={cfg.M} N={cfg.N} K={cfg.K}, two weights",
@@ -283,8 +404,8 @@ def bench_qkv(args, dev, K=2560, parts=(4096, 1024, 1024), wtype=None):
         dc.mul_mat(wtype, big[i % copies], n_all, K, x, y=y, workspace=ws,
                    stream=torch.cuda.current_stream().cuda_stream)
 
-    s_ms, s_k = time_graph(separate, args.steps, args.warmup, args.replays)
-    f_ms, f_k = time_graph(fused, args.steps, args.warmup, args.replays)
+    s_ms, s_k, _ = time_graph(separate, args.steps, args.warmup, args.replays)
+    f_ms, f_k, _ = time_graph(fused, args.steps, args.warmup, args.replays)
     del big, wq
     torch.cuda.empty_cache()
     return {"shape": f"Q4_K q/k/v {list(parts)} x K={K}, M=1", "separate_us": s_ms * 1e3, "separate_kernels": s_k,
@@ -320,8 +441,8 @@ def bench_residual(args, dev, wtype, N=2560, K=9728):
         dc.mul_mat_add(wtype, big[i % copies], N, K, x, resid, y=resid, workspace=ws,
                        stream=torch.cuda.current_stream().cuda_stream)
 
-    s_ms, s_k = time_graph(separate, args.steps, args.warmup, args.replays)
-    f_ms, f_k = time_graph(fused, args.steps, args.warmup, args.replays)
+    s_ms, s_k, _ = time_graph(separate, args.steps, args.warmup, args.replays)
+    f_ms, f_k, _ = time_graph(fused, args.steps, args.warmup, args.replays)
     del big, wq
     torch.cuda.empty_cache()
     return {"shape": f"{dc.TYPE_NAMES[wtype]} ffn_down {N} x K={K}, M=1, residual in place",
@@ -360,7 +481,7 @@ def bench_kv_attention(args, dev, ct, n_tokens=1, n_past=4095, n_layer=36, n_hea
         cache.attention(i % n_layer, table, q, kc, vc, n_past, 1.0 / hd ** 0.5, out=out, workspace=ws,
                         stream=torch.cuda.current_stream().cuda_stream)
 
-    ms, kern = time_graph(step, args.steps, args.warmup, args.replays)
+    ms, kern, _ = time_graph(step, args.steps, args.warmup, args.replays)
     hist_bytes = 2 * n_past * cache.slot_bytes
     io_bytes = 4 * (2 * q.numel() + kc.numel() + vc.numel())
     pairs = n_tokens * n_past + n_tokens * (n_tokens + 1) // 2  # (query, visible key) pairs
@@ -429,6 +550,123 @@ def profile_config(cfg, args, dev):
     torch.cuda.empty_cache()
 
 
+def profile_read(args, dev):
+    """Eager pure-read launches (dcq_probe_stream_read) at each config's weight size over the same
+    rotation as the operator, every sweep variant, for rocprofv3 --kernel-trace: the per-size
+    read ceiling in the committed profile."""
+    import torch
+    import densecore_amd as dc
+    wanted = [int(c) for c in args.configs.split(",") if c.strip()]
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    for cfg in dc.CONFIGS:
+        if cfg.index not in wanted:
+            continue
+        wbytes = cfg.N * dc.row_size(cfg.wtype, cfg.K)
+        copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+        big = torch.empty((copies, wbytes), dtype=torch.uint8, device=dev)
+        for u, g in READ_VARIANTS:
+            for i in range(args.warmup + args.steps):
+                dc.probe_stream_read(big[i % copies], wbytes, u, g, sink)
+        torch.cuda.synchronize()
+        print(f"# read probe: config {cfg.index}, {wbytes} bytes, {len(READ_VARIANTS)} variants x "
+              f"{args.warmup + args.steps} launches", file=sys.stderr, flush=True)
+        del big
+        torch.cuda.empty_cache()
+
+
+def summarize_read(path, configs, launches):
+    """profiles/read_ceiling.txt lines from the rocprofv3 kernel trace of a --profile-read run:
+    per config, the mean duration of each read variant (its first two launches skipped) and the
+    best. Dispatches are assigned to configs and variants by their order, as --profile-read issues
+    them (configs ascending, READ_VARIANTS in order, `launches` launches each)."""
+    import csv
+    import densecore_amd as dc
+    rows = [r for r in csv.DictReader(open(path)) if "stream_read_kernel" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    wanted = [c for c in dc.CONFIGS if c.index in configs]
+    per_cfg = len(READ_VARIANTS) * launches
+    if len(rows) != per_cfg * len(wanted):
+        raise SystemExit(f"{len(rows)} probe dispatches in the trace, expected {per_cfg * len(wanted)}")
+    lines = ["# config bytes | mean us per variant (loads per lane x workgroup cap; 0 = one pass) | best"]
+    for ci, cfg in enumerate(wanted):
+        wbytes = cfg.N * dc.row_size(cfg.wtype, cfg.K)
+        means = []
+        for vi, (u, g) in enumerate(READ_VARIANTS):
+            sub = rows[ci * per_cfg + vi * launches: ci * per_cfg + (vi + 1) * launches][2:]
+            means.append(float(np.mean([(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in sub])))
+        b = int(np.argmin(means))
+        lines.append(f"config={cfg.index} bytes={wbytes} " +
+                     " ".join(f"u{u}g{g}={m:.2f}" for (u, g), m in zip(READ_VARIANTS, means)) +
+                     f" best_us={means[b]:.2f} best_GBps={wbytes / means[b] / 1e3:.0f} "
+                     f"best=u{READ_VARIANTS[b][0]}g{READ_VARIANTS[b][1]}")
+    return "\n".join(lines)
+
+
+# the kernel that dominates each config's step (for --summarize-pmc)
+DOMINANT = {1: "decode_q8_0_kernel", 2: "decode_kq_kernel", 3: "decode_q6k_lds_kernel", 4: "batch_q4k_kernel",
+            5: "prefill_q8_0_kernel"}
+
+
+def summarize_pmc(paths):
+    """profiles/counters.txt lines from rocprofv3 --pmc counter_collection.csv files of --profile
+    runs (one pass per file; passes are joined by kernel name). Per config, the medians over that
+    kernel's dispatches of:
+      mfma_busy_pct  = 100 * sum SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs * GRBM_GUI_ACTIVE per XCD)
+                       (rocprofv3's MfmaUtil)
+      valu_busy_pct  = 100 * sum SQ_ACTIVE_INST_VALU / (CUs * GRBM_GUI_ACTIVE per XCD)
+                       (rocprofv3's VALUBusy: quad-cycles over the CU's 4 SIMDs)
+      valu_per_mfma  = SQ_INSTS_VALU / SQ_INSTS_MFMA (SQ_INSTS_VALU counts the MFMAs too)
+      coexec_pct     = 100 * SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES
+    GRBM_GUI_ACTIVE is reported summed over the XCDs and covers the counting window around the
+    dispatch, which adds a few microseconds to short kernels: their busy percentages are lower
+    bounds."""
+    import csv
+    import collections
+    per = collections.defaultdict(dict)  # (file, dispatch) -> counters
+    names = {}
+    agent = {"simds": 1024, "cus": 256, "xcds": 8}
+    for p in paths:
+        info = os.path.join(os.path.dirname(p), os.path.basename(p).replace("counter_collection", "agent_info"))
+        if os.path.exists(info):
+            for a in csv.DictReader(open(info)):
+                if a.get("Agent_Type") == "GPU":
+                    agent = {"simds": int(a["Simd_Count"]), "cus": int(a["Cu_Count"]), "xcds": int(a["Num_Xcc"])}
+        for r in csv.DictReader(open(p)):
+            key = (p, r["Dispatch_Id"])
+            per[key][r["Counter_Name"]] = float(r["Counter_Value"])
+            names[key] = r["Kernel_Name"]
+    lines = [f"# per-dispatch medians; {agent['simds']} SIMDs, {agent['cus']} CUs, {agent['xcds']} XCDs"]
+    for cfg_i, kname in sorted(DOMINANT.items()):
+        rows = collections.defaultdict(list)
+        for key, cnt in per.items():
+            if kname in names[key]:
+                for c, v in cnt.items():
+                    rows[c].append(v)
+        if not rows:
+            continue
+        med = {c: float(np.median(v)) for c, v in rows.items()}
+        n_disp = max(len(v) for v in rows.values())
+        gui = med.get("GRBM_GUI_ACTIVE")
+        kv = [f"config={cfg_i}", f"kernel={kname}", f"samples={n_disp}"]
+        if gui:
+            gui_x = gui / agent["xcds"]
+            kv.append(f"gui_cycles_per_xcd={gui_x:.0f}")
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in med:
+                kv.append(f"mfma_busy_pct={100 * med['SQ_VALU_MFMA_BUSY_CYCLES'] / (agent['simds'] * gui_x):.2f}")
+            if "SQ_ACTIVE_INST_VALU" in med:
+                kv.append(f"valu_busy_pct={100 * med['SQ_ACTIVE_INST_VALU'] / (agent['cus'] * gui_x):.2f}")
+        if med.get("SQ_INSTS_MFMA"):
+            kv.append(f"valu_per_mfma={med['SQ_INSTS_VALU'] / med['SQ_INSTS_MFMA']:.2f}")
+        if med.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in med:
+            kv.append(f"coexec_pct={100 * med['SQ_VALU_MFMA_COEXEC_CYCLES'] / med['SQ_VALU_MFMA_BUSY_CYCLES']:.2f}")
+        for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_I8", "SQ_VALU_MFMA_BUSY_CYCLES",
+                  "SQ_ACTIVE_INST_VALU", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES", "SQ_VALU_MFMA_COEXEC_CYCLES"):
+            if c in med:
+                kv.append(f"{c}={med[c]:.6g}")
+        lines.append(" ".join(kv))
+    return "\n".join(lines)
+
+
 def calibration_copy(dev, nbytes=64 << 20):
     """One device-to-device copy of nbytes: the known-size kernel the traffic counters are scaled by."""
     import torch
@@ -439,38 +677,75 @@ def calibration_copy(dev, nbytes=64 << 20):
     print(f"# calibration copy: {nbytes} bytes read, {nbytes} bytes written", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(cfg, seconds, threads):
-    """The oracle's restatement of the reference CPU path on this host's cores, bounded sample."""
+def host_cpu_info():
+    """Model name (lscpu), logical CPUs in this process's affinity mask, and one logical CPU per
+    physical core among them (sysfs topology)."""
+    import subprocess
+    from oracle import oracle as O
+    model = ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((ln.split(":", 1)[1].strip() for ln in out.splitlines() if ln.startswith("Model name")), "")
+    except (OSError, subprocess.SubprocessError):
+        pass
+    cpus, logical = O.physical_cpus()
+    return {"model": model, "logical_cpus": logical, "physical_cores": len(cpus), "cpus": cpus,
+            "nproc": os.cpu_count()}
+
+
+def cpu_baseline(cfg, seconds, threads, host):
+    """The reference CPU path restated with SIMD int8 dots (oracle/dcq_cpu_simd.c: quantize X once,
+    then row-partitioned AVX2 / AVX-512 VNNI vec_dots on a persistent pool pinned one worker per
+    physical core, as core/src/worker.cpp:63-77 sizes the reference's pool), on the full config:
+    3 warm-up runs, then the median of at least 10 runs (more while under `seconds`)."""
     from oracle import oracle as O
     from densecore_amd import synth
     w = synth.normal(cfg.N * cfg.K, cfg.w_seed, 0.0, cfg.w_std).reshape(cfg.N, cfg.K)
     wq = O.quantize_matrix(cfg.wtype, w)
     x = synth.normal(cfg.M * cfg.K, cfg.x_seed).reshape(cfg.M, cfg.K)
-    nt = threads or min(16, os.cpu_count() or 1)
-    O.mul_mat(cfg.wtype, wq, x, nthreads=nt, want_l1=False)  # warm
+    if cfg.n_outliers:
+        for m in range(cfg.M):
+            synth.set_outliers(x[m], cfg.n_outliers, cfg.outlier_value, cfg.x_seed + 17 * m)
+    # one worker per physical core, within the box's CPU share of 16
+    nt = threads or min(16, host["physical_cores"])
+    cpus = host["cpus"][:nt] if len(host["cpus"]) >= nt else None
+    isa = O.simd_isa()
+    for _ in range(3):
+        O.simd_mul_mat(cfg.wtype, wq, x, nthreads=nt, cpus=cpus, isa=isa)
     times = []
     t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
+    while len(times) < 10 or time.perf_counter() < t_end:
         t0 = time.perf_counter()
-        O.mul_mat(cfg.wtype, wq, x, nthreads=nt, want_l1=False)
+        O.simd_mul_mat(cfg.wtype, wq, x, nthreads=nt, cpus=cpus, isa=isa)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
-    wbytes = wq.nbytes
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
-    except OSError:
-        pass
-    return {"value": wbytes / med / 1e9, "unit": "GB/s", "cores": nt, "kind": "port",
-            "sample": f"config {cfg.index} full ({cfg.M}x{cfg.N}x{cfg.K} {cfg.name}): quantize X once + "
-                      f"row-partitioned scalar vec_dot (oracle/dcq_oracle.c), {len(times)} runs over "
-                      f"{sum(times):.1f} s, median {med * 1e3:.2f} ms",
-            "host_cpu": model, "nproc": os.cpu_count()}
+    if cfg.bound == "hbm":
+        value, unit = wq.nbytes / med / 1e9, "GB/s"
+    else:
+        value, unit = 2.0 * cfg.M * cfg.N * cfg.K / med / 1e12, "TOPS"
+    return {"value": value, "unit": unit, "cores": nt, "kind": "port",
+            "sample": f"config {cfg.index} in full ({cfg.M}x{cfg.N}x{cfg.K} {dc_type_name(cfg.wtype)}): CPU restatement "
+                      f"(not ggml) of the reference path, quantize X once + row-partitioned {O.ISA_NAMES[isa]} "
+                      f"vec_dots on {nt} workers pinned to distinct physical cores; median of {len(times)} runs "
+                      f"({sum(times):.1f} s), {med * 1e3:.3f} ms per run",
+            "ms_per_run": med * 1e3, "isa": O.ISA_NAMES[isa], "host_cpu": host["model"],
+            "physical_cores": host["physical_cores"], "logical_cpus": host["logical_cpus"], "nproc": host["nproc"]}
+
+
+def dc_type_name(t):
+    import densecore_amd as dc
+    return dc.TYPE_NAMES[t]
 
 
 def main():
     args = parse()
+    if args.summarize_pmc:
+        print(summarize_pmc(args.summarize_pmc))
+        return 0
+    if args.summarize_read:
+        print(summarize_read(args.summarize_read, [int(c) for c in args.configs.split(",") if c.strip()],
+                             args.warmup + args.steps))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
               "Run with --gpus 1.", file=sys.stderr)
@@ -486,6 +761,9 @@ def main():
             if c.index in wanted:
                 profile_config(c, args, dev)
         calibration_copy(dev)
+        return 0
+    if args.profile_read:
+        profile_read(args, dev)
         return 0
     results = []
     for c in dc.CONFIGS:
@@ -546,7 +824,13 @@ def main():
         "extras": extras,
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(hcfg, args.cpu_seconds, args.cpu_threads)
+        host = host_cpu_info()
+        for r in results:
+            if r["config"] in (HEADLINE, 5):
+                cb = r["cpu_baseline"] = cpu_baseline(dc.by_index(r["config"]), args.cpu_seconds, args.cpu_threads, host)
+                print(f"# CPU baseline config {r['config']}: {cb['value']:.3g} {cb['unit']} on {cb['cores']} cores "
+                      f"({cb['ms_per_run']:.3f} ms per run)", file=sys.stderr, flush=True)
+        line["cpu_baseline"] = head.get("cpu_baseline")
     print(json.dumps(line))
     return 0
 

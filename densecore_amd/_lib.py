@@ -19,6 +19,7 @@ SYMBOLS = [
     "dcq_gguf_open", "dcq_gguf_close", "dcq_gguf_tensor_count", "dcq_gguf_find_tensor", "dcq_gguf_tensor_info",
     "dcq_gguf_get_int", "dcq_gguf_get_str", "dcq_gguf_load_tensor",
     "dcq_kv_slot_bytes", "dcq_kv_write", "dcq_kv_gather", "dcq_kv_attention_workspace_size", "dcq_kv_attention",
+    "dcq_probe_stream_read",  # include/dcq_probe.h: measurement aid
 ]
 
 KV_BLOCK_SIZE = 16
@@ -86,6 +87,7 @@ def lib():
             "dcq_kv_attention_workspace_size": (sz, [i32, i32, i32, i64, i64]),
             "dcq_kv_attention": (i32, [i32, vp, vp, i64, i32, i32, vp, i64, i32, i32, i32, vp, sz, vp, vp, sz,
                                        i64, i64, ctypes.c_float, vp, sz, vp, sz, vp]),
+            "dcq_probe_stream_read": (i32, [vp, sz, i32, i32, vp, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -417,3 +419,9 @@ class PagedKVCache:
 def kv_attention_workspace_size(n_head, n_head_kv, head_dim, n_tokens, n_past):
     return int(lib().dcq_kv_attention_workspace_size(n_head, n_head_kv, head_dim, n_tokens, n_past))
 
+
+# ---------------------------------------------------------------- measurement aid (include/dcq_probe.h)
+def probe_stream_read(src, nbytes, per_lane, max_workgroups, sink, stream=None):
+    """Read nbytes of the device tensor src with the pure streaming kernel (no result)."""
+    _check("dcq_probe_stream_read", lib().dcq_probe_stream_read(_ptr(src), nbytes, per_lane, max_workgroups,
+                                                                _ptr(sink), _stream(stream)))

@@ -53,6 +53,10 @@ def lib():
             "dcqo_block_sums_bruteforce": (i32, [i32, i64, vp, vp, vp]),
             "dcqo_dot_rows": (i32, [i32, vp, sz, vp, i64, vp, i64, i64]),
             "dcqo_mul_mat": (i32, [i32, vp, i64, i64, sz, vp, i64, i64, vp, i64, vp, i32, i32]),
+            "dcqs_isa": (i32, []),
+            "dcqs_vec_dot": (fp, [i32, i32, i64, vp, vp]),
+            "dcqs_physical_cpus": (i32, [vp, i32, vp]),
+            "dcqs_mul_mat": (i32, [i32, i32, vp, i64, i64, sz, vp, i64, i64, vp, i64, i32, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -253,3 +257,45 @@ def assert_close(y, y_ref, l1, rtol=1e-4, what=""):
             f"got {y[tuple(idx[0])]}, want {y_ref[tuple(idx[0])]}, bound {bound[tuple(idx[0])]}")
     rel = err / np.maximum(np.abs(y_ref), 1e-30)
     return float(np.max(err / np.maximum(bound / rtol, 1e-30))), float(np.median(rel))
+
+
+# ---------------------------------------------------------------- SIMD CPU restatement (the timed baseline)
+ISA_SCALAR, ISA_AVX2, ISA_AVX512VNNI = 0, 1, 2
+ISA_NAMES = {ISA_SCALAR: "scalar", ISA_AVX2: "AVX2 (vpmaddubsw/vpmaddwd)",
+             ISA_AVX512VNNI: "AVX-512 VNNI (vpdpbusd) for Q8_0, AVX2 for Q4_K/Q6_K"}
+
+
+def simd_isa():
+    """The widest int8 dot the host CPU supports (CPUID at run time)."""
+    return int(lib().dcqs_isa())
+
+
+def simd_vec_dot(isa, wt, k, w_row, xq_row):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
+    return float(lib().dcqs_vec_dot(isa, wt, k, _p(w_row), _p(xq_row)))
+
+
+def physical_cpus(limit=4096):
+    """(logical CPUs to pin one worker per physical core, logical CPUs in the affinity mask)."""
+    cpus = np.zeros(limit, dtype=np.int32)
+    logical = ctypes.c_int(0)
+    n = lib().dcqs_physical_cpus(_p(cpus), limit, ctypes.byref(logical))
+    return (cpus[:max(n, 0)].tolist(), logical.value)
+
+
+def simd_mul_mat(wt, wq, x, nthreads=1, cpus=None, isa=-1):
+    """The timed CPU baseline: quantize every X row once, then row-partitioned SIMD vec_dots on
+    nthreads workers (pinned to `cpus` when given). Y [m, n] float32."""
+    wq = np.ascontiguousarray(wq, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    m, k = x.shape
+    n = wq.shape[0]
+    y = np.zeros((m, n), dtype=np.float32)
+    cp = np.ascontiguousarray(cpus, dtype=np.int32) if cpus is not None else None
+    rc = lib().dcqs_mul_mat(isa, wt, _p(wq), n, k, wq.shape[1], _p(x), m, k, _p(y), n, nthreads,
+                            _p(cp) if cp is not None else None)
+    assert rc == 0, rc
+    return y
