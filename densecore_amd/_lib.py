@@ -149,12 +149,41 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
 
 
+def _need(name, t, dtype, ndim=(1, 2), cuda=True):
+    """Raise ValueError unless t is a tensor of `dtype` with a dimension count in `ndim`, on a GPU
+    (when `cuda`), whose last dimension is contiguous: the ABI takes raw pointers and row strides,
+    so anything else would be read as the wrong bytes."""
+    import torch
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name}: expected a torch tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if t.dim() not in ndim:
+        raise ValueError(f"{name}: {t.dim()} dimensions, expected {' or '.join(map(str, ndim))}")
+    if t.numel() > 1 and t.stride(-1) != 1:
+        raise ValueError(f"{name}: last dimension has stride {t.stride(-1)}, expected 1")
+    if cuda and not t.is_cuda:
+        raise ValueError(f"{name}: tensor on {t.device}, expected a GPU tensor")
+
+
+def _f32(name, t, ndim=(2,)):
+    import torch
+    _need(name, t, torch.float32, ndim)
+
+
+def _u8(name, t, ndim=(1, 2)):
+    import torch
+    _need(name, t, torch.uint8, ndim)
+
+
 def quantize_rows(vdt, x, out=None, stream=None):
     """x: float32 cuda [M, K] -> uint8 cuda [M, row_size(vdt, K)] in ggml block layout."""
     import torch
+    _f32("x", x)
     m, k = x.shape
     if out is None:
         out = torch.empty((m, row_size(vdt, k)), dtype=torch.uint8, device=x.device)
+    _u8("out", out)
     _check("dcq_quantize_rows", lib().dcq_quantize_rows(vdt, _ptr(x), m, k, x.stride(0) * 4, _ptr(out),
                                                         _stream(stream)))
     return out
@@ -164,10 +193,15 @@ def mul_mat_ex(wt, wq, n, k, x, y=None, workspace=None, path=PATH_AUTO, block_su
                stream=None):
     """Y[M, N] = W[N, K] (quantized rows, uint8 cuda) x X[M, K]^T (float32 cuda)."""
     import torch
+    _u8("wq", wq)
+    _f32("x", x)
     m = x.shape[0]
     if y is None:
         y = torch.empty((m, n), dtype=torch.float32, device=x.device)
     wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    _f32("y", y)
+    if block_sums is not None:
+        _need("block_sums", block_sums, torch.int32, (1, 2, 3))
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check("dcq_mul_mat_ex", lib().dcq_mul_mat_ex(
         wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace), ws_bytes,
@@ -177,10 +211,13 @@ def mul_mat_ex(wt, wq, n, k, x, y=None, workspace=None, path=PATH_AUTO, block_su
 
 def mul_mat(wt, wq, n, k, x, y=None, workspace=None, w_row_bytes=None, stream=None):
     import torch
+    _u8("wq", wq)
+    _f32("x", x)
     m = x.shape[0]
     if y is None:
         y = torch.empty((m, n), dtype=torch.float32, device=x.device)
     wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    _f32("y", y)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check("dcq_mul_mat", lib().dcq_mul_mat(
         wt, _ptr(wq), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace), ws_bytes,
@@ -194,6 +231,9 @@ NOALLOC_SCRATCH_BYTES = 8 << 20  # DCQ_NOALLOC_SCRATCH_BYTES
 def mul_mat_noalloc(wt, wq, n, k, x, y, w_row_bytes=None, stream=None):
     """dcq_mul_mat_noalloc: dcq_mul_mat with the library's static device scratch as workspace
     (no allocation on the library side; y must be given)."""
+    _u8("wq", wq)
+    _f32("x", x)
+    _f32("y", y)
     m = x.shape[0]
     wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
     _check("dcq_mul_mat_noalloc", lib().dcq_mul_mat_noalloc(
@@ -209,9 +249,13 @@ def mul_mat_add(wt, wq, n, k, x, r, y=None, workspace=None, w_row_bytes=None, st
     """Y[M, N] = W x + R: a projection and its residual (R [M, N], may be y itself) or bias (R [N],
     broadcast over the rows)."""
     import torch
+    _u8("wq", wq)
+    _f32("x", x)
+    _f32("r", r, (1, 2))
     m = x.shape[0]
     if y is None:
         y = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    _f32("y", y)
     r_stride = 0 if r.dim() == 1 else r.stride(0) * 4
     wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
@@ -228,10 +272,14 @@ def ffn_gate_up_workspace_size(wt, m, n, k):
 def ffn_gate_up(wt, wg, wu, n, k, x, y=None, workspace=None, w_row_bytes=None, stream=None):
     """Y[M, N] = silu(Wg x) * (Wu x): the SwiGLU gate/up pair with one activation quantization."""
     import torch
+    _u8("wg", wg)
+    _u8("wu", wu)
+    _f32("x", x)
     m = x.shape[0]
     if y is None:
         y = torch.empty((m, n), dtype=torch.float32, device=x.device)
     wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    _f32("y", y)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check("dcq_ffn_gate_up", lib().dcq_ffn_gate_up(
         wt, _ptr(wg), _ptr(wu), n, k, wrb, _ptr(x), m, x.stride(0) * 4, _ptr(y), y.stride(0) * 4, _ptr(workspace),
@@ -305,6 +353,8 @@ class GGUF:
 def dot_rows(wt, wq, xq_row, k, n0, n1, y=None, w_row_bytes=None, stream=None):
     """ComputeDotProductBatch: y[r - n0] = vec_dot(W row r, xq_row), xq_row pre-quantized (ggml layout)."""
     import torch
+    _u8("wq", wq)
+    _u8("xq_row", xq_row)
     if y is None:
         y = torch.empty((max(n1 - n0, 0),), dtype=torch.float32, device=wq.device)
     wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
@@ -316,6 +366,9 @@ def dot_rows(wt, wq, xq_row, k, n0, n1, y=None, w_row_bytes=None, stream=None):
 def quantize_weights(wt, w, out=None, stream=None):
     """w: float32 cuda [N, K] -> uint8 cuda [N, row_size(wt, K)] (ggml_quantize_chunk)."""
     import torch
+    _f32("w", w)
+    if not w.is_contiguous():
+        raise ValueError("w: rows must be packed (contiguous)")
     n, k = w.shape
     if out is None:
         out = torch.empty((n, row_size(wt, k)), dtype=torch.uint8, device=w.device)
@@ -325,6 +378,7 @@ def quantize_weights(wt, w, out=None, stream=None):
 
 def dequantize_rows(t, wq, n, k, y=None, w_row_bytes=None, stream=None):
     import torch
+    _u8("wq", wq)
     if y is None:
         y = torch.empty((n, k), dtype=torch.float32, device=wq.device)
     wrb = w_row_bytes if w_row_bytes is not None else row_size(t, k)
@@ -334,6 +388,8 @@ def dequantize_rows(t, wq, n, k, y=None, w_row_bytes=None, stream=None):
 
 def quantize_src1(wt, x, workspace, stream=None):
     """Quantize X [M, K] once into `workspace` (uint8 cuda, mul_mat_workspace_size bytes)."""
+    _f32("x", x)
+    _u8("workspace", workspace, (1,))
     m, k = x.shape
     _check("dcq_quantize_src1", lib().dcq_quantize_src1(wt, _ptr(x), m, k, x.stride(0) * 4, _ptr(workspace),
                                                         workspace.numel(), _stream(stream)))
@@ -343,6 +399,8 @@ def quantize_src1(wt, x, workspace, stream=None):
 def mul_mat_q(wt, wq, n, k, workspace, m, y=None, path=PATH_AUTO, w_row_bytes=None, stream=None):
     """Y[M, N] from W and activations already quantized by quantize_src1 into `workspace`."""
     import torch
+    _u8("wq", wq)
+    _u8("workspace", workspace, (1,))
     if y is None:
         y = torch.empty((m, n), dtype=torch.float32, device=wq.device)
     wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
@@ -379,6 +437,9 @@ class PagedKVCache:
 
     def write(self, which, layer, table, pos0, rows, stream=None):
         """WriteKSlot / WriteVSlot for rows [N, row_elems] at positions pos0 .. pos0 + N - 1."""
+        import torch
+        _f32("rows", rows, (1, 2))
+        _need("table", table, torch.int32, (1,))
         _check("dcq_kv_write", lib().dcq_kv_write(
             self.cache_type, _ptr(self._arena(which)), self.n_blocks, self.n_layer, layer, self.row_elems,
             _ptr(table), table.numel(), pos0, _ptr(rows), rows.stride(0) * 4 if rows.dim() == 2 else 0,
@@ -387,9 +448,13 @@ class PagedKVCache:
     def gather(self, which, layer, table, n_past, cur, out=None, stream=None):
         """[n_past + N, row_elems] fp32: history from the cache, then cur (cb_kv_update_and_gather)."""
         import torch
+        _f32("cur", cur)
+        if table is not None:
+            _need("table", table, torch.int32, (1,))
         n = cur.shape[0]
         if out is None:
             out = torch.empty((n_past + n, self.row_elems), dtype=torch.float32, device=cur.device)
+        _f32("out", out)
         _check("dcq_kv_gather", lib().dcq_kv_gather(
             self.cache_type, _ptr(self._arena(which)), self.n_blocks, self.n_layer, layer, self.row_elems,
             _ptr(table), table.numel() if table is not None else 0, n_past, _ptr(cur), cur.stride(0) * 4, n,
@@ -400,10 +465,18 @@ class PagedKVCache:
         """q [N, n_head * head_dim] fp32 -> out [N, n_head * head_dim]: causal attention of the N
         batch tokens (positions n_past ..) over the cached history and their own k_cur / v_cur rows."""
         import torch
+        if k_cur.stride(0) != v_cur.stride(0):
+            raise ValueError(f"k_cur and v_cur must share a row stride (the ABI takes one): "
+                             f"{k_cur.stride(0)} != {v_cur.stride(0)}")
+        for name, t in (("q", q), ("k_cur", k_cur), ("v_cur", v_cur)):
+            _f32(name, t)
+        if table is not None:
+            _need("table", table, torch.int32, (1,))
         n = q.shape[0]
         n_head = q.shape[1] // self.head_dim
         if out is None:
             out = torch.empty((n, n_head * self.head_dim), dtype=torch.float32, device=q.device)
+        _f32("out", out)
         need = kv_attention_workspace_size(n_head, self.n_head_kv, self.head_dim, n, n_past)
         if workspace is None and need:
             workspace = torch.empty(need, dtype=torch.uint8, device=q.device)

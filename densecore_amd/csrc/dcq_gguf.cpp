@@ -189,7 +189,8 @@ int parse(dcq_gguf* g) {
             return DCQ_ERR_FORMAT;
         }
         if (!r.ok) return DCQ_ERR_FORMAT;
-        g->kv[key] = v;
+        // a key may appear once (gguf_init_from_file rejects duplicates as well)
+        if (!g->kv.emplace(key, v).second) return DCQ_ERR_FORMAT;
     }
     auto al = g->kv.find("general.alignment");
     if (al != g->kv.end()) {
@@ -240,9 +241,13 @@ int dcq_gguf_open(const char* path, dcq_gguf** out) {
     const int fd = open(path, O_RDONLY | O_CLOEXEC);
     if (fd < 0) return DCQ_ERR_IO;
     struct stat st;
-    if (fstat(fd, &st) != 0 || st.st_size < 24) {
+    if (fstat(fd, &st) != 0) {
         close(fd);
-        return st.st_size < 24 ? DCQ_ERR_FORMAT : DCQ_ERR_IO;
+        return DCQ_ERR_IO;
+    }
+    if (st.st_size < 24) {
+        close(fd);
+        return DCQ_ERR_FORMAT;
     }
     void* map = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
     if (map == MAP_FAILED) {

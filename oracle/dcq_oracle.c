@@ -286,9 +286,13 @@ void dcqo_quantize_row_q8_0_weights(const float* x, void* y, int64_t k) {
     dcqo_quantize_row_q8_0(x, y, k, DCQO_Q8_0_REF);
 }
 
-/* weighted least-squares fit of x ~ scale*L + min, L in [0,nmax], min <= 0 */
+/* weighted least-squares fit of x ~ scale*L + min, L in [0,nmax], min <= 0: the best of the
+ * rounding at iscale = nmax/(max-min) and the nstep+1 grid points iscale = (rmin + rdelta*is +
+ * nmax)/(max-min), each refitted by weighted least squares (min clamped to <= 0).
+ * flags (test hooks only, 0 in the quantizers): DCQO_PLANT_NO_MIN_CLAMP drops the clamp of the
+ * refitted min. */
 static float make_qkx2_quants(int n, int nmax, const float* x, const float* weights, uint8_t* L,
-                              float* the_min, uint8_t* Laux, float rmin, float rdelta, int nstep) {
+                              float* the_min, uint8_t* Laux, float rmin, float rdelta, int nstep, int flags) {
     float min = x[0], max = x[0];
     float sum_w = weights[0];
     float sum_x = sum_w * x[0];
@@ -330,7 +334,7 @@ static float make_qkx2_quants(int n, int nmax, const float* x, const float* weig
         if (D > 0) {
             float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
             float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
-            if (this_min > 0) {
+            if (this_min > 0 && !(flags & DCQO_PLANT_NO_MIN_CLAMP)) {
                 this_min = 0;
                 this_scale = sum_xl / sum_l2;
             }
@@ -349,6 +353,23 @@ static float make_qkx2_quants(int n, int nmax, const float* x, const float* weig
     }
     *the_min = -min;
     return scale;
+}
+
+/* the 12-byte packing of eight 6-bit (scale, min) pairs that get_scale_min_k4 reads back:
+ * j < 4 in the low 6 bits of bytes j and j+4; j >= 4 as nibbles of byte j+4, with their top two
+ * bits in the high bits of bytes j-4 (scale) and j (min) */
+void dcqo_pack_scale_min_k4(const uint8_t ls[8], const uint8_t lm[8], uint8_t s[12]) {
+    memset(s, 0, 12);
+    for (int j = 0; j < 8; ++j) {
+        if (j < 4) {
+            s[j] = ls[j];
+            s[j + 4] = lm[j];
+        } else {
+            s[j + 4] = (uint8_t)((ls[j] & 0xF) | ((lm[j] & 0xF) << 4));
+            s[j - 4] |= (uint8_t)((ls[j] >> 4) << 6);
+            s[j - 0] |= (uint8_t)((lm[j] >> 4) << 6);
+        }
+    }
 }
 
 static void get_scale_min_k4(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
@@ -374,27 +395,20 @@ void dcqo_quantize_row_q4_K(const float* x, void* vy, int64_t k) {
             float av_x = sqrtf(sum_x2 / 32);
             for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
             scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux,
-                                         -1.f, 0.1f, 20);
+                                         -1.f, 0.1f, 20, 0);
             if (scales[j] > max_scale) max_scale = scales[j];
             if (mins[j] > max_min) max_min = mins[j];
         }
         float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
         float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
-        memset(y[i].scales, 0, 12);
+        uint8_t ls[QK_K / 32], lm[QK_K / 32];
         for (int j = 0; j < QK_K / 32; ++j) {
-            int ls = nearest_int(inv_scale * scales[j]);
-            int lm = nearest_int(inv_min * mins[j]);
-            ls = ls < 63 ? ls : 63;
-            lm = lm < 63 ? lm : 63;
-            if (j < 4) {
-                y[i].scales[j] = (uint8_t)ls;
-                y[i].scales[j + 4] = (uint8_t)lm;
-            } else {
-                y[i].scales[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
-                y[i].scales[j - 4] |= (uint8_t)((ls >> 4) << 6);
-                y[i].scales[j - 0] |= (uint8_t)((lm >> 4) << 6);
-            }
+            const int a = nearest_int(inv_scale * scales[j]);
+            const int b = nearest_int(inv_min * mins[j]);
+            ls[j] = (uint8_t)(a < 63 ? a : 63);
+            lm[j] = (uint8_t)(b < 63 ? b : 63);
         }
+        dcqo_pack_scale_min_k4(ls, lm, y[i].scales);
         y[i].d = dcqo_fp32_to_fp16(max_scale / 63.f);
         y[i].dmin = dcqo_fp32_to_fp16(max_min / 63.f);
         for (int j = 0; j < QK_K / 32; ++j) {
@@ -417,8 +431,12 @@ void dcqo_quantize_row_q4_K(const float* x, void* vy, int64_t k) {
     }
 }
 
-/* least-squares symmetric fit, L in [-nmax, nmax-1] stored offset by nmax */
-static float make_qx_quants(int n, int nmax, const float* x, int8_t* L) {
+/* least-squares symmetric fit, L in [-nmax, nmax-1] stored offset by nmax: the best, by the
+ * x^2-weighted fit quality (sum w x l)^2 / sum w l^2, of the rounding at iscale = -nmax/max and at
+ * iscale = -(nmax + 0.1*is)/max for is in [-9, 9], is != 0.
+ * flags (test hooks only, 0 in the quantizer): DCQO_PLANT_UNIT_WEIGHTS weighs every element 1,
+ * DCQO_PLANT_GRID_8 searches is in [-8, 8] only. */
+static float make_qx_quants(int n, int nmax, const float* x, int8_t* L, int flags) {
     float max = 0, amax = 0;
     for (int i = 0; i < n; ++i) {
         float ax = fabsf(x[i]);
@@ -437,20 +455,21 @@ static float make_qx_quants(int n, int nmax, const float* x, int8_t* L) {
         int l = nearest_int(iscale * x[i]);
         l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
         L[i] = (int8_t)(l + nmax);
-        float w = x[i] * x[i];
+        float w = (flags & DCQO_PLANT_UNIT_WEIGHTS) ? 1.0f : x[i] * x[i];
         sumlx += w * x[i] * l;
         suml2 += w * l * l;
     }
     float scale = suml2 ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx;
-    for (int is = -9; is <= 9; ++is) {
+    const int grid = (flags & DCQO_PLANT_GRID_8) ? 8 : 9;
+    for (int is = -grid; is <= grid; ++is) {
         if (is == 0) continue;
         iscale = -(nmax + 0.1f * is) / max;
         sumlx = suml2 = 0;
         for (int i = 0; i < n; ++i) {
             int l = nearest_int(iscale * x[i]);
             l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
-            float w = x[i] * x[i];
+            float w = (flags & DCQO_PLANT_UNIT_WEIGHTS) ? 1.0f : x[i] * x[i];
             sumlx += w * x[i] * l;
             suml2 += w * l * l;
         }
@@ -475,7 +494,7 @@ void dcqo_quantize_row_q6_K(const float* x, void* vy, int64_t k) {
     for (int64_t i = 0; i < nb; ++i) {
         float max_scale = 0, max_abs_scale = 0;
         for (int ib = 0; ib < QK_K / 16; ++ib) {
-            const float scale = make_qx_quants(16, 32, x + 16 * ib, L + 16 * ib);
+            const float scale = make_qx_quants(16, 32, x + 16 * ib, L + 16 * ib, 0);
             scales[ib] = scale;
             const float abs_scale = fabsf(scale);
             if (abs_scale > max_abs_scale) {
@@ -521,6 +540,18 @@ void dcqo_quantize_row_q6_K(const float* x, void* vy, int64_t k) {
         }
         x += QK_K;
     }
+}
+
+/* ---- test hooks: the quantizers' inner fits, for the optimality checks of the tests ---- */
+float dcqo_make_qkx2_quants(int n, int nmax, const float* x, const float* weights, uint8_t* L, float* the_min,
+                            float rmin, float rdelta, int nstep, int flags) {
+    uint8_t Laux[256];
+    if (n <= 0 || n > 256) return 0.0f;
+    return make_qkx2_quants(n, nmax, x, weights, L, the_min, Laux, rmin, rdelta, nstep, flags);
+}
+
+float dcqo_make_qx_quants(int n, int nmax, const float* x, int8_t* L, int flags) {
+    return make_qx_quants(n, nmax, x, L, flags);
 }
 
 /* ---- threaded matrix quantization (pure data-parallel over rows) ---- */

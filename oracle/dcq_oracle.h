@@ -23,11 +23,15 @@
  *     max |q| = 127, dequant error <= d/2, bsums invariant).
  *   - integer block sums: brute force in int64 from the dequantized integers.
  *   - fp32 vec_dot: fp64 dequantize-and-dot brute force.
+ *   - weight quantizers: each sub-block fit is the result of its grid search, recomputed
+ *     independently in the tests; packing inverts; final quants are nearest grid points.
  * "parity unpinned" (only an import of ggml could pin them; ggml is absent):
  *   - the exact fp32 summation order of ggml's SIMD vec_dot;
  *   - the choice between the two Q8_0 from_float variants (x86 SIMD vs ref);
- *   - byte-exactness of the Q4_K / Q6_K / Q8_0 weight quantizers
- *     (make_qkx2_quants / make_qx_quants) — used only to generate inputs.
+ *   - the Q8_K scale constant: iscale = -127/max (ggml's quantize_row_q8_K_ref in the
+ *     type-traits-cpu API era the reference's calls imply; older ggml used -128);
+ *   - the constants of the Q4_K / Q6_K weight quantizers' grid searches, and so their bytes
+ *     against a ggml build — used only to generate inputs.
  */
 #ifndef DCQ_ORACLE_H
 #define DCQ_ORACLE_H
@@ -80,6 +84,21 @@ void dcqo_quantize_row_q4_K(const float* x, void* y, int64_t k);
 void dcqo_quantize_row_q6_K(const float* x, void* y, int64_t k);
 /* quantize an [n][k] fp32 matrix to `type`, rows packed; nthreads <= 0 -> auto */
 int dcqo_quantize_matrix(int type, const float* x, int64_t n, int64_t k, void* y, int nthreads);
+
+/* ---- test hooks into the weight quantizers ----
+ * make_qkx2_quants (Q4_K, with the arguments ggml's quantize_row_q4_K_ref passes: nmax 15,
+ * rmin -1, rdelta 0.1, nstep 20) and make_qx_quants (Q6_K: nmax 32), and the Q4_K 6-bit scale/min
+ * packing. flags plant a mistake on purpose (DCQO_PLANT_*), so the tests can show that their
+ * optimality checks reject it; the quantizers always pass 0. */
+enum {
+    DCQO_PLANT_NO_MIN_CLAMP = 1,  /* make_qkx2_quants: refitted min may stay > 0 */
+    DCQO_PLANT_UNIT_WEIGHTS = 2,  /* make_qx_quants: weights 1 instead of x^2 */
+    DCQO_PLANT_GRID_8 = 4,        /* make_qx_quants: grid is in [-8, 8] instead of [-9, 9] */
+};
+float dcqo_make_qkx2_quants(int n, int nmax, const float* x, const float* weights, uint8_t* L, float* the_min,
+                            float rmin, float rdelta, int nstep, int flags);
+float dcqo_make_qx_quants(int n, int nmax, const float* x, int8_t* L, int flags);
+void dcqo_pack_scale_min_k4(const uint8_t ls[8], const uint8_t lm[8], uint8_t s[12]);
 
 /* ---- dequantization ---- */
 int dcqo_dequantize_row(int type, const void* x, float* y, int64_t k);

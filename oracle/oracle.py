@@ -53,6 +53,9 @@ def lib():
             "dcqo_block_sums_bruteforce": (i32, [i32, i64, vp, vp, vp]),
             "dcqo_dot_rows": (i32, [i32, vp, sz, vp, i64, vp, i64, i64]),
             "dcqo_mul_mat": (i32, [i32, vp, i64, i64, sz, vp, i64, i64, vp, i64, vp, i32, i32]),
+            "dcqo_make_qkx2_quants": (fp, [i32, i32, vp, vp, vp, ctypes.POINTER(fp), fp, fp, i32, i32]),
+            "dcqo_make_qx_quants": (fp, [i32, i32, vp, vp, i32]),
+            "dcqo_pack_scale_min_k4": (None, [vp, vp, vp]),
             "dcqs_isa": (i32, []),
             "dcqs_vec_dot": (fp, [i32, i32, i64, vp, vp]),
             "dcqs_physical_cpus": (i32, [vp, i32, vp]),
@@ -257,6 +260,37 @@ def assert_close(y, y_ref, l1, rtol=1e-4, what=""):
             f"got {y[tuple(idx[0])]}, want {y_ref[tuple(idx[0])]}, bound {bound[tuple(idx[0])]}")
     rel = err / np.maximum(np.abs(y_ref), 1e-30)
     return float(np.max(err / np.maximum(bound / rtol, 1e-30))), float(np.median(rel))
+
+
+# ---------------------------------------------------------------- weight-quantizer test hooks
+PLANT_NO_MIN_CLAMP, PLANT_UNIT_WEIGHTS, PLANT_GRID_8 = 1, 2, 4
+
+
+def make_qkx2_quants(x, weights, nmax=15, rmin=-1.0, rdelta=0.1, nstep=20, flags=0):
+    """The Q4_K sub-block fit x ~ scale * L + min (min <= 0): returns (scale, min, L uint8)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    weights = np.ascontiguousarray(weights, dtype=np.float32)
+    L = np.zeros(x.size, dtype=np.uint8)
+    the_min = ctypes.c_float(0)
+    scale = lib().dcqo_make_qkx2_quants(x.size, nmax, _p(x), _p(weights), _p(L), ctypes.byref(the_min),
+                                        rmin, rdelta, nstep, flags)
+    return float(scale), -float(the_min.value), L
+
+
+def make_qx_quants(x, nmax=32, flags=0):
+    """The Q6_K group fit x ~ scale * (L - nmax): returns (scale, L - nmax as int)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    L = np.zeros(x.size, dtype=np.int8)
+    scale = lib().dcqo_make_qx_quants(x.size, nmax, _p(x), _p(L), flags)
+    return float(scale), L.astype(np.int64) - nmax
+
+
+def pack_scale_min_k4(ls, lm):
+    ls = np.ascontiguousarray(ls, dtype=np.uint8)
+    lm = np.ascontiguousarray(lm, dtype=np.uint8)
+    out = np.zeros(12, dtype=np.uint8)
+    lib().dcqo_pack_scale_min_k4(_p(ls), _p(lm), _p(out))
+    return out
 
 
 # ---------------------------------------------------------------- SIMD CPU restatement (the timed baseline)

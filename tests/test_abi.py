@@ -179,6 +179,40 @@ def test_mul_mat_add_workspace_and_validation():
         assert mma(rs=0) == NO_DEVICE             # bias broadcast
 
 
+def test_binding_checks_tensors_before_the_abi():
+    """The ctypes wrappers pass raw pointers and row strides, so a tensor of the wrong dtype, rank,
+    inner stride or device is refused before any call (a transposed or fp16 X would otherwise be
+    read as other bytes)."""
+    import torch
+    need = dc._lib._need
+    with pytest.raises(ValueError, match="dtype"):
+        need("x", torch.zeros((1, 256), dtype=torch.float16), torch.float32, (2,), cuda=False)
+    with pytest.raises(ValueError, match="stride"):
+        need("x", torch.zeros((256, 2)).t(), torch.float32, (2,), cuda=False)
+    with pytest.raises(ValueError, match="dimensions"):
+        need("x", torch.zeros(256), torch.float32, (2,), cuda=False)
+    need("x", torch.zeros((3, 256))[:, :128], torch.float32, (2,), cuda=False)  # padded rows are fine
+    if not torch.cuda.is_available():
+        with pytest.raises(ValueError, match="GPU"):
+            need("x", torch.zeros((1, 256)), torch.float32, (2,))
+    # every compute wrapper checks before calling the ABI
+    w = torch.zeros((4, 144), dtype=torch.uint8)
+    for bad in (torch.zeros((1, 256), dtype=torch.float16), torch.zeros((256, 2)).t(), torch.zeros(256)):
+        for fn in (lambda x: dc.mul_mat(12, w, 4, 256, x), lambda x: dc.mul_mat_ex(12, w, 4, 256, x),
+                   lambda x: dc.ffn_gate_up(12, w, w, 4, 256, x), lambda x: dc.quantize_rows(15, x),
+                   lambda x: dc.mul_mat_add(12, w, 4, 256, x, torch.zeros(4))):
+            with pytest.raises(ValueError):
+                fn(bad)
+    with pytest.raises(ValueError):
+        dc.quantize_weights(12, torch.zeros((4, 256), dtype=torch.float64))
+    cache = dc.PagedKVCache(8, 2, 1, 1, 64, device="cpu")
+    q, kc, vc = torch.zeros((1, 64)), torch.zeros((1, 64)), torch.zeros((1, 128))[:, :64]
+    with pytest.raises(ValueError, match="row stride"):
+        cache.attention(0, torch.zeros(2, dtype=torch.int32), q, kc, vc, 0, 0.125)
+    with pytest.raises(ValueError):
+        cache.write("k", 0, torch.zeros(2, dtype=torch.int64), 0, torch.zeros((1, 64)))
+
+
 def test_binding_raises_on_error():
     with pytest.raises(dc.DcqError):
         dc._lib._check("dcq_mul_mat", MISALIGNED)

@@ -134,7 +134,11 @@ def test_malformed_headers_and_tables(tmp_path):
     unknown_kv = b"GGUF" + struct.pack("<IQQ", 3, 0, 1) + struct.pack("<Q", 1) + b"k" + struct.pack("<I", 13) + bytes(8)
     assert rc(unknown_kv) == FORMAT                                            # unknown value type
     assert rc(build_gguf([("k", T_ARR, (T_STR, ["a"]))], [])[0]) == 0
+    # a metadata key given twice
+    assert rc(build_gguf([("k", T_U32, 1), ("k", T_U32, 2)], [("a", F32, [4], data)])[0]) == FORMAT
+    assert rc(build_gguf([("k", T_U32, 1), ("k2", T_U32, 2)], [("a", F32, [4], data)])[0]) == 0
     assert status_of(tmp_path / "does_not_exist.gguf") == IO
+    assert status_of(tmp_path) == IO                                           # a directory: no mapping
 
 
 def test_load_needs_room_and_an_index(tmp_path):

@@ -260,8 +260,8 @@ def test_dequantize_rows(O, dev, wt):
 # ---------------------------------------------------------------- BASELINE configurations
 @pytest.mark.parametrize("cfg", dc.CONFIGS, ids=lambda c: f"cfg{c.index}")
 def test_baseline_config_parity(O, dev, cfg):
-    """Full-size configs. 1-4: every output against the oracle. 5 (M = 2048): a sample of 24
-    activation rows against the oracle, plus the MMQ kernel against the GEMV kernel on all rows."""
+    """Full-size configs, every output against the oracle (config 5: all 2048 x 8192 outputs, so
+    every 128-row m-tile and every n-tile of the XCD band remap is covered)."""
     w = synth.normal(cfg.N * cfg.K, cfg.w_seed, 0.0, cfg.w_std).reshape(cfg.N, cfg.K)
     wq = O.quantize_matrix(cfg.wtype, w)
     x = synth.normal(cfg.M * cfg.K, cfg.x_seed).reshape(cfg.M, cfg.K)
@@ -269,22 +269,38 @@ def test_baseline_config_parity(O, dev, cfg):
         for m in range(cfg.M):
             synth.set_outliers(x[m], cfg.n_outliers, cfg.outlier_value, cfg.x_seed + 17 * m)
     wd, xd = to_dev(wq, dev), to_dev(x, dev)
+    print(f"config {cfg.index}: {cfg.name} M={cfg.M} N={cfg.N} K={cfg.K}", flush=True)
     y = to_host(dc.mul_mat(cfg.wtype, wd, cfg.N, cfg.K, xd))
-    if cfg.M <= 64:
-        y_ref, l1 = O.mul_mat(cfg.wtype, wq, x)
-        O.assert_close(y, y_ref, l1, RTOL, what=cfg.name)
-    else:
-        rows = np.linspace(0, cfg.M - 1, 24).astype(np.int64)
-        y_ref, l1 = O.mul_mat(cfg.wtype, wq, x[rows])
-        O.assert_close(y[rows], y_ref, l1, RTOL, what=cfg.name)
-        y_gemv = to_host(dc.mul_mat_ex(cfg.wtype, wd, cfg.N, cfg.K, xd, path=dc.PATH_GEMV))
-        # both kernels are within RTOL of the exact result, so within 2*RTOL of each other
-        err = np.abs(y - y_gemv)
-        scale = np.maximum(np.abs(y_gemv), np.median(l1))
-        assert np.max(err / scale) < 2 * RTOL, np.max(err / scale)
+    y_ref, l1 = O.mul_mat(cfg.wtype, wq, x)
+    O.assert_close(y, y_ref, l1, RTOL, what=cfg.name)
     # the GPU weight quantizer produces the same bytes as the oracle on the config shape
     if cfg.index in (1, 2, 3):
         assert np.array_equal(to_host(dc.quantize_weights(cfg.wtype, to_dev(w, dev))), wq)
+
+
+def test_config5_block_sums_full_shape_corner(O, dev):
+    """Config 5 at its full shape through dcq_mul_mat_ex with the per-block int32 sums dumped by
+    the production prefill kernel (the same tiling and XCD band remap): the last 8 activation
+    rows x the first and last 64 weight rows, bit for bit against the oracle's block sums."""
+    import torch
+    cfg = dc.by_index(5)
+    w = synth.normal(cfg.N * cfg.K, cfg.w_seed, 0.0, cfg.w_std).reshape(cfg.N, cfg.K)
+    wq = O.quantize_matrix(cfg.wtype, w)
+    x = synth.normal(cfg.M * cfg.K, cfg.x_seed).reshape(cfg.M, cfg.K)
+    per = dc.block_sums_per_row(cfg.wtype, cfg.K)
+    sums = torch.zeros((cfg.M, cfg.N, per), dtype=torch.int32, device=dev)  # 4.3 GB
+    y = dc.mul_mat_ex(cfg.wtype, to_dev(wq, dev), cfg.N, cfg.K, to_dev(x, dev), path=dc.PATH_AUTO, block_sums=sums)
+    rows = np.arange(cfg.M - 8, cfg.M)
+    cols = np.r_[0:64, cfg.N - 64:cfg.N]
+    got = to_host(sums[rows[0]:, :, :])[:, cols, :]
+    yc = to_host(y[rows[0]:, :])[:, cols]
+    del sums
+    torch.cuda.empty_cache()
+    xq = O.quantize_rows(O.vec_dot_type(cfg.wtype), x[rows])
+    want = O.block_sums_matrix(cfg.wtype, cfg.K, wq[cols], xq)
+    assert np.array_equal(got, want)
+    y_ref, l1 = O.mul_mat(cfg.wtype, wq[cols], x[rows])
+    O.assert_close(yc, y_ref, l1, RTOL, what="config 5 corner")
 
 
 # ---------------------------------------------------------------- split operator (shared quantization)
