@@ -11,9 +11,10 @@
 // int8 rows, Q8_0 weight block pairs re-sliced into int8 rows and fp32 scales, activation
 // scales) are issued before the current stage's MFMAs and land in the other half of a
 // double-buffered LDS tile. Activation rows and scales go global -> LDS directly
-// (global_load_lds_dwordx4, no registers in flight); weight block pairs pass through
-// registers to be re-sliced. LDS rows are 128 bytes whose 16-byte slots are XOR-swizzled
-// by row % 8, so the 32 rows a ds_read_b128 touches spread over the banks.
+// (global_load_lds_dwordx4 from a scalar base, no registers in flight); weight block pairs
+// pass through registers to be re-sliced, and the commit also stores each block's epilogue
+// constants (dW, -dW * 1.5*2^23) beside the quants. LDS rows are 128 bytes whose 16-byte slots
+// are XOR-swizzled by row % 8, so the 32 rows a ds_read_b128 touches spread over the banks.
 //
 // Epilogue per MFMA (16 values per lane; lane = one weight row n, 16 activation rows m):
 // the accumulator is seeded with the bit pattern of 1.5 * 2^23, so the int32 result read
@@ -22,6 +23,8 @@
 //   acc = fma(t, dA, acc)
 // two VALU ops per value per block — the bound of this kernel (VALU at 4 cycles per
 // wave64 op against 32 cycles per MFMA: 25 % of the int8 MFMA peak without packed fp32).
+// The seed is held in 16 VGPRs for the whole loop; everything else per block is the LDS
+// reads, four MFMAs and ~4 address instructions (about 37 VALU per MFMA over the kernel).
 //
 // Workgroup order is XCD-aware: consecutive workgroup ids go to different XCDs, so the
 // id is remapped to give each XCD a contiguous band of n tiles (its weight rows stay in
@@ -47,10 +50,10 @@ constexpr float kMagicF = 12582912.0f;
 constexpr int kXcds = 8;
 
 struct __align__(16) Stage {
-    int8_t a[kBM * kRow];  // activation int8, [m][k] (swizzled 16-byte slots)
-    int8_t b[kBN * kRow];  // weight int8, [n][k] (swizzled 16-byte slots)
-    float dw[kKB][kBN];    // weight block scales (fp16 widened)
-    float da[kKB][kBM];    // activation block scales
+    int8_t a[kBM * kRow];    // activation int8, [m][k] (swizzled 16-byte slots)
+    int8_t b[kBN * kRow];    // weight int8, [n][k] (swizzled 16-byte slots)
+    float2 dwc[kKB][kBN];    // per weight row and block: (dW, -dW * 1.5*2^23), the epilogue's constants
+    float da[kKB][kBM];      // activation block scales
 };
 
 // LDS byte offset of logical 16-byte slot `slot` (= 2*block + half) of tile row `row`.
@@ -58,17 +61,17 @@ __device__ __forceinline__ int swz(int row, int slot) { return row * kRow + 16 *
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// 16 bytes per lane from global memory straight into LDS at base + 16 * lane (base
-// wave-uniform, in M0): global_load_lds_dwordx4, no registers held while in flight.
-// Written as inline asm because the compiler's builtin form waits for every earlier
-// LDS-direct load before the next one (it cannot tell the destinations apart). The
-// compiler does not count these loads, so every call must precede the ordinary loads
-// of the same stage (loads retire in order, so its own vmcnt waits stay conservative),
-// and the stage ends with an explicit s_waitcnt vmcnt(0) before the barrier. M0 has no
-// other use in this kernel.
-__device__ __forceinline__ void dma16(const void* g, const void* lds_base) {
+// 16 bytes per lane from global memory (uniform base `g` + per-lane byte offset `off`) straight
+// into LDS at lds_base + 16 * lane (lds_base wave-uniform, in M0): global_load_lds_dwordx4 with an
+// SGPR base, so advancing a stage costs scalar adds only and no registers are held while the load
+// is in flight. Written as inline asm because the compiler's builtin form waits for every earlier
+// LDS-direct load before the next one (it cannot tell the destinations apart). The compiler does
+// not count these loads, so every call precedes the ordinary loads of the same stage (loads retire
+// in order, so its own vmcnt waits stay conservative), and the stage ends with an explicit
+// s_waitcnt vmcnt(0) before the barrier. M0 has no other use in this kernel.
+__device__ __forceinline__ void dma16(const void* g, uint32_t off, const void* lds_base) {
     const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(g), "s"(m0) : "memory", "m0");
 }
 
 __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
@@ -77,66 +80,9 @@ __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
 
 }  // namespace
 
-// fragments of one block for a wave's 2 x 2 MFMA tiles: A (2 m-tiles), B (2 n-tiles) and
-// the weight scales of the B rows
-struct Frag {
-    v4i a[2], b[2];
-    float dw[2];
-};
-
-__device__ __forceinline__ void load_frag(const Stage& S, int kb, int wm, int wn, int col, int hl, Frag& f) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        f.a[i] = *reinterpret_cast<const v4i*>(S.a + swz(wm + 32 * i + col, 2 * kb + hl));
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        f.b[j] = *reinterpret_cast<const v4i*>(S.b + swz(wn + 32 * j + col, 2 * kb + hl));
-        f.dw[j] = S.dw[kb][wn + 32 * j + col];
-    }
-}
-
-// One block's MFMAs and epilogue for the wave's 2 x 2 tiles.
-template <bool DUMP>
-__device__ __forceinline__ void block_step(const Stage& S, int kb, const Frag& f, const v16i& cmagic, int wm, int col,
-                                           int hl, float (&acc)[2][2][16], int32_t* sums, int m_base, int n_base,
-                                           int M, int N, int nkb, int kblk) {
-    float cw[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) cw[j] = -f.dw[j] * kMagicF;  // exact: 11-bit significand times 3*2^22
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const v16i D0 = mfma32(f.a[i], f.b[0], cmagic);
-        const v16i D1 = mfma32(f.a[i], f.b[1], cmagic);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 v4 = *reinterpret_cast<const float4*>(&S.da[kb][wm + 32 * i + 8 * q + 4 * hl]);
-            const float da4[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int v = 4 * q + e;
-                const float t0 = fmaf(__int_as_float(D0[v]), f.dw[0], cw[0]);
-                acc[i][0][v] = fmaf(t0, da4[e], acc[i][0][v]);
-                const float t1 = fmaf(__int_as_float(D1[v]), f.dw[1], cw[1]);
-                acc[i][1][v] = fmaf(t1, da4[e], acc[i][1][v]);
-            }
-        }
-        if (DUMP) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int n = n_base + 32 * j + col;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int m = m_base + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
-                    const int I = (j == 0 ? D0[v] : D1[v]) - kMagic;
-                    if (m < M && n < N) sums[((int64_t)m * N + n) * nkb + kblk] = I;
-                }
-            }
-        }
-    }
-}
-
 // W: Q8_0 rows (w_row_bytes % 4 == 0); xqs: int8 [M][K]; xd: float [K/32][m_ld]; K % 128 == 0.
-template <bool DUMP>
+// FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
+template <bool DUMP, bool FULL>
 __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                               int N, int K, const int8_t* __restrict__ xqs,
                                                               const float* __restrict__ xd, int64_t m_ld, int M,
@@ -159,44 +105,54 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
         tile_m = bid / tiles_n;
     }
     const int m0 = tile_m * kBM, n0 = tile_n * kBN;
-    const int nkb = K / 32;
     const int nstages = K / kKS;
 
-    // ---- staging assignment ----
+    // ---- staging assignment (per-lane byte offsets, fixed for the whole K loop) ----
     // activation rows: straight to LDS, 4 x 1 KB per wave per stage; instruction i of wave w
     // fills tile rows 8*(4w+i) .. +8, lane l the 16-byte slot (l % 8) of row 8*(4w+i) + l/8,
-    // which holds logical slot (l % 8) ^ (row % 8)
+    // which holds logical slot (l % 8) ^ (row % 8); rows past M clamp to M - 1
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    // instruction i: rows 8*(4w + i) + lane/8 share the slot pattern; one base row pointer,
-    // the other rows at +8*K per instruction (rows past M clamp to M - 1)
     const int a_row0 = 8 * (4 * wave_u) + (lane >> 3);
     const int a_slot = (lane & 7) ^ (a_row0 & 7);
+    uint32_t a_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = FULL ? m0 + a_row0 + 8 * i : min(m0 + a_row0 + 8 * i, M - 1);
+        a_off[i] = (uint32_t)row * (uint32_t)K + 16u * (uint32_t)a_slot;
+    }
     // activation scales: waves 0 and 1, one 1 KB instruction each: lane l of wave w holds
     // block (64w + l) / 32, rows 4 * ((64w + l) % 32) .. +4
     const int dc = 64 * (wave_u & 1) + lane;
-    const float* da_src = xd + (int64_t)(dc >> 5) * m_ld + m0 + 4 * (dc & 31);
-    // weight rows: row rw = tid / 2, block pair (tid & 1) * 2 of the stage (68 bytes), through
-    // registers (the 34-byte blocks are re-sliced into int8 rows and fp32 scales)
+    const uint32_t da_off = (uint32_t)(((int64_t)(dc >> 5) * m_ld + m0 + 4 * (dc & 31)) * 4);
+    // weight rows: row rw = tid / 2, block pair hw of the stage (68 bytes: d0, q0, d1, q1), through
+    // registers: q0 sits 2 bytes off a dword and is re-sliced; d1 and q1 start on dwords
     const int rw = tid >> 1, hw = tid & 1;
-    const uint8_t* w_src = W + (int64_t)min(n0 + rw, N - 1) * w_row_bytes + hw * 68;
+    const uint8_t* w_src = W + (int64_t)(FULL ? n0 + rw : min(n0 + rw, N - 1)) * w_row_bytes + hw * 68;
     uint32_t gw[17];
 #define DCQ_ISSUE(s_, S_)                                                                      \
     do {                                                                                       \
+        const int8_t* ab_ = xqs + (int64_t)(s_) * kKS;                                         \
         _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                                       \
-            dma16(xqs + (int64_t)min(m0 + a_row0 + 8 * i_, M - 1) * K + 16 * a_slot + (s_) * kKS, \
-                  (S_).a + 1024 * (4 * wave_u + i_));                                          \
-        if (wave_u < 2) dma16(da_src + (int64_t)(s_) * kKB * m_ld, &(S_).da[0][0] + 256 * wave_u); \
+            dma16(ab_, a_off[i_], (S_).a + 1024 * (4 * wave_u + i_));                          \
+        if (wave_u < 2) dma16(xd + (int64_t)(s_) * kKB * m_ld, da_off, &(S_).da[0][0] + 256 * wave_u); \
         const uint8_t* wp_ = w_src + (int64_t)(s_) * (kKB * 34);                               \
-        _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_) {                                     \
+        _Pragma("unroll") for (int i_ = 0; i_ < 2; ++i_) {                                     \
             const U32x4 v_ = ld4(wp_ + 16 * i_);                                               \
             gw[4 * i_] = v_.x;                                                                 \
             gw[4 * i_ + 1] = v_.y;                                                             \
             gw[4 * i_ + 2] = v_.z;                                                             \
             gw[4 * i_ + 3] = v_.w;                                                             \
         }                                                                                      \
-        gw[16] = ld1(wp_ + 64);                                                                \
+        gw[8] = ld1(wp_ + 32);                                                                 \
+        _Pragma("unroll") for (int i_ = 0; i_ < 2; ++i_) {                                     \
+            const U32x4 v_ = ld4(wp_ + 36 + 16 * i_);                                          \
+            gw[9 + 4 * i_] = v_.x;                                                             \
+            gw[10 + 4 * i_] = v_.y;                                                            \
+            gw[11 + 4 * i_] = v_.z;                                                            \
+            gw[12 + 4 * i_] = v_.w;                                                            \
+        }                                                                                      \
     } while (0)
-    // weight block pair bytes: [0,2) d0, [2,34) q0, [34,36) d1, [36,68) q1 (dword aligned);
+    // weight block pair bytes: [0,2) d0, [2,34) q0, [34,36) d1, [36,68) q1;
     // logical slots 4hw .. 4hw+3 of row rw
 #define DCQ_COMMIT(S_)                                                                         \
     do {                                                                                       \
@@ -208,8 +164,11 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
                        align_bytes(gw[7], gw[6], 2), align_bytes(gw[8], gw[7], 2));            \
         *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 2)) = make_uint4(gw[9], gw[10], gw[11], gw[12]); \
         *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 3)) = make_uint4(gw[13], gw[14], gw[15], gw[16]); \
-        (S_).dw[2 * hw][rw] = half_bits_to_float(gw[0] & 0xFFFFu);                            \
-        (S_).dw[2 * hw + 1][rw] = half_bits_to_float(gw[8] >> 16);                            \
+        const float d0_ = half_bits_to_float(gw[0] & 0xFFFFu);                                 \
+        const float d1_ = half_bits_to_float(gw[8] >> 16);                                     \
+        /* -dW * 1.5 * 2^23 is exact: an 11-bit significand times 3 * 2^22 */                  \
+        (S_).dwc[2 * hw][rw] = make_float2(d0_, -d0_ * kMagicF);                               \
+        (S_).dwc[2 * hw + 1][rw] = make_float2(d1_, -d1_ * kMagicF);                           \
     } while (0)
 
     // ---- wave tile: 64 x 64 at (wm, wn) inside the workgroup tile ----
@@ -218,6 +177,9 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
     v16i cmagic;
 #pragma unroll
     for (int v = 0; v < 16; ++v) cmagic[v] = kMagic;
+    // opaque to the compiler: it keeps the seed in 16 VGPRs for the whole loop instead of
+    // rematerialising it from scalar registers before every block (8 moves per block)
+    asm volatile("" : "+v"(cmagic));
     float acc[2][2][16];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -235,17 +197,62 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
         const Stage& S = st[s & 1];
         const bool more = s + 1 < nstages;
         if (more) DCQ_ISSUE(s + 1, st[(s + 1) & 1]);  // in flight while this stage computes
-        // software pipeline over the stage's blocks: the next block's fragments are read
-        // from LDS while this block's MFMAs and epilogue run (two named fragment sets)
-        Frag f0, f1;
-        load_frag(S, 0, wm, wn, col, hl, f0);
 #pragma unroll 1
-        for (int kb = 0; kb < kKB; kb += 2) {
-            load_frag(S, kb + 1, wm, wn, col, hl, f1);
-            block_step<DUMP>(S, kb, f0, cmagic, wm, col, hl, acc, sums, m0 + wm, n0 + wn, M, N, nkb, s * kKB + kb);
-            if (kb + 2 < kKB) load_frag(S, kb + 2, wm, wn, col, hl, f0);
-            block_step<DUMP>(S, kb + 1, f1, cmagic, wm, col, hl, acc, sums, m0 + wm, n0 + wn, M, N, nkb,
-                             s * kKB + kb + 1);
+        for (int kb = 0; kb < kKB; ++kb) {
+            // this lane's fragment rows wm + 32i + col and wn + 32j + col share row % 8 = col % 8, so
+            // the swizzled slot of block kb depends on (kb, hl, col) only; the rows are immediates
+            const int fo = col * kRow + 16 * ((2 * kb + hl) ^ (col & 7));
+            v4i fa[2], fb[2];
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const v4i*>(S.a + fo + (wm + 32 * ii) * kRow);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) fb[jj] = *reinterpret_cast<const v4i*>(S.b + fo + (wn + 32 * jj) * kRow);
+            float2 wc[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) wc[j] = S.dwc[kb][wn + 32 * j + col];
+            // the wave's 2 x 2 MFMAs, then their epilogues
+            v16i D[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) D[i][j] = mfma32(fa[i], fb[j], cmagic);
+            float4 da_v[2][4];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    da_v[i][q] = *reinterpret_cast<const float4*>(&S.da[kb][wm + 32 * i + 8 * q + 4 * hl]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v4 = da_v[i][q];
+                    const float da4[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int v = 4 * q + e;
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const float t = fmaf(__int_as_float(D[i][j][v]), wc[j].x, wc[j].y);
+                            acc[i][j][v] = fmaf(t, da4[e], acc[i][j][v]);
+                        }
+                    }
+                }
+            }
+            if (DUMP) {
+                const int kblk = s * kKB + kb, nkb = K / 32;
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int n = n0 + wn + 32 * j + col;
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int m = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
+                            if (m < M && n < N) sums[((int64_t)m * N + n) * nkb + kblk] = D[i][j][v] - kMagic;
+                        }
+                    }
+            }
         }
         if (more) {
             // the other buffer was last read in stage s - 1, which every wave finished before
@@ -258,17 +265,18 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
 #undef DCQ_ISSUE
 #undef DCQ_COMMIT
 
-    // ---- store: lane owns column n, rows m_v ----
+    // ---- store: lane owns column n, rows m_v = m0 + wm + 32i + 8(v/4) + 4hl + v%4; the row
+    // offsets beyond the lane's first row are uniform multiples of y_stride (scalar arithmetic) ----
+    float* yl = Y + (int64_t)(m0 + wm + 4 * hl) * y_stride + (n0 + wn + col);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn + 32 * j + col;
-        if (n >= N) continue;
+        if (!FULL && n0 + wn + 32 * j + col >= N) continue;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int m = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
-                if (m < M) Y[(int64_t)m * y_stride + n] = acc[i][j][v];
+                const int r = 32 * i + 8 * (v >> 2) + (v & 3);  // row within the wave tile, minus 4hl
+                if (FULL || m0 + wm + 4 * hl + r < M) yl[(int64_t)r * y_stride + 32 * j] = acc[i][j][v];
             }
     }
 }
@@ -278,9 +286,14 @@ size_t prefill_q8_0_lds_bytes() { return 2 * sizeof(Stage); }
 hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                                int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
     if (K % kKS || w_row_bytes % 4 || N > (1 << 30) || M > (1 << 30) || K > (1 << 30)) return hipErrorNotSupported;
+    // the DMA offsets are 32-bit: every activation row, weight row and scale row must lie within 4 GiB
+    if ((uint64_t)M * (uint64_t)K >= (1ull << 32) || (uint64_t)(K / 32) * (uint64_t)act.m_ld * 4 >= (1ull << 32))
+        return hipErrorNotSupported;
     const int tiles_n = (int)((N + kBN - 1) / kBN), tiles_m = (int)((M + kBM - 1) / kBM);
     const size_t lds = prefill_q8_0_lds_bytes();
-    auto fn = block_sums ? prefill_q8_0_kernel<true> : prefill_q8_0_kernel<false>;
+    const bool full = M % kBM == 0 && N % kBN == 0;
+    auto fn = block_sums ? (full ? prefill_q8_0_kernel<true, true> : prefill_q8_0_kernel<true, false>)
+                         : (full ? prefill_q8_0_kernel<false, true> : prefill_q8_0_kernel<false, false>);
     hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, (const uint8_t*)W, w_row_bytes,
                        (int)N, (int)K, act.qs, act.d, act.m_ld, (int)M, Y, y_stride, block_sums, tiles_n, tiles_m);
     return hipGetLastError();

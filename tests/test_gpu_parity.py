@@ -93,6 +93,9 @@ def test_quantize_rows_strided_input(O, dev):
 CASES = [
     (Q8_0, 1, 96, 1024), (Q8_0, 3, 70, 2048), (Q8_0, 1, 33, 96), (Q8_0, 2, 40, 160), (Q8_0, 40, 100, 512),
     (Q8_0, 130, 257, 256),
+    # the prefill kernel's unguarded variant (M and N multiples of its 128 x 128 tile), and more
+    # m-tiles: full, then ragged M and N
+    (Q8_0, 256, 384, 1024), (Q8_0, 512, 256, 512), (Q8_0, 700, 300, 640),
     (Q4_K, 1, 97, 2560), (Q4_K, 2, 64, 256), (Q4_K, 5, 40, 512), (Q4_K, 64, 96, 2048), (Q4_K, 70, 33, 768),
     # single-row decode at full width: 5-wave workgroups (rows spread evenly over the CUs)
     (Q4_K, 1, 9728, 2560), (Q4_K, 1, 2570, 4096), (Q4_K, 1, 2561, 9728),
