@@ -500,6 +500,44 @@ def bench_kv_attention(args, dev, ct, n_tokens=1, n_past=4095, n_layer=36, n_hea
                           "frac": flops / (ms * 1e-3) / 1e12 / 157.3})}
 
 
+def bench_lm_head(args, dev, wtype, K, M, N=151936):
+    """The LM head (ggml_mul_mat(output, cur), core/src/inference.cpp:1817), the largest weight
+    stream of a decode step: Qwen3's 151,936-token vocabulary, random valid quants (the kernels do
+    not depend on their values), W rotated over >= 1 GiB, with the pure-read time of the same bytes."""
+    import torch
+    import densecore_amd as dc
+    rb = dc.row_size(wtype, K)
+    wbytes = N * rb
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
+    big = torch.randint(0, 256, (copies, N, rb), dtype=torch.uint8, device=dev, generator=g)
+    bs = 34 if wtype == dc.TYPE_Q8_0 else 210
+    off = 0 if wtype == dc.TYPE_Q8_0 else 208
+    blocks = big.view(copies, N, rb // bs, bs)
+    half = torch.from_numpy(np.frombuffer(np.float16(0.0004).tobytes(), dtype=np.uint8).copy()).to(dev)
+    blocks[..., off:off + 2] = half
+    x = torch.randn((M, K), device=dev, generator=g)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ws = torch.empty(dc.mul_mat_workspace_size(wtype, M, K), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        dc.mul_mat(wtype, big[i % copies], N, K, x, y=y, workspace=ws, stream=torch.cuda.current_stream().cuda_stream)
+
+    ms, kern, _ = time_graph(step, args.steps, args.warmup, args.replays)
+    out = {"shape": f"{dc.TYPE_NAMES[wtype]} lm head N={N} K={K}, M={M}", "w_bytes": wbytes, "us": ms * 1e3,
+           "kernels": kern, "weight_GBps": wbytes / (ms * 1e-3) / 1e9,
+           "frac_of_peak": wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    if not args.no_read_ceiling:
+        c = read_ceiling(big.view(copies, -1), wbytes, copies, args)
+        out["read_ceiling_us"] = c["us"]
+        out["frac_of_read_ceiling"] = c["us"] / (ms * 1e3)
+    del big, ws, y, x
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_gguf_load(args, dev, mib=512):
     """GGUF ingest: a file of Q4_K tensors (mib MiB, in the page cache after it is written) loaded
     tensor by tensor into HBM with dcq_gguf_load_tensor; host-to-device GB/s (PCIe bound)."""
@@ -795,6 +833,12 @@ def main():
             e = extras[name] = bench_kv_attention(args, dev, **kw)
             print(f"# {name}: {e['us']:.2f} us ({e['kernels']} kernels), {e['GBps']:.0f} GB/s, "
                   f"{e['TFLOPs']:.2f} TFLOP/s", file=sys.stderr, flush=True)
+        for wt, K in ((dc.TYPE_Q8_0, 1024), (dc.TYPE_Q6_K, 2560)):
+            for M in (1, 4):
+                e = extras[f"lm_head_{dc.TYPE_NAMES[wt].lower()}_m{M}"] = bench_lm_head(args, dev, wt, K, M)
+                print(f"# {e['shape']}: {e['us']:.2f} us ({e['kernels']} kernels), {e['weight_GBps']:.0f} GB/s "
+                      f"({100 * e['frac_of_peak']:.1f} % of 8 TB/s; read ceiling {e.get('read_ceiling_us', 0):.2f} us)",
+                      file=sys.stderr, flush=True)
         extras["gguf_load"] = bench_gguf_load(args, dev)
         print(f"# GGUF ingest: {extras['gguf_load']['GBps']:.1f} GB/s host-to-HBM over "
               f"{extras['gguf_load']['bytes'] >> 20} MiB", file=sys.stderr, flush=True)

@@ -121,13 +121,15 @@ constexpr size_t kMaxLds = 160 * 1024;
 struct Q6Lds {
     int q_ld, b_ld, pitch;
     size_t act_bytes, total;
-    __host__ __device__ Q6Lds(int nsb, int MT, int nw) {
+    // nbuf: row images per wave (2 when a wave streams several rows: the next one lands while the
+    // current one computes)
+    __host__ __device__ Q6Lds(int nsb, int MT, int nw, int nbuf = 1) {
         q_ld = (int)round_up(256 * nsb, 1024);
         b_ld = (int)round_up(32 * nsb, 1024);
         // image at 16 - head (head < 16): 16 + 16-byte interior (1 KB pieces) + the tail dwords
         pitch = (int)round_up(16 + round_up(210 * nsb, 1024) + 256, 256);
         act_bytes = (size_t)MT * (q_ld + b_ld + 256);
-        total = act_bytes + (size_t)nw * pitch;
+        total = act_bytes + (size_t)nw * nbuf * pitch;
     }
 };
 
@@ -145,9 +147,10 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     const int8_t* __restrict__ xqs, const float* __restrict__ xd, const int16_t* __restrict__ xbs, int64_t m_ld,
     const float* __restrict__ X, int64_t x_stride,
     int M, float* Y, int64_t y_stride, int32_t* __restrict__ sums, int64_t sums_n_stride,
-    const float* R, int64_t r_stride) {
+    const float* R, int64_t r_stride, int rpw) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const Q6Lds L(nsb, MT, kWaves);
+    const int nbuf = rpw > 1 ? 2 : 1;
+    const Q6Lds L(nsb, MT, kWaves, nbuf);
     const int K = 256 * nsb;
     const int row_bytes = 210 * nsb, row_dw = row_bytes / 4;
     const int lane = threadIdx.x & 63;
@@ -155,9 +158,10 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     int8_t* aq = reinterpret_cast<int8_t*>(smem);
     int8_t* abb = reinterpret_cast<int8_t*>(smem + (size_t)MT * L.q_ld);
     float* ad = reinterpret_cast<float*>(smem + (size_t)MT * (L.q_ld + L.b_ld));
-    uint8_t* lw = smem + L.act_bytes + (size_t)wave * L.pitch;
-    const int64_t row = n0 + (int64_t)blockIdx.x * kWaves + wave;
-    const bool row_ok = row < n1;
+    uint8_t* const lw0 = smem + L.act_bytes + (size_t)wave * nbuf * L.pitch;
+    // this wave's rows: row0 + j * kWaves for j < rpw (for a fixed j the workgroup's waves read
+    // consecutive rows)
+    const int64_t row0 = n0 + (int64_t)blockIdx.x * kWaves * rpw + wave;
 
     // ---- 1. activation share: qs and bsums in 1 KB pieces, the scales gathered ----
 #pragma unroll
@@ -195,11 +199,36 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
 
     // ---- 2. this wave's row: head dwords, 16-byte interior, tail dwords ----
     // row byte b sits at img + b; img + head is 16-byte aligned like src + head
-    const uint8_t* src = W + (row_ok ? row : n1 - 1) * w_row_bytes;
-    const int head = (int)((16u - ((uint32_t)(uintptr_t)src & 15u)) & 15u);
-    uint8_t* img = lw + 16 - head;
-    const int nfull = (row_bytes - head) / 16;  // whole 16-byte chunks after the head
-    const int nx4 = (nfull + 63) / 64;
+    struct RowImg {
+        const uint8_t* src;
+        uint8_t* lw;
+        uint8_t* img;
+        int head, nfull, nx4, issued;
+    };
+    auto row_image = [&](int64_t row, uint8_t* lw) {
+        RowImg r;
+        r.src = W + (row < n1 ? row : n1 - 1) * w_row_bytes;
+        r.head = (int)((16u - ((uint32_t)(uintptr_t)r.src & 15u)) & 15u);
+        r.lw = lw;
+        r.img = lw + 16 - r.head;
+        r.nfull = (row_bytes - r.head) / 16;  // whole 16-byte chunks after the head
+        r.nx4 = (r.nfull + 63) / 64;
+        r.issued = r.nx4 + 2;  // every row load, in issue order: head, pieces, tail
+        return r;
+    };
+    const int tail0 = row_dw > 64 ? row_dw - 64 : 0;
+    auto issue_head = [&](const RowImg& r) { dma4(r.src + 4 * (lane < row_dw ? lane : row_dw - 1), r.img); };
+    auto issue_pieces = [&](const RowImg& r, int j0, int j1) {
+        for (int j = j0; j < j1; ++j) {
+            const int c = 64 * j + lane;
+            dma16(r.src + r.head + 16 * (c < r.nfull ? c : r.nfull - 1), r.lw + 16 + 1024 * j);
+        }
+    };
+    auto issue_tail = [&](const RowImg& r) {
+        dma4(r.src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), r.img + 4 * tail0);
+    };
+    RowImg cur = row_image(row0, lw0);
+    const int issued = cur.issued;
     // fused workgroups of 8+ waves (K > 4096): only the head and the first 40 % of the row go
     // out before the activation is waited for (fewer loads ahead of it), the rest once it is
     // quantized (measured at M = 1: 2560 x 9728 9.5 -> 8.7 us; with 4-wave workgroups rows of
@@ -209,15 +238,10 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     // every wave staging, the last-dispatched waves' activation landed about 1.1 us after
     // the first's, and the barrier waited for them).
     constexpr bool split = FUSE && kWaves > 4;
-    const int n_early = split && stager ? (2 * nx4) / 5 : nx4;
-    dma4(src + 4 * (lane < row_dw ? lane : row_dw - 1), img);
-    for (int j = 0; j < n_early; ++j) {
-        const int c = 64 * j + lane;
-        dma16(src + head + 16 * (c < nfull ? c : nfull - 1), lw + 16 + 1024 * j);
-    }
-    const int tail0 = row_dw > 64 ? row_dw - 64 : 0;
-    if (!split || !stager) dma4(src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), img + 4 * tail0);
-    const int issued = nx4 + 2;  // every row load, in issue order: head, pieces, tail
+    const int n_early = split && stager ? (2 * cur.nx4) / 5 : cur.nx4;
+    issue_head(cur);
+    issue_pieces(cur, 0, n_early);
+    if (!split || !stager) issue_tail(cur);
     if (FUSE && stager) {
         // quantize the activation (QC passes of 4 * SW (superblock, row) pairs, one per 16-lane
         // group) while the row streams: wait for the activation loads only (issued before it)
@@ -246,88 +270,103 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
         }
         if constexpr (split) {
             __builtin_amdgcn_sched_barrier(0);
-            for (int j = n_early; j < nx4; ++j) {
-                const int c = 64 * j + lane;
-                dma16(src + head + 16 * (c < nfull ? c : nfull - 1), lw + 16 + 1024 * j);
-            }
-            dma4(src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), img + 4 * tail0);
+            issue_pieces(cur, n_early, cur.nx4);
+            issue_tail(cur);
         }
     } else {
         wait_vmcnt_rt<0, 63>(issued);  // the activation share (issued before the row) is in
     }
     __syncthreads();
 
-    // ---- 3. steps of 16 superblocks, each computed once its bytes are in ----
-    float acc[MT];
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
+    // ---- 3. per row: the next row's loads go out (two images per wave), then steps of 16
+    // superblocks, each computed once its bytes are in; then the row's sum over the wave ----
     const int c4 = lane & 3, h = c4 >> 1, lh = c4 & 1;
     const int nsteps = (nsb + kSbStep - 1) / kSbStep;
-    for (int k = 0; k < nsteps; ++k) {
-        // loads holding row bytes < 210*16*(k+1): the head and the 16-byte pieces up to that
-        // byte; the last step also needs the tail
-        const int endb = 3360 * (k + 1) < row_bytes ? 3360 * (k + 1) : row_bytes;
-        const int need = (endb - head + 1023) / 1024;
-        const int done = k == nsteps - 1 ? issued : 1 + (need < nx4 ? need : nx4);
-        wait_vmcnt_rt<0, 63>(issued - done);
-        const int s_raw = kSbStep * k + (lane >> 2);
-        const bool valid = s_raw < nsb;
-        const int s = valid ? s_raw : nsb - 1;
-        const uint8_t* sb = img + 210 * s;
-        uint32_t qa[4], qb[4], qh[4], scw[2];
-        lds16_a2(sb + 64 * h + 16 * lh, qa);
-        lds16_a2(sb + 64 * h + 32 + 16 * lh, qb);
-        lds16_a2(sb + 128 + 32 * h + 16 * lh, qh);
-        lds8_a2(sb + 192 + 8 * h, scw);
-        const float dW = half_bits_to_float(*reinterpret_cast<const uint16_t*>(sb + 208));
-        // scales of groups 8h + 2t + lh: bytes lh + 2t of the half's eight
-        const uint32_t ssh = (uint32_t)lh * 8u;
-        const int sc[4] = {(int)(int8_t)(scw[0] >> ssh), (int)(int8_t)(scw[0] >> (16 + ssh)),
-                           (int)(int8_t)(scw[1] >> ssh), (int)(int8_t)(scw[1] >> (16 + ssh))};
-        // 6-bit values of the four quarters t for each dword i (4 elements):
-        //   t = 0: ql_a low nibble | qh bits 0-1 << 4     t = 2: ql_a high nibble | qh bits 4-5
-        //   t = 1: ql_b low nibble | qh bits 2-3 << 2     t = 3: ql_b high nibble | qh bits 6-7 >> 2
-        uint32_t q6[4][4];
+    for (int jr = 0; jr < rpw; ++jr) {
+        const int64_t row = row0 + (int64_t)jr * kWaves;
+        const bool row_ok = row < n1;
+        int after = 0;  // loads issued after this row's (the next row's)
+        RowImg nxt = cur;
+        if (jr + 1 < rpw) {
+            // the next image overwrites the one of row jr - 1: its LDS reads have all returned
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) alone
+            __builtin_amdgcn_sched_barrier(0);
+            nxt = row_image(row + kWaves, lw0 + (size_t)((jr + 1) & 1) * L.pitch);
+            issue_head(nxt);
+            issue_pieces(nxt, 0, nxt.nx4);
+            issue_tail(nxt);
+            after = nxt.issued;
+        }
+        const uint8_t* img = cur.img;
+        float acc[MT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t m = 0x0F0F0F0Fu;
-            const uint32_t ev = qh[i] & 0x33333333u, od = qh[i] & 0xCCCCCCCCu;
-            q6[0][i] = bfi(m, qa[i], ev << 4);
-            q6[1][i] = bfi(m, qb[i], od << 2);
-            q6[2][i] = bfi(m, qa[i] >> 4, ev);
-            q6[3][i] = bfi(m, qb[i] >> 4, od >> 2);
+        for (int mi = 0; mi < MT; ++mi) acc[mi] = 0.0f;
+        for (int k = 0; k < nsteps; ++k) {
+            // loads holding row bytes < 210*16*(k+1): the head and the 16-byte pieces up to that
+            // byte; the last step also needs the tail
+            const int endb = 3360 * (k + 1) < row_bytes ? 3360 * (k + 1) : row_bytes;
+            const int need = (endb - cur.head + 1023) / 1024;
+            const int done = k == nsteps - 1 ? cur.issued : 1 + (need < cur.nx4 ? need : cur.nx4);
+            wait_vmcnt_rt<0, 63>(cur.issued - done + after);
+            const int s_raw = kSbStep * k + (lane >> 2);
+            const bool valid = s_raw < nsb;
+            const int s = valid ? s_raw : nsb - 1;
+            const uint8_t* sb = img + 210 * s;
+            uint32_t qa[4], qb[4], qh[4], scw[2];
+            lds16_a2(sb + 64 * h + 16 * lh, qa);
+            lds16_a2(sb + 64 * h + 32 + 16 * lh, qb);
+            lds16_a2(sb + 128 + 32 * h + 16 * lh, qh);
+            lds8_a2(sb + 192 + 8 * h, scw);
+            const float dW = half_bits_to_float(*reinterpret_cast<const uint16_t*>(sb + 208));
+            // scales of groups 8h + 2t + lh: bytes lh + 2t of the half's eight
+            const uint32_t ssh = (uint32_t)lh * 8u;
+            const int sc[4] = {(int)(int8_t)(scw[0] >> ssh), (int)(int8_t)(scw[0] >> (16 + ssh)),
+                               (int)(int8_t)(scw[1] >> ssh), (int)(int8_t)(scw[1] >> (16 + ssh))};
+            // 6-bit values of the four quarters t for each dword i (4 elements):
+            //   t = 0: ql_a low nibble | qh bits 0-1 << 4     t = 2: ql_a high nibble | qh bits 4-5
+            //   t = 1: ql_b low nibble | qh bits 2-3 << 2     t = 3: ql_b high nibble | qh bits 6-7 >> 2
+            uint32_t q6[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = 0x0F0F0F0Fu;
+                const uint32_t ev = qh[i] & 0x33333333u, od = qh[i] & 0xCCCCCCCCu;
+                q6[0][i] = bfi(m, qa[i], ev << 4);
+                q6[1][i] = bfi(m, qb[i], od << 2);
+                q6[2][i] = bfi(m, qa[i] >> 4, ev);
+                q6[3][i] = bfi(m, qb[i] >> 4, od >> 2);
+            }
+#pragma unroll
+            for (int mi = 0; mi < MT; ++mi) {
+                const int8_t* ap = aq + mi * L.q_ld + 256 * s + 128 * h + 16 * lh;
+                // bsums of groups 8h + 2t + lh, t = 0..3: every other int16 of [16s + 8h, +8)
+                const uint4 bq = *reinterpret_cast<const uint4*>(abb + mi * L.b_ld + 32 * s + 16 * h);
+                const uint32_t bsh = (uint32_t)lh * 16u;
+                const int bs[4] = {(int)(int16_t)(bq.x >> bsh), (int)(int16_t)(bq.y >> bsh),
+                                   (int)(int16_t)(bq.z >> bsh), (int)(int16_t)(bq.w >> bsh)};
+                int iS = 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint4 av = *reinterpret_cast<const uint4*>(ap + 32 * t);
+                    int I = sdot4((int)q6[t][0], (int)av.x, 0);
+                    I = sdot4((int)q6[t][1], (int)av.y, I);
+                    I = sdot4((int)q6[t][2], (int)av.z, I);
+                    I = sdot4((int)q6[t][3], (int)av.w, I);
+                    iS += __mul24(sc[t], I - 32 * bs[t]);  // |sc| < 128, |I - 32 bs| < 2^18
+                }
+                if (DUMP && valid && row_ok && mi < M)
+                    atomicAdd(sums + ((int64_t)mi * sums_n_stride + (row - n0)) * nsb + s, iS);
+                const float v = (dW * ad[64 * mi + s]) * (float)iS;
+                acc[mi] = valid ? acc[mi] + v : acc[mi];
+            }
         }
 #pragma unroll
         for (int mi = 0; mi < MT; ++mi) {
-            const int8_t* ap = aq + mi * L.q_ld + 256 * s + 128 * h + 16 * lh;
-            // bsums of groups 8h + 2t + lh, t = 0..3: every other int16 of [16s + 8h, +8)
-            const uint4 bq = *reinterpret_cast<const uint4*>(abb + mi * L.b_ld + 32 * s + 16 * h);
-            const uint32_t bsh = (uint32_t)lh * 16u;
-            const int bs[4] = {(int)(int16_t)(bq.x >> bsh), (int)(int16_t)(bq.y >> bsh), (int)(int16_t)(bq.z >> bsh),
-                               (int)(int16_t)(bq.w >> bsh)};
-            int iS = 0;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint4 av = *reinterpret_cast<const uint4*>(ap + 32 * t);
-                int I = sdot4((int)q6[t][0], (int)av.x, 0);
-                I = sdot4((int)q6[t][1], (int)av.y, I);
-                I = sdot4((int)q6[t][2], (int)av.z, I);
-                I = sdot4((int)q6[t][3], (int)av.w, I);
-                iS += __mul24(sc[t], I - 32 * bs[t]);  // |sc| < 128, |I - 32 bs| < 2^18
-            }
-            if (DUMP && valid && row_ok && mi < M)
-                atomicAdd(sums + ((int64_t)mi * sums_n_stride + (row - n0)) * nsb + s, iS);
-            const float v = (dW * ad[64 * mi + s]) * (float)iS;
-            acc[mi] = valid ? acc[mi] + v : acc[mi];
+            const float v = lanes_sum<64>(acc[mi]);
+            if (lane == 0 && row_ok && mi < M)  // R (optional, may alias Y): Y = W x + R
+                Y[(int64_t)mi * y_stride + (row - n0)] = R ? v + R[(int64_t)mi * r_stride + (row - n0)] : v;
         }
-    }
-
-    // ---- 4. reduce the row over the wave ----
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi) {
-        const float v = lanes_sum<64>(acc[mi]);
-        if (lane == 0 && row_ok && mi < M)  // R (optional, may alias Y): Y = W x + R
-            Y[(int64_t)mi * y_stride + (row - n0)] = R ? v + R[(int64_t)mi * r_stride + (row - n0)] : v;
+        cur = nxt;
     }
 }
 
@@ -335,7 +374,7 @@ namespace {
 
 using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, const int16_t*,
                       int64_t, const float*, int64_t, int, float*, int64_t, int32_t*, int64_t, const float*,
-                      int64_t);
+                      int64_t, int);
 
 // fused activation: M <= 2 rows, nsb <= 64. 4-wave workgroups: every wave stages, at most 8
 // passes of 16 (superblock, row) pairs. 8..12 waves: the first 4 waves stage, at most 4 passes
@@ -366,6 +405,19 @@ Q6Fn q6_pick_fused(int mt, int qc, int nw) {
     }
 }
 
+// Rows per wave of the 4-wave kernels. One row per wave while the grid is a few workgroups per
+// CU; for very tall matrices (LM heads: 151936 rows) every workgroup would otherwise restage
+// (and, fused, re-quantize) the whole activation for four rows, so each wave streams several
+// rows through two LDS images, keeping about 16 workgroups per CU over the launch.
+int q6_rows_per_wave(int64_t rows, int nw) {
+    int rpw = knob(Knob::Q6KRows);
+    if (rpw < 1) {
+        const int64_t per_wave = rows / ((int64_t)nw * cu_count() * 16);
+        rpw = per_wave >= 8 ? 8 : per_wave >= 4 ? 4 : per_wave >= 2 ? 2 : 1;
+    }
+    return rpw > 16 ? 16 : rpw;
+}
+
 template <bool DUMP>
 Q6Fn q6_pick(int mt) {
     switch (mt) {
@@ -386,22 +438,26 @@ hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0,
     // the weight base is 16-byte aligned (checked by the C ABI)
     if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb) return hipErrorNotSupported;
     if (knob(Knob::Q6KLdsOff)) return hipErrorNotSupported;
+    const int nw = 4;  // 5-wave workgroups (rows spread more evenly) measured no faster here
+    // several rows per wave only where a step of 16 superblocks covers the row (the waits count
+    // two rows' loads)
+    const int rpw = nsb <= kSbStep ? q6_rows_per_wave(n1 - n0, nw) : 1;
+    const int nbuf = rpw > 1 ? 2 : 1;
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
-        if (Q6Lds(nsb, mt, 4).total > kMaxLds) return hipErrorNotSupported;
+        if (Q6Lds(nsb, mt, nw, nbuf).total > kMaxLds) return hipErrorNotSupported;
     }
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
-        const int nw = 4;  // 5-wave workgroups (rows spread more evenly) measured no faster here
-        const unsigned grid = (unsigned)((n1 - n0 + nw - 1) / nw);
+        const unsigned grid = (unsigned)((n1 - n0 + (int64_t)nw * rpw - 1) / ((int64_t)nw * rpw));
         Q6Fn fn = block_sums ? q6_pick<true>(mt) : q6_pick<false>(mt);
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), Q6Lds(nsb, mt, nw).total, st, (const uint8_t*)W, w_row_bytes,
-                           n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.bs + m0 * (K / 16), act.m_ld,
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), Q6Lds(nsb, mt, nw, nbuf).total, st, (const uint8_t*)W,
+                           w_row_bytes, n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.bs + m0 * (K / 16), act.m_ld,
                            (const float*)nullptr, (int64_t)0, (int)mc, Y + m0 * y_stride, y_stride,
                            block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr, sums_n_stride,
-                           R ? R + m0 * r_stride : nullptr, r_stride);
+                           R ? R + m0 * r_stride : nullptr, r_stride, rpw);
     }
     return hipGetLastError();
 }
@@ -430,13 +486,15 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
     const int mt = M == 1 ? 1 : 2;
     const int sw = q6_stage_waves(kWaves);
     const int qc = (nsb * mt + 4 * sw - 1) / (4 * sw);
-    if (Q6Lds(nsb, mt, kWaves).total > kMaxLds) return hipErrorNotSupported;
+    const int rpw = kWaves == 4 && nsb <= kSbStep ? q6_rows_per_wave(N, kWaves) : 1;
+    const Q6Lds lds(nsb, mt, kWaves, rpw > 1 ? 2 : 1);
+    if (lds.total > kMaxLds) return hipErrorNotSupported;
     Q6Fn fn = block_sums ? q6_pick_fused<true>(mt, qc, kWaves) : q6_pick_fused<false>(mt, qc, kWaves);
     if (!fn) return hipErrorNotSupported;
-    const unsigned grid = (unsigned)((N + kWaves - 1) / kWaves);
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), Q6Lds(nsb, mt, kWaves).total, st, (const uint8_t*)W,
-                       w_row_bytes, (int64_t)0, N, nsb, (const int8_t*)nullptr, (const float*)nullptr, (const int16_t*)nullptr,
-                       (int64_t)0, X, x_stride, (int)M, Y, y_stride, block_sums, N, R, r_stride);
+    const unsigned grid = (unsigned)((N + (int64_t)kWaves * rpw - 1) / ((int64_t)kWaves * rpw));
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), lds.total, st, (const uint8_t*)W, w_row_bytes, (int64_t)0,
+                       N, nsb, (const int8_t*)nullptr, (const float*)nullptr, (const int16_t*)nullptr, (int64_t)0, X,
+                       x_stride, (int)M, Y, y_stride, block_sums, N, R, r_stride, rpw);
     return hipGetLastError();
 }
 

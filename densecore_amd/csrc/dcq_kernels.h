@@ -46,6 +46,7 @@ enum class Knob {
     GemvGeneric,  // DCQ_GEMV_GENERIC: 1 forces the generic GEMV kernel
     GemvLanes,    // DCQ_GEMV_LG: log2 lanes per row of the generic GEMV (-1: rule)
     AttnNoMfma,   // DCQ_ATTN_NO_MFMA: 1 keeps prompts on the VALU attention kernel
+    Q6KRows,      // DCQ_Q6K_RPW: rows per wave of the 4-wave Q6_K decode (-1: launch rule)
     kCount
 };
 int knob(Knob k);

@@ -462,3 +462,67 @@ def test_mul_mat_large_tiles(O, dev, wt, M, N, K):
     assert np.array_equal(got, want)
     y2 = dc.mul_mat(wt, to_dev(wq, dev), N, K, to_dev(x, dev))
     O.assert_close(to_host(y2), y_ref, l1, RTOL, what="production kernel")
+
+
+# ---------------------------------------------------------------- the LM head (output projection)
+def _random_blocks(wt, N, K, rng):
+    """Valid weight rows of random quants with small positive fp16 scales (generating N(0, 0.02)
+    floats and quantizing 150 k rows would dominate the test; the kernels see the same bytes
+    either way)."""
+    rb = dc.row_size(wt, K)
+    q = rng.integers(0, 256, size=(N, rb), dtype=np.uint8)
+    scale = np.frombuffer(np.float16(0.0004).tobytes(), dtype=np.uint8)
+    if wt == Q8_0:
+        blk = q.reshape(N, K // 32, 34)
+        blk[:, :, 0:2] = scale
+    else:  # Q6_K: 16 int8 sub-scales (random), d last
+        blk = q.reshape(N, K // 256, 210)
+        blk[:, :, 208:210] = scale
+    return q
+
+
+@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("wt,K", [(Q8_0, 1024), (Q6_K, 2560)])
+def test_lm_head_parity(O, dev, wt, K, M):
+    """The LM head, the largest weight stream of a decode step (ggml_mul_mat(output, cur),
+    core/src/inference.cpp:1817): Qwen3's 151,936-token vocabulary at Qwen3-0.6B's width (Q8_0,
+    K = 1024, 165 MB) and at Qwen3-4B's (Q6_K, the Q4_K_M type of output.weight, K = 2560, 319 MB),
+    one and four tokens, every output against the oracle."""
+    N = 151936
+    rng = np.random.default_rng(151936 + K + M)
+    wq = _random_blocks(wt, N, K, rng)
+    x = synth.normal(M * K, 4000 + M + K).reshape(M, K)
+    print(f"lm head type {wt} M={M} N={N} K={K}", flush=True)
+    y = to_host(dc.mul_mat(wt, to_dev(wq, dev), N, K, to_dev(x, dev)))
+    y_ref, l1 = O.mul_mat(wt, wq, x)
+    O.assert_close(y, y_ref, l1, RTOL, what=f"lm head type {wt} M={M}")
+
+
+# Tall Q6_K matrices (32768+ rows at K <= 4096): each wave streams 2, 4 or 8 rows through two LDS
+# images, the next row's loads in flight while the current one computes. Rows not a multiple of
+# the rows per workgroup (tails of every length), the fused kernel (M <= 2) and the one over a
+# quantized activation (M = 3, M = 9: two tiles of rows), block sums and the residual add.
+TALL_Q6 = [(1, 40001, 1024), (2, 70003, 512), (3, 70001, 1024), (9, 40003, 512), (1, 139999, 1536)]
+
+
+@pytest.mark.parametrize("M,N,K", TALL_Q6)
+def test_q6k_rows_per_wave(O, dev, M, N, K):
+    import torch
+    rng = np.random.default_rng(N + K + M)
+    wq = _random_blocks(Q6_K, N, K, rng)
+    x = synth.normal(M * K, 500 + M + K).reshape(M, K)
+    synth.set_outliers(x[0], max(1, K // 100), 20.0, 3)
+    print(f"tall q6_k M={M} N={N} K={K}", flush=True)
+    y_ref, l1 = O.mul_mat(Q6_K, wq, x)
+    per = dc.block_sums_per_row(Q6_K, K)
+    sums = torch.zeros((M, N, per), dtype=torch.int32, device=dev)
+    wd, xd = to_dev(wq, dev), to_dev(x, dev)
+    y = dc.mul_mat_ex(Q6_K, wd, N, K, xd, path=dc.PATH_GEMV, block_sums=sums)
+    O.assert_close(to_host(y), y_ref, l1, RTOL, what=f"tall q6_k M{M} N{N} K{K}")
+    want = O.block_sums_matrix(Q6_K, K, wq, O.quantize_rows(Q8_K, x))
+    assert np.array_equal(to_host(sums), want)
+    y2 = to_host(dc.mul_mat(Q6_K, wd, N, K, xd))
+    O.assert_close(y2, y_ref, l1, RTOL, what="tall q6_k production kernel")
+    r = synth.normal(M * N, 700 + M, 0.0, 3.0).reshape(M, N)
+    y3 = to_host(dc.mul_mat_add(Q6_K, wd, N, K, xd, to_dev(r, dev)))
+    assert np.array_equal(y3.view(np.uint32), (y2 + r).astype(np.float32).view(np.uint32))
