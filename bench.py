@@ -538,6 +538,51 @@ def bench_lm_head(args, dev, wtype, K, M, N=151936):
     return out
 
 
+def bench_kquant_prefill(args, dev, wtype, M=2048, N=8192, K=2048):
+    """A K-quant prompt projection (ggml MUL_MAT at M > 1, core/src/inference.cpp:1049-1063,
+    1794-1797) at config 5's shape with Q4_K / Q6_K weights (random valid quants, W rotated like
+    the configs): the whole step (activation quantization + product) and the product kernel alone
+    on the pre-quantized activation, against the int8 MFMA peak."""
+    import torch
+    import densecore_amd as dc
+    rb = dc.row_size(wtype, K)
+    wbytes = N * rb
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    g = torch.Generator(device=dev)
+    g.manual_seed(29)
+    big = torch.randint(0, 256, (copies, N, rb), dtype=torch.uint8, device=dev, generator=g)
+    blocks = big.view(copies, N, K // 256, rb // (K // 256))
+    d = torch.from_numpy(np.frombuffer(np.float16(0.0004).tobytes(), dtype=np.uint8).copy()).to(dev)
+    if wtype == dc.TYPE_Q6_K:
+        blocks[..., 208:210] = d
+    else:
+        blocks[..., 0:2] = d
+        blocks[..., 2:4] = torch.from_numpy(np.frombuffer(np.float16(0.0002).tobytes(), dtype=np.uint8).copy()).to(dev)
+    x = torch.randn((M, K), device=dev, generator=g)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ws = torch.empty(dc.mul_mat_workspace_size(wtype, M, K), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        dc.mul_mat(wtype, big[i % copies], N, K, x, y=y, workspace=ws, stream=torch.cuda.current_stream().cuda_stream)
+
+    def kernel_only(i):
+        dc.mul_mat_q(wtype, big[i % copies], N, K, ws, M, y=y, stream=torch.cuda.current_stream().cuda_stream)
+
+    steps = max(5, args.steps // 10)
+    step_ms, kern, _ = time_graph(step, steps, args.warmup, args.replays)
+    dc.quantize_src1(wtype, x, ws)
+    torch.cuda.synchronize()
+    k_ms, _, _ = time_graph(kernel_only, steps, args.warmup, args.replays)
+    ops = 2.0 * M * N * K
+    out = {"shape": f"{dc.TYPE_NAMES[wtype]} M={M} N={N} K={K}", "step_us": step_ms * 1e3, "kernels": kern,
+           "kernel_us": k_ms * 1e3, "TOPS_kernel": ops / (k_ms * 1e-3) / 1e12,
+           "frac_of_int8_peak": ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS}
+    del big, ws, y, x
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_gguf_load(args, dev, mib=512):
     """GGUF ingest: a file of Q4_K tensors (mib MiB, in the page cache after it is written) loaded
     tensor by tensor into HBM with dcq_gguf_load_tensor; host-to-device GB/s (PCIe bound)."""
@@ -839,6 +884,11 @@ def main():
                 print(f"# {e['shape']}: {e['us']:.2f} us ({e['kernels']} kernels), {e['weight_GBps']:.0f} GB/s "
                       f"({100 * e['frac_of_peak']:.1f} % of 8 TB/s; read ceiling {e.get('read_ceiling_us', 0):.2f} us)",
                       file=sys.stderr, flush=True)
+        for wt in (dc.TYPE_Q4_K, dc.TYPE_Q6_K):
+            e = extras[f"prefill_{dc.TYPE_NAMES[wt].lower()}"] = bench_kquant_prefill(args, dev, wt)
+            print(f"# {e['shape']}: kernel {e['kernel_us']:.1f} us ({e['TOPS_kernel']:.0f} TOPS, "
+                  f"{100 * e['frac_of_int8_peak']:.1f} % of int8 peak), step {e['step_us']:.1f} us "
+                  f"({e['kernels']} kernels)", file=sys.stderr, flush=True)
         extras["gguf_load"] = bench_gguf_load(args, dev)
         print(f"# GGUF ingest: {extras['gguf_load']['GBps']:.1f} GB/s host-to-HBM over "
               f"{extras['gguf_load']['bytes'] >> 20} MiB", file=sys.stderr, flush=True)

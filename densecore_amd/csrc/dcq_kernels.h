@@ -107,6 +107,11 @@ hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t 
 hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                                int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
 
+// Q6_K prefill: the same tiling over the planar Q8_K activation (K % 512 == 0, w_row_bytes % 4
+// == 0, m_ld % 128 == 0); hipErrorNotSupported otherwise (nothing launched).
+hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+
 // Q4_K batched decode (M <= 128): 8-wave workgroups per 32 weight rows x 64 activation
 // rows, K split over the waves; hipErrorNotSupported when the shape is outside it.
 hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,

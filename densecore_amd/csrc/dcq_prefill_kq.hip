@@ -1,0 +1,318 @@
+// dcq_prefill_kq.hip — prefill / batched mul_mat for Q6_K weights on gfx950 int8 MFMA.
+//
+// Replaces ggml's CPU MUL_MAT at M > 1 for Q6_K weights (core/src/inference.cpp:1049-1063 and
+// 1794-1797 route every M > 1 projection there; executed at core/src/worker.cpp:544), with
+// vec_dot_q6_K_q8_K's arithmetic per (activation row m, weight row n):
+//   Y[m][n] = sum_s (d[n][s] * dA[m][s]) * iS,  iS = sum_g sc[n][s][g] * I_g  (exact int32)
+//   I_g = sum over the 16 elements k of group g of qa[m][k] * (q[n][k] - 32)
+//
+// Tiling (as the Q8_0 prefill). A 256-thread workgroup computes a 128 (m) x 128 (n) tile of Y;
+// each wave owns 64 x 64 = 2 x 2 MFMA tiles. K advances in stages of 128 (half a superblock:
+// 8 groups of 16), double-buffered in LDS; the next stage's loads are issued before the current
+// stage's MFMAs. Activation rows go global -> LDS directly (global_load_lds_dwordx4 from a
+// scalar base); weight bytes pass through registers: thread (row, part) holds the ql, qh bytes of
+// 64 of the stage's elements and, at commit, writes them to LDS as signed int8 q - 32, so the
+// MFMA reads weight operands like activation operands. Per dword the conversion is a v_perm table
+// lookup (the two qh bits select the high nibble of q - 32: 0xE0, 0xF0, 0x00, 0x10) and a v_bfi
+// that merges the ql nibble. LDS rows are 128 bytes of 16-byte slots (one group each) XOR-swizzled
+// by row % 8.
+//
+// Per group: v_mfma_i32_32x32x16_i8 (K = 16, one group) into a zero accumulator, then
+// iS += sc_g * I_g with v_mad_i32_i24 (|I_g| <= 16*32*127 < 2^23; |iS| <= 256*128*32*127 < 2^31);
+// per superblock acc += (d * dA) * iS. The 16 integer multiply-adds per lane and group (against
+// 4 MFMAs per wave and group) are the VALU work that bounds the kernel.
+//
+// Workgroup order is XCD-aware (consecutive ids go to different XCDs): each XCD takes a
+// contiguous band of n tiles, so its weight rows stay in that XCD's L2.
+#include "dcq_common.h"
+#include "dcq_kernels.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 in the clobber list (see dma16)
+
+namespace dcq {
+
+namespace {
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 128, kBN = 128;  // workgroup tile
+constexpr int kKS = 128;             // k per stage: half a Q6_K superblock, 8 groups of 16
+constexpr int kRow = kKS;            // LDS row: 8 slots of 16 bytes (one group each), slot XOR (row % 8)
+constexpr int kXcds = 8;
+
+struct __align__(16) StageQ6 {
+    int8_t a[kBM * kRow];  // activation int8, [m][k] (swizzled 16-byte slots)
+    int8_t b[kBN * kRow];  // weight q - 32 as int8, [n][k] (swizzled 16-byte slots)
+    uint2 sc[kBN];         // the stage's 8 int8 group scales per weight row
+    float dw[kBN];         // weight superblock scale d
+    float da[kBM];         // activation superblock scale
+};
+
+__device__ __forceinline__ int swz(int row, int slot) { return row * kRow + 16 * (slot ^ (row & 7)); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane from global memory (uniform base `g` + per-lane byte offset `off`) straight
+// into LDS at lds_base + 16 * lane (lds_base wave-uniform, in M0): global_load_lds_dwordx4 with an
+// SGPR base. Inline asm: the compiler's builtin form waits for every earlier LDS-direct load before
+// the next. The compiler does not count these loads, so they are issued before the ordinary loads
+// of the same stage, and the stage ends with an explicit s_waitcnt vmcnt(0) before the barrier.
+// M0 has no other use in this kernel.
+__device__ __forceinline__ void dma16(const void* g, uint32_t off, const void* lds_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(g), "s"(m0) : "memory", "m0");
+}
+
+__device__ __forceinline__ v16i mfma32k16(long a, long b) {
+    v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, z, 0, 0, 0);
+}
+
+// Signed q - 32 bytes of four 6-bit quants: low nibbles from `ql` (bits 0-3 of each byte), the
+// two high bits from `qh2` (bits 0-1 of each byte). (qh2 - 2) << 4 is the high nibble of q - 32:
+// byte qh2 of the table 0x1000F0E0.
+__device__ __forceinline__ uint32_t q6_minus32(uint32_t ql, uint32_t qh2) {
+    const uint32_t hi = __builtin_amdgcn_perm(0u, 0x1000F0E0u, qh2);
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(0x0F0F0F0Fu), "v"(ql), "v"(hi));
+    return r;
+}
+
+}  // namespace
+
+// W: Q6_K rows (w_row_bytes % 4 == 0, 16-byte aligned base); xqs: int8 [M][K]; xd: float
+// [K/256][m_ld] with m_ld a multiple of 128; K % 512 == 0.
+// FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
+template <bool DUMP, bool FULL>
+__global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+                                                              int N, int K, const int8_t* __restrict__ xqs,
+                                                              const float* __restrict__ xd, int64_t m_ld, int M,
+                                                              float* __restrict__ Y, int64_t y_stride,
+                                                              int32_t* __restrict__ sums, int tiles_n, int tiles_m) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    StageQ6* st = reinterpret_cast<StageQ6*>(smem);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    // ---- XCD-aware tile order: XCD x (= id % 8) takes n-tile band x, walked m-first ----
+    const int bid = blockIdx.x;
+    int tile_m, tile_n;
+    if (tiles_n % kXcds == 0) {
+        const int band = tiles_n / kXcds;
+        const int xcd = bid % kXcds, local = bid / kXcds;
+        tile_n = xcd * band + local % band;
+        tile_m = local / band;
+    } else {
+        tile_n = bid % tiles_n;
+        tile_m = bid / tiles_n;
+    }
+    const int m0 = tile_m * kBM, n0 = tile_n * kBN;
+    const int nstages = K / kKS, nsb = K / 256;
+
+    // ---- staging assignment (fixed for the whole K loop) ----
+    // activation rows: instruction i of wave w fills tile rows 8*(4w+i) .. +8, lane l the 16-byte
+    // slot (l % 8) of row 8*(4w+i) + l/8, which holds logical slot (l % 8) ^ (row % 8)
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const int a_row0 = 8 * (4 * wave_u) + (lane >> 3);
+    const int a_slot = (lane & 7) ^ (a_row0 & 7);
+    uint32_t a_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = FULL ? m0 + a_row0 + 8 * i : min(m0 + a_row0 + 8 * i, M - 1);
+        a_off[i] = (uint32_t)row * (uint32_t)K + 16u * (uint32_t)a_slot;
+    }
+    // weight rows: row rw = tid / 2 of the tile, part p = tid % 2: elements 32t + 16p + [0, 16) of
+    // the stage's half h for t = 0..3 (ql bytes 64h + 16p and 64h + 32 + 16p, qh bytes
+    // 128 + 32h + 16p, 16 each); part 0 also loads the half's 8 scales, part 1 the fp16 d.
+    // Superblock s starts 210 s bytes into the row (rows are dword aligned): its dword offset
+    // sh = (210 s) & 3 is 0 or 2 for every row of the stage; loads start at the dword below.
+    const int rw = tid >> 1, p = tid & 1;
+    const uint8_t* w_row = W + (int64_t)(FULL ? n0 + rw : min(n0 + rw, N - 1)) * w_row_bytes;
+    const int da_row = m0 + (tid & (kBM - 1));  // m_ld >= m0 + 128: in bounds for every tile
+    uint32_t gw[15], gx[3];
+    float gda;
+    auto issue = [&](int stg, StageQ6& S) {
+        const int8_t* ab = xqs + (int64_t)stg * kKS;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16(ab, a_off[i], S.a + 1024 * (4 * wave_u + i));
+        const int s = stg >> 1, h = stg & 1;
+        const uint8_t* sb = w_row + 210 * s - ((210 * s) & 3);
+#pragma unroll
+        for (int piece = 0; piece < 3; ++piece) {
+            const uint8_t* q = sb + (piece == 2 ? 128 + 32 * h : 64 * h + 32 * piece) + 16 * p;
+            const U32x4 v = ld4(q);
+            gw[5 * piece] = v.x;
+            gw[5 * piece + 1] = v.y;
+            gw[5 * piece + 2] = v.z;
+            gw[5 * piece + 3] = v.w;
+            gw[5 * piece + 4] = ld1(q + 16);
+        }
+        if (p == 0) {
+            gx[0] = ld1(sb + 192 + 8 * h);
+            gx[1] = ld1(sb + 196 + 8 * h);
+            gx[2] = ld1(sb + 200 + 8 * h);
+        } else {
+            gx[0] = ld1(sb + 208);
+        }
+        gda = xd[(int64_t)s * m_ld + da_row];
+    };
+    auto commit = [&](int stg, StageQ6& S) {
+        const uint32_t sh = (uint32_t)((210 * (stg >> 1)) & 3);
+        uint32_t qa[4], qb[4], qh[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            qa[i] = align_bytes(gw[i + 1], gw[i], sh);
+            qb[i] = align_bytes(gw[i + 6], gw[i + 5], sh);
+            qh[i] = align_bytes(gw[i + 11], gw[i + 10], sh);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t* src = (t & 1) ? qb : qa;
+            uint32_t v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                v[i] = q6_minus32(src[i] >> (4 * (t >> 1)), (qh[i] >> (2 * t)) & 0x03030303u);
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 2 * t + p)) = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+        if (p == 0)
+            S.sc[rw] = make_uint2(align_bytes(gx[1], gx[0], sh), align_bytes(gx[2], gx[1], sh));
+        else
+            S.dw[rw] = half_bits_to_float((gx[0] >> (8 * sh)) & 0xFFFFu);
+        if (tid < kBM) S.da[tid] = gda;
+    };
+
+    // ---- wave tile: 64 x 64 at (wm, wn) inside the workgroup tile ----
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int col = lane & 31, hl = lane >> 5;
+    float acc[2][2][16];
+    int ai[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f, ai[i][j][v] = 0;
+
+    issue(0, st[0]);
+    commit(0, st[0]);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
+    __syncthreads();
+
+    for (int stg = 0; stg < nstages; ++stg) {
+        const StageQ6& S = st[stg & 1];
+        const bool more = stg + 1 < nstages;
+        if (more) issue(stg + 1, st[(stg + 1) & 1]);  // in flight while this stage computes
+        uint2 scw[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) scw[j] = S.sc[wn + 32 * j + col];
+#pragma unroll
+        for (int kg = 0; kg < 8; ++kg) {
+            // fragment rows wm + 32i + col and wn + 32j + col share row % 8 = col % 8; lane half hl
+            // takes bytes 8hl .. 8hl + 8 of the group's slot
+            const int fo = col * kRow + 16 * (kg ^ (col & 7)) + 8 * hl;
+            long fa[2], fb[2];
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const long*>(S.a + fo + (wm + 32 * ii) * kRow);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) fb[jj] = *reinterpret_cast<const long*>(S.b + fo + (wn + 32 * jj) * kRow);
+            int sc[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t w = kg < 4 ? scw[j].x : scw[j].y;
+                sc[j] = __builtin_amdgcn_sbfe((int)w, 8 * (kg & 3), 8);
+            }
+            v16i D[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) D[i][j] = mfma32k16(fa[i], fb[j]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) ai[i][j][v] = __mul24(sc[j], D[i][j][v]) + ai[i][j][v];
+        }
+        if (stg & 1) {
+            // end of superblock s: acc += (d * dA) * iS, the scales from this (second-half) stage
+            const int s = stg >> 1;
+            float dwj[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) dwj[j] = S.dw[wn + 32 * j + col];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v4 = *reinterpret_cast<const float4*>(&S.da[wm + 32 * i + 8 * q + 4 * hl]);
+                    const float da4[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) {
+                            const int v = 4 * q + e;
+                            acc[i][j][v] = fmaf(dwj[j] * da4[e], (float)ai[i][j][v], acc[i][j][v]);
+                        }
+                }
+            }
+            if (DUMP) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int n = n0 + wn + 32 * j + col;
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int m = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
+                            if (m < M && n < N) sums[((int64_t)m * N + n) * nsb + s] = ai[i][j][v];
+                        }
+                    }
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) ai[i][j][v] = 0;
+        }
+        if (more) {
+            // the other buffer was last read in stage stg - 1, which every wave finished before
+            // the barrier that ended it: one barrier per stage is enough
+            commit(stg + 1, st[(stg + 1) & 1]);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
+            __syncthreads();
+        }
+    }
+
+    // ---- store: lane owns column n, rows m0 + wm + 32i + 8(v/4) + 4hl + v%4 ----
+    float* yl = Y + (int64_t)(m0 + wm + 4 * hl) * y_stride + (n0 + wn + col);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        if (!FULL && n0 + wn + 32 * j + col >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int r = 32 * i + 8 * (v >> 2) + (v & 3);
+                if (FULL || m0 + wm + 4 * hl + r < M) yl[(int64_t)r * y_stride + 32 * j] = acc[i][j][v];
+            }
+    }
+}
+
+hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+    // K % 512: an even number of superblocks, so the 2-byte overreach of the scale and d loads of
+    // an even superblock (dword offset 0) stays inside the next one
+    if (K % 512 || w_row_bytes % 4 || act.m_ld % kBM || N > (1 << 30) || M > (1 << 30) || K > (1 << 30))
+        return hipErrorNotSupported;
+    // the DMA offsets are 32-bit: every activation row must lie within 4 GiB of the base
+    if ((uint64_t)M * (uint64_t)K >= (1ull << 32)) return hipErrorNotSupported;
+    const int tiles_n = (int)((N + kBN - 1) / kBN), tiles_m = (int)((M + kBM - 1) / kBM);
+    const size_t lds = 2 * sizeof(StageQ6);
+    const bool full = M % kBM == 0 && N % kBN == 0;
+    auto fn = block_sums ? (full ? prefill_q6_k_kernel<true, true> : prefill_q6_k_kernel<true, false>)
+                         : (full ? prefill_q6_k_kernel<false, true> : prefill_q6_k_kernel<false, false>);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, (const uint8_t*)W, w_row_bytes,
+                       (int)N, (int)K, act.qs, act.d, act.m_ld, (int)M, Y, y_stride, block_sums, tiles_n, tiles_m);
+    return hipGetLastError();
+}
+
+}  // namespace dcq

@@ -101,6 +101,9 @@ CASES = [
     (Q4_K, 1, 9728, 2560), (Q4_K, 1, 2570, 4096), (Q4_K, 1, 2561, 9728),
     (Q6_K, 1, 50, 9728), (Q6_K, 1, 3, 256), (Q6_K, 8, 64, 512), (Q6_K, 33, 65, 1024), (Q6_K, 3, 17, 768),
     (Q6_K, 2, 9, 16384), (Q6_K, 1, 5, 16896),
+    # the Q6_K prefill kernel (M > 32, an even number of superblocks): unguarded 128 x 128 tiles,
+    # ragged M and N, one superblock pair; an odd count (K = 768) takes the generic kernel
+    (Q6_K, 256, 384, 1024), (Q6_K, 200, 300, 2048), (Q6_K, 130, 129, 512), (Q6_K, 40, 50, 768),
     # Q6_K decode with the activation quantized in the workgroup (M <= 2, K <= 4096)
     (Q6_K, 1, 1000, 2560), (Q6_K, 2, 70, 4096),
     # fused Q4_K decode at the concatenated Q/K/V rows of Qwen3-4B and at twice the ffn width
@@ -475,6 +478,10 @@ def _random_blocks(wt, N, K, rng):
     if wt == Q8_0:
         blk = q.reshape(N, K // 32, 34)
         blk[:, :, 0:2] = scale
+    elif wt == Q4_K:  # d, dmin, then 12 bytes of 6-bit scales and mins (random), nibbles
+        blk = q.reshape(N, K // 256, 144)
+        blk[:, :, 0:2] = scale
+        blk[:, :, 2:4] = np.frombuffer(np.float16(0.0002).tobytes(), dtype=np.uint8)
     else:  # Q6_K: 16 int8 sub-scales (random), d last
         blk = q.reshape(N, K // 256, 210)
         blk[:, :, 208:210] = scale
@@ -526,3 +533,34 @@ def test_q6k_rows_per_wave(O, dev, M, N, K):
     r = synth.normal(M * N, 700 + M, 0.0, 3.0).reshape(M, N)
     y3 = to_host(dc.mul_mat_add(Q6_K, wd, N, K, xd, to_dev(r, dev)))
     assert np.array_equal(y3.view(np.uint32), (y2 + r).astype(np.float32).view(np.uint32))
+
+
+# K-quant prefill at config 5's shape (2048 x 8192 x 2048), the projection shape of a Q4_K_M
+# prompt: every 128-row m-tile boundary row and interior rows against the oracle on all 8192
+# outputs, and the per-superblock int32 sums of a full-shape corner bit for bit.
+@pytest.mark.parametrize("wt", [Q4_K, Q6_K])
+def test_kquant_prefill_full_shape(O, dev, wt):
+    import torch
+    M, N, K = 2048, 8192, 2048
+    rng = np.random.default_rng(2048 + wt)
+    wq = _random_blocks(wt, N, K, rng)
+    x = synth.normal(M * K, 9000 + wt).reshape(M, K)
+    for m in range(0, M, 97):
+        synth.set_outliers(x[m], 20, 20.0, m)
+    wd, xd = to_dev(wq, dev), to_dev(x, dev)
+    print(f"k-quant prefill type {wt} M={M} N={N} K={K}", flush=True)
+    y = to_host(dc.mul_mat(wt, wd, N, K, xd))
+    rows = np.unique(np.r_[np.arange(0, M, 128), np.arange(127, M, 128), 1, 500, 1000, 1234, 1999])
+    y_ref, l1 = O.mul_mat(wt, wq, x[rows])
+    O.assert_close(y[rows], y_ref, l1, RTOL, what=f"k-quant prefill type {wt}")
+    per = dc.block_sums_per_row(wt, K)
+    sums = torch.zeros((M, N, per), dtype=torch.int32, device=dev)
+    y2 = dc.mul_mat_ex(wt, wd, N, K, xd, path=dc.PATH_AUTO, block_sums=sums)
+    corner = np.arange(M - 8, M)
+    cols = np.r_[0:64, N - 64:N]
+    got = to_host(sums[corner[0]:, :, :])[:, cols, :]
+    del sums
+    torch.cuda.empty_cache()
+    want = O.block_sums_matrix(wt, K, wq[cols], O.quantize_rows(Q8_K, x[corner]))
+    assert np.array_equal(got, want)
+    assert np.array_equal(to_host(y2), y)  # the dump does not change the outputs
