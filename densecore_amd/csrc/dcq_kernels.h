@@ -111,6 +111,9 @@ hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, in
 // == 0, m_ld % 128 == 0); hipErrorNotSupported otherwise (nothing launched).
 hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                                int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+// Q4_K prefill: the same tiling (K % 256 == 0, w_row_bytes % 16 == 0, m_ld % 128 == 0).
+hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
 
 // Q4_K batched decode (M <= 128): 8-wave workgroups per 32 weight rows x 64 activation
 // rows, K split over the waves; hipErrorNotSupported when the shape is outside it.

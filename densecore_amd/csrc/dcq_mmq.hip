@@ -579,6 +579,10 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
         const hipError_t e = launch_prefill_q6_k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st);
         if (e != hipErrorNotSupported) return e;
     }
+    if (wtype == kTypeQ4_K && M > 128) {
+        const hipError_t e = launch_prefill_q4_k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st);
+        if (e != hipErrorNotSupported) return e;
+    }
     if (wtype == kTypeQ4_K && M <= 128) {
         const hipError_t e = launch_batch_q4k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st);
         if (e != hipErrorNotSupported) return e;

@@ -1,7 +1,8 @@
-// dcq_prefill_kq.hip — prefill / batched mul_mat for Q6_K weights on gfx950 int8 MFMA.
+// dcq_prefill_kq.hip — prefill / batched mul_mat for K-quant weights (Q6_K, Q4_K) on gfx950
+// int8 MFMA.
 //
-// Replaces ggml's CPU MUL_MAT at M > 1 for Q6_K weights (core/src/inference.cpp:1049-1063 and
-// 1794-1797 route every M > 1 projection there; executed at core/src/worker.cpp:544), with
+// Replaces ggml's CPU MUL_MAT at M > 1 for K-quant weights (core/src/inference.cpp:1049-1063 and
+// 1794-1797 route every M > 1 projection there; executed at core/src/worker.cpp:544). Q6_K has
 // vec_dot_q6_K_q8_K's arithmetic per (activation row m, weight row n):
 //   Y[m][n] = sum_s (d[n][s] * dA[m][s]) * iS,  iS = sum_g sc[n][s][g] * I_g  (exact int32)
 //   I_g = sum over the 16 elements k of group g of qa[m][k] * (q[n][k] - 32)
@@ -21,6 +22,15 @@
 // iS += sc_g * I_g with v_mad_i32_i24 (|I_g| <= 16*32*127 < 2^23; |iS| <= 256*128*32*127 < 2^31);
 // per superblock acc += (d * dA) * iS. The 16 integer multiply-adds per lane and group (against
 // 4 MFMAs per wave and group) are the VALU work that bounds the kernel.
+//
+// Q4_K, vec_dot_q4_K_q8_K's arithmetic, has 8 sub-blocks of 32 with 6-bit scales and mins:
+//   Y[m][n] = sum_s dA[m][s] * (d[n][s] * iA - dmin[n][s] * iM)
+//   iA = sum_j sc_j * I_j,  iM = sum_j m_j * S_j   (exact int32; S_j = the activation's sub-block sum)
+// Same tiling and stages (half a superblock: 4 sub-blocks); the nibbles are unpacked to one int8
+// per element at commit. Per sub-block: v_mfma_i32_32x32x32_i8 (K = 32) into a zero accumulator,
+// then iA += sc_j * I_j. iM runs on the MFMA once per superblock: S_j = 64 hi_j + lo_j (lo_j in
+// [0, 63], hi_j in [-64, 63], split at commit from the 16-element bsums) as int8 bytes
+// [hi_0..7, lo_0..7] against the bytes m_j in the first or the second eight k of a K = 16 MFMA.
 //
 // Workgroup order is XCD-aware (consecutive ids go to different XCDs): each XCD takes a
 // contiguous band of n tiles, so its weight rows stay in that XCD's L2.
@@ -48,6 +58,16 @@ struct __align__(16) StageQ6 {
     float da[kBM];         // activation superblock scale
 };
 
+struct __align__(16) StageQ4 {
+    int8_t a[kBM * kRow];  // activation int8, [m][k] (swizzled 16-byte slots)
+    int8_t b[kBN * kRow];  // weight nibbles as int8 0..15, [n][k] (swizzled 16-byte slots)
+    uint32_t sc[kBN];      // the stage's 4 sub-block scales (6-bit) per weight row
+    uint2 mn[kBN];         // the superblock's 8 sub-block mins (6-bit) per weight row
+    float2 dw[kBN];        // weight (d, dmin)
+    float da[kBM];         // activation superblock scale
+    uint2 sm[kBM][2];      // per activation row: bytes hi_0..7, then lo_0..7 of S_j = 64 hi_j + lo_j
+};
+
 __device__ __forceinline__ int swz(int row, int slot) { return row * kRow + 16 * (slot ^ (row & 7)); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -61,6 +81,13 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 __device__ __forceinline__ void dma16(const void* g, uint32_t off, const void* lds_base) {
     const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(g), "s"(m0) : "memory", "m0");
+}
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v16i mfma32k32(v4i a, v4i b) {
+    v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 }
 
 __device__ __forceinline__ v16i mfma32k16(long a, long b) {
@@ -295,6 +322,244 @@ __global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(const uint8_t* __r
                 if (FULL || m0 + wm + 4 * hl + r < M) yl[(int64_t)r * y_stride + 32 * j] = acc[i][j][v];
             }
     }
+}
+
+// W: Q4_K rows (w_row_bytes % 16 == 0, 16-byte aligned base); xqs: int8 [M][K]; xd: float
+// [K/256][m_ld] with m_ld a multiple of 128; xbs: int16 [M][K/16]; K % 256 == 0.
+// FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
+template <bool DUMP, bool FULL>
+__global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+                                                              int N, int K, const int8_t* __restrict__ xqs,
+                                                              const float* __restrict__ xd, int64_t m_ld,
+                                                              const int16_t* __restrict__ xbs, int M,
+                                                              float* __restrict__ Y, int64_t y_stride,
+                                                              int32_t* __restrict__ sums, int tiles_n, int tiles_m) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    StageQ4* st = reinterpret_cast<StageQ4*>(smem);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    // ---- XCD-aware tile order: XCD x (= id % 8) takes n-tile band x, walked m-first ----
+    const int bid = blockIdx.x;
+    int tile_m, tile_n;
+    if (tiles_n % kXcds == 0) {
+        const int band = tiles_n / kXcds;
+        const int xcd = bid % kXcds, local = bid / kXcds;
+        tile_n = xcd * band + local % band;
+        tile_m = local / band;
+    } else {
+        tile_n = bid % tiles_n;
+        tile_m = bid / tiles_n;
+    }
+    const int m0 = tile_m * kBM, n0 = tile_n * kBN;
+    const int nstages = K / kKS, nsb = K / 256;
+
+    // ---- staging assignment (fixed for the whole K loop) ----
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const int a_row0 = 8 * (4 * wave_u) + (lane >> 3);
+    const int a_slot = (lane & 7) ^ (a_row0 & 7);
+    uint32_t a_off[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = FULL ? m0 + a_row0 + 8 * i : min(m0 + a_row0 + 8 * i, M - 1);
+        a_off[i] = (uint32_t)row * (uint32_t)K + 16u * (uint32_t)a_slot;
+    }
+    // weight rows: row rw = tid / 2 of the tile, part p = tid % 2: the 32 nibble bytes of chunk
+    // 2h + p of the stage's half h (bytes 16 + 64h + 32p: elements 64p + [0, 32) of the stage in
+    // the low nibbles, 64p + 32 + [0, 32) in the high ones); part 0 also loads the 16-byte header
+    // (d, dmin, 12 bytes of scales and mins). Threads 0..127 load activation row m0 + tid's scale
+    // and its superblock's 16 bsums.
+    const int rw = tid >> 1, p = tid & 1;
+    const uint8_t* w_row = W + (int64_t)(FULL ? n0 + rw : min(n0 + rw, N - 1)) * w_row_bytes;
+    const int arow = tid & (kBM - 1);
+    const int da_row = m0 + arow;  // m_ld >= m0 + 128: in bounds for every tile
+    const int16_t* bs_row = xbs + (int64_t)(FULL ? m0 + arow : min(m0 + arow, M - 1)) * (K / 16);
+    uint4 gq[2], ghdr, gbs[2];
+    float gda;
+    auto issue = [&](int stg, StageQ4& S) {
+        const int8_t* ab = xqs + (int64_t)stg * kKS;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16(ab, a_off[i], S.a + 1024 * (4 * wave_u + i));
+        const int s = stg >> 1, h = stg & 1;
+        const uint8_t* sb = w_row + 144 * (int64_t)s;
+        gq[0] = ld16(sb + 16 + 64 * h + 32 * p);
+        gq[1] = ld16(sb + 32 + 64 * h + 32 * p);
+        if (p == 0) ghdr = ld16(sb);
+        gda = xd[(int64_t)s * m_ld + da_row];
+        gbs[0] = ld16(bs_row + 16 * s);
+        gbs[1] = ld16(bs_row + 16 * s + 8);
+    };
+    auto commit = [&](int stg, StageQ4& S) {
+        const int h = stg & 1;
+        const uint32_t lo = 0x0F0F0F0Fu;
+        const uint32_t q[8] = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w};
+        *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p)) = make_uint4(q[0] & lo, q[1] & lo, q[2] & lo, q[3] & lo);
+        *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 1)) = make_uint4(q[4] & lo, q[5] & lo, q[6] & lo, q[7] & lo);
+        *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 2)) =
+            make_uint4((q[0] >> 4) & lo, (q[1] >> 4) & lo, (q[2] >> 4) & lo, (q[3] >> 4) & lo);
+        *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 3)) =
+            make_uint4((q[4] >> 4) & lo, (q[5] >> 4) & lo, (q[6] >> 4) & lo, (q[7] >> 4) & lo);
+        if (p == 0) {
+            // 6-bit scales and mins of the 8 sub-blocks (get_scale_min_k4): j < 4 from bytes j, j + 4;
+            // j >= 4 from the low / high nibble of byte j + 4 and the top two bits of bytes j - 4, j
+            const uint32_t s0 = ghdr.y, s1 = ghdr.z, s2 = ghdr.w;
+            const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+            const uint32_t mn_lo = s1 & 0x3F3F3F3Fu, mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+            S.sc[rw] = h ? sc_hi : sc_lo;
+            S.mn[rw] = make_uint2(mn_lo, mn_hi);
+            S.dw[rw] = make_float2(half_bits_to_float(ghdr.x & 0xFFFFu), half_bits_to_float(ghdr.x >> 16));
+        }
+        if (tid < kBM) {
+            S.da[tid] = gda;
+            // S_j = bsums 2j + 2j + 1, then its bytes: hi_j = S_j >> 6, lo_j = S_j & 63
+            const uint32_t b[8] = {gbs[0].x, gbs[0].y, gbs[0].z, gbs[0].w, gbs[1].x, gbs[1].y, gbs[1].z, gbs[1].w};
+            uint32_t hw[2] = {0u, 0u}, lw[2] = {0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int sj = (int)(int16_t)(b[j] & 0xFFFFu) + ((int)b[j] >> 16);
+                hw[j >> 2] |= ((uint32_t)(sj >> 6) & 0xFFu) << (8 * (j & 3));
+                lw[j >> 2] |= ((uint32_t)sj & 63u) << (8 * (j & 3));
+            }
+            S.sm[tid][0] = make_uint2(hw[0], hw[1]);
+            S.sm[tid][1] = make_uint2(lw[0], lw[1]);
+        }
+    };
+
+    // ---- wave tile: 64 x 64 at (wm, wn) inside the workgroup tile ----
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int col = lane & 31, hl = lane >> 5;
+    float acc[2][2][16];
+    int ai[2][2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f, ai[i][j][v] = 0;
+
+    issue(0, st[0]);
+    commit(0, st[0]);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
+    __syncthreads();
+
+    for (int stg = 0; stg < nstages; ++stg) {
+        const StageQ4& S = st[stg & 1];
+        const bool more = stg + 1 < nstages;
+        if (more) issue(stg + 1, st[(stg + 1) & 1]);  // in flight while this stage computes
+        uint32_t scw[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) scw[j] = S.sc[wn + 32 * j + col];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            // sub-block kb: lane half hl takes the 16-byte slot 2 kb + hl
+            const int fo = col * kRow + 16 * ((2 * kb + hl) ^ (col & 7));
+            v4i fa[2], fb[2];
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const v4i*>(S.a + fo + (wm + 32 * ii) * kRow);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) fb[jj] = *reinterpret_cast<const v4i*>(S.b + fo + (wn + 32 * jj) * kRow);
+            int sc[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) sc[j] = (int)((scw[j] >> (8 * kb)) & 0xFFu);
+            v16i D[2][2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) D[i][j] = mfma32k32(fa[i], fb[j]);
+            // |I_j| <= 32*15*127 < 2^23; |iA| <= 8*63*32*15*127 < 2^31
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) ai[i][j][v] = __mul24(sc[j], D[i][j][v]) + ai[i][j][v];
+        }
+        if (stg & 1) {
+            // end of superblock s: iM on the MFMA, then acc += dA * (d * iA - dmin * iM)
+            const int s = stg >> 1;
+            long am[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint2 v = S.sm[wm + 32 * i + col][hl];
+                am[i] = (long)(((uint64_t)v.y << 32) | v.x);
+            }
+            long bh[2], bl[2];
+            float2 dmj[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint2 v = S.mn[wn + 32 * j + col];
+                const long mb = (long)(((uint64_t)v.y << 32) | v.x);
+                bh[j] = hl ? 0 : mb;  // k 0..7 (the hi bytes) against the mins
+                bl[j] = hl ? mb : 0;  // k 8..15 (the lo bytes)
+                dmj[j] = S.dw[wn + 32 * j + col];
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                float da[16];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float4 v4 = *reinterpret_cast<const float4*>(&S.da[wm + 32 * i + 8 * q + 4 * hl]);
+                    da[4 * q] = v4.x, da[4 * q + 1] = v4.y, da[4 * q + 2] = v4.z, da[4 * q + 3] = v4.w;
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const v16i Mh = mfma32k16(am[i], bh[j]);
+                    const v16i Ml = mfma32k16(am[i], bl[j]);
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int iM = (Mh[v] << 6) + Ml[v];  // |iM| <= 8*63*4064 < 2^31
+                        const float t = fmaf(-dmj[j].y, (float)iM, dmj[j].x * (float)ai[i][j][v]);
+                        acc[i][j][v] = fmaf(da[v], t, acc[i][j][v]);
+                        if (DUMP) {
+                            const int n = n0 + wn + 32 * j + col;
+                            const int m = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
+                            if (m < M && n < N) {
+                                int32_t* o = sums + (((int64_t)m * N + n) * nsb + s) * 2;
+                                o[0] = ai[i][j][v];
+                                o[1] = iM;
+                            }
+                        }
+                        ai[i][j][v] = 0;
+                    }
+                }
+            }
+        }
+        if (more) {
+            commit(stg + 1, st[(stg + 1) & 1]);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
+            __syncthreads();
+        }
+    }
+
+    // ---- store: lane owns column n, rows m0 + wm + 32i + 8(v/4) + 4hl + v%4 ----
+    float* yl = Y + (int64_t)(m0 + wm + 4 * hl) * y_stride + (n0 + wn + col);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        if (!FULL && n0 + wn + 32 * j + col >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int r = 32 * i + 8 * (v >> 2) + (v & 3);
+                if (FULL || m0 + wm + 4 * hl + r < M) yl[(int64_t)r * y_stride + 32 * j] = acc[i][j][v];
+            }
+    }
+}
+
+hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+    if (K % 256 || w_row_bytes % 16 || act.m_ld % kBM || !act.bs || N > (1 << 30) || M > (1 << 30) ||
+        K > (1 << 30))
+        return hipErrorNotSupported;
+    if ((uint64_t)M * (uint64_t)K >= (1ull << 32)) return hipErrorNotSupported;  // 32-bit DMA offsets
+    const int tiles_n = (int)((N + kBN - 1) / kBN), tiles_m = (int)((M + kBM - 1) / kBM);
+    const size_t lds = 2 * sizeof(StageQ4);
+    const bool full = M % kBM == 0 && N % kBN == 0;
+    auto fn = block_sums ? (full ? prefill_q4_k_kernel<true, true> : prefill_q4_k_kernel<true, false>)
+                         : (full ? prefill_q4_k_kernel<false, true> : prefill_q4_k_kernel<false, false>);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, (const uint8_t*)W, w_row_bytes,
+                       (int)N, (int)K, act.qs, act.d, act.m_ld, (const int16_t*)act.bs, (int)M, Y, y_stride,
+                       block_sums, tiles_n, tiles_m);
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,

@@ -97,6 +97,8 @@ CASES = [
     # m-tiles: full, then ragged M and N
     (Q8_0, 256, 384, 1024), (Q8_0, 512, 256, 512), (Q8_0, 700, 300, 640),
     (Q4_K, 1, 97, 2560), (Q4_K, 2, 64, 256), (Q4_K, 5, 40, 512), (Q4_K, 64, 96, 2048), (Q4_K, 70, 33, 768),
+    # the Q4_K prefill kernel (M > 128): unguarded 128 x 128 tiles, ragged M and N, one superblock
+    (Q4_K, 256, 384, 1024), (Q4_K, 200, 300, 2048), (Q4_K, 130, 129, 256),
     # single-row decode at full width: 5-wave workgroups (rows spread evenly over the CUs)
     (Q4_K, 1, 9728, 2560), (Q4_K, 1, 2570, 4096), (Q4_K, 1, 2561, 9728),
     (Q6_K, 1, 50, 9728), (Q6_K, 1, 3, 256), (Q6_K, 8, 64, 512), (Q6_K, 33, 65, 1024), (Q6_K, 3, 17, 768),
