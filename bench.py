@@ -172,10 +172,10 @@ def load_traffic(cfg_index):
     return None
 
 
-def load_counters(cfg_index):
+def load_counters(cfg_index, key="config"):
     """The dominant kernel's utilisation counters from the committed PMC summary
     (profiles/counters.txt, written by --summarize-pmc from rocprofv3 --pmc runs of --profile),
-    or None."""
+    or None. key="extra" looks up an extra's line by its label instead of a config index."""
     path = os.path.join(ROOT, "profiles", "counters.txt")
     if not os.path.exists(path):
         return None
@@ -184,14 +184,14 @@ def load_counters(cfg_index):
             if line.startswith("#") or not line.strip():
                 continue
             kv = dict(tok.split("=", 1) for tok in line.split() if "=" in tok)
-            if kv.get("config") == str(cfg_index):
+            if kv.get(key) == str(cfg_index):
                 out = {}
                 for k, v in kv.items():
                     try:
                         out[k] = float(v)
                     except ValueError:
                         out[k] = v
-                out.pop("config", None)
+                out.pop(key, None)
                 out["source"] = "profiles/counters.txt"
                 return out
     return None
@@ -500,6 +500,31 @@ def bench_kv_attention(args, dev, ct, n_tokens=1, n_past=4095, n_layer=36, n_hea
                           "frac": flops / (ms * 1e-3) / 1e12 / 157.3})}
 
 
+def random_weights(dev, wtype, N, K, copies, seed):
+    """copies x N rows of valid random quants of `wtype` with small positive fp16 scales (d =
+    0.0004, Q4_K dmin = 0.0002): the kernels' work does not depend on the values, and quantizing
+    hundreds of MB of floats would dominate the run."""
+    import torch
+    import densecore_amd as dc
+    rb = dc.row_size(wtype, K)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    big = torch.randint(0, 256, (copies, N, rb), dtype=torch.uint8, device=dev, generator=g)
+    bs = {dc.TYPE_Q8_0: 34, dc.TYPE_Q4_K: 144, dc.TYPE_Q6_K: 210}[wtype]
+    blocks = big.view(copies, N, rb // bs, bs)
+
+    def f16(v):
+        return torch.from_numpy(np.frombuffer(np.float16(v).tobytes(), dtype=np.uint8).copy()).to(dev)
+
+    if wtype == dc.TYPE_Q6_K:
+        blocks[..., 208:210] = f16(0.0004)
+    else:
+        blocks[..., 0:2] = f16(0.0004)
+        if wtype == dc.TYPE_Q4_K:
+            blocks[..., 2:4] = f16(0.0002)
+    return big
+
+
 def bench_lm_head(args, dev, wtype, K, M, N=151936):
     """The LM head (ggml_mul_mat(output, cur), core/src/inference.cpp:1817), the largest weight
     stream of a decode step: Qwen3's 151,936-token vocabulary, random valid quants (the kernels do
@@ -509,14 +534,9 @@ def bench_lm_head(args, dev, wtype, K, M, N=151936):
     rb = dc.row_size(wtype, K)
     wbytes = N * rb
     copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    big = random_weights(dev, wtype, N, K, copies, 17)
     g = torch.Generator(device=dev)
-    g.manual_seed(17)
-    big = torch.randint(0, 256, (copies, N, rb), dtype=torch.uint8, device=dev, generator=g)
-    bs = 34 if wtype == dc.TYPE_Q8_0 else 210
-    off = 0 if wtype == dc.TYPE_Q8_0 else 208
-    blocks = big.view(copies, N, rb // bs, bs)
-    half = torch.from_numpy(np.frombuffer(np.float16(0.0004).tobytes(), dtype=np.uint8).copy()).to(dev)
-    blocks[..., off:off + 2] = half
+    g.manual_seed(18)
     x = torch.randn((M, K), device=dev, generator=g)
     y = torch.empty((M, N), dtype=torch.float32, device=dev)
     ws = torch.empty(dc.mul_mat_workspace_size(wtype, M, K), dtype=torch.uint8, device=dev)
@@ -533,6 +553,9 @@ def bench_lm_head(args, dev, wtype, K, M, N=151936):
         c = read_ceiling(big.view(copies, -1), wbytes, copies, args)
         out["read_ceiling_us"] = c["us"]
         out["frac_of_read_ceiling"] = c["us"] / (ms * 1e3)
+    counters = load_counters(f"lm_head_{dc.TYPE_NAMES[wtype].lower()}_m{M}", key="extra")
+    if counters is not None:
+        out["counters"] = counters
     del big, ws, y, x
     torch.cuda.empty_cache()
     return out
@@ -548,16 +571,9 @@ def bench_kquant_prefill(args, dev, wtype, M=2048, N=8192, K=2048):
     rb = dc.row_size(wtype, K)
     wbytes = N * rb
     copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    big = random_weights(dev, wtype, N, K, copies, 29)
     g = torch.Generator(device=dev)
-    g.manual_seed(29)
-    big = torch.randint(0, 256, (copies, N, rb), dtype=torch.uint8, device=dev, generator=g)
-    blocks = big.view(copies, N, K // 256, rb // (K // 256))
-    d = torch.from_numpy(np.frombuffer(np.float16(0.0004).tobytes(), dtype=np.uint8).copy()).to(dev)
-    if wtype == dc.TYPE_Q6_K:
-        blocks[..., 208:210] = d
-    else:
-        blocks[..., 0:2] = d
-        blocks[..., 2:4] = torch.from_numpy(np.frombuffer(np.float16(0.0002).tobytes(), dtype=np.uint8).copy()).to(dev)
+    g.manual_seed(30)
     x = torch.randn((M, K), device=dev, generator=g)
     y = torch.empty((M, N), dtype=torch.float32, device=dev)
     ws = torch.empty(dc.mul_mat_workspace_size(wtype, M, K), dtype=torch.uint8, device=dev)
@@ -578,6 +594,9 @@ def bench_kquant_prefill(args, dev, wtype, M=2048, N=8192, K=2048):
     out = {"shape": f"{dc.TYPE_NAMES[wtype]} M={M} N={N} K={K}", "step_us": step_ms * 1e3, "kernels": kern,
            "kernel_us": k_ms * 1e3, "TOPS_kernel": ops / (k_ms * 1e-3) / 1e12,
            "frac_of_int8_peak": ops / (k_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS}
+    counters = load_counters(f"prefill_{dc.TYPE_NAMES[wtype].lower()}", key="extra")
+    if counters is not None:
+        out["counters"] = counters
     del big, ws, y, x
     torch.cuda.empty_cache()
     return out
@@ -631,6 +650,33 @@ def profile_config(cfg, args, dev):
     print(f"# profiled config {cfg.index}: {args.warmup + args.steps} eager steps", file=sys.stderr, flush=True)
     del big, ws, y, x, wq
     torch.cuda.empty_cache()
+
+
+# Extras whose kernels the counter passes cover: (label, kernel, weight type, M, N, K). The LM heads
+# share their kernels with configs 1 and 3 and are told apart by grid size (PROFILED below).
+PROFILE_EXTRAS = [("lm_head_q8_0_m1", "decode_q8_0_kernel", "Q8_0", 1, 151936, 1024),
+                  ("lm_head_q6_k_m1", "decode_q6k_lds_kernel", "Q6_K", 1, 151936, 2560),
+                  ("prefill_q4_k", "prefill_q4_k_kernel", "Q4_K", 2048, 8192, 2048),
+                  ("prefill_q6_k", "prefill_q6_k_kernel", "Q6_K", 2048, 8192, 2048)]
+
+
+def profile_extras(args, dev):
+    """Eager calls of the PROFILE_EXTRAS shapes (random valid quants, W rotated like the configs)."""
+    import torch
+    import densecore_amd as dc
+    for label, _, tname, M, N, K in PROFILE_EXTRAS:
+        wt = getattr(dc, "TYPE_" + tname)
+        copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / (N * dc.row_size(wt, K)))))
+        big = random_weights(dev, wt, N, K, copies, 41)
+        x = torch.randn((M, K), device=dev)
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
+        ws = torch.empty(dc.mul_mat_workspace_size(wt, M, K), dtype=torch.uint8, device=dev)
+        for i in range(args.warmup + args.steps):
+            dc.mul_mat(wt, big[i % copies], N, K, x, y=y, workspace=ws)
+        torch.cuda.synchronize()
+        print(f"# profiled {label}: {args.warmup + args.steps} eager calls", file=sys.stderr, flush=True)
+        del big, ws, y, x
+        torch.cuda.empty_cache()
 
 
 def profile_read(args, dev):
@@ -688,6 +734,12 @@ def summarize_read(path, configs, launches):
 # the kernel that dominates each config's step (for --summarize-pmc)
 DOMINANT = {1: "decode_q8_0_kernel", 2: "decode_kq_kernel", 3: "decode_q6k_lds_kernel", 4: "batch_q4k_kernel",
             5: "prefill_q8_0_kernel"}
+# counter summary lines: (label, kernel, smallest and largest grid in threads). The configs' decode
+# grids stay below 300 k threads; the LM heads' (151936 rows) are above.
+LM_GRID = 300_000
+PROFILED = ([(f"config={i}", k, 0, LM_GRID) for i, k in sorted(DOMINANT.items())] +
+            [(f"extra={lab}", k, LM_GRID if lab.startswith("lm_head") else 0, 1 << 62)
+             for lab, k, *_ in PROFILE_EXTRAS])
 
 
 def summarize_pmc(paths):
@@ -717,12 +769,12 @@ def summarize_pmc(paths):
         for r in csv.DictReader(open(p)):
             key = (p, r["Dispatch_Id"])
             per[key][r["Counter_Name"]] = float(r["Counter_Value"])
-            names[key] = r["Kernel_Name"]
+            names[key] = (r["Kernel_Name"], int(r["Grid_Size"]))
     lines = [f"# per-dispatch medians; {agent['simds']} SIMDs, {agent['cus']} CUs, {agent['xcds']} XCDs"]
-    for cfg_i, kname in sorted(DOMINANT.items()):
+    for label, kname, gmin, gmax in PROFILED:
         rows = collections.defaultdict(list)
         for key, cnt in per.items():
-            if kname in names[key]:
+            if kname in names[key][0] and gmin <= names[key][1] < gmax:
                 for c, v in cnt.items():
                     rows[c].append(v)
         if not rows:
@@ -730,7 +782,7 @@ def summarize_pmc(paths):
         med = {c: float(np.median(v)) for c, v in rows.items()}
         n_disp = max(len(v) for v in rows.values())
         gui = med.get("GRBM_GUI_ACTIVE")
-        kv = [f"config={cfg_i}", f"kernel={kname}", f"samples={n_disp}"]
+        kv = [label, f"kernel={kname}", f"samples={n_disp}"]
         if gui:
             gui_x = gui / agent["xcds"]
             kv.append(f"gui_cycles_per_xcd={gui_x:.0f}")
@@ -843,6 +895,8 @@ def main():
         for c in dc.CONFIGS:
             if c.index in wanted:
                 profile_config(c, args, dev)
+        if not args.no_extras:
+            profile_extras(args, dev)
         calibration_copy(dev)
         return 0
     if args.profile_read:
