@@ -370,6 +370,254 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     }
 }
 
+// ---------------------------------------------------------------- tall matrices on the MFMA
+// Matrices of many rows (an LM head: 151936) at M <= 8: the weight rows go through the int8 MFMA
+// in tiles of 32, v_mfma_i32_32x32x16_i8 per 16-element group with the activation as the A
+// operand (MFMA rows m; rows >= M repeat the last real one and are never stored) and 32 weight
+// rows as the B operand (columns n). Lane (n, hl) of the result holds rows m = 4 hl + v, v < 4,
+// of column n: iS += sc_g * I_g is MV (= min(M tile, 4)) v_mad_i32_i24 per group for 32 rows,
+// where the lane-per-superblock kernel above spends its VALU on one row at a time (and at
+// K = 2560 leaves 24 of 64 lanes idle). The weight bytes are unpacked to signed q - 32 in
+// registers (a v_perm table lookup for the two qh bits, v_bfi for the ql nibble).
+//
+// Staging: each wave streams its tiles superblock by superblock through two LDS buffers (32
+// rows x 264 bytes: 8-byte aligned rows, 8-byte reads of the 32 rows conflict-free). A row's
+// superblock is one direct-to-LDS instruction: lanes 0..52 the 53 dwords from the dword at or
+// below it (lanes 53..63 repeat lane 52's dword into the row's padding), so an odd superblock
+// (210 s = 2 mod 4) sits 2 bytes into its LDS row; the next superblock's 32 loads are in flight
+// while the current one computes. The activation (planar Q8_K: qs and d; the bsums
+// are not needed, the -32 is in the operand) is staged once per workgroup. A workgroup owns tiles
+// blockIdx.x + k * gridDim.x; its 8 waves take k from an LDS counter, so the tiles of a CU spread
+// over its waves whatever their count.
+constexpr int kTallWaves = 8;
+constexpr int kTallPitch = 264;             // LDS bytes per staged row (66 dwords)
+constexpr int kTallBuf = 32 * kTallPitch;   // one superblock of a 32-row tile
+constexpr int64_t kTallMinRows = 32768;     // rows from which the MFMA form is used
+
+__host__ __device__ inline size_t tall_act_bytes(int MT, int nsb) {
+    return (size_t)round_up((int64_t)MT * 256 * nsb + (int64_t)nsb * MT * 4 + 16, 256);
+}
+__host__ __device__ inline size_t tall_lds_bytes(int MT, int nsb) {
+    return tall_act_bytes(MT, nsb) + (size_t)kTallWaves * 2 * kTallBuf;
+}
+
+// one dword per lane from global memory (uniform base `g` + per-lane offset) into LDS at
+// lds_base + 4 * lane; the base is an SGPR pair, M0 the LDS base
+__device__ __forceinline__ void dma4s(const void* g, uint32_t off, const void* lds_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(g), "s"(m0) : "memory", "m0");
+}
+
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16i_t mfma_32x32x16(long a, long b) {
+    v16i_t z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, z, 0, 0, 0);
+}
+
+// Signed q - 32 bytes of four 6-bit quants: ql nibbles in bits 0-3 of each byte, the two high
+// bits in bits 0-1 of each byte of qh2 ((qh2 - 2) << 4 is byte qh2 of the table 0x1000F0E0).
+__device__ __forceinline__ uint32_t q6_signed(uint32_t ql, uint32_t qh2) {
+    return bfi(0x0F0F0F0Fu, ql, __builtin_amdgcn_perm(0u, 0x1000F0E0u, qh2));
+}
+
+// 8 bytes at p + SH (p 8-byte aligned, SH 0 or 2): one ds_read_b64, or three dwords realigned
+template <int SH>
+__device__ __forceinline__ uint2 lds8_sh(const uint8_t* p) {
+    if constexpr (SH == 0) {
+        return *reinterpret_cast<const uint2*>(p);
+    } else {
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+        const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
+        return make_uint2(align_bytes(w1, w0, 2), align_bytes(w2, w1, 2));
+    }
+}
+
+// One superblock s of a 32-row tile: the lane's column n = col (LDS row `row`, superblock byte 0
+// at row + SH), activation rows min(col, MT - 1) as the A operand.
+template <int MT, int SH>
+__device__ __forceinline__ void tall_superblock(const uint8_t* row, const int8_t* arow, int hl, int (&ai)[4]) {
+    constexpr int MV = MT < 4 ? MT : 4;
+    uint32_t scw[4];
+    if constexpr (SH == 0) {  // rows are 8-byte aligned: two 8-byte reads
+        const uint2 v0 = *reinterpret_cast<const uint2*>(row + 192), v1 = *reinterpret_cast<const uint2*>(row + 200);
+        scw[0] = v0.x, scw[1] = v0.y, scw[2] = v1.x, scw[3] = v1.y;
+    } else {
+        const uint32_t* q = reinterpret_cast<const uint32_t*>(row + 192);
+        const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3], w4 = q[4];
+        scw[0] = align_bytes(w1, w0, 2), scw[1] = align_bytes(w2, w1, 2);
+        scw[2] = align_bytes(w3, w2, 2), scw[3] = align_bytes(w4, w3, 2);
+    }
+    // Four blocks (h, gg) of four groups each, software-pipelined: the MFMAs of block i run while
+    // the operands of block i + 1 are read and unpacked, then block i's results are consumed.
+    // The compiler let the VALU read these MFMAs' results and overwrite their operand registers a
+    // few cycles after issue (wrong sums from the later MFMAs of a block), so the order is pinned
+    // with scheduling barriers, the operands and all 16 result registers of each MFMA are kept
+    // allocated until consumed, and at least the unpacking of the next block (plus 8 wait
+    // states; 48 after the last block) separates an MFMA from the read of its result.
+    long aw[2][4], bw[2][4];
+    auto prep = [&](int blk, long (&a)[4], long (&b)[4]) {
+        const int h = blk >> 1, gg = blk & 1, l = 16 * gg + 8 * hl;
+        const uint2 qa = lds8_sh<SH>(row + 64 * h + l);       // quarters 0 (low nibbles), 2 (high)
+        const uint2 qb = lds8_sh<SH>(row + 64 * h + 32 + l);  // quarters 1, 3
+        const uint2 qh = lds8_sh<SH>(row + 128 + 32 * h + l);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int g = 8 * h + 2 * t + gg;  // group of elements 128h + 32t + 16gg + [0, 16)
+            const uint2 src = (t & 1) ? qb : qa;
+            const uint32_t nsh = 4u * (uint32_t)(t >> 1), hsh = 2u * (uint32_t)t;
+            const uint32_t b0 = q6_signed(src.x >> nsh, (qh.x >> hsh) & 0x03030303u);
+            const uint32_t b1 = q6_signed(src.y >> nsh, (qh.y >> hsh) & 0x03030303u);
+            b[t] = (long)(((uint64_t)b1 << 32) | b0);
+            a[t] = *reinterpret_cast<const long*>(arow + 16 * g);
+        }
+    };
+    prep(0, aw[0], bw[0]);
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk) {
+        const int cur = blk & 1;
+        v16i_t D[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) D[t] = mfma_32x32x16(aw[cur][t], bw[cur][t]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (blk < 3) {
+            prep(blk + 1, aw[cur ^ 1], bw[cur ^ 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 7");
+        } else {
+            asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15");
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) asm volatile("" ::"v"(aw[cur][t]), "v"(bw[cur][t]));
+        __builtin_amdgcn_sched_barrier(0);
+        const int h = blk >> 1, gg = blk & 1;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int g = 8 * h + 2 * t + gg;
+            const int sc = __builtin_amdgcn_sbfe((int)scw[g >> 2], 8 * (g & 3), 8);
+#pragma unroll
+            for (int v = 0; v < MV; ++v) ai[v] = __mul24(sc, D[t][v]) + ai[v];  // |I_g| < 2^16
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) asm volatile("" ::"v"(D[t]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+template <int MT, bool DUMP>
+__global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
+    const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
+    const int8_t* __restrict__ xqs, const float* __restrict__ xd, int64_t m_ld, int M, float* Y, int64_t y_stride,
+    int32_t* __restrict__ sums, int64_t sums_n_stride, const float* R, int64_t r_stride) {
+    constexpr int MV = MT < 4 ? MT : 4;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int K = nsb * 256;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 31, hl = lane >> 5;
+    int8_t* aq = reinterpret_cast<int8_t*>(smem);                        // [MT][K]
+    float* ad = reinterpret_cast<float*>(smem + (size_t)MT * K);         // [nsb][MT]
+    int* ctr = reinterpret_cast<int*>(smem + (size_t)MT * K + (size_t)nsb * MT * 4);
+    uint8_t* wb = smem + tall_act_bytes(MT, nsb) + (size_t)wave * 2 * kTallBuf;
+
+    // ---- activation: MT rows of qs (rows >= M repeat row M - 1) and the superblock scales ----
+    for (int i = tid; i < MT * K / 16; i += 64 * kTallWaves) {
+        const int m = i / (K / 16), c = i % (K / 16);
+        *reinterpret_cast<uint4*>(aq + (size_t)m * K + 16 * c) =
+            *reinterpret_cast<const uint4*>(xqs + (int64_t)(m < M ? m : M - 1) * K + 16 * c);
+    }
+    for (int i = tid; i < nsb * MT; i += 64 * kTallWaves) ad[i] = xd[(int64_t)(i / MT) * m_ld + i % MT];
+    if (tid == 0) *ctr = 0;
+    __syncthreads();
+
+    const int64_t tiles = (n1 - n0 + 31) / 32;
+    const int G = gridDim.x, c0 = blockIdx.x;
+    const int cnt = (int)((tiles - c0 + G - 1) / G);  // this workgroup's tiles: c0 + k * G
+    auto claim = [&]() {
+        int v = 0;
+        if (lane == 0) v = atomicAdd(ctr, 1);
+        return __builtin_amdgcn_readfirstlane(v);
+    };
+    // 53 dwords of row r of the tile (superblock s, from the dword at or below it) into buffer b;
+    // rows past n1 (the last tile) repeat row n1 - 1
+    const uint32_t dma_off = 4u * (uint32_t)(lane < 53 ? lane : 52);
+    // (rows r0 .. r1 - 1 of the tile: the loop issues 31 rows, waits, then the last one, so that
+    // at most 63 loads are ever outstanding, what vmcnt counts)
+    auto issue = [&](int k, int s, int b, int r0, int r1) {
+        const int64_t rbase = n0 + (int64_t)(c0 + (int64_t)k * G) * 32;
+        const int64_t sboff = 210 * (int64_t)s - ((210 * s) & 3);
+        uint8_t* dst = wb + b * kTallBuf;
+        if (rbase + 32 <= n1) {
+            const uint8_t* src = W + rbase * w_row_bytes + sboff;
+#pragma unroll 8
+            for (int r = r0; r < r1; ++r) dma4s(src + r * w_row_bytes, dma_off, dst + r * kTallPitch);
+        } else {
+            for (int r = r0; r < r1; ++r) {
+                const int64_t row = rbase + r < n1 ? rbase + r : n1 - 1;
+                dma4s(W + row * w_row_bytes + sboff, dma_off, dst + r * kTallPitch);
+            }
+        }
+    };
+
+    int k_cur = claim();
+    if (k_cur >= cnt) return;  // no barrier follows: a wave without a tile may leave
+    int k_next = claim();
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    int ai[4] = {0, 0, 0, 0};
+    const int8_t* arow = aq + (size_t)(col < MT ? col : MT - 1) * K + 8 * hl;
+    issue(k_cur, 0, 0, 0, 32);
+    int s = 0, b = 0;
+    for (;;) {
+        const bool last_sb = s + 1 == nsb;
+        const bool more = !last_sb || k_next < cnt;
+        if (more) {
+            const int nk = last_sb ? k_next : k_cur, ns = last_sb ? 0 : s + 1;
+            // the other buffer's previous reads have returned (lgkmcnt(0)) before it is refilled
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            issue(nk, ns, b ^ 1, 0, 31);
+            wait_vmcnt<31>();  // this superblock's 32 loads (issued before the next one's) are in
+            issue(nk, ns, b ^ 1, 31, 32);
+        } else {
+            wait_vmcnt<0>();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const uint8_t* row = wb + b * kTallBuf + col * kTallPitch;
+        if ((210 * s) & 3)
+            tall_superblock<MT, 2>(row, arow + 256 * s, hl, ai);
+        else
+            tall_superblock<MT, 0>(row, arow + 256 * s, hl, ai);
+        const float dW = half_bits_to_float(*reinterpret_cast<const uint16_t*>(row + 208 + ((210 * s) & 3)));
+        const int64_t n = n0 + (int64_t)(c0 + (int64_t)k_cur * G) * 32 + col;
+#pragma unroll
+        for (int v = 0; v < MV; ++v) {
+            const int m = 4 * hl + v;
+            acc[v] = fmaf(dW * ad[s * MT + (m < MT ? m : MT - 1)], (float)ai[v], acc[v]);
+            if (DUMP && m < M && n < n1) sums[((int64_t)m * sums_n_stride + (n - n0)) * nsb + s] = ai[v];
+            ai[v] = 0;
+        }
+        if (last_sb) {
+            if (n < n1) {
+#pragma unroll
+                for (int v = 0; v < MV; ++v) {
+                    const int m = 4 * hl + v;
+                    if (m < M)  // R (optional, may alias Y): Y = W x + R
+                        Y[(int64_t)m * y_stride + (n - n0)] =
+                            R ? acc[v] + R[(int64_t)m * r_stride + (n - n0)] : acc[v];
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[v] = 0.0f;
+            if (!more) break;
+            k_cur = k_next;
+            k_next = claim();
+            s = 0;
+        } else {
+            ++s;
+        }
+        b ^= 1;
+    }
+}
+
 namespace {
 
 using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, const int16_t*,
@@ -418,6 +666,28 @@ int q6_rows_per_wave(int64_t rows, int nw) {
     return rpw > 16 ? 16 : rpw;
 }
 
+using TallFn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, int64_t, int,
+                        float*, int64_t, int32_t*, int64_t, const float*, int64_t);
+
+template <bool DUMP>
+TallFn tall_pick(int mt) {
+    switch (mt) {
+        case 1: return decode_q6k_mfma_kernel<1, DUMP>;
+        case 2: return decode_q6k_mfma_kernel<2, DUMP>;
+        case 4: return decode_q6k_mfma_kernel<4, DUMP>;
+        default: return decode_q6k_mfma_kernel<8, DUMP>;
+    }
+}
+
+// The MFMA form for tall matrices (DCQ_Q6K_MFMA=0 keeps the lane-per-superblock kernels): an even
+// number of superblocks (the 53-dword staging of an even superblock reads 2 bytes into the next)
+// and the activation tile within the LDS left by the weight buffers.
+bool q6_use_mfma(int64_t rows, int nsb, int64_t M) {
+    if (rows < kTallMinRows || nsb % 2 != 0 || knob(Knob::Q6KMfma) == 0) return false;
+    const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
+    return tall_lds_bytes(mt, nsb) <= kMaxLds;
+}
+
 template <bool DUMP>
 Q6Fn q6_pick(int mt) {
     switch (mt) {
@@ -438,6 +708,21 @@ hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0,
     // the weight base is 16-byte aligned (checked by the C ABI)
     if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb) return hipErrorNotSupported;
     if (knob(Knob::Q6KLdsOff)) return hipErrorNotSupported;
+    if (q6_use_mfma(n1 - n0, nsb, M)) {
+        const int64_t tiles = (n1 - n0 + 31) / 32;
+        const unsigned grid = (unsigned)(tiles < cu_count() ? tiles : cu_count());
+        for (int64_t m0 = 0; m0 < M; m0 += 8) {
+            const int64_t mc = M - m0 < 8 ? M - m0 : 8;
+            const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
+            TallFn fn = block_sums ? tall_pick<true>(mt) : tall_pick<false>(mt);
+            hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kTallWaves), tall_lds_bytes(mt, nsb), st, (const uint8_t*)W,
+                               w_row_bytes, n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.m_ld, (int)mc,
+                               Y + m0 * y_stride, y_stride,
+                               block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr, sums_n_stride,
+                               R ? R + m0 * r_stride : nullptr, r_stride);
+        }
+        return hipGetLastError();
+    }
     const int nw = 4;  // 5-wave workgroups (rows spread more evenly) measured no faster here
     // several rows per wave only where a step of 16 superblocks covers the row (the waits count
     // two rows' loads)
@@ -468,6 +753,8 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
     const int nsb = (int)(K / 256);
     if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || M > 2) return hipErrorNotSupported;
     if (knob(Knob::Q6KLdsOff) || knob(Knob::Q6KNoFuse)) return hipErrorNotSupported;
+    // tall matrices: the MFMA kernel over the separately quantized activation
+    if (q6_use_mfma(N, nsb, M)) return hipErrorNotSupported;
     // Workgroup width (one row per wave). Up to K = 4096, 4 waves (measured at M = 1 against
     // quantize + decode: 2560 x 4096 5.7 vs 7.2 us; 1024 x 2560 3.8 vs 5.8 us). Beyond, every
     // workgroup re-reads and re-quantizes the whole activation (39 KB at K = 9728: 4-wave

@@ -47,6 +47,7 @@ enum class Knob {
     GemvLanes,    // DCQ_GEMV_LG: log2 lanes per row of the generic GEMV (-1: rule)
     AttnNoMfma,   // DCQ_ATTN_NO_MFMA: 1 keeps prompts on the VALU attention kernel
     Q6KRows,      // DCQ_Q6K_RPW: rows per wave of the 4-wave Q6_K decode (-1: launch rule)
+    Q6KMfma,      // DCQ_Q6K_MFMA: 0 keeps tall Q6_K matrices on the lane-per-superblock kernels
     kCount
 };
 int knob(Knob k);
