@@ -197,16 +197,20 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
         const Stage& S = st[s & 1];
         const bool more = s + 1 < nstages;
         if (more) DCQ_ISSUE(s + 1, st[(s + 1) & 1]);  // in flight while this stage computes
-#pragma unroll 1
-        for (int kb = 0; kb < kKB; ++kb) {
-            // this lane's fragment rows wm + 32i + col and wn + 32j + col share row % 8 = col % 8, so
-            // the swizzled slot of block kb depends on (kb, hl, col) only; the rows are immediates
-            const int fo = col * kRow + 16 * ((2 * kb + hl) ^ (col & 7));
-            v4i fa[2], fb[2];
+        // fragments of block kb are read one block ahead (block 0 here, block kb + 1 after block
+        // kb's MFMAs issue), so the MFMAs of a block do not wait for their LDS reads
+        // this lane's fragment rows wm + 32i + col and wn + 32j + col share row % 8 = col % 8, so
+        // the swizzled slot of block kb depends on (kb, hl, col) only; the rows are immediates
+        v4i fa[2], fb[2];
+        {
+            const int fo = col * kRow + 16 * (hl ^ (col & 7));
 #pragma unroll
             for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const v4i*>(S.a + fo + (wm + 32 * ii) * kRow);
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) fb[jj] = *reinterpret_cast<const v4i*>(S.b + fo + (wn + 32 * jj) * kRow);
+        }
+#pragma unroll 1
+        for (int kb = 0; kb < kKB; ++kb) {
             float2 wc[2];
 #pragma unroll
             for (int j = 0; j < 2; ++j) wc[j] = S.dwc[kb][wn + 32 * j + col];
@@ -216,6 +220,13 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) D[i][j] = mfma32(fa[i], fb[j], cmagic);
+            if (kb + 1 < kKB) {
+                const int fo = col * kRow + 16 * ((2 * kb + 2 + hl) ^ (col & 7));
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const v4i*>(S.a + fo + (wm + 32 * ii) * kRow);
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) fb[jj] = *reinterpret_cast<const v4i*>(S.b + fo + (wn + 32 * jj) * kRow);
+            }
             float4 da_v[2][4];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
