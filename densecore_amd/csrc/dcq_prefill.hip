@@ -14,7 +14,8 @@
 // (global_load_lds_dwordx4 from a scalar base, no registers in flight); weight block pairs
 // pass through registers to be re-sliced, and the commit also stores each block's epilogue
 // constants (dW, -dW * 1.5*2^23) beside the quants. LDS rows are 128 bytes whose 16-byte slots
-// are XOR-swizzled by row % 8, so the 32 rows a ds_read_b128 touches spread over the banks.
+// are XOR-swizzled by a key of the row (swz_key), so the rows a ds_read_b128 touches spread over
+// the banks.
 //
 // Epilogue per MFMA (16 values per lane; lane = one weight row n, 16 activation rows m):
 // the accumulator is seeded with the bit pattern of 1.5 * 2^23, so the int32 result read
@@ -44,7 +45,7 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kBM = 128, kBN = 128;  // workgroup tile
 constexpr int kKB = 4;               // Q8_0 blocks per stage
 constexpr int kKS = kKB * 32;        // k per stage = bytes per LDS row
-constexpr int kRow = kKS;            // LDS row: 8 slots of 16 bytes, slot index XOR (row % 8)
+constexpr int kRow = kKS;            // LDS row: 8 slots of 16 bytes, slot index XOR swz_key(row)
 constexpr int kMagic = 0x4B400000;   // bit pattern of 12582912.0f = 1.5 * 2^23
 constexpr float kMagicF = 12582912.0f;
 constexpr int kXcds = 8;
@@ -57,7 +58,11 @@ struct __align__(16) Stage {
 };
 
 // LDS byte offset of logical 16-byte slot `slot` (= 2*block + half) of tile row `row`.
-__device__ __forceinline__ int swz(int row, int slot) { return row * kRow + 16 * (slot ^ (row & 7)); }
+// The XOR key is row % 8 with bit 3 of the row folded in, so the 16 rows one ds_read_b128 pass
+// serves (8 of each parity: 64 banks) hit 16 distinct 4-bank groups; with row % 8 alone, rows r and
+// r + 8 collided.
+__device__ __forceinline__ int swz_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int swz(int row, int slot) { return row * kRow + 16 * (slot ^ swz_key(row)); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -110,13 +115,13 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
     // ---- staging assignment (per-lane byte offsets, fixed for the whole K loop) ----
     // activation rows: straight to LDS, 4 x 1 KB per wave per stage; instruction i of wave w
     // fills tile rows 8*(4w+i) .. +8, lane l the 16-byte slot (l % 8) of row 8*(4w+i) + l/8,
-    // which holds logical slot (l % 8) ^ (row % 8); rows past M clamp to M - 1
+    // which holds logical slot (l % 8) ^ swz_key(row); rows past M clamp to M - 1
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
     const int a_row0 = 8 * (4 * wave_u) + (lane >> 3);
-    const int a_slot = (lane & 7) ^ (a_row0 & 7);
     uint32_t a_off[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+        const int a_slot = (lane & 7) ^ swz_key(a_row0 + 8 * i);
         const int row = FULL ? m0 + a_row0 + 8 * i : min(m0 + a_row0 + 8 * i, M - 1);
         a_off[i] = (uint32_t)row * (uint32_t)K + 16u * (uint32_t)a_slot;
     }
@@ -199,11 +204,12 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
         if (more) DCQ_ISSUE(s + 1, st[(s + 1) & 1]);  // in flight while this stage computes
         // fragments of block kb are read one block ahead (block 0 here, block kb + 1 after block
         // kb's MFMAs issue), so the MFMAs of a block do not wait for their LDS reads
-        // this lane's fragment rows wm + 32i + col and wn + 32j + col share row % 8 = col % 8, so
-        // the swizzled slot of block kb depends on (kb, hl, col) only; the rows are immediates
+        // this lane's fragment rows wm + 32i + col and wn + 32j + col share swz_key(col) (wm, wn and
+        // 32i are multiples of 16), so the swizzled slot of block kb depends on (kb, hl, col) only;
+        // the rows are immediates
         v4i fa[2], fb[2];
         {
-            const int fo = col * kRow + 16 * (hl ^ (col & 7));
+            const int fo = col * kRow + 16 * (hl ^ swz_key(col));
 #pragma unroll
             for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const v4i*>(S.a + fo + (wm + 32 * ii) * kRow);
 #pragma unroll
@@ -221,7 +227,7 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __r
 #pragma unroll
                 for (int j = 0; j < 2; ++j) D[i][j] = mfma32(fa[i], fb[j], cmagic);
             if (kb + 1 < kKB) {
-                const int fo = col * kRow + 16 * ((2 * kb + 2 + hl) ^ (col & 7));
+                const int fo = col * kRow + 16 * ((2 * kb + 2 + hl) ^ swz_key(col));
 #pragma unroll
                 for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const v4i*>(S.a + fo + (wm + 32 * ii) * kRow);
 #pragma unroll
