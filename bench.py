@@ -655,7 +655,7 @@ def profile_config(cfg, args, dev):
 # Extras whose kernels the counter passes cover: (label, kernel, weight type, M, N, K). The LM heads
 # share their kernels with configs 1 and 3 and are told apart by grid size (PROFILED below).
 PROFILE_EXTRAS = [("lm_head_q8_0_m1", "decode_q8_0_kernel", "Q8_0", 1, 151936, 1024),
-                  ("lm_head_q6_k_m1", "decode_q6k_lds_kernel", "Q6_K", 1, 151936, 2560),
+                  ("lm_head_q6_k_m1", "decode_q6k_mfma_kernel", "Q6_K", 1, 151936, 2560),
                   ("prefill_q4_k", "prefill_q4_k_kernel", "Q4_K", 2048, 8192, 2048),
                   ("prefill_q6_k", "prefill_q6_k_kernel", "Q6_K", 2048, 8192, 2048)]
 
@@ -734,12 +734,14 @@ def summarize_read(path, configs, launches):
 # the kernel that dominates each config's step (for --summarize-pmc)
 DOMINANT = {1: "decode_q8_0_kernel", 2: "decode_kq_kernel", 3: "decode_q6k_lds_kernel", 4: "batch_q4k_kernel",
             5: "prefill_q8_0_kernel"}
-# counter summary lines: (label, kernel, smallest and largest grid in threads). The configs' decode
-# grids stay below 300 k threads; the LM heads' (151936 rows) are above.
+# counter summary lines: (label, kernel, smallest and largest grid in threads). The Q8_0 LM head
+# shares its kernel with config 1 and is told apart by grid size: the configs' decode grids stay
+# below 300 k threads, the Q8_0 LM head's (151936 rows) is above. The other extras' kernels are
+# their own.
 LM_GRID = 300_000
-PROFILED = ([(f"config={i}", k, 0, LM_GRID) for i, k in sorted(DOMINANT.items())] +
-            [(f"extra={lab}", k, LM_GRID if lab.startswith("lm_head") else 0, 1 << 62)
-             for lab, k, *_ in PROFILE_EXTRAS])
+_SHARED = {k for _, k, *_ in PROFILE_EXTRAS} & set(DOMINANT.values())
+PROFILED = ([(f"config={i}", k, 0, LM_GRID if k in _SHARED else 1 << 62) for i, k in sorted(DOMINANT.items())] +
+            [(f"extra={lab}", k, LM_GRID if k in _SHARED else 0, 1 << 62) for lab, k, *_ in PROFILE_EXTRAS])
 
 
 def summarize_pmc(paths):
