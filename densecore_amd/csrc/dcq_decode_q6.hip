@@ -504,11 +504,15 @@ __device__ __forceinline__ void tall_superblock(const uint8_t* row, const int8_t
     }
 }
 
-template <int MT, bool DUMP>
+// FUSE: X is fp32 [M][x_stride] and every workgroup quantizes the rows it needs to Q8_K itself (the
+// shared 16-lane quantizer: the same bytes as the quantize kernel), saving that launch; else the
+// planar workspace (xqs, xd).
+template <int MT, bool DUMP, bool FUSE>
 __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
     const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
-    const int8_t* __restrict__ xqs, const float* __restrict__ xd, int64_t m_ld, int M, float* Y, int64_t y_stride,
-    int32_t* __restrict__ sums, int64_t sums_n_stride, const float* R, int64_t r_stride) {
+    const int8_t* __restrict__ xqs, const float* __restrict__ xd, int64_t m_ld, const float* __restrict__ X,
+    int64_t x_stride, int M, float* Y, int64_t y_stride, int32_t* __restrict__ sums, int64_t sums_n_stride,
+    const float* R, int64_t r_stride) {
     constexpr int MV = MT < 4 ? MT : 4;
     extern __shared__ __align__(16) uint8_t smem[];
     const int K = nsb * 256;
@@ -521,12 +525,34 @@ __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
     uint8_t* wb = smem + tall_act_bytes(MT, nsb) + (size_t)wave * 2 * kTallBuf;
 
     // ---- activation: MT rows of qs (rows >= M repeat row M - 1) and the superblock scales ----
-    for (int i = tid; i < MT * K / 16; i += 64 * kTallWaves) {
-        const int m = i / (K / 16), c = i % (K / 16);
-        *reinterpret_cast<uint4*>(aq + (size_t)m * K + 16 * c) =
-            *reinterpret_cast<const uint4*>(xqs + (int64_t)(m < M ? m : M - 1) * K + 16 * c);
+    if constexpr (FUSE) {
+        // (superblock, row) pairs, one per 16-lane group (32 groups a pass)
+        const int g = tid & 15;
+        for (int pr = tid >> 4; pr < nsb * MT; pr += 4 * kTallWaves) {
+            const int sb = pr / MT, m = pr % MT;
+            const float4* xp = reinterpret_cast<const float4*>(X + (int64_t)(m < M ? m : M - 1) * x_stride + 256 * sb + 16 * g);
+            float x[16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = xp[j];
+                x[4 * j] = v.x, x[4 * j + 1] = v.y, x[4 * j + 2] = v.z, x[4 * j + 3] = v.w;
+            }
+            uint32_t packed[4];
+            int bsum;
+            float dval;
+            quantize_q8k_row16(x, g, packed, bsum, dval);
+            *reinterpret_cast<uint4*>(aq + (size_t)m * K + 256 * sb + 16 * g) =
+                make_uint4(packed[0], packed[1], packed[2], packed[3]);
+            if (g == 0) ad[sb * MT + m] = dval;
+        }
+    } else {
+        for (int i = tid; i < MT * K / 16; i += 64 * kTallWaves) {
+            const int m = i / (K / 16), c = i % (K / 16);
+            *reinterpret_cast<uint4*>(aq + (size_t)m * K + 16 * c) =
+                *reinterpret_cast<const uint4*>(xqs + (int64_t)(m < M ? m : M - 1) * K + 16 * c);
+        }
+        for (int i = tid; i < nsb * MT; i += 64 * kTallWaves) ad[i] = xd[(int64_t)(i / MT) * m_ld + i % MT];
     }
-    for (int i = tid; i < nsb * MT; i += 64 * kTallWaves) ad[i] = xd[(int64_t)(i / MT) * m_ld + i % MT];
     if (tid == 0) *ctr = 0;
     __syncthreads();
 
@@ -666,17 +692,40 @@ int q6_rows_per_wave(int64_t rows, int nw) {
     return rpw > 16 ? 16 : rpw;
 }
 
-using TallFn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, int64_t, int,
-                        float*, int64_t, int32_t*, int64_t, const float*, int64_t);
+using TallFn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, int64_t,
+                        const float*, int64_t, int, float*, int64_t, int32_t*, int64_t, const float*, int64_t);
 
-template <bool DUMP>
+template <bool DUMP, bool FUSE>
 TallFn tall_pick(int mt) {
     switch (mt) {
-        case 1: return decode_q6k_mfma_kernel<1, DUMP>;
-        case 2: return decode_q6k_mfma_kernel<2, DUMP>;
-        case 4: return decode_q6k_mfma_kernel<4, DUMP>;
-        default: return decode_q6k_mfma_kernel<8, DUMP>;
+        case 1: return decode_q6k_mfma_kernel<1, DUMP, FUSE>;
+        case 2: return decode_q6k_mfma_kernel<2, DUMP, FUSE>;
+        case 4: return decode_q6k_mfma_kernel<4, DUMP, FUSE>;
+        default: return decode_q6k_mfma_kernel<8, DUMP, FUSE>;
     }
+}
+
+// Tall matrices: the MFMA kernel over rows [n0, n1), M tiled by 8; X (fp32, quantized in every
+// workgroup) or the planar activation `act`.
+hipError_t launch_tall_q6k(const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K, const float* X,
+                           int64_t x_stride, const PlanarBuffers* act, int64_t M, float* Y, int64_t y_stride,
+                           int32_t* block_sums, int64_t sums_n_stride, hipStream_t st, const float* R, int64_t r_stride) {
+    const int nsb = (int)(K / 256);
+    const int64_t tiles = (n1 - n0 + 31) / 32;
+    const unsigned grid = (unsigned)(tiles < cu_count() ? tiles : cu_count());
+    for (int64_t m0 = 0; m0 < M; m0 += 8) {
+        const int64_t mc = M - m0 < 8 ? M - m0 : 8;
+        const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
+        const bool fuse = X != nullptr;
+        TallFn fn = block_sums ? (fuse ? tall_pick<true, true>(mt) : tall_pick<true, false>(mt))
+                               : (fuse ? tall_pick<false, true>(mt) : tall_pick<false, false>(mt));
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kTallWaves), tall_lds_bytes(mt, nsb), st, (const uint8_t*)W,
+                           w_row_bytes, n0, n1, nsb, fuse ? nullptr : act->qs + m0 * K, fuse ? nullptr : act->d + m0,
+                           fuse ? (int64_t)0 : act->m_ld, fuse ? X + m0 * x_stride : nullptr, x_stride, (int)mc,
+                           Y + m0 * y_stride, y_stride, block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr,
+                           sums_n_stride, R ? R + m0 * r_stride : nullptr, r_stride);
+    }
+    return hipGetLastError();
 }
 
 // The MFMA form for tall matrices (DCQ_Q6K_MFMA=0 keeps the lane-per-superblock kernels): an even
@@ -708,21 +757,9 @@ hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0,
     // the weight base is 16-byte aligned (checked by the C ABI)
     if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb) return hipErrorNotSupported;
     if (knob(Knob::Q6KLdsOff)) return hipErrorNotSupported;
-    if (q6_use_mfma(n1 - n0, nsb, M)) {
-        const int64_t tiles = (n1 - n0 + 31) / 32;
-        const unsigned grid = (unsigned)(tiles < cu_count() ? tiles : cu_count());
-        for (int64_t m0 = 0; m0 < M; m0 += 8) {
-            const int64_t mc = M - m0 < 8 ? M - m0 : 8;
-            const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
-            TallFn fn = block_sums ? tall_pick<true>(mt) : tall_pick<false>(mt);
-            hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kTallWaves), tall_lds_bytes(mt, nsb), st, (const uint8_t*)W,
-                               w_row_bytes, n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.m_ld, (int)mc,
-                               Y + m0 * y_stride, y_stride,
-                               block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr, sums_n_stride,
-                               R ? R + m0 * r_stride : nullptr, r_stride);
-        }
-        return hipGetLastError();
-    }
+    if (q6_use_mfma(n1 - n0, nsb, M))
+        return launch_tall_q6k(W, w_row_bytes, n0, n1, K, nullptr, 0, &act, M, Y, y_stride, block_sums, sums_n_stride,
+                               st, R, r_stride);
     const int nw = 4;  // 5-wave workgroups (rows spread more evenly) measured no faster here
     // several rows per wave only where a step of 16 superblocks covers the row (the waits count
     // two rows' loads)
@@ -751,10 +788,13 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                    hipStream_t st, const float* R, int64_t r_stride) {
     const int nsb = (int)(K / 256);
-    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || M > 2) return hipErrorNotSupported;
+    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb) return hipErrorNotSupported;
     if (knob(Knob::Q6KLdsOff) || knob(Knob::Q6KNoFuse)) return hipErrorNotSupported;
-    // tall matrices: the MFMA kernel over the separately quantized activation
-    if (q6_use_mfma(N, nsb, M)) return hipErrorNotSupported;
+    // tall matrices (M <= 8): the MFMA kernel, every workgroup quantizing the activation
+    if (M <= 8 && q6_use_mfma(N, nsb, M))
+        return launch_tall_q6k(W, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums, N, st, R,
+                               r_stride);
+    if (M > 2) return hipErrorNotSupported;
     // Workgroup width (one row per wave). Up to K = 4096, 4 waves (measured at M = 1 against
     // quantize + decode: 2560 x 4096 5.7 vs 7.2 us; 1024 x 2560 3.8 vs 5.8 us). Beyond, every
     // workgroup re-reads and re-quantizes the whole activation (39 KB at K = 9728: 4-wave
