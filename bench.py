@@ -60,6 +60,9 @@ def parse():
     ap.add_argument("--summarize-pmc", nargs="+", metavar="CSV",
                     help="print profiles/counters.txt lines from rocprofv3 --pmc counter_collection.csv files "
                          "of --profile runs (no GPU needed)")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print profiles/traffic.txt lines from the counter_collection.csv files of a "
+                         "rocprofv3 --pmc FETCH_SIZE and a --pmc WRITE_SIZE run of --profile (no GPU needed)")
     ap.add_argument("--summarize-read", metavar="CSV",
                     help="print profiles/read_ceiling.txt lines from the rocprofv3 kernel_trace.csv of a "
                          "--profile-read run made with the same --configs/--steps/--warmup (no GPU needed)")
@@ -744,6 +747,51 @@ PROFILED = ([(f"config={i}", k, 0, LM_GRID if k in _SHARED else 1 << 62) for i, 
             [(f"extra={lab}", k, LM_GRID if k in _SHARED else 0, 1 << 62) for lab, k, *_ in PROFILE_EXTRAS])
 
 
+def summarize_traffic(fetch_csv, write_csv):
+    """profiles/traffic.txt lines: per PROFILED kernel, the median over its dispatches (the first two
+    of each skipped) of FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each scaled by what the same
+    counter reads for the run's last dispatch, calibration_copy's device copy of 64 MiB (read and
+    written once), against the algorithmic bytes (quantized W + fp32 X + fp32 Y) of one launch."""
+    import csv
+    import collections
+    import densecore_amd as dc
+
+    def per_dispatch(path, counter):
+        rows = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                rows[int(r["Dispatch_Id"])] = (r["Kernel_Name"], int(r["Grid_Size"]), float(r["Counter_Value"]))
+        return rows
+
+    fetch, write = per_dispatch(fetch_csv, "FETCH_SIZE"), per_dispatch(write_csv, "WRITE_SIZE")
+    copy_kib = (64 << 20) / 1024
+    fetch_scale = copy_kib / fetch[max(fetch)][2]
+    write_scale = copy_kib / write[max(write)][2]
+    shapes = {f"config={c.index}": (c.wtype, c.M, c.N, c.K) for c in dc.CONFIGS}
+    shapes.update({f"extra={lab}": (getattr(dc, "TYPE_" + t), M, N, K) for lab, _, t, M, N, K in PROFILE_EXTRAS})
+    lines = [f"# scale: the calibration copy of 64 MiB reads FETCH_SIZE={fetch[max(fetch)][2]:.1f} KiB and "
+             f"WRITE_SIZE={write[max(write)][2]:.1f} KiB: fetch_scale={fetch_scale:.4f}, write_scale={write_scale:.4f}",
+             "# traffic (bytes) = fetch_kib*1024*fetch_scale + write_kib*1024*write_scale; medians over each "
+             "kernel's dispatches after its first two"]
+    for label, kname, gmin, gmax in PROFILED:
+        vals = collections.defaultdict(list)
+        for name, table in (("fetch", fetch), ("write", write)):
+            for d in sorted(table):
+                k, grid, v = table[d]
+                if kname in k and gmin <= grid < gmax:
+                    vals[name].append(v)
+        if not vals["fetch"] or not vals["write"]:
+            continue
+        f_kib = float(np.median(vals["fetch"][2:] or vals["fetch"]))
+        w_kib = float(np.median(vals["write"][2:] or vals["write"]))
+        wt, M, N, K = shapes[label]
+        algo = N * dc.row_size(wt, K) + M * K * 4 + M * N * 4
+        traffic = f_kib * 1024 * fetch_scale + w_kib * 1024 * write_scale
+        lines.append(f"{label} kernel={kname} fetch_kib={f_kib:.1f} write_kib={w_kib:.1f} fetch_scale={fetch_scale:.4f} "
+                     f"write_scale={write_scale:.4f} traffic_bytes={traffic:.0f} algorithmic_bytes={algo}")
+    return "\n".join(lines)
+
+
 def summarize_pmc(paths):
     """profiles/counters.txt lines from rocprofv3 --pmc counter_collection.csv files of --profile
     runs (one pass per file; passes are joined by kernel name). Per config, the medians over that
@@ -796,8 +844,12 @@ def summarize_pmc(paths):
             kv.append(f"valu_per_mfma={med['SQ_INSTS_VALU'] / med['SQ_INSTS_MFMA']:.2f}")
         if med.get("SQ_VALU_MFMA_BUSY_CYCLES") and "SQ_VALU_MFMA_COEXEC_CYCLES" in med:
             kv.append(f"coexec_pct={100 * med['SQ_VALU_MFMA_COEXEC_CYCLES'] / med['SQ_VALU_MFMA_BUSY_CYCLES']:.2f}")
+        if med.get("SQ_WAVE_CYCLES") and "SQ_WAIT_INST_ANY" in med:
+            # share of the waves' lifetime spent in s_waitcnt (loads, LDS, scalar memory)
+            kv.append(f"wait_inst_pct={100 * med['SQ_WAIT_INST_ANY'] / med['SQ_WAVE_CYCLES']:.2f}")
         for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_I8", "SQ_VALU_MFMA_BUSY_CYCLES",
-                  "SQ_ACTIVE_INST_VALU", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES", "SQ_VALU_MFMA_COEXEC_CYCLES"):
+                  "SQ_ACTIVE_INST_VALU", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES", "SQ_VALU_MFMA_COEXEC_CYCLES",
+                  "SQ_WAIT_INST_ANY", "SQ_INSTS_SALU"):
             if c in med:
                 kv.append(f"{c}={med[c]:.6g}")
         lines.append(" ".join(kv))
@@ -878,6 +930,9 @@ def main():
     args = parse()
     if args.summarize_pmc:
         print(summarize_pmc(args.summarize_pmc))
+        return 0
+    if args.summarize_traffic:
+        print(summarize_traffic(*args.summarize_traffic))
         return 0
     if args.summarize_read:
         print(summarize_read(args.summarize_read, [int(c) for c in args.configs.split(",") if c.strip()],
