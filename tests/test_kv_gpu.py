@@ -92,6 +92,11 @@ ATTN = [
     (Q8_0, 2, 50, 8, 4, 128),      # the 4-row workgroup with two tokens of two heads each
     (F16, 4, 20, 4, 4, 64),        # the 4-row workgroup with four tokens of one head
     (F16, 1, 4095, 32, 8, 128),
+    # the split merge's forms: 17..64 splits, 97..128 (32 lanes per output), over 128 (a workgroup
+    # per row)
+    (Q8_0, 1, 2000, 32, 8, 128),   # 33 splits
+    (Q8_0, 1, 7000, 32, 8, 128),   # 111 splits
+    (F16, 1, 20000, 4, 4, 64),     # 158 splits
     (F16, 5, 33, 16, 4, 64),
     (F32, 1, 200, 8, 2, 128),
     (F32, 17, 40, 4, 2, 256),
