@@ -195,12 +195,14 @@ __host__ __device__ constexpr int stage_chunks(int P, int NS, int MT, bool fuse,
 // silu(W x) * (W2 x) (the SwiGLU gate and up projections).
 template <class Fmt, int P, int MT, int NS, bool FUSE, bool DUMP, bool GLU = false, int NW = 4,
           int QC = stage_chunks(P, NS, MT, FUSE, NW)>
-__global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const uint8_t* __restrict__ W,
-                                                         const uint8_t* __restrict__ W2, int64_t w_row_bytes,
-                                                         int64_t n0, int64_t n1, int nsb,
-                                                         const float* __restrict__ X, int64_t x_stride,
+// The arguments the first loads need come first: the first 56 bytes of arguments are preloaded
+// into scalar registers at dispatch (-amdgpu-kernarg-preload-count), the rest take a dependent
+// scalar load.
+__global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const float* __restrict__ X, int64_t x_stride, int M,
+                                                         int nsb, const uint8_t* __restrict__ W, int64_t w_row_bytes,
+                                                         int64_t n0, int64_t n1, const uint8_t* __restrict__ W2,
                                                          const int8_t* __restrict__ xqs, const float* __restrict__ xd,
-                                                         const int16_t* __restrict__ xbs, int64_t m_ld, int M,
+                                                         const int16_t* __restrict__ xbs, int64_t m_ld,
                                                          float* Y, int64_t y_stride,  // R may alias Y
                                                          int32_t* __restrict__ sums, int64_t sums_n_stride,
                                                          const float* R, int64_t r_stride) {
@@ -386,9 +388,9 @@ int cu_count() {
 
 namespace {
 
-using DecodeFn = void (*)(const uint8_t*, const uint8_t*, int64_t, int64_t, int64_t, int, const float*, int64_t,
-                          const int8_t*, const float*, const int16_t*, int64_t, int, float*, int64_t, int32_t*,
-                          int64_t, const float*, int64_t);
+using DecodeFn = void (*)(const float*, int64_t, int, int, const uint8_t*, int64_t, int64_t, int64_t, const uint8_t*,
+                          const int8_t*, const float*, const int16_t*, int64_t, float*, int64_t, int32_t*, int64_t,
+                          const float*, int64_t);
 
 // Launch shapes (P superblocks of a row per step, NS steps): a row of nsb <= P*NS
 // superblocks. Other K fall back to the generic kernel.
@@ -546,11 +548,10 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
         DecodeFn fn = wtype == kTypeQ4_K ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, glu, idx, mt, nw)
                                          : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, false, idx, mt, nw);
         // rows beyond mc in an MT tile stage the last real activation row and are never stored
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), lds, st, (const uint8_t*)W, (const uint8_t*)W2, w_row_bytes,
-                           n0, n1, nsb,
-                           fuse ? X + m0 * x_stride : nullptr, x_stride, fuse ? nullptr : act->qs + m0 * K,
-                           fuse ? nullptr : act->d + m0, fuse ? nullptr : act->bs + m0 * (K / 16),
-                           fuse ? 0 : act->m_ld, (int)mc, Y + m0 * y_stride, y_stride,
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), lds, st, fuse ? X + m0 * x_stride : nullptr, x_stride,
+                           (int)mc, nsb, (const uint8_t*)W, w_row_bytes, n0, n1, (const uint8_t*)W2,
+                           fuse ? nullptr : act->qs + m0 * K, fuse ? nullptr : act->d + m0,
+                           fuse ? nullptr : act->bs + m0 * (K / 16), fuse ? 0 : act->m_ld, Y + m0 * y_stride, y_stride,
                            block_sums ? block_sums + m0 * sums_n_stride * per_row_sums : nullptr, sums_n_stride,
                            R ? R + m0 * r_stride : nullptr, r_stride);
     }

@@ -142,12 +142,14 @@ struct Q6Lds {
 // and the quantizer runs while the row streams. The first SW waves stage the activation, QC
 // passes of 4 * SW (superblock, row) pairs; the other waves only stream their rows.
 template <int MT, bool DUMP, bool FUSE = false, int QC = 1, int kWaves = 4, int SW = kWaves>
+// The arguments the first loads need come first: the first 56 bytes of arguments are preloaded
+// into scalar registers at dispatch (-amdgpu-kernarg-preload-count), the rest take a dependent
+// scalar load.
 __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
-    const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
-    const int8_t* __restrict__ xqs, const float* __restrict__ xd, const int16_t* __restrict__ xbs, int64_t m_ld,
-    const float* __restrict__ X, int64_t x_stride,
-    int M, float* Y, int64_t y_stride, int32_t* __restrict__ sums, int64_t sums_n_stride,
-    const float* R, int64_t r_stride, int rpw) {
+    const float* __restrict__ X, int64_t x_stride, const uint8_t* __restrict__ W, int64_t n0, int64_t n1,
+    int w_row_bytes, int M, int nsb, int rpw, const int8_t* __restrict__ xqs, const float* __restrict__ xd,
+    const int16_t* __restrict__ xbs, int64_t m_ld, float* Y, int64_t y_stride, int32_t* __restrict__ sums,
+    int64_t sums_n_stride, const float* R, int64_t r_stride) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int nbuf = rpw > 1 ? 2 : 1;
     const Q6Lds L(nsb, MT, kWaves, nbuf);
@@ -646,9 +648,9 @@ __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
 
 namespace {
 
-using Q6Fn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, const int16_t*,
-                      int64_t, const float*, int64_t, int, float*, int64_t, int32_t*, int64_t, const float*,
-                      int64_t, int);
+using Q6Fn = void (*)(const float*, int64_t, const uint8_t*, int64_t, int64_t, int, int, int, int, const int8_t*,
+                      const float*, const int16_t*, int64_t, float*, int64_t, int32_t*, int64_t, const float*,
+                      int64_t);
 
 // fused activation: M <= 2 rows, nsb <= 64. 4-wave workgroups: every wave stages, at most 8
 // passes of 16 (superblock, row) pairs. 8..12 waves: the first 4 waves stage, at most 4 passes
@@ -755,7 +757,8 @@ hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0,
     const int nsb = (int)(K / 256);
     // dword-granular head/tail loads: the row's bytes and its stride must be whole dwords;
     // the weight base is 16-byte aligned (checked by the C ABI)
-    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb) return hipErrorNotSupported;
+    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || w_row_bytes > INT32_MAX)
+        return hipErrorNotSupported;
     if (knob(Knob::Q6KLdsOff)) return hipErrorNotSupported;
     if (q6_use_mfma(n1 - n0, nsb, M))
         return launch_tall_q6k(W, w_row_bytes, n0, n1, K, nullptr, 0, &act, M, Y, y_stride, block_sums, sums_n_stride,
@@ -775,11 +778,11 @@ hipError_t launch_decode_q6k_lds(const void* W, int64_t w_row_bytes, int64_t n0,
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         const unsigned grid = (unsigned)((n1 - n0 + (int64_t)nw * rpw - 1) / ((int64_t)nw * rpw));
         Q6Fn fn = block_sums ? q6_pick<true>(mt) : q6_pick<false>(mt);
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), Q6Lds(nsb, mt, nw, nbuf).total, st, (const uint8_t*)W,
-                           w_row_bytes, n0, n1, nsb, act.qs + m0 * K, act.d + m0, act.bs + m0 * (K / 16), act.m_ld,
-                           (const float*)nullptr, (int64_t)0, (int)mc, Y + m0 * y_stride, y_stride,
-                           block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr, sums_n_stride,
-                           R ? R + m0 * r_stride : nullptr, r_stride, rpw);
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), Q6Lds(nsb, mt, nw, nbuf).total, st, (const float*)nullptr,
+                           (int64_t)0, (const uint8_t*)W, n0, n1, (int)w_row_bytes, (int)mc, nsb, rpw,
+                           act.qs + m0 * K, act.d + m0, act.bs + m0 * (K / 16), act.m_ld, Y + m0 * y_stride,
+                           y_stride, block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr, sums_n_stride,
+                           R ? R + m0 * r_stride : nullptr, r_stride);
     }
     return hipGetLastError();
 }
@@ -788,7 +791,8 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                    hipStream_t st, const float* R, int64_t r_stride) {
     const int nsb = (int)(K / 256);
-    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb) return hipErrorNotSupported;
+    if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || w_row_bytes > INT32_MAX)
+        return hipErrorNotSupported;
     if (knob(Knob::Q6KLdsOff) || knob(Knob::Q6KNoFuse)) return hipErrorNotSupported;
     // tall matrices (M <= 8): the MFMA kernel, every workgroup quantizing the activation
     if (M <= 8 && q6_use_mfma(N, nsb, M))
@@ -819,9 +823,9 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
     Q6Fn fn = block_sums ? q6_pick_fused<true>(mt, qc, kWaves) : q6_pick_fused<false>(mt, qc, kWaves);
     if (!fn) return hipErrorNotSupported;
     const unsigned grid = (unsigned)((N + (int64_t)kWaves * rpw - 1) / ((int64_t)kWaves * rpw));
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), lds.total, st, (const uint8_t*)W, w_row_bytes, (int64_t)0,
-                       N, nsb, (const int8_t*)nullptr, (const float*)nullptr, (const int16_t*)nullptr, (int64_t)0, X,
-                       x_stride, (int)M, Y, y_stride, block_sums, N, R, r_stride, rpw);
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kWaves), lds.total, st, X, x_stride, (const uint8_t*)W, (int64_t)0,
+                       N, (int)w_row_bytes, (int)M, nsb, rpw, (const int8_t*)nullptr, (const float*)nullptr,
+                       (const int16_t*)nullptr, (int64_t)0, Y, y_stride, block_sums, N, R, r_stride);
     return hipGetLastError();
 }
 

@@ -82,10 +82,13 @@ __host__ __device__ constexpr int q8_stage_passes(int G, int NS, int MT, int NW)
 
 // GLU: a second weight matrix W2 shares the activation; the output is silu(W x) * (W2 x).
 template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, int QC = q8_stage_passes(G, NS, MT, NW)>
-__global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __restrict__ W,
+// The arguments the first loads need come first: the first 56 bytes of arguments are preloaded
+// into scalar registers at dispatch (-amdgpu-kernarg-preload-count), the rest take a dependent
+// scalar load.
+__global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __restrict__ X, int64_t x_stride,
+                                                           const uint8_t* __restrict__ W,
                                                            const uint8_t* __restrict__ W2, int64_t w_row_bytes,
-                                                           int64_t N, int K, const float* __restrict__ X,
-                                                           int64_t x_stride, int M, float* Y,  // R may alias Y
+                                                           int64_t N, int K, int M, float* Y,  // R may alias Y
                                                            int64_t y_stride, int32_t* __restrict__ sums,
                                                            int64_t sums_n_stride, const float* R, int64_t r_stride) {
     if constexpr (QC <= kMaxStagePasses) {
@@ -216,7 +219,7 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const uint8_t* __r
 
 namespace {
 
-using DecodeQ8Fn = void (*)(const uint8_t*, const uint8_t*, int64_t, int64_t, int, const float*, int64_t, int,
+using DecodeQ8Fn = void (*)(const float*, int64_t, const uint8_t*, const uint8_t*, int64_t, int64_t, int, int,
                             float*, int64_t, int32_t*, int64_t, const float*, int64_t);
 
 // (G lanes per row, NS pairs per lane): a row of U = K/64 pairs needs G*NS >= U
@@ -314,8 +317,9 @@ hipError_t launch_q8(const void* W, const void* W2, int64_t w_row_bytes, int64_t
         const size_t lds = (size_t)mt * K * 9 / 8;
         DecodeQ8Fn fn = W2 ? q8_pick_shape<false, true>(idx, mt)
                            : (block_sums ? q8_pick_shape<true>(idx, mt) : q8_pick_shape<false>(idx, mt));
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kQ8Waves), lds, st, (const uint8_t*)W, (const uint8_t*)W2,
-                           w_row_bytes, N, (int)K, X + m0 * x_stride, x_stride, (int)mc, Y + m0 * y_stride, y_stride,
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kQ8Waves), lds, st, X + m0 * x_stride, x_stride,
+                           (const uint8_t*)W, (const uint8_t*)W2, w_row_bytes, N, (int)K, (int)mc, Y + m0 * y_stride,
+                           y_stride,
                            block_sums ? block_sums + m0 * N * per_row_sums : nullptr, N,
                            R ? R + m0 * r_stride : nullptr, r_stride);
     }
