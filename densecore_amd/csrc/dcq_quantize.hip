@@ -19,9 +19,9 @@ namespace dcq {
 // ---- Q8_0: 4 lanes per 32-element block, 8 floats per lane ----
 template <bool kPlanar>
 __global__ void __launch_bounds__(256) quantize_q8_0_kernel(const float* __restrict__ X, int64_t x_stride,
-                                                            int64_t M, int64_t K, uint8_t* __restrict__ out,
-                                                            int64_t out_row_bytes, int8_t* __restrict__ qs,
-                                                            float* __restrict__ dpl, int64_t m_ld) {
+                                                            int64_t M, int64_t K, int64_t m_ld,
+                                                            int8_t* __restrict__ qs, float* __restrict__ dpl,
+                                                            uint8_t* __restrict__ out, int64_t out_row_bytes) {
     const int64_t nb = K / QK8_0;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t blk = gid >> 2;       // global block index over [m_ld][nb]
@@ -69,10 +69,10 @@ __global__ void __launch_bounds__(256) quantize_q8_0_kernel(const float* __restr
 // ---- Q8_K: 16 lanes (one DPP row) per 256-element superblock, 16 floats per lane ----
 template <bool kPlanar>
 __global__ void __launch_bounds__(256) quantize_q8_K_kernel(const float* __restrict__ X, int64_t x_stride,
-                                                            int64_t M, int64_t K, uint8_t* __restrict__ out,
-                                                            int64_t out_row_bytes, int8_t* __restrict__ qs,
-                                                            float* __restrict__ dpl, int16_t* __restrict__ bsp,
-                                                            int64_t m_ld) {
+                                                            int64_t M, int64_t K, int64_t m_ld,
+                                                            int8_t* __restrict__ qs, int16_t* __restrict__ bsp,
+                                                            float* __restrict__ dpl, uint8_t* __restrict__ out,
+                                                            int64_t out_row_bytes) {
     const int64_t nsb = K / QK_K;
     const int g = threadIdx.x & 15;
     const int64_t sbg = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // global superblock
@@ -165,14 +165,14 @@ hipError_t launch_quantize_ggml(int vdt, const float* X, int64_t x_stride, int64
         const int64_t threads = M * (K / QK8_0) * 4;
         const int bs = quant_block(threads);
         const int64_t grid = (threads + bs - 1) / bs;
-        hipLaunchKernelGGL(quantize_q8_0_kernel<false>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
-                           (uint8_t*)out, out_row_bytes, (int8_t*)nullptr, (float*)nullptr, M);
+        hipLaunchKernelGGL(quantize_q8_0_kernel<false>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K, M,
+                           (int8_t*)nullptr, (float*)nullptr, (uint8_t*)out, out_row_bytes);
     } else {
         const int64_t threads = M * (K / QK_K) * 16;
         const int bs = quant_block(threads);
         const int64_t grid = (threads + bs - 1) / bs;
-        hipLaunchKernelGGL(quantize_q8_K_kernel<false>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
-                           (uint8_t*)out, out_row_bytes, (int8_t*)nullptr, (float*)nullptr, (int16_t*)nullptr, M);
+        hipLaunchKernelGGL(quantize_q8_K_kernel<false>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K, M,
+                           (int8_t*)nullptr, (int16_t*)nullptr, (float*)nullptr, (uint8_t*)out, out_row_bytes);
     }
     return hipGetLastError();
 }
@@ -184,13 +184,13 @@ hipError_t launch_quantize_planar(int vdt, const float* X, int64_t x_stride, int
         const int bs = quant_block(threads);
         const int64_t grid = (threads + bs - 1) / bs;
         hipLaunchKernelGGL(quantize_q8_0_kernel<true>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
-                           (uint8_t*)nullptr, (int64_t)0, pb.qs, pb.d, pb.m_ld);
+                           pb.m_ld, pb.qs, pb.d, (uint8_t*)nullptr, (int64_t)0);
     } else {
         const int64_t threads = pb.m_ld * (K / QK_K) * 16;
         const int bs = quant_block(threads);
         const int64_t grid = (threads + bs - 1) / bs;
         hipLaunchKernelGGL(quantize_q8_K_kernel<true>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
-                           (uint8_t*)nullptr, (int64_t)0, pb.qs, pb.d, pb.bs, pb.m_ld);
+                           pb.m_ld, pb.qs, pb.bs, pb.d, (uint8_t*)nullptr, (int64_t)0);
     }
     return hipGetLastError();
 }
