@@ -249,7 +249,7 @@ struct AttnTile {
 // chunk's loads are issued, so their latency overlaps.
 template <int SRC, bool FROM_CUR, int HD, int RM, int QPT>
 __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w, AttnSmem<HD, RM>& sm, int kbase,
-                                           int klim, bool& q_stored, const float (&qreg)[QPT]) {
+                                           int klim, bool& q_stored, const float (&qreg)[QPT], int blk_pre = -2) {
     using S = AttnShape<HD>;
     constexpr int LPK = S::LPK, KPW = S::KPW, KC = S::KC, DPL = S::DPL;
     constexpr int HBW = AttnSmem<HD, RM>::HBW, NST = AttnSmem<HD, RM>::NST;
@@ -264,7 +264,8 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
     bool have = kt < klim;
     if (!FROM_CUR) {
         const int lb = kt / kKvBlock;
-        const int blk = have && lb < a.n_table ? a.table[lb] : -1;
+        // blk_pre >= -1: this lane's table entry, already loaded by the caller (the first chunk)
+        const int blk = blk_pre >= -1 ? blk_pre : have && lb < a.n_table ? a.table[lb] : -1;
         have = blk >= 0 && blk < a.n_blocks;
         off = (((int64_t)blk * a.n_layer + a.layer) * kKvBlock + kt % kKvBlock) * a.sb + w.h_kv * w.hb;
     } else {
@@ -468,11 +469,23 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
     __syncthreads();
 }
 
+// The fields the query and block-table loads need come as scalar arguments ahead of the struct:
+// the first 56 bytes of arguments are preloaded into scalar registers at dispatch
+// (-amdgpu-kernarg-preload-count), so those loads issue without waiting for the struct's.
+// hpw_nq = hpw | nq << 8; rep = n_head / n_head_kv.
 template <int CT, int HD, int RMAX>
-__global__ void __launch_bounds__(256, RMAX <= 4 ? 3 : 1) attn_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, RMAX <= 4 ? 3 : 1) attn_kernel(const int32_t* table, const float* q,
+                                                                    int64_t q_stride, int n_table, int n_tokens,
+                                                                    int n_past, int splits, int groups, int cps,
+                                                                    int rep, int hpw_nq, AttnArgs a) {
     using S = AttnShape<HD>;
     constexpr int KC = S::KC, DPL = S::DPL;
     __shared__ AttnSmem<HD, RMAX> sm;
+    a.table = table, a.q = q, a.q_stride = q_stride, a.n_table = n_table, a.n_tokens = n_tokens;
+    a.n_past = n_past, a.splits = splits, a.groups = groups, a.cps = cps;
+    a.hpw = hpw_nq & 0xFF, a.nq = hpw_nq >> 8;
+    a.nch_hist = (n_past + KC - 1) / KC;  // as the host's plan, with KC = 8192 / HD
+    a.nch_total = a.nch_hist + (n_tokens + KC - 1) / KC;
 
     AttnTile w;
     w.tid = threadIdx.x, w.wave = w.tid >> 6, w.lane = w.tid & 63;
@@ -497,9 +510,9 @@ __global__ void __launch_bounds__(256, RMAX <= 4 ? 3 : 1) attn_kernel(AttnArgs a
             qt = id / a.groups;
         }
     }
-    const int groups_per_kv = (a.n_head / a.n_head_kv) / a.hpw;
+    const int groups_per_kv = rep / a.hpw;
     w.h_kv = group / groups_per_kv;
-    const int h0 = w.h_kv * (a.n_head / a.n_head_kv) + (group % groups_per_kv) * a.hpw;
+    const int h0 = w.h_kv * rep + (group % groups_per_kv) * a.hpw;
     w.i0 = qt * a.nq;
     w.R = a.nq * a.hpw;
     w.hb = head_bytes<CT>(HD);
@@ -528,10 +541,18 @@ __global__ void __launch_bounds__(256, RMAX <= 4 ? 3 : 1) attn_kernel(AttnArgs a
     const int c_begin = split * a.cps;
     const int c_vis = a.nch_hist + i_last / KC;
     const int c_end = min(min(c_begin + a.cps, a.nch_total), c_vis + 1);
+    // the first chunk's block-table entry, loaded from the preloaded arguments before anything
+    // waits for the struct's fields (the same lookup attn_chunk makes for a history chunk)
+    int blk_first = -1;
+    if (c_begin < c_end && c_begin < a.nch_hist) {
+        const int kt = c_begin * KC + wave * S::KPW + lane / S::LPK, lb = kt / kKvBlock;
+        blk_first = kt < n_past && lb < n_table ? table[lb] : -1;
+    }
     bool q_stored = false;
     for (int c = c_begin; c < c_end; ++c) {
         if (c < a.nch_hist)
-            attn_chunk<CT, false, HD, RMAX, QPT>(a, w, sm, c * KC, a.n_past, q_stored, qreg);
+            attn_chunk<CT, false, HD, RMAX, QPT>(a, w, sm, c * KC, a.n_past, q_stored, qreg,
+                                                 c == c_begin ? blk_first : -2);
         else
             attn_chunk<kTypeF32, true, HD, RMAX, QPT>(a, w, sm, a.n_past + (c - a.nch_hist) * KC, a.n_past + a.n_tokens,
                                                 q_stored, qreg);
@@ -1034,10 +1055,13 @@ size_t attn_workspace_bytes(int hd, int n_head, int n_head_kv, int n_tokens, int
 
 template <int CT, int HD>
 static void launch_attn_t(const AttnArgs& a, int rmax, dim3 grid, hipStream_t st) {
+    const int rep = a.n_head / a.n_head_kv, hpw_nq = a.hpw | a.nq << 8;
+#define DCQ_ATTN_ARGS a.table, a.q, a.q_stride, a.n_table, a.n_tokens, a.n_past, a.splits, a.groups, a.cps, rep, hpw_nq, a
     if (rmax == 4)
-        hipLaunchKernelGGL((attn_kernel<CT, HD, 4>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<CT, HD, 4>), grid, dim3(256), 0, st, DCQ_ATTN_ARGS);
     else
-        hipLaunchKernelGGL((attn_kernel<CT, HD, attn_rmax_large<HD>()>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((attn_kernel<CT, HD, attn_rmax_large<HD>()>), grid, dim3(256), 0, st, DCQ_ATTN_ARGS);
+#undef DCQ_ATTN_ARGS
 }
 
 // The merge of the key splits: one thread per 4 output elements for up to 16 splits (prompts:
