@@ -87,12 +87,15 @@ __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
 
 // W: Q8_0 rows (w_row_bytes % 4 == 0); xqs: int8 [M][K]; xd: float [K/32][m_ld]; K % 128 == 0.
 // FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
+// Arguments: the ones the first loads need come first (the first 56 bytes of arguments are
+// preloaded into scalar registers at dispatch).
 template <bool DUMP, bool FULL>
-__global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
-                                                              int N, int K, const int8_t* __restrict__ xqs,
-                                                              const float* __restrict__ xd, int64_t m_ld, int M,
+__global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
+                                                              int w_row_bytes, const uint8_t* __restrict__ W,
+                                                              const int8_t* __restrict__ xqs,
+                                                              const float* __restrict__ xd, int M,
                                                               float* __restrict__ Y, int64_t y_stride,
-                                                              int32_t* __restrict__ sums, int tiles_n, int tiles_m) {
+                                                              int32_t* __restrict__ sums) {
     extern __shared__ __align__(16) uint8_t smem[];
     Stage* st = reinterpret_cast<Stage*>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -302,7 +305,9 @@ size_t prefill_q8_0_lds_bytes() { return 2 * sizeof(Stage); }
 
 hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                                int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
-    if (K % kKS || w_row_bytes % 4 || N > (1 << 30) || M > (1 << 30) || K > (1 << 30)) return hipErrorNotSupported;
+    if (K % kKS || w_row_bytes % 4 || w_row_bytes > INT32_MAX || act.m_ld > INT32_MAX || N > (1 << 30) ||
+        M > (1 << 30) || K > (1 << 30))
+        return hipErrorNotSupported;
     // the DMA offsets are 32-bit: every activation row, weight row and scale row must lie within 4 GiB
     if ((uint64_t)M * (uint64_t)K >= (1ull << 32) || (uint64_t)(K / 32) * (uint64_t)act.m_ld * 4 >= (1ull << 32))
         return hipErrorNotSupported;
@@ -311,8 +316,9 @@ hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, in
     const bool full = M % kBM == 0 && N % kBN == 0;
     auto fn = block_sums ? (full ? prefill_q8_0_kernel<true, true> : prefill_q8_0_kernel<true, false>)
                          : (full ? prefill_q8_0_kernel<false, true> : prefill_q8_0_kernel<false, false>);
-    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, (const uint8_t*)W, w_row_bytes,
-                       (int)N, (int)K, act.qs, act.d, act.m_ld, (int)M, Y, y_stride, block_sums, tiles_n, tiles_m);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, tiles_n, tiles_m, (int)N, (int)K,
+                       (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (int)M, Y, y_stride,
+                       block_sums);
     return hipGetLastError();
 }
 

@@ -110,12 +110,15 @@ __device__ __forceinline__ uint32_t q6_minus32(uint32_t ql, uint32_t qh2) {
 // W: Q6_K rows (w_row_bytes % 4 == 0, 16-byte aligned base); xqs: int8 [M][K]; xd: float
 // [K/256][m_ld] with m_ld a multiple of 128; K % 512 == 0.
 // FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
+// Arguments: the ones the first loads need come first (the first 56 bytes of arguments are
+// preloaded into scalar registers at dispatch).
 template <bool DUMP, bool FULL>
-__global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
-                                                              int N, int K, const int8_t* __restrict__ xqs,
-                                                              const float* __restrict__ xd, int64_t m_ld, int M,
+__global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
+                                                              int w_row_bytes, const uint8_t* __restrict__ W,
+                                                              const int8_t* __restrict__ xqs,
+                                                              const float* __restrict__ xd, int M,
                                                               float* __restrict__ Y, int64_t y_stride,
-                                                              int32_t* __restrict__ sums, int tiles_n, int tiles_m) {
+                                                              int32_t* __restrict__ sums) {
     extern __shared__ __align__(16) uint8_t smem[];
     StageQ6* st = reinterpret_cast<StageQ6*>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -327,13 +330,16 @@ __global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(const uint8_t* __r
 // W: Q4_K rows (w_row_bytes % 16 == 0, 16-byte aligned base); xqs: int8 [M][K]; xd: float
 // [K/256][m_ld] with m_ld a multiple of 128; xbs: int16 [M][K/16]; K % 256 == 0.
 // FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
+// Arguments: the ones the first loads need come first (the first 56 bytes of arguments are
+// preloaded into scalar registers at dispatch).
 template <bool DUMP, bool FULL>
-__global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
-                                                              int N, int K, const int8_t* __restrict__ xqs,
-                                                              const float* __restrict__ xd, int64_t m_ld,
+__global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
+                                                              int w_row_bytes, const uint8_t* __restrict__ W,
+                                                              const int8_t* __restrict__ xqs,
+                                                              const float* __restrict__ xd,
                                                               const int16_t* __restrict__ xbs, int M,
                                                               float* __restrict__ Y, int64_t y_stride,
-                                                              int32_t* __restrict__ sums, int tiles_n, int tiles_m) {
+                                                              int32_t* __restrict__ sums) {
     extern __shared__ __align__(16) uint8_t smem[];
     StageQ4* st = reinterpret_cast<StageQ4*>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -547,8 +553,8 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(const uint8_t* __r
 
 hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                                int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
-    if (K % 256 || w_row_bytes % 16 || act.m_ld % kBM || !act.bs || N > (1 << 30) || M > (1 << 30) ||
-        K > (1 << 30))
+    if (K % 256 || w_row_bytes % 16 || w_row_bytes > INT32_MAX || act.m_ld % kBM || act.m_ld > INT32_MAX ||
+        !act.bs || N > (1 << 30) || M > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
     if ((uint64_t)M * (uint64_t)K >= (1ull << 32)) return hipErrorNotSupported;  // 32-bit DMA offsets
     const int tiles_n = (int)((N + kBN - 1) / kBN), tiles_m = (int)((M + kBM - 1) / kBM);
@@ -556,9 +562,9 @@ hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, in
     const bool full = M % kBM == 0 && N % kBN == 0;
     auto fn = block_sums ? (full ? prefill_q4_k_kernel<true, true> : prefill_q4_k_kernel<true, false>)
                          : (full ? prefill_q4_k_kernel<false, true> : prefill_q4_k_kernel<false, false>);
-    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, (const uint8_t*)W, w_row_bytes,
-                       (int)N, (int)K, act.qs, act.d, act.m_ld, (const int16_t*)act.bs, (int)M, Y, y_stride,
-                       block_sums, tiles_n, tiles_m);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, tiles_n, tiles_m, (int)N, (int)K,
+                       (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (const int16_t*)act.bs,
+                       (int)M, Y, y_stride, block_sums);
     return hipGetLastError();
 }
 
@@ -566,7 +572,8 @@ hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, in
                                int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
     // K % 512: an even number of superblocks, so the 2-byte overreach of the scale and d loads of
     // an even superblock (dword offset 0) stays inside the next one
-    if (K % 512 || w_row_bytes % 4 || act.m_ld % kBM || N > (1 << 30) || M > (1 << 30) || K > (1 << 30))
+    if (K % 512 || w_row_bytes % 4 || w_row_bytes > INT32_MAX || act.m_ld % kBM || act.m_ld > INT32_MAX ||
+        N > (1 << 30) || M > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
     // the DMA offsets are 32-bit: every activation row must lie within 4 GiB of the base
     if ((uint64_t)M * (uint64_t)K >= (1ull << 32)) return hipErrorNotSupported;
@@ -575,8 +582,9 @@ hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, in
     const bool full = M % kBM == 0 && N % kBN == 0;
     auto fn = block_sums ? (full ? prefill_q6_k_kernel<true, true> : prefill_q6_k_kernel<true, false>)
                          : (full ? prefill_q6_k_kernel<false, true> : prefill_q6_k_kernel<false, false>);
-    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, (const uint8_t*)W, w_row_bytes,
-                       (int)N, (int)K, act.qs, act.d, act.m_ld, (int)M, Y, y_stride, block_sums, tiles_n, tiles_m);
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, tiles_n, tiles_m, (int)N, (int)K,
+                       (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (int)M, Y, y_stride,
+                       block_sums);
     return hipGetLastError();
 }
 
