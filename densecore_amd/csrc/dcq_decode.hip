@@ -481,12 +481,19 @@ int choose_shape(int nsb) {
 
 // Launch shape and waves per workgroup for the fused single-row decode. A decode GEMV streams
 // each row once, and its time follows the most rows any one CU has to read (measured on
-// MI355X at K = 2560: 32 rows per CU 4.7 us, 40 rows 5.7 us, 48 rows 6.0 us, one workgroup per
-// CU beating two at the same row count). Among the shapes that leave at most a quarter of their
-// superblock slots idle, and 4- or 5-wave workgroups, take the fewest rows on the busiest CU,
-// then the fewest workgroups per CU. Other variants keep choose_shape with 4 waves. (8- and
-// 10-wave workgroups of 4-row waves, more waves for the same rows, measured slower: 6.3-7.0 us
-// against 5.7 us at N = 9728; bytes in flight per lane matter more than waves per CU.)
+// MI355X at K = 2560: 32 rows per CU 4.7 us, 40 rows 5.7 us, 48 rows 6.0 us). Candidates: the
+// shapes that leave at most a quarter of their superblock slots idle, in 4- or 5-wave
+// workgroups. Many workgroups per CU cost more than their rows say (each quantizes the
+// activation, and beyond what is resident they run in rounds): shapes within 15 % of the fewest
+// busiest-CU rows that need at most 4 workgroups per CU come first (14336 x 4096: 60 rows in
+// 3 workgroups per CU 9.05 us against 56 rows in 14, 9.74 us). Then the fewest busiest-CU rows;
+// on a tie, up to 2 workgroups per CU with the most waves (9728 x 2560: 40 rows as 2 x 5 waves
+// of 4 rows 4.54 us against 1 x 5 waves of 8 rows 4.68 us), else the fewest workgroups per CU
+// (8192 x 2048: 32 rows as 1 workgroup 3.81 us against 4, 4.03 us). Measured with kernel
+// arguments preloaded, over eight model shapes; the rule picks the fastest or within 0.15 us of
+// it on each. Other variants keep choose_shape with 4 waves. (8- and 10-wave workgroups of
+// 4-row waves, more waves for the same rows, measured slower: 6.3-7.0 us against 5.7 us at
+// N = 9728.)
 struct Launch {
     int idx, nw;
 };
@@ -494,23 +501,37 @@ Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
     const int forced = knob(Knob::Q4KShape);
     if (forced >= 0) return {choose_shape(nsb), knob(Knob::Q4KWaves) == 5 ? 5 : 4};
     const int cus = cu_count();
-    Launch best{choose_shape(nsb), 4};
-    int64_t best_rows = INT64_MAX, best_per_cu = INT64_MAX;
+    struct Cand {
+        int idx, nw;
+        int64_t busiest, per_cu;
+    };
+    Cand cands[2 * kNumShapes];
+    int nc = 0;
+    int64_t min_busiest = INT64_MAX;
     for (int i = 0; i < kNumShapes; ++i) {
         const int cap = kShapes[i].P * kShapes[i].NS;
         if (cap < nsb || 4 * (cap - nsb) > cap) continue;
         for (int nw = 4; nw <= (nw5_ok ? 5 : 4); ++nw) {
             const int64_t rpw = nw * (64 / (4 * kShapes[i].P));
             const int64_t wgs = (rows + rpw - 1) / rpw, per_cu = (wgs + cus - 1) / cus;
-            const int64_t busiest = per_cu * rpw;
-            if (busiest < best_rows || (busiest == best_rows && per_cu < best_per_cu)) {
-                best = {i, nw};
-                best_rows = busiest;
-                best_per_cu = per_cu;
-            }
+            cands[nc++] = {i, nw, per_cu * rpw, per_cu};
+            min_busiest = cands[nc - 1].busiest < min_busiest ? cands[nc - 1].busiest : min_busiest;
         }
     }
-    return best;
+    if (nc == 0) return {choose_shape(nsb), 4};
+    auto preferred = [&](const Cand& c) { return c.per_cu <= 4 && 20 * c.busiest <= 23 * min_busiest; };
+    bool any_preferred = false;
+    for (int k = 0; k < nc; ++k) any_preferred |= preferred(cands[k]);
+    // tie order: up to 2 workgroups per CU first, more waves per CU better; beyond, fewer workgroups
+    auto tie_key = [](const Cand& c) { return c.per_cu <= 2 ? -c.per_cu * c.nw : 1000 + c.per_cu; };
+    const Cand* best = nullptr;
+    for (int k = 0; k < nc; ++k) {
+        const Cand& c = cands[k];
+        if (any_preferred && !preferred(c)) continue;
+        if (!best || c.busiest < best->busiest || (c.busiest == best->busiest && tie_key(c) < tie_key(*best)))
+            best = &c;
+    }
+    return {best->idx, best->nw};
 }
 
 // W2 != nullptr: the gate/up pair (Q4_K, fused activation, no block sums): Y = silu(W x) * (W2 x)
