@@ -228,7 +228,7 @@ struct AttnSmem {
     using S = AttnShape<HD>;
     static constexpr int HBW = (HD / 32) * 34 / 4;  // dwords per Q8_0 head piece
     static constexpr int NST = (S::KPW * HBW + 63) / 64;
-    float q[RM][HD];
+    alignas(16) float q[RM][HD];  // 16-byte aligned: the score loop reads it as float4
     float p[RM][S::KC];
     float m[RM], l[RM], alpha[RM];
     float o[4][RM][HD];  // running V sums of each wave's keys
@@ -558,8 +558,9 @@ __global__ void __launch_bounds__(256, RMAX <= 4 ? 3 : 1) attn_kernel(const int3
                                                 q_stored, qreg);
     }
 
-    // ---- merge the four waves' partial sums and write
-    __syncthreads();
+    // ---- merge the four waves' partial sums and write (after a chunk's closing barrier; with no
+    // chunk, after the zeroing above)
+    if (c_begin >= c_end) __syncthreads();
     const bool direct = a.ws_o == nullptr;
     for (int e = tid; e < w.R * HD; e += 256) {
         const int r = e / HD, d = e % HD;
