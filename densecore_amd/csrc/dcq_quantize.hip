@@ -23,11 +23,20 @@ __global__ void __launch_bounds__(256) quantize_q8_0_kernel(const float* __restr
                                                             int8_t* __restrict__ qs, float* __restrict__ dpl,
                                                             uint8_t* __restrict__ out, int64_t out_row_bytes) {
     const int64_t nb = K / QK8_0;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t blk = gid >> 2;       // global block index over [m_ld][nb]
-    const int q = (int)(gid & 3);       // quarter of the block
-    const int64_t m = blk / nb;
-    const int64_t b = blk - m * nb;
+    const int q = (int)(threadIdx.x & 3);  // quarter of the block
+    int64_t m, b;
+    if (kPlanar) {
+        // a 256-thread workgroup takes 32 rows x 2 blocks (lane group g: row g % 32, block g / 32),
+        // so each block's 32 scales go out as one 128-byte run of the [nb][m_ld] scale array
+        const int64_t tiles_b = (nb + 1) / 2, g = threadIdx.x >> 2;
+        m = (int64_t)(blockIdx.x / tiles_b) * 32 + (g & 31);
+        b = (int64_t)(blockIdx.x % tiles_b) * 2 + (g >> 5);
+        if (b >= nb) return;            // whole groups of 4 lanes exit together
+    } else {
+        const int64_t blk = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 2;  // over [M][nb]
+        m = blk / nb;
+        b = blk - m * nb;
+    }
     if (m >= m_ld) return;              // whole groups of 4 lanes exit together
     if (m >= M) {                       // planar padding rows: scale 0
         if (kPlanar && q == 0) dpl[b * m_ld + m] = 0.0f;
@@ -75,9 +84,17 @@ __global__ void __launch_bounds__(256) quantize_q8_K_kernel(const float* __restr
                                                             int64_t out_row_bytes) {
     const int64_t nsb = K / QK_K;
     const int g = threadIdx.x & 15;
-    const int64_t sbg = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // global superblock
-    const int64_t m = sbg / nsb;
-    const int64_t s = sbg - m * nsb;
+    int64_t m, s;
+    if (kPlanar) {
+        // a 256-thread workgroup takes 16 rows of one superblock, so their scales go out as one
+        // 64-byte run of the [nsb][m_ld] scale array
+        m = (int64_t)(blockIdx.x / nsb) * 16 + (threadIdx.x >> 4);
+        s = blockIdx.x % nsb;
+    } else {
+        const int64_t sbg = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // over [M][nsb]
+        m = sbg / nsb;
+        s = sbg - m * nsb;
+    }
     if (m >= m_ld) return;  // whole 16-lane rows exit together
     if (m >= M) {
         if (kPlanar && g == 0) dpl[s * m_ld + m] = 0.0f;
@@ -179,17 +196,17 @@ hipError_t launch_quantize_ggml(int vdt, const float* X, int64_t x_stride, int64
 
 hipError_t launch_quantize_planar(int vdt, const float* X, int64_t x_stride, int64_t M, int64_t K,
                                   const PlanarBuffers& pb, hipStream_t st) {
+    // m_ld is a multiple of 128 (planar_bytes): whole 32-row (Q8_0) or 16-row (Q8_K) tiles
+    if (pb.m_ld % 32) return hipErrorInvalidValue;
     if (vdt == kTypeQ8_0) {
-        const int64_t threads = pb.m_ld * (K / QK8_0) * 4;
-        const int bs = quant_block(threads);
-        const int64_t grid = (threads + bs - 1) / bs;
-        hipLaunchKernelGGL(quantize_q8_0_kernel<true>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
+        const int64_t grid = (pb.m_ld / 32) * ((K / QK8_0 + 1) / 2);
+        if (grid > UINT32_MAX) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(quantize_q8_0_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
                            pb.m_ld, pb.qs, pb.d, (uint8_t*)nullptr, (int64_t)0);
     } else {
-        const int64_t threads = pb.m_ld * (K / QK_K) * 16;
-        const int bs = quant_block(threads);
-        const int64_t grid = (threads + bs - 1) / bs;
-        hipLaunchKernelGGL(quantize_q8_K_kernel<true>, dim3((unsigned)grid), dim3(bs), 0, st, X, x_stride, M, K,
+        const int64_t grid = (pb.m_ld / 16) * (K / QK_K);
+        if (grid > UINT32_MAX) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(quantize_q8_K_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, X, x_stride, M, K,
                            pb.m_ld, pb.qs, pb.bs, pb.d, (uint8_t*)nullptr, (int64_t)0);
     }
     return hipGetLastError();
