@@ -80,6 +80,53 @@ def test_quantize_q8_K_ties_bit_exact(O, dev):
     assert np.array_equal(got, O.quantize_rows(Q8_K, x))
 
 
+def _planar_regions(vdt, M, K):
+    """Byte layout of dcq_quantize_src1's workspace (planar_bytes in dcq_api.cpp): int8 qs [M][K],
+    fp32 scales [K/bs][m_ld] with m_ld = M rounded up to 128 (rows >= M hold 0), then for Q8_K the
+    int16 16-element sums [M][K/16]; each region starts on a 256-byte boundary."""
+    up = lambda v, a: (v + a - 1) // a * a
+    bs = 32 if vdt == Q8_0 else 256
+    m_ld = up(M, 128)
+    qs_b = up(M * K, 256)
+    d_b = up((K // bs) * m_ld * 4, 256)
+    return bs, m_ld, qs_b, d_b
+
+
+@pytest.mark.parametrize("wt,M,K", [(Q8_0, 1, 96), (Q8_0, 33, 96), (Q8_0, 130, 1024), (Q4_K, 1, 256),
+                                    (Q4_K, 17, 2560), (Q4_K, 130, 512)])
+def test_quantize_src1_planar_bit_exact(O, dev, wt, M, K):
+    """The planar activation the prefill, batch and MMQ kernels read, byte for byte against the
+    oracle's row quantization: int8 values, scales (Q8_0's fp16 d widened to fp32), the Q8_K
+    16-element sums, and zero scales on the padding rows. Covers an odd block count per row
+    (K = 96: three Q8_0 blocks) and row counts that leave part of a row tile empty."""
+    import torch
+    vdt = Q8_0 if wt == Q8_0 else Q8_K
+    x = synth.normal(M * K, 500 + M + K).reshape(M, K)
+    synth.set_outliers(x[-1], max(1, K // 100), 20.0, 7)
+    ws = torch.full((dc.mul_mat_workspace_size(wt, M, K),), 0xAB, dtype=torch.uint8, device=dev)
+    dc.quantize_src1(wt, to_dev(x, dev), ws)
+    raw = to_host(ws)
+    bs, m_ld, qs_b, d_b = _planar_regions(vdt, M, K)
+    nb = K // bs
+    qs = raw[:M * K].view(np.int8).reshape(M, K)
+    d = raw[qs_b:qs_b + nb * m_ld * 4].view(np.float32).reshape(nb, m_ld)
+    want = O.quantize_rows(vdt, x)
+    if vdt == Q8_0:
+        blocks = want.reshape(M, nb, 34)
+        want_d = blocks[:, :, :2].copy().view(np.float16).reshape(M, nb).astype(np.float32)
+        want_qs = blocks[:, :, 2:].copy().view(np.int8).reshape(M, K)
+    else:
+        blocks = want.reshape(M, nb, 292)
+        want_d = blocks[:, :, :4].copy().view(np.float32).reshape(M, nb)
+        want_qs = blocks[:, :, 4:260].copy().view(np.int8).reshape(M, K)
+        want_bs = blocks[:, :, 260:].copy().view(np.int16).reshape(M, K // 16)
+        got_bs = raw[qs_b + d_b:qs_b + d_b + M * (K // 16) * 2].view(np.int16).reshape(M, K // 16)
+        assert np.array_equal(got_bs, want_bs)
+    assert np.array_equal(qs, want_qs)
+    assert np.array_equal(d[:, :M].T, want_d)
+    assert np.all(d[:, M:] == 0.0)
+
+
 def test_quantize_rows_strided_input(O, dev):
     import torch
     x = synth.normal(4 * 1024, 91).reshape(4, 1024)
