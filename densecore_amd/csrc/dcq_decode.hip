@@ -193,11 +193,11 @@ __host__ __device__ constexpr int stage_chunks(int P, int NS, int MT, bool fuse,
 // (xqs, xd, xbs, m_ld). M <= MT activation rows; LDS holds MT rows, rows >= M unused.
 // GLU: a second weight matrix W2 of the same shape shares the activation; the output is
 // silu(W x) * (W2 x) (the SwiGLU gate and up projections).
-template <class Fmt, int P, int MT, int NS, bool FUSE, bool DUMP, bool GLU = false, int NW = 4,
-          int QC = stage_chunks(P, NS, MT, FUSE, NW)>
 // The arguments the first loads need come first: the first 56 bytes of arguments are preloaded
 // into scalar registers at dispatch (-amdgpu-kernarg-preload-count), the rest take a dependent
 // scalar load.
+template <class Fmt, int P, int MT, int NS, bool FUSE, bool DUMP, bool GLU = false, int NW = 4,
+          int QC = stage_chunks(P, NS, MT, FUSE, NW)>
 __global__ void __launch_bounds__(64 * NW) decode_kq_kernel(const float* __restrict__ X, int64_t x_stride, int M,
                                                          int nsb, const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                          int64_t n0, int64_t n1, const uint8_t* __restrict__ W2,

@@ -141,10 +141,10 @@ struct Q6Lds {
 // loads: loads retire in order, so an explicit wait for all but the row's loads covers them,
 // and the quantizer runs while the row streams. The first SW waves stage the activation, QC
 // passes of 4 * SW (superblock, row) pairs; the other waves only stream their rows.
-template <int MT, bool DUMP, bool FUSE = false, int QC = 1, int kWaves = 4, int SW = kWaves>
 // The arguments the first loads need come first: the first 56 bytes of arguments are preloaded
 // into scalar registers at dispatch (-amdgpu-kernarg-preload-count), the rest take a dependent
 // scalar load.
+template <int MT, bool DUMP, bool FUSE = false, int QC = 1, int kWaves = 4, int SW = kWaves>
 __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     const float* __restrict__ X, int64_t x_stride, const uint8_t* __restrict__ W, int64_t n0, int64_t n1,
     int w_row_bytes, int M, int nsb, int rpw, const int8_t* __restrict__ xqs, const float* __restrict__ xd,

@@ -81,10 +81,10 @@ __host__ __device__ constexpr int q8_stage_passes(int G, int NS, int MT, int NW)
 }  // namespace
 
 // GLU: a second weight matrix W2 shares the activation; the output is silu(W x) * (W2 x).
-template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, int QC = q8_stage_passes(G, NS, MT, NW)>
 // The arguments the first loads need come first: the first 56 bytes of arguments are preloaded
 // into scalar registers at dispatch (-amdgpu-kernarg-preload-count), the rest take a dependent
 // scalar load.
+template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, int QC = q8_stage_passes(G, NS, MT, NW)>
 __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __restrict__ X, int64_t x_stride,
                                                            const uint8_t* __restrict__ W,
                                                            const uint8_t* __restrict__ W2, int64_t w_row_bytes,
