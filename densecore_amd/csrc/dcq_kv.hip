@@ -308,12 +308,28 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
     const int e0 = DPL * lane;
     uint32_t vst[STAGED ? NST : 1];
     if constexpr (STAGED) {
+        // A wave's KPW keys start on a multiple of min(KPW, kKvBlock) (kbase is a multiple of
+        // KC = 4 KPW), so key pk lies in the wave's KV block pk / kKvBlock at position
+        // pk % kKvBlock past that block's first key of the wave: its slot offset is that key's
+        // (one scalar read per block) plus (pk % kKvBlock) slots, no lane exchange per load.
+        constexpr int NB = KPW > kKvBlock ? KPW / kKvBlock : 1;
+        static_assert(KPW % kKvBlock == 0 || kKvBlock % KPW == 0, "keys of a wave tile KV blocks");
+        int64_t ob[NB];
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+            const int src = bb * kKvBlock * LPK;  // the lane of key bb * kKvBlock (compile-time)
+            ob[bb] = ((int64_t)__builtin_amdgcn_readlane((int)(off >> 32), src) << 32) |
+                     (uint32_t)__builtin_amdgcn_readlane((int)off, src);
+        }
 #pragma unroll
         for (int j = 0; j < NST; ++j) {
             const int f = lane + 64 * j, pk = f / HBW, dw = f - pk * HBW;
-            const int src = (pk < KPW ? pk : 0) * LPK;
-            const int64_t op = ((int64_t)__shfl((int)(off >> 32), src, 64) << 32) | (uint32_t)__shfl((int)off, src, 64);
-            const bool ok = f < KPW * HBW && ((present >> src) & 1);
+            const int pkc = pk < KPW ? pk : 0, bb = NB > 1 ? pkc / kKvBlock : 0;
+            int64_t o0 = ob[0];
+#pragma unroll
+            for (int k = 1; k < NB; ++k) o0 = bb == k ? ob[k] : o0;
+            const int64_t op = o0 + (int64_t)(pkc % kKvBlock) * a.sb;
+            const bool ok = f < KPW * HBW && ((present >> (pkc * LPK)) & 1);
             vst[j] = ok ? ld1(vbase_p + op + 4 * dw) : 0u;
         }
     } else {
