@@ -185,6 +185,18 @@ __device__ __forceinline__ float lanes_sum(float v) {
     return v;
 }
 
+// Maximum over aligned groups of L lanes, in the same steps as lanes_sum.
+template <int L>
+__device__ __forceinline__ float lanes_max(float v) {
+    if (L >= 2) v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));
+    if (L >= 4) v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));
+    if (L >= 8) v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));
+    if (L >= 16) v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));
+    if (L >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if (L >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
 // SiLU of the SwiGLU gate, g / (1 + e^-g) (ggml_silu's definition). expf is within a few ulp,
 // far inside the fp32 tolerance of the dot products it multiplies.
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }

@@ -692,8 +692,8 @@ __global__ void __launch_bounds__(256) attn_combine_few_kernel(const float* __re
 
 // Many splits over few rows (decode): the splits of each 4-element output are dealt to P
 // consecutive lanes (lane p takes splits p, p + P, ..., at most NS of them, all loads issued
-// together), and the lanes combine by exchange: the row maximum first, then the weighted sums,
-// one exp2 per split. A decode call at n_past = 4095 (65 splits over 32 rows x 32 quads) runs
+// together), and the lanes combine by exchange (DPP inside 16-lane rows, one lane permute
+// across rows): the row maximum first, then the weighted sums, one exp2 per split. A decode call at n_past = 4095 (65 splits over 32 rows x 32 quads) runs
 // 32768 threads with at most three splits each: 15.4 us per call with the attention kernel,
 // against 15.7 us with 16 lanes per output and 16.7 us with the workgroup-per-row kernel.
 template <int P, int NS>
@@ -722,8 +722,7 @@ __global__ void __launch_bounds__(256) attn_combine_lanes_kernel(const float* __
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < NS; ++k) m = fmaxf(m, ml[k].x);
-#pragma unroll
-    for (int off = 1; off < P; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));  // finite for a real row
+    m = lanes_max<P>(m);  // finite for a real row
     float l = 0.0f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -735,14 +734,11 @@ __global__ void __launch_bounds__(256) attn_combine_lanes_kernel(const float* __
         acc.z = fmaf(ov[k].z, c, acc.z);
         acc.w = fmaf(ov[k].w, c, acc.w);
     }
-#pragma unroll
-    for (int off = 1; off < P; off <<= 1) {
-        l += __shfl_xor(l, off, 64);
-        acc.x += __shfl_xor(acc.x, off, 64);
-        acc.y += __shfl_xor(acc.y, off, 64);
-        acc.z += __shfl_xor(acc.z, off, 64);
-        acc.w += __shfl_xor(acc.w, off, 64);
-    }
+    l = lanes_sum<P>(l);
+    acc.x = lanes_sum<P>(acc.x);
+    acc.y = lanes_sum<P>(acc.y);
+    acc.z = lanes_sum<P>(acc.z);
+    acc.w = lanes_sum<P>(acc.w);
     if (!ok || p != 0) return;
     const float inv = 1.0f / l;
     const int i = (int)(row / n_head), h = (int)(row % n_head);
