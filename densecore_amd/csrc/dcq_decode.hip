@@ -413,8 +413,9 @@ DecodeFn fn_of() {
     return decode_kq_kernel<Fmt, kShapes[I].P, MT, kShapes[I].NS, FUSE, DUMP, GLU, NW>;
 }
 
-// the fused single-row decode (the common decode step) also comes in 5-wave workgroups: rows
-// per workgroup then spread the matrix over the CUs more evenly for some N (see choose_waves)
+// the fused single-row decode (the common decode step, and the gate/up pair) also comes in
+// 5-wave workgroups: rows per workgroup then spread the matrix over the CUs more evenly for some
+// N (see choose_launch)
 template <class Fmt, int I, bool FUSE, bool DUMP, bool GLU>
 DecodeFn pick_mt(int mt, int nw) {
     if constexpr (FUSE && !DUMP) {
@@ -544,9 +545,10 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
     const bool glu = W2 != nullptr;
     if (glu && (wtype != kTypeQ4_K || !fuse || block_sums)) return hipErrorNotSupported;
     if (wtype == kTypeQ4_K ? (w_row_bytes % 16 != 0) : (w_row_bytes % 2 != 0)) return hipErrorNotSupported;
-    // the 5-wave variants exist for the fused, sum-free single-row decode only; the gate/up pair
-    // (two weights per lane) keeps its 4-wave shape (fused pair 8.5 us against 9.1 us with 5)
-    const bool single = fuse && !block_sums && M == 1 && !glu;
+    // the 5-wave variants exist for the fused, sum-free single-row decode and the gate/up pair at
+    // M = 1, which take the launch rule (the pair at config 2's shape: 7.44 -> 7.22 us with it,
+    // kernel arguments preloaded); other variants keep choose_shape with 4 waves
+    const bool single = fuse && !block_sums && M == 1;
     const Launch ln = single ? choose_launch(nsb, n1 - n0, true) : Launch{choose_shape(nsb), 4};
     const int idx = ln.idx;
     if (idx < 0) return hipErrorNotSupported;
