@@ -190,13 +190,13 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
         __builtin_amdgcn_wave_barrier();  // the region is rewritten by the next superblock's loads
     }
 
-    // ---- fixed-order reduction of the 8 partial tiles through LDS ----
-    __syncthreads();  // every wave is done with its activation region
-    float* part = reinterpret_cast<float*>(smem);  // [wave][i][v][64]
+    // ---- fixed-order reduction of the 8 partial tiles through LDS: each wave's partial tile
+    // ([i][v][64], 8 KB) goes into its own region, which only it has read, so one barrier ----
+    auto part = [&](int w) { return reinterpret_cast<float*>(smem + w * kRegion); };
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) part[((wave * 2 + i) * 16 + v) * 64 + lane] = acc[i][v];
+        for (int v = 0; v < 16; ++v) part(wave)[(i * 16 + v) * 64 + lane] = acc[i][v];
     __syncthreads();
     // every wave sums 4 of the 32 (m-tile, value) pairs over the 8 partial tiles, in wave order
     {
@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
             const int pv = wave * 4 + k, i = pv >> 4, v = pv & 15;
             float p8[kWaves];
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) p8[w] = part[((w * 2 + i) * 16 + v) * 64 + lane];
+            for (int w = 0; w < kWaves; ++w) p8[w] = part(w)[(i * 16 + v) * 64 + lane];
             float y = p8[0];
 #pragma unroll
             for (int w = 1; w < kWaves; ++w) y += p8[w];
