@@ -32,6 +32,22 @@ size_t planar_bytes(int vdt, int64_t M, int64_t K, PlanarBuffers* pb, void* base
     return qs_b + d_b + bs_b;
 }
 
+// Room for the split-K partial tiles of the MFMA prefill kernels (used at M > 8 when the output
+// tiles cannot give every CU a workgroup): one fp32 128 x 128 tile per CU of a 256-CU device,
+// i.e. M * 128 KB up to M = 128 (16 MB).
+size_t split_tail_bytes(int64_t M) { return M > 8 ? (size_t)(M < 128 ? M : 128) * 128 * 1024 : 0; }
+
+// the bytes of a workspace past its first `used` ones, as split-K scratch (none if too small)
+SplitScratch tail_of(void* ws, size_t ws_bytes, size_t used) {
+    SplitScratch sc;
+    used = (size_t)round_up((int64_t)used, 256);
+    if (ws && ws_bytes > used) {
+        sc.p = reinterpret_cast<float*>(static_cast<char*>(ws) + used);
+        sc.bytes = ws_bytes - used;
+    }
+    return sc;
+}
+
 int knob(Knob k) {
     struct Entry {
         const char* name;
@@ -41,7 +57,7 @@ int knob(Knob k) {
         {"DCQ_Q4K_SHAPE", -1}, {"DCQ_Q4K_NW", 4},      {"DCQ_NO_FUSE", 0},      {"DCQ_Q6K_DECODE", 0},
         {"DCQ_Q6K_LDS_OFF", 0}, {"DCQ_Q6K_NO_FUSE", 0}, {"DCQ_Q6K_FUSE_NW", -1}, {"DCQ_Q8_SHAPE", -1},
         {"DCQ_GEMV_GENERIC", 0}, {"DCQ_GEMV_LG", -1},   {"DCQ_ATTN_NO_MFMA", 0}, {"DCQ_Q6K_RPW", -1},
-        {"DCQ_Q6K_MFMA", 1},
+        {"DCQ_Q6K_MFMA", 1},    {"DCQ_SPLIT_K", -1},
     };
     // read once (thread-safe static initialisation), not per call: getenv walks the environment
     static const std::array<int, (int)Knob::kCount> values = [] {
@@ -191,7 +207,7 @@ int64_t dcq_block_sums_per_row(int wtype, int64_t k) {
 size_t dcq_mul_mat_workspace_size(int wtype, int64_t M, int64_t K) {
     const int vdt = dcq_vec_dot_type(wtype);
     if (vdt < 0 || M <= 0 || K <= 0 || K % dcq_block_size(wtype)) return 0;
-    return planar_bytes(vdt, M, K, nullptr, nullptr);
+    return planar_bytes(vdt, M, K, nullptr, nullptr) + split_tail_bytes(M);
 }
 
 int dcq_quantize_rows(int vdt, const float* X, int64_t M, int64_t K, size_t x_stride_bytes, void* Xq, void* stream) {
@@ -230,9 +246,12 @@ int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_
                                            Y, (int64_t)(y_stride_bytes / 4), block_sums, st);
         if (e != hipErrorNotSupported) return hip_status(e);
     }
+    // the workspace past the quantized activation (when there is room) holds split-K partial sums
     void* ws = workspace;
+    size_t ws_total = workspace_bytes;
     if (!ws) {
-        if (hipMallocAsync(&ws, need, st) != hipSuccess) return DCQ_ERR_HIP;
+        ws_total = need + split_tail_bytes(M);
+        if (hipMallocAsync(&ws, ws_total, st) != hipSuccess) return DCQ_ERR_HIP;
     }
     PlanarBuffers pb;
     planar_bytes(vdt, M, K, &pb, ws);
@@ -242,7 +261,8 @@ int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_
         if (use_gemv)
             e = launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, block_sums, N, st);
         else
-            e = launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, block_sums, st);
+            e = launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, block_sums, st,
+                           tail_of(ws, ws_total, need));
     }
     if (!workspace) {
         hipError_t e2 = hipFreeAsync(ws, st);
@@ -296,9 +316,10 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
         const uintptr_t r0 = (uintptr_t)R, r1 = r0 + (size_t)(M - 1) * r_stride_bytes + (size_t)N * 4;
         if (r0 < y1 && y0 < r1) return DCQ_ERR_INVALID_ARG;
     }
+    // required: the activation and the [M][N] temporary; the split-K room after them is optional
     const size_t need = dcq_mul_mat_add_workspace_size(wtype, M, N, K);
     if (workspace) {
-        if (workspace_bytes < need) return DCQ_ERR_WORKSPACE;
+        if (workspace_bytes < need - split_tail_bytes(M)) return DCQ_ERR_WORKSPACE;
         if (!aligned(workspace, 256)) return DCQ_ERR_MISALIGNED;
     }
     rc = check_device();
@@ -321,6 +342,8 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
     // the product goes to Y when R is elsewhere, else to a workspace temporary [M][N]
     float* T = in_place ? reinterpret_cast<float*>(static_cast<char*>(ws) + act_bytes) : Y;
     const int64_t t_stride = in_place ? N : y_stride;
+    // split-K partial sums after the temporary
+    const SplitScratch sc = tail_of(ws, workspace ? workspace_bytes : need, act_bytes + (size_t)M * N * 4);
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
     bool added = false;
     if (e == hipSuccess && M <= 8) {
@@ -331,7 +354,7 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
     }
     if (e == hipSuccess && !added) {
         e = M <= 8 ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, T, t_stride, nullptr, N, st)
-                   : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, T, t_stride, nullptr, st);
+                   : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, T, t_stride, nullptr, st, sc);
         if (e == hipSuccess) e = launch_add_rows(Y, y_stride, T, t_stride, R, r_stride, M, N, st);
     }
     if (!workspace) {
@@ -354,9 +377,10 @@ int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_
     if (rc) return rc;
     if (!Wu) return DCQ_ERR_INVALID_ARG;
     if (!aligned(Wu, 16)) return DCQ_ERR_MISALIGNED;
+    // required: the activation and the [M][N] temporary; the split-K room after them is optional
     const size_t need = dcq_ffn_gate_up_workspace_size(wtype, M, N, K);
     if (workspace) {
-        if (workspace_bytes < need) return DCQ_ERR_WORKSPACE;
+        if (workspace_bytes < need - split_tail_bytes(M)) return DCQ_ERR_WORKSPACE;
         if (!aligned(workspace, 256)) return DCQ_ERR_MISALIGNED;
     }
     rc = check_device();
@@ -377,14 +401,16 @@ int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_
     PlanarBuffers pb;
     const size_t act_bytes = planar_bytes(vdt, M, K, &pb, ws);
     float* U = reinterpret_cast<float*>(static_cast<char*>(ws) + act_bytes);  // [M][N]
+    // split-K partial sums after U (the two products run one after the other on the stream)
+    const SplitScratch sc = tail_of(ws, workspace ? workspace_bytes : need, act_bytes + (size_t)M * N * 4);
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
     const bool use_gemv = M <= 8;
     if (e == hipSuccess)
         e = use_gemv ? launch_gemv(wtype, Wg, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
-                     : launch_mmq(wtype, Wg, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st);
+                     : launch_mmq(wtype, Wg, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st, sc);
     if (e == hipSuccess)
         e = use_gemv ? launch_gemv(wtype, Wu, (int64_t)w_row_bytes, 0, N, K, pb, M, U, N, nullptr, N, st)
-                     : launch_mmq(wtype, Wu, (int64_t)w_row_bytes, N, K, pb, M, U, N, nullptr, st);
+                     : launch_mmq(wtype, Wu, (int64_t)w_row_bytes, N, K, pb, M, U, N, nullptr, st, sc);
     if (e == hipSuccess) e = launch_silu_mul(Y, y_stride, U, N, M, N, st);
     if (!workspace) {
         hipError_t e2 = hipFreeAsync(ws, st);
@@ -429,7 +455,9 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
     const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= 8);
     hipError_t e = use_gemv ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
-                            : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st);
+                            : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st,
+                                         tail_of((void*)workspace, workspace_bytes,
+                                                 planar_bytes(vdt, M, K, nullptr, nullptr)));
     return hip_status(e);
 }
 

@@ -48,6 +48,7 @@ enum class Knob {
     AttnNoMfma,   // DCQ_ATTN_NO_MFMA: 1 keeps prompts on the VALU attention kernel
     Q6KRows,      // DCQ_Q6K_RPW: rows per wave of the 4-wave Q6_K decode (-1: launch rule)
     Q6KMfma,      // DCQ_Q6K_MFMA: 0 keeps tall Q6_K matrices on the lane-per-superblock kernels
+    SplitK,       // DCQ_SPLIT_K: force the K splits of the MFMA prefill kernels (-1: rule, 1: none)
     kCount
 };
 int knob(Knob k);
@@ -103,27 +104,49 @@ hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t 
                                     hipStream_t st, const float* R = nullptr,
                                    int64_t r_stride = 0);
 
+// Room for the partial tiles of a split-K product (fp32 planes of M x N); bytes == 0: no split.
+struct SplitScratch {
+    float* p = nullptr;
+    size_t bytes = 0;
+};
+
+// Split-K for the 128 x 128-tile MFMA kernels when their tiles cannot fill the chip: the K stages
+// are cut into `splits` ranges of `stps` stages (a multiple of `align`), each a workgroup per
+// tile writing its partial tile to a plane of the scratch; then launch_sum_splits adds the planes
+// in split order (deterministic). splits == 1: no split (stps = nstages).
+struct SplitPlan {
+    int splits, stps;
+};
+SplitPlan plan_split_k(int64_t tiles, int nstages, int align, int64_t M, int64_t N, const SplitScratch& sc);
+// Y[m][n] = sum over s (in order) of P[s][m][n], P planes of M x N floats.
+hipError_t launch_sum_splits(const float* P, int splits, int64_t M, int64_t N, float* Y, int64_t y_stride,
+                             hipStream_t st);
+
 // Q8_0 prefill: LDS-staged 128 x 128 int8-MFMA tiles (K % 128 == 0, w_row_bytes % 4 == 0);
 // hipErrorNotSupported otherwise (nothing launched).
 hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                               const SplitScratch& sc = SplitScratch());
 
 // Q6_K prefill: the same tiling over the planar Q8_K activation (K % 512 == 0, w_row_bytes % 4
 // == 0, m_ld % 128 == 0); hipErrorNotSupported otherwise (nothing launched).
 hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                               const SplitScratch& sc = SplitScratch());
 // Q4_K prefill: the same tiling (K % 256 == 0, w_row_bytes % 16 == 0, m_ld % 128 == 0).
 hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                               const SplitScratch& sc = SplitScratch());
 
 // Q4_K batched decode (M <= 128): 8-wave workgroups per 32 weight rows x 64 activation
 // rows, K split over the waves; hipErrorNotSupported when the shape is outside it.
 hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                             int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
 
-// Int8-MFMA tiles for any M.
+// Int8-MFMA tiles for any M; sc: room for split-K partial tiles (optional).
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                      int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+                      int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                      const SplitScratch& sc = SplitScratch());
 
 // Paged KV cache (arena layout of the reference's PagedKVCache; row_elems % 32 == 0, pointers
 // and strides 16-byte aligned, checked by the caller).

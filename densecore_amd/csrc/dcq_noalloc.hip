@@ -3,8 +3,10 @@
 // dcq_mul_mat needs a workspace for the quantized activations whenever the product does not
 // run in one fused decode kernel (M > 8, or shapes outside the fused kernels). A caller that
 // cannot allocate (code under stream capture, a serving loop that forbids hipMalloc) gets it
-// from `scratch`, a static device array of DCQ_NOALLOC_SCRATCH_BYTES that every GPU the
-// library runs on holds from the module's load until the process ends.
+// from `scratch`, a static device array that every GPU the library runs on holds from the
+// module's load until the process ends: DCQ_NOALLOC_SCRATCH_BYTES for the quantized activation
+// and 16 MiB after it for split-K partial sums, the room dcq_mul_mat_workspace_size gives at most
+// (so the kernels split K exactly as dcq_mul_mat with a workspace of that size does).
 //
 // In host code `scratch` names a host-side stand-in, not the device array: the device address
 // is looked up once per device with hipGetSymbolAddress (with that device current) and kept;
@@ -16,7 +18,8 @@
 #include "../../include/dcq.h"
 #include "dcq_kernels.h"
 
-static __device__ __align__(256) unsigned char scratch[DCQ_NOALLOC_SCRATCH_BYTES];
+constexpr size_t kSplitRoom = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[DCQ_NOALLOC_SCRATCH_BYTES + kSplitRoom];
 
 namespace dcq {
 
@@ -37,7 +40,7 @@ int noalloc_scratch(void** ptr, size_t* bytes) {
         g_scratch_ptr[dev] = p;
     }
     *ptr = g_scratch_ptr[dev];
-    *bytes = DCQ_NOALLOC_SCRATCH_BYTES;
+    *bytes = DCQ_NOALLOC_SCRATCH_BYTES + kSplitRoom;
     return DCQ_OK;
 }
 

@@ -93,15 +93,20 @@ template <bool DUMP, bool FULL>
 __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
                                                               int w_row_bytes, const uint8_t* __restrict__ W,
                                                               const int8_t* __restrict__ xqs,
-                                                              const float* __restrict__ xd, int M,
+                                                              const float* __restrict__ xd, int M, int stps,
                                                               float* __restrict__ Y, int64_t y_stride,
                                                               int32_t* __restrict__ sums) {
     extern __shared__ __align__(16) uint8_t smem[];
     Stage* st = reinterpret_cast<Stage*>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
+    // ---- split-K: workgroup id = split * tiles + tile. Split s computes stages [s * stps,
+    // (s + 1) * stps) and stores its partial tile in plane s of Y (planes of M rows; with one split
+    // Y is the output itself) ----
+    const int tiles = tiles_n * tiles_m;
+    const int split = (int)blockIdx.x / tiles;
+    const int bid = (int)blockIdx.x - split * tiles;
     // ---- XCD-aware tile order: XCD x (= id % 8) takes n-tile band x, walked m-first ----
-    const int bid = blockIdx.x;
     int tile_m, tile_n;
     if (tiles_n % kXcds == 0) {
         const int band = tiles_n / kXcds;  // n tiles per XCD
@@ -114,6 +119,8 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
     }
     const int m0 = tile_m * kBM, n0 = tile_n * kBN;
     const int nstages = K / kKS;
+    const int s_begin = split * stps, s_end = min(nstages, s_begin + stps);
+    Y += (int64_t)split * M * y_stride;
 
     // ---- staging assignment (per-lane byte offsets, fixed for the whole K loop) ----
     // activation rows: straight to LDS, 4 x 1 KB per wave per stage; instruction i of wave w
@@ -196,14 +203,14 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    DCQ_ISSUE(0, st[0]);
-    DCQ_COMMIT(st[0]);
+    DCQ_ISSUE(s_begin, st[s_begin & 1]);
+    DCQ_COMMIT(st[s_begin & 1]);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
     __syncthreads();
 
-    for (int s = 0; s < nstages; ++s) {
+    for (int s = s_begin; s < s_end; ++s) {
         const Stage& S = st[s & 1];
-        const bool more = s + 1 < nstages;
+        const bool more = s + 1 < s_end;
         if (more) DCQ_ISSUE(s + 1, st[(s + 1) & 1]);  // in flight while this stage computes
         // fragments of block kb are read one block ahead (block 0 here, block kb + 1 after block
         // kb's MFMAs issue), so the MFMAs of a block do not wait for their LDS reads
@@ -304,7 +311,8 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
 size_t prefill_q8_0_lds_bytes() { return 2 * sizeof(Stage); }
 
 hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                               const SplitScratch& sc) {
     if (K % kKS || w_row_bytes % 4 || w_row_bytes > INT32_MAX || act.m_ld > INT32_MAX || N > (1 << 30) ||
         M > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
@@ -316,10 +324,16 @@ hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, in
     const bool full = M % kBM == 0 && N % kBN == 0;
     auto fn = block_sums ? (full ? prefill_q8_0_kernel<true, true> : prefill_q8_0_kernel<true, false>)
                          : (full ? prefill_q8_0_kernel<false, true> : prefill_q8_0_kernel<false, false>);
-    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, tiles_n, tiles_m, (int)N, (int)K,
-                       (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (int)M, Y, y_stride,
-                       block_sums);
-    return hipGetLastError();
+    // split-K when the tiles cannot fill the chip: partial planes in the scratch, then their sum
+    const SplitPlan sp = plan_split_k((int64_t)tiles_n * tiles_m, (int)(K / kKS), 1, M, N, sc);
+    float* out = sp.splits > 1 ? sc.p : Y;
+    const int64_t out_stride = sp.splits > 1 ? N : y_stride;
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m * sp.splits)), dim3(256), lds, st, tiles_n, tiles_m,
+                       (int)N, (int)K, (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (int)M,
+                       sp.stps, out, out_stride, block_sums);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && sp.splits > 1) e = launch_sum_splits(sc.p, sp.splits, M, N, Y, y_stride, st);
+    return e;
 }
 
 }  // namespace dcq

@@ -116,15 +116,20 @@ template <bool DUMP, bool FULL>
 __global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
                                                               int w_row_bytes, const uint8_t* __restrict__ W,
                                                               const int8_t* __restrict__ xqs,
-                                                              const float* __restrict__ xd, int M,
+                                                              const float* __restrict__ xd, int M, int stps,
                                                               float* __restrict__ Y, int64_t y_stride,
                                                               int32_t* __restrict__ sums) {
     extern __shared__ __align__(16) uint8_t smem[];
     StageQ6* st = reinterpret_cast<StageQ6*>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
+    // ---- split-K: workgroup id = split * tiles + tile. Split s computes stages [s * stps,
+    // (s + 1) * stps) and stores its partial tile in plane s of Y (planes of M rows; with one split
+    // Y is the output itself) ----
+    const int tiles = tiles_n * tiles_m;
+    const int split = (int)blockIdx.x / tiles;
+    const int bid = (int)blockIdx.x - split * tiles;
     // ---- XCD-aware tile order: XCD x (= id % 8) takes n-tile band x, walked m-first ----
-    const int bid = blockIdx.x;
     int tile_m, tile_n;
     if (tiles_n % kXcds == 0) {
         const int band = tiles_n / kXcds;
@@ -137,6 +142,9 @@ __global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(int tiles_n, int t
     }
     const int m0 = tile_m * kBM, n0 = tile_n * kBN;
     const int nstages = K / kKS, nsb = K / 256;
+    // stps is even: a split covers whole superblocks (two stages each)
+    const int s_begin = split * stps, s_end = min(nstages, s_begin + stps);
+    Y += (int64_t)split * M * y_stride;
 
     // ---- staging assignment (fixed for the whole K loop) ----
     // activation rows: instruction i of wave w fills tile rows 8*(4w+i) .. +8, lane l the 16-byte
@@ -222,14 +230,14 @@ __global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(int tiles_n, int t
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f, ai[i][j][v] = 0;
 
-    issue(0, st[0]);
-    commit(0, st[0]);
+    issue(s_begin, st[s_begin & 1]);
+    commit(s_begin, st[s_begin & 1]);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
     __syncthreads();
 
-    for (int stg = 0; stg < nstages; ++stg) {
+    for (int stg = s_begin; stg < s_end; ++stg) {
         const StageQ6& S = st[stg & 1];
-        const bool more = stg + 1 < nstages;
+        const bool more = stg + 1 < s_end;
         if (more) issue(stg + 1, st[(stg + 1) & 1]);  // in flight while this stage computes
         uint2 scw[2];
 #pragma unroll
@@ -337,15 +345,20 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int t
                                                               int w_row_bytes, const uint8_t* __restrict__ W,
                                                               const int8_t* __restrict__ xqs,
                                                               const float* __restrict__ xd,
-                                                              const int16_t* __restrict__ xbs, int M,
+                                                              const int16_t* __restrict__ xbs, int M, int stps,
                                                               float* __restrict__ Y, int64_t y_stride,
                                                               int32_t* __restrict__ sums) {
     extern __shared__ __align__(16) uint8_t smem[];
     StageQ4* st = reinterpret_cast<StageQ4*>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
+    // ---- split-K: workgroup id = split * tiles + tile. Split s computes stages [s * stps,
+    // (s + 1) * stps) and stores its partial tile in plane s of Y (planes of M rows; with one split
+    // Y is the output itself) ----
+    const int tiles = tiles_n * tiles_m;
+    const int split = (int)blockIdx.x / tiles;
+    const int bid = (int)blockIdx.x - split * tiles;
     // ---- XCD-aware tile order: XCD x (= id % 8) takes n-tile band x, walked m-first ----
-    const int bid = blockIdx.x;
     int tile_m, tile_n;
     if (tiles_n % kXcds == 0) {
         const int band = tiles_n / kXcds;
@@ -358,6 +371,9 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int t
     }
     const int m0 = tile_m * kBM, n0 = tile_n * kBN;
     const int nstages = K / kKS, nsb = K / 256;
+    // stps is even: a split covers whole superblocks (two stages each)
+    const int s_begin = split * stps, s_end = min(nstages, s_begin + stps);
+    Y += (int64_t)split * M * y_stride;
 
     // ---- staging assignment (fixed for the whole K loop) ----
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -442,14 +458,14 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int t
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f, ai[i][j][v] = 0;
 
-    issue(0, st[0]);
-    commit(0, st[0]);
+    issue(s_begin, st[s_begin & 1]);
+    commit(s_begin, st[s_begin & 1]);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
     __syncthreads();
 
-    for (int stg = 0; stg < nstages; ++stg) {
+    for (int stg = s_begin; stg < s_end; ++stg) {
         const StageQ4& S = st[stg & 1];
-        const bool more = stg + 1 < nstages;
+        const bool more = stg + 1 < s_end;
         if (more) issue(stg + 1, st[(stg + 1) & 1]);  // in flight while this stage computes
         uint32_t scw[2];
 #pragma unroll
@@ -552,7 +568,8 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int t
 }
 
 hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                               const SplitScratch& sc) {
     if (K % 256 || w_row_bytes % 16 || w_row_bytes > INT32_MAX || act.m_ld % kBM || act.m_ld > INT32_MAX ||
         !act.bs || N > (1 << 30) || M > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
@@ -562,14 +579,21 @@ hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, in
     const bool full = M % kBM == 0 && N % kBN == 0;
     auto fn = block_sums ? (full ? prefill_q4_k_kernel<true, true> : prefill_q4_k_kernel<true, false>)
                          : (full ? prefill_q4_k_kernel<false, true> : prefill_q4_k_kernel<false, false>);
-    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, tiles_n, tiles_m, (int)N, (int)K,
-                       (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (const int16_t*)act.bs,
-                       (int)M, Y, y_stride, block_sums);
-    return hipGetLastError();
+    // split-K when the tiles cannot fill the chip (ranges of whole superblocks: two stages each)
+    const SplitPlan sp = plan_split_k((int64_t)tiles_n * tiles_m, (int)(K / kKS), 2, M, N, sc);
+    float* out = sp.splits > 1 ? sc.p : Y;
+    const int64_t out_stride = sp.splits > 1 ? N : y_stride;
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m * sp.splits)), dim3(256), lds, st, tiles_n, tiles_m,
+                       (int)N, (int)K, (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d,
+                       (const int16_t*)act.bs, (int)M, sp.stps, out, out_stride, block_sums);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && sp.splits > 1) e = launch_sum_splits(sc.p, sp.splits, M, N, Y, y_stride, st);
+    return e;
 }
 
 hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                               const SplitScratch& sc) {
     // K % 512: an even number of superblocks, so the 2-byte overreach of the scale and d loads of
     // an even superblock (dword offset 0) stays inside the next one
     if (K % 512 || w_row_bytes % 4 || w_row_bytes > INT32_MAX || act.m_ld % kBM || act.m_ld > INT32_MAX ||
@@ -582,10 +606,15 @@ hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, in
     const bool full = M % kBM == 0 && N % kBN == 0;
     auto fn = block_sums ? (full ? prefill_q6_k_kernel<true, true> : prefill_q6_k_kernel<true, false>)
                          : (full ? prefill_q6_k_kernel<false, true> : prefill_q6_k_kernel<false, false>);
-    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m)), dim3(256), lds, st, tiles_n, tiles_m, (int)N, (int)K,
-                       (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (int)M, Y, y_stride,
-                       block_sums);
-    return hipGetLastError();
+    const SplitPlan sp = plan_split_k((int64_t)tiles_n * tiles_m, (int)(K / kKS), 2, M, N, sc);
+    float* out = sp.splits > 1 ? sc.p : Y;
+    const int64_t out_stride = sp.splits > 1 ? N : y_stride;
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m * sp.splits)), dim3(256), lds, st, tiles_n, tiles_m,
+                       (int)N, (int)K, (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (int)M,
+                       sp.stps, out, out_stride, block_sums);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && sp.splits > 1) e = launch_sum_splits(sc.p, sp.splits, M, N, Y, y_stride, st);
+    return e;
 }
 
 }  // namespace dcq

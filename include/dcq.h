@@ -102,8 +102,13 @@ int dcq_quantize_rows(int vec_dot_type, const float* X, int64_t M, int64_t K, si
  * Requirements: K % block_size(wtype) == 0; W 16-byte aligned; w_row_bytes >= row_size, even, and
  * a multiple of 16 for Q4_K; X 16-byte aligned with x_stride_bytes % 16 == 0; Y 4-byte aligned
  * with y_stride_bytes % 4 == 0.
- * workspace may be NULL (the library then takes stream-ordered scratch); otherwise it must
- * hold dcq_mul_mat_workspace_size(wtype, M, K) bytes and be 256-byte aligned. */
+ * workspace may be NULL (the library then takes stream-ordered scratch); otherwise it must be
+ * 256-byte aligned and should hold dcq_mul_mat_workspace_size(wtype, M, K) bytes: the quantized
+ * activation, and at M > 8 room for split-K partial sums (M * 128 KB, at most 16 MB) that the
+ * MFMA kernels use when the output tiles cannot occupy every CU (few weight rows, long K). A
+ * workspace that holds only the quantized activation is accepted and runs without split-K
+ * (smaller returns DCQ_ERR_WORKSPACE). The split count depends on the shape, the device's CU
+ * count and that room; for a given one the result bits are fixed. */
 size_t dcq_mul_mat_workspace_size(int wtype, int64_t M, int64_t K);
 int dcq_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X,
                 int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes, void* workspace,
@@ -126,7 +131,9 @@ int64_t dcq_block_sums_per_row(int wtype, int64_t k);
  * dcq_mul_mat_workspace_size(wtype, M, K)); dcq_mul_mat_q then computes Y from W and that
  * workspace. One quantization can feed several weights that share X (ffn gate and up,
  * core/src/inference.cpp:1794-1797). dcq_mul_mat == dcq_quantize_src1 + dcq_mul_mat_q. The
- * workspace must not be written between the two calls. */
+ * workspace must not be written between the two calls. dcq_mul_mat_q writes the split-K room
+ * past the quantized activation (when the workspace has it), so calls that share a workspace
+ * must be ordered on one stream. */
 int dcq_quantize_src1(int wtype, const float* X, int64_t M, int64_t K, size_t x_stride_bytes,
                       void* workspace, size_t workspace_bytes, void* stream);
 int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes,
@@ -137,10 +144,11 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
  * No counterpart in the reference: for callers that cannot allocate device memory (code under
  * stream capture, serving loops or harnesses that forbid hipMalloc). Same arguments, result and
  * kernels as dcq_mul_mat with workspace = NULL, except that the workspace is a static device
- * array of DCQ_NOALLOC_SCRATCH_BYTES (8 MiB) that the library holds on each GPU it runs on until
- * the process ends, instead of stream-ordered scratch. No hipMalloc, hipFree or other
- * allocating call is made. A product whose dcq_mul_mat_workspace_size(wtype, M, K) exceeds the
- * array returns DCQ_ERR_SCRATCH_LIMIT before any device work (M*K up to about 7.4 M elements).
+ * array that the library holds on each GPU it runs on until the process ends, instead of
+ * stream-ordered scratch: DCQ_NOALLOC_SCRATCH_BYTES (8 MiB) for the quantized activation and
+ * 16 MiB of split-K room after it. No hipMalloc, hipFree or other allocating call is made. A
+ * product whose quantized activation exceeds DCQ_NOALLOC_SCRATCH_BYTES returns
+ * DCQ_ERR_SCRATCH_LIMIT before any device work (M*K up to about 7.4 M elements).
  * Every call on one GPU shares that GPU's array: calls on one stream are ordered, but calls that
  * overlap on one GPU (different streams, or host threads without ordering) race on it. */
 #define DCQ_NOALLOC_SCRATCH_BYTES ((size_t)8 << 20)
@@ -157,8 +165,8 @@ int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w
  * in-place residual) or must not overlap Y. R 4-byte aligned, strides multiples of 4; the rest
  * as dcq_mul_mat. At M <= 8 the add is the fused decode kernel's store; otherwise the product
  * goes to Y (or, when R is Y, a workspace temporary) and one add kernel follows. workspace may
- * be NULL; otherwise it must hold dcq_mul_mat_add_workspace_size(wtype, M, N, K) bytes,
- * 256-byte aligned. */
+ * be NULL; otherwise it should hold dcq_mul_mat_add_workspace_size(wtype, M, N, K) bytes,
+ * 256-byte aligned (the split-K room at its end is optional, as in dcq_mul_mat). */
 size_t dcq_mul_mat_add_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
 int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes,
                     const float* X, int64_t M, size_t x_stride_bytes, const float* R,
@@ -171,8 +179,9 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
  * (core/src/inference.cpp:1794-1796) in one call. Both weights share wtype, shape and row
  * stride, and X's quantization. At M <= 8 (Q4_K, Q8_0) one fused kernel streams both weight
  * rows; otherwise X is quantized once, both projections run, then the product.
- * Requirements as dcq_mul_mat's, for both weights. workspace may be NULL; otherwise it must hold
- * dcq_ffn_gate_up_workspace_size(wtype, M, N, K) bytes, 256-byte aligned. */
+ * Requirements as dcq_mul_mat's, for both weights. workspace may be NULL; otherwise it should hold
+ * dcq_ffn_gate_up_workspace_size(wtype, M, N, K) bytes, 256-byte aligned (the split-K room at its
+ * end is optional, as in dcq_mul_mat). */
 size_t dcq_ffn_gate_up_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
 int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_t K, size_t w_row_bytes,
                     const float* X, int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes,

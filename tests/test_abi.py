@@ -55,10 +55,13 @@ def test_type_traits_match_gguf():
 
 
 def test_workspace_size():
-    # planar: int8 [M][K] + fp32 scales [K/bs][roundup(M, 128)] (+ int16 bsums [M][K/16] for Q8_K)
+    # planar: int8 [M][K] + fp32 scales [K/bs][roundup(M, 128)] (+ int16 bsums [M][K/16] for Q8_K),
+    # then at M > 8 the split-K room, min(M, 128) * 128 KB
     assert dc.mul_mat_workspace_size(8, 1, 1024) == 1024 + 32 * 128 * 4
-    assert dc.mul_mat_workspace_size(12, 64, 2048) == 64 * 2048 + 8 * 128 * 4 + 64 * 128 * 2
-    assert dc.mul_mat_workspace_size(8, 130, 1024) == 130 * 1024 + 32 * 256 * 4
+    assert dc.mul_mat_workspace_size(8, 8, 1024) == 8 * 1024 + 32 * 128 * 4
+    assert dc.mul_mat_workspace_size(8, 32, 1024) == 32 * 1024 + 32 * 128 * 4 + 32 * 131072
+    assert dc.mul_mat_workspace_size(12, 64, 2048) == 64 * 2048 + 8 * 128 * 4 + 64 * 128 * 2 + 64 * 131072
+    assert dc.mul_mat_workspace_size(8, 130, 1024) == 130 * 1024 + 32 * 256 * 4 + 128 * 131072
     assert dc.mul_mat_workspace_size(12, 1, 100) == 0
 
 
@@ -103,8 +106,9 @@ def test_noalloc_validation_and_limit():
     assert dc.mul_mat_workspace_size(8, big_m, 1024) > dc.NOALLOC_SCRATCH_BYTES
     assert na(M=big_m) == SCRATCH_LIMIT
     assert "scratch" in dc._lib.status_string(SCRATCH_LIMIT)
-    # config 5 (M = 2048, K = 2048, Q8_0) fits
-    assert dc.mul_mat_workspace_size(8, 2048, 2048) <= dc.NOALLOC_SCRATCH_BYTES
+    # config 5 (M = 2048, K = 2048, Q8_0): its quantized activation fits (int8 rows + fp32 scales;
+    # the workspace size adds the optional split-K room)
+    assert 2048 * 2048 + 64 * 2048 * 4 <= dc.NOALLOC_SCRATCH_BYTES
     import torch
     if not torch.cuda.is_available():
         assert na(M=2048, K=2048) == NO_DEVICE

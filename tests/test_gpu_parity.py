@@ -613,3 +613,54 @@ def test_kquant_prefill_full_shape(O, dev, wt):
     want = O.block_sums_matrix(wt, K, wq[cols], O.quantize_rows(Q8_K, x[corner]))
     assert np.array_equal(got, want)
     assert np.array_equal(to_host(y2), y)  # the dump does not change the outputs
+
+
+# Split-K: products whose 128 x 128 output tiles cannot occupy every CU (few weight rows, long K:
+# ffn_down-like 2048 x 8192 at batch sizes) cut K into ranges whose partial tiles go to the
+# workspace's split-K room and are summed in range order. Each case against the oracle on every
+# output, with the full workspace (split) and with one that holds only the quantized activation
+# (no split); repeated calls give the same bits.
+SPLIT_K = [(Q8_0, 64, 2048, 8192), (Q6_K, 64, 2048, 8192), (Q4_K, 256, 2048, 8192), (Q8_0, 40, 1000, 4096),
+           (Q6_K, 200, 384, 2048), (Q4_K, 130, 256, 4096), (Q8_0, 16, 2048, 8192), (Q6_K, 9, 2048, 8192),
+           (Q8_0, 256, 8192, 2048)]
+
+
+def _split_tail(M):
+    return min(M, 128) * 128 * 1024 if M > 8 else 0
+
+
+@pytest.mark.parametrize("wt,M,N,K", SPLIT_K)
+def test_split_k_parity(O, dev, wt, M, N, K):
+    import torch
+    rng = np.random.default_rng(7000 + M + N)
+    wq = _random_blocks(wt, N, K, rng)
+    x = synth.normal(M * K, 7100 + N).reshape(M, K)
+    wd, xd = to_dev(wq, dev), to_dev(x, dev)
+    full = dc.mul_mat_workspace_size(wt, M, K)
+    print(f"split-K type {wt} M={M} N={N} K={K}", flush=True)
+    y_ref, l1 = O.mul_mat(wt, wq, x)
+    outs = []
+    for nbytes in (full, full - _split_tail(M), full):
+        ws = torch.full((nbytes,), 0xAB, dtype=torch.uint8, device=dev)
+        y = to_host(dc.mul_mat(wt, wd, N, K, xd, workspace=ws))
+        O.assert_close(y, y_ref, l1, RTOL, what=f"split-K type {wt} M={M} N={N} K={K} ws={nbytes}")
+        outs.append(y)
+    assert np.array_equal(outs[0].view(np.uint32), outs[2].view(np.uint32))
+
+
+@pytest.mark.parametrize("wt,M,N,K", [(Q6_K, 64, 256, 4096), (Q8_0, 48, 384, 2048), (Q4_K, 160, 256, 2048)])
+def test_split_k_block_sums(O, dev, wt, M, N, K):
+    """The per-block int32 sums dumped by split-K ranges: every block written once, bit-exact."""
+    import torch
+    rng = np.random.default_rng(7300 + wt)
+    wq = _random_blocks(wt, N, K, rng)
+    x = synth.normal(M * K, 7400 + wt).reshape(M, K)
+    per = dc.block_sums_per_row(wt, K)
+    sums = torch.zeros((M, N, per), dtype=torch.int32, device=dev)
+    ws = torch.empty(dc.mul_mat_workspace_size(wt, M, K), dtype=torch.uint8, device=dev)
+    y = to_host(dc.mul_mat_ex(wt, to_dev(wq, dev), N, K, to_dev(x, dev), path=dc.PATH_AUTO, block_sums=sums,
+                              workspace=ws))
+    want = O.block_sums_matrix(wt, K, wq, O.quantize_rows(O.vec_dot_type(wt), x))
+    assert np.array_equal(to_host(sums), want)
+    y_ref, l1 = O.mul_mat(wt, wq, x)
+    O.assert_close(y, y_ref, l1, RTOL, what=f"split-K sums type {wt}")
