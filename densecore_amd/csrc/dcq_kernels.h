@@ -117,7 +117,9 @@ struct SplitScratch {
 struct SplitPlan {
     int splits, stps;
 };
-SplitPlan plan_split_k(int64_t tiles, int nstages, int align, int64_t M, int64_t N, const SplitScratch& sc);
+// us_per_stage: the estimated time of one stage of one workgroup (the cost model's unit)
+SplitPlan plan_split_k(int64_t tiles, int nstages, int align, int64_t M, int64_t N, const SplitScratch& sc,
+                       double us_per_stage = 2.0);
 // Y[m][n] = sum over s (in order) of P[s][m][n], P planes of M x N floats.
 hipError_t launch_sum_splits(const float* P, int splits, int64_t M, int64_t N, float* Y, int64_t y_stride,
                              hipStream_t st);
@@ -142,6 +144,13 @@ hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, in
 // rows, K split over the waves; hipErrorNotSupported when the shape is outside it.
 hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                             int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+
+// Q8_0 batched decode (4 < M <= 64): 8-wave workgroups per 32 weight rows x 32 or 64 activation
+// rows, K split over the waves (and over workgroups when the rows are few and sc has room);
+// hipErrorNotSupported when the shape is outside it.
+hipError_t launch_batch_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                             int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                             const SplitScratch& sc);
 
 // Int8-MFMA tiles for any M; sc: room for split-K partial tiles (optional).
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,

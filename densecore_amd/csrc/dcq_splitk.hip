@@ -44,10 +44,11 @@ __global__ void __launch_bounds__(256) sum_splits_kernel(const float* __restrict
 // Splits while the tiles cannot give every CU a workgroup: at most one workgroup per CU, at least
 // two stages per range (a range's first stage is not overlapped with loads) and no more planes
 // than the scratch holds. Among those counts the one with the least estimated time: a lone
-// workgroup per CU takes about 2 us per stage (measured 1.9 - 2.6 us: 2048 x 8192 and 8192 x 2048
-// at M = 64 - 256), and splitting adds about 2 us for the sum launch plus the partial planes
+// workgroup per CU takes about us_per_stage per stage (2 us for the 128 x 128-tile kernels:
+// measured 1.9 - 2.6 us on 2048 x 8192 and 8192 x 2048 at M = 64 - 256), and splitting adds about 2 us for the sum launch plus the partial planes
 // written and read back at about 5 TB/s. DCQ_SPLIT_K forces the count (tuning).
-SplitPlan plan_split_k(int64_t tiles, int nstages, int align, int64_t M, int64_t N, const SplitScratch& sc) {
+SplitPlan plan_split_k(int64_t tiles, int nstages, int align, int64_t M, int64_t N, const SplitScratch& sc,
+                       double us_per_stage) {
     const SplitPlan none{1, nstages};
     const int64_t plane_bytes = M * N * (int64_t)sizeof(float);
     const int min_stps = align > 2 ? align : 2;
@@ -69,11 +70,11 @@ SplitPlan plan_split_k(int64_t tiles, int nstages, int align, int64_t M, int64_t
     if (tiles >= cus) return none;
     if (smax > cus / tiles) smax = cus / tiles;
     SplitPlan best = none;
-    double best_us = 2.0 * nstages;  // no split
+    double best_us = us_per_stage * nstages;  // no split
     for (int64_t s = 2; s <= smax; ++s) {
         const SplitPlan p = plan_of(s);
         if (p.splits < 2) continue;
-        const double us = 2.0 * p.stps + 2.0 + 2.0 * (double)p.splits * (double)plane_bytes / 5.0e6;
+        const double us = us_per_stage * p.stps + 2.0 + 2.0 * (double)p.splits * (double)plane_bytes / 5.0e6;
         if (us < best_us) {
             best_us = us;
             best = p;

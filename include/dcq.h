@@ -104,7 +104,7 @@ int dcq_quantize_rows(int vec_dot_type, const float* X, int64_t M, int64_t K, si
  * with y_stride_bytes % 4 == 0.
  * workspace may be NULL (the library then takes stream-ordered scratch); otherwise it must be
  * 256-byte aligned and should hold dcq_mul_mat_workspace_size(wtype, M, K) bytes: the quantized
- * activation, and at M > 8 room for split-K partial sums (M * 128 KB, at most 16 MB) that the
+ * activation, and at M > 4 room for split-K partial sums (M * 128 KB, at most 16 MB) that the
  * MFMA kernels use when the output tiles cannot occupy every CU (few weight rows, long K). A
  * workspace that holds only the quantized activation is accepted and runs without split-K
  * (smaller returns DCQ_ERR_WORKSPACE). The split count depends on the shape, the device's CU

@@ -56,9 +56,10 @@ def test_type_traits_match_gguf():
 
 def test_workspace_size():
     # planar: int8 [M][K] + fp32 scales [K/bs][roundup(M, 128)] (+ int16 bsums [M][K/16] for Q8_K),
-    # then at M > 8 the split-K room, min(M, 128) * 128 KB
+    # then at M > 4 the split-K room, min(M, 128) * 128 KB
     assert dc.mul_mat_workspace_size(8, 1, 1024) == 1024 + 32 * 128 * 4
-    assert dc.mul_mat_workspace_size(8, 8, 1024) == 8 * 1024 + 32 * 128 * 4
+    assert dc.mul_mat_workspace_size(8, 4, 1024) == 4 * 1024 + 32 * 128 * 4
+    assert dc.mul_mat_workspace_size(8, 8, 1024) == 8 * 1024 + 32 * 128 * 4 + 8 * 131072
     assert dc.mul_mat_workspace_size(8, 32, 1024) == 32 * 1024 + 32 * 128 * 4 + 32 * 131072
     assert dc.mul_mat_workspace_size(12, 64, 2048) == 64 * 2048 + 8 * 128 * 4 + 64 * 128 * 2 + 64 * 131072
     assert dc.mul_mat_workspace_size(8, 130, 1024) == 130 * 1024 + 32 * 256 * 4 + 128 * 131072

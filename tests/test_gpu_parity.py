@@ -626,7 +626,7 @@ SPLIT_K = [(Q8_0, 64, 2048, 8192), (Q6_K, 64, 2048, 8192), (Q4_K, 256, 2048, 819
 
 
 def _split_tail(M):
-    return min(M, 128) * 128 * 1024 if M > 8 else 0
+    return min(M, 128) * 128 * 1024 if M > 4 else 0
 
 
 @pytest.mark.parametrize("wt,M,N,K", SPLIT_K)
@@ -664,3 +664,33 @@ def test_split_k_block_sums(O, dev, wt, M, N, K):
     assert np.array_equal(to_host(sums), want)
     y_ref, l1 = O.mul_mat(wt, wq, x)
     O.assert_close(y, y_ref, l1, RTOL, what=f"split-K sums type {wt}")
+
+
+# Batched decode past four rows: Q8_0 on its batch kernel (one or two 32-row m-tiles, K split over
+# the waves and, with few weight rows, over workgroups), Q4_K at M = 5..8 on its batch kernel.
+# Every output against the oracle, and the per-block int32 sums bit for bit.
+BATCH_SMALL_M = [(Q8_0, 5, 100, 1024), (Q8_0, 8, 8192, 2048), (Q8_0, 16, 2048, 8192), (Q8_0, 32, 96, 256),
+                 (Q8_0, 33, 130, 2048), (Q8_0, 64, 2048, 8192), (Q8_0, 64, 8192, 2048), (Q8_0, 7, 33, 4096),
+                 (Q4_K, 6, 300, 2048), (Q4_K, 8, 2048, 8192)]
+
+
+@pytest.mark.parametrize("wt,M,N,K", BATCH_SMALL_M)
+def test_batch_small_m(O, dev, wt, M, N, K):
+    import torch
+    rng = np.random.default_rng(7500 + M + N)
+    wq = _random_blocks(wt, N, K, rng)
+    x = synth.normal(M * K, 7600 + K).reshape(M, K)
+    x[0, :32] = 0.0  # an all-zero block (scale 0)
+    wd, xd = to_dev(wq, dev), to_dev(x, dev)
+    print(f"batch small M type {wt} M={M} N={N} K={K}", flush=True)
+    ws = torch.full((dc.mul_mat_workspace_size(wt, M, K),), 0xAB, dtype=torch.uint8, device=dev)
+    y = to_host(dc.mul_mat(wt, wd, N, K, xd, workspace=ws))
+    y_ref, l1 = O.mul_mat(wt, wq, x)
+    O.assert_close(y, y_ref, l1, RTOL, what=f"batch type {wt} M={M} N={N} K={K}")
+    if N * K <= 2048 * 8192:
+        per = dc.block_sums_per_row(wt, K)
+        sums = torch.zeros((M, N, per), dtype=torch.int32, device=dev)
+        y2 = to_host(dc.mul_mat_ex(wt, wd, N, K, xd, path=dc.PATH_AUTO, block_sums=sums, workspace=ws))
+        want = O.block_sums_matrix(wt, K, wq, O.quantize_rows(O.vec_dot_type(wt), x))
+        assert np.array_equal(to_host(sums), want)
+        O.assert_close(y2, y_ref, l1, RTOL, what=f"batch type {wt} with sums")
