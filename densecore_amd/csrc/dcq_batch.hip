@@ -22,7 +22,9 @@
 //   - per superblock: acc += dA * (d * sum_j sc_j I_j - dmin * sum_j m_j S_j)
 //     (vec_dot_q4_K_q8_K's per-superblock form).
 // The 8 partial tiles are summed in wave order through LDS at the end (deterministic), each
-// wave summing an eighth of the tile.
+// wave summing an eighth of the tile. With few weight rows the superblocks are also split over
+// workgroups (grid z): each stores its partial tile in a plane of the split-K scratch and
+// launch_sum_splits adds them in order.
 #include "dcq_common.h"
 #include "dcq_kernels.h"
 
@@ -65,13 +67,17 @@ template <bool DUMP>
 __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                                    int N, int nsb, const int8_t* __restrict__ xqs,
                                                                    const float* __restrict__ xd, int64_t m_ld, int M,
-                                                                   float* __restrict__ Y, int64_t y_stride,
+                                                                   int cpz, float* __restrict__ Y, int64_t y_stride,
                                                                    int32_t* __restrict__ sums) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = nsb * 256;
     const int n0 = blockIdx.x * kNT, m0 = blockIdx.y * kMT;
+    // workgroup z takes superblocks [z * cpz, (z + 1) * cpz) and stores plane z of Y (planes of M
+    // rows; with one plane Y is the output itself)
+    const int s_begin = blockIdx.z * cpz, s_end = min(nsb, s_begin + cpz);
+    Y += (int64_t)blockIdx.z * M * y_stride;
     const int col = lane & 31, hl = lane >> 5;
     uint8_t* region = smem + wave * kRegion;
     int8_t* a_lds = reinterpret_cast<int8_t*>(region);
@@ -97,7 +103,7 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
 
-    for (int s = wave; s < nsb; s += kWaves) {
+    for (int s = s_begin + wave; s < s_end; s += kWaves) {
         // ---- loads: activation + scales into this wave's LDS region, weights into registers ----
 #pragma unroll
         for (int i = 0; i < 16; ++i) dma16(a_src[i] + 256 * s, a_lds + 1024 * i);
@@ -217,18 +223,27 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
 }
 
 hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st) {
+                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                            const SplitScratch& sc) {
     if (w_row_bytes % 16 || N > (1 << 30) || M > (1 << 30) || K > (1 << 30)) return hipErrorNotSupported;
     // the per-superblock scale DMA reads 64 scales at [s][m0 .. m0 + 63]: m_ld must cover the
     // last m-tile (it is M rounded up to 128)
     if (act.m_ld < ((M + kMT - 1) / kMT) * kMT) return hipErrorNotSupported;
     const int nsb = (int)(K / 256);
-    dim3 grid((unsigned)((N + kNT - 1) / kNT), (unsigned)((M + kMT - 1) / kMT));
+    const int64_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
+    // with few weight rows the superblocks are also split over workgroups (at least one per wave;
+    // about 0.25 us per superblock of a workgroup)
+    const SplitPlan sp = plan_split_k(tiles, nsb, kWaves, M, N, sc, 0.25);
+    float* out = sp.splits > 1 ? sc.p : Y;
+    const int64_t out_stride = sp.splits > 1 ? N : y_stride;
+    dim3 grid((unsigned)((N + kNT - 1) / kNT), (unsigned)((M + kMT - 1) / kMT), (unsigned)sp.splits);
     const size_t lds = (size_t)kWaves * kRegion;
     auto fn = block_sums ? batch_q4k_kernel<true> : batch_q4k_kernel<false>;
     hipLaunchKernelGGL(fn, grid, dim3(64 * kWaves), lds, st, (const uint8_t*)W, w_row_bytes, (int)N, nsb, act.qs,
-                       act.d, act.m_ld, (int)M, Y, y_stride, block_sums);
-    return hipGetLastError();
+                       act.d, act.m_ld, (int)M, sp.stps, out, out_stride, block_sums);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess && sp.splits > 1) e = launch_sum_splits(sc.p, sp.splits, M, N, Y, y_stride, st);
+    return e;
 }
 
 }  // namespace dcq

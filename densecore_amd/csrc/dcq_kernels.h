@@ -141,9 +141,11 @@ hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, in
                                const SplitScratch& sc = SplitScratch());
 
 // Q4_K batched decode (M <= 128): 8-wave workgroups per 32 weight rows x 64 activation
-// rows, K split over the waves; hipErrorNotSupported when the shape is outside it.
+// rows, K split over the waves (and over workgroups when the rows are few and sc has room);
+// hipErrorNotSupported when the shape is outside it.
 hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st);
+                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                            const SplitScratch& sc = SplitScratch());
 
 // Q8_0 batched decode (4 < M <= 64): 8-wave workgroups per 32 weight rows x 32 or 64 activation
 // rows, K split over the waves (and over workgroups when the rows are few and sc has room);

@@ -596,7 +596,7 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
         if (e != hipErrorNotSupported) return e;
     }
     if (wtype == kTypeQ4_K && M <= 128) {
-        const hipError_t e = launch_batch_q4k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st);
+        const hipError_t e = launch_batch_q4k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
     MmqShape s;

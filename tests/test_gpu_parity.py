@@ -671,7 +671,7 @@ def test_split_k_block_sums(O, dev, wt, M, N, K):
 # Every output against the oracle, and the per-block int32 sums bit for bit.
 BATCH_SMALL_M = [(Q8_0, 5, 100, 1024), (Q8_0, 8, 8192, 2048), (Q8_0, 16, 2048, 8192), (Q8_0, 32, 96, 256),
                  (Q8_0, 33, 130, 2048), (Q8_0, 64, 2048, 8192), (Q8_0, 64, 8192, 2048), (Q8_0, 7, 33, 4096),
-                 (Q4_K, 6, 300, 2048), (Q4_K, 8, 2048, 8192)]
+                 (Q4_K, 6, 300, 2048), (Q4_K, 8, 2048, 8192), (Q4_K, 64, 2048, 8192), (Q4_K, 100, 1000, 4096)]
 
 
 @pytest.mark.parametrize("wt,M,N,K", BATCH_SMALL_M)
