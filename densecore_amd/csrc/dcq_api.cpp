@@ -38,9 +38,11 @@ size_t planar_bytes(int vdt, int64_t M, int64_t K, PlanarBuffers* pb, void* base
 size_t split_tail_bytes(int64_t M) { return M > 4 ? (size_t)(M < 128 ? M : 128) * 128 * 1024 : 0; }
 
 // Activation rows up to which the decode (GEMV) kernels serve a product. Past four rows their
-// per-row VALU work falls behind the batch MFMA kernels for Q8_0 and Q4_K (8192 x 2048 at M = 8:
-// Q8_0 23.3 -> batch, Q4_K 10.8 -> 9.6 us); Q6_K has no batch kernel and keeps them to M = 8.
-int gemv_rows(int wtype) { return wtype == kTypeQ6_K ? 8 : 4; }
+// per-row VALU work falls behind the batch MFMA kernels (8192 x 2048 at M = 8: Q8_0 23.3 ->
+// 11.5 us, Q4_K 10.8 -> 9.4 us, Q6_K 17.7 -> 9.5 us). The Q6_K batch kernel already wins at three
+// rows on wide matrices (8192 x 2048: 12.1 -> 9.4 us) but not on narrow ones (2048 x 8192: 10.0
+// against 18.7 us unsplit).
+int gemv_rows(int wtype, int64_t N) { return wtype == kTypeQ6_K && N >= 4096 ? 2 : 4; }
 
 // the bytes of a workspace past its first `used` ones, as split-K scratch (none if too small)
 SplitScratch tail_of(void* ws, size_t ws_bytes, size_t used) {
@@ -244,7 +246,7 @@ int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_
     rc = check_device();
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
-    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype));
+    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N));
     if (use_gemv) {
         // decode: the activation quantization runs inside the GEMV kernel where it can
         hipError_t e = launch_decode_fused(wtype, W, (int64_t)w_row_bytes, N, K, X, (int64_t)(x_stride_bytes / 4), M,
@@ -331,7 +333,7 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4), r_stride = (int64_t)(r_stride_bytes / 4);
-    if (M <= gemv_rows(wtype)) {
+    if (M <= gemv_rows(wtype, N)) {
         // decode: the add is the fused kernel's store epilogue
         hipError_t e = launch_decode_fused(wtype, W, (int64_t)w_row_bytes, N, K, X, (int64_t)(x_stride_bytes / 4), M,
                                            Y, y_stride, nullptr, st, R, r_stride);
@@ -351,14 +353,14 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
     const SplitScratch sc = tail_of(ws, workspace ? workspace_bytes : need, act_bytes + (size_t)M * N * 4);
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
     bool added = false;
-    if (e == hipSuccess && M <= gemv_rows(wtype)) {
+    if (e == hipSuccess && M <= gemv_rows(wtype, N)) {
         // the LDS-staged decode kernels add R in their store
         e = launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st, R, r_stride);
         added = e != hipErrorNotSupported;
         if (!added) e = hipSuccess;
     }
     if (e == hipSuccess && !added) {
-        e = M <= gemv_rows(wtype)
+        e = M <= gemv_rows(wtype, N)
                 ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, T, t_stride, nullptr, N, st)
                 : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, T, t_stride, nullptr, st, sc);
         if (e == hipSuccess) e = launch_add_rows(Y, y_stride, T, t_stride, R, r_stride, M, N, st);
@@ -393,7 +395,7 @@ int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
-    if (M <= gemv_rows(wtype)) {
+    if (M <= gemv_rows(wtype, N)) {
         // one launch: both weight rows per lane group, the activation quantized in the workgroup
         hipError_t e = launch_decode_fused_glu(wtype, Wg, Wu, (int64_t)w_row_bytes, N, K, X,
                                                (int64_t)(x_stride_bytes / 4), M, Y, y_stride, st);
@@ -410,7 +412,7 @@ int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_
     // split-K partial sums after U (the two products run one after the other on the stream)
     const SplitScratch sc = tail_of(ws, workspace ? workspace_bytes : need, act_bytes + (size_t)M * N * 4);
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
-    const bool use_gemv = M <= gemv_rows(wtype);
+    const bool use_gemv = M <= gemv_rows(wtype, N);
     if (e == hipSuccess)
         e = use_gemv ? launch_gemv(wtype, Wg, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
                      : launch_mmq(wtype, Wg, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st, sc);
@@ -459,7 +461,7 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
     planar_bytes(vdt, M, K, &pb, (void*)workspace);
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
-    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype));
+    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N));
     hipError_t e = use_gemv ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
                             : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st,
                                          tail_of((void*)workspace, workspace_bytes,

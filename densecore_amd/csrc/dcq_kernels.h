@@ -154,6 +154,12 @@ hipError_t launch_batch_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int6
                              int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
                              const SplitScratch& sc);
 
+// Q6_K batched decode (4 < M <= 64, K % 512 == 0): the same launch shape, one int8 MFMA per
+// 16-element scale group; hipErrorNotSupported when the shape is outside it.
+hipError_t launch_batch_q6k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
+                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
+                            const SplitScratch& sc);
+
 // Int8-MFMA tiles for any M; sc: room for split-K partial tiles (optional).
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                       int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,

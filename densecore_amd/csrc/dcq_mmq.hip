@@ -576,6 +576,10 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
         const hipError_t e = launch_batch_q8_0(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
+    if (wtype == kTypeQ6_K && M <= 64) {
+        const hipError_t e = launch_batch_q6k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
+        if (e != hipErrorNotSupported) return e;
+    }
     // Q8_0 / Q6_K at 8 < M <= 32 also take the 128 x 128-tile kernels when the MMQ kernel's 32 x 32
     // tiles would leave most CUs idle and the workspace has room to split K (2048 x 8192 at
     // M = 16: 70 -> 25 us)

@@ -666,12 +666,15 @@ def test_split_k_block_sums(O, dev, wt, M, N, K):
     O.assert_close(y, y_ref, l1, RTOL, what=f"split-K sums type {wt}")
 
 
-# Batched decode past four rows: Q8_0 on its batch kernel (one or two 32-row m-tiles, K split over
-# the waves and, with few weight rows, over workgroups), Q4_K at M = 5..8 on its batch kernel.
+# Batched decode past four rows (Q6_K on matrices of 4096+ rows: past two): Q8_0 and Q6_K on their
+# batch kernels (one or two 32-row m-tiles, K split over the waves and, with few weight rows, over
+# workgroups), Q4_K at M = 5..8 on its own.
 # Every output against the oracle, and the per-block int32 sums bit for bit.
 BATCH_SMALL_M = [(Q8_0, 5, 100, 1024), (Q8_0, 8, 8192, 2048), (Q8_0, 16, 2048, 8192), (Q8_0, 32, 96, 256),
                  (Q8_0, 33, 130, 2048), (Q8_0, 64, 2048, 8192), (Q8_0, 64, 8192, 2048), (Q8_0, 7, 33, 4096),
-                 (Q4_K, 6, 300, 2048), (Q4_K, 8, 2048, 8192), (Q4_K, 64, 2048, 8192), (Q4_K, 100, 1000, 4096)]
+                 (Q4_K, 6, 300, 2048), (Q4_K, 8, 2048, 8192), (Q4_K, 64, 2048, 8192), (Q4_K, 100, 1000, 4096),
+                 (Q6_K, 5, 100, 1024), (Q6_K, 8, 8192, 2048), (Q6_K, 16, 2048, 8192), (Q6_K, 33, 130, 2048),
+                 (Q6_K, 64, 2048, 8192), (Q6_K, 20, 77, 512), (Q6_K, 3, 4096, 1024), (Q6_K, 4, 8192, 2048)]
 
 
 @pytest.mark.parametrize("wt,M,N,K", BATCH_SMALL_M)
