@@ -41,8 +41,12 @@ size_t split_tail_bytes(int64_t M) { return M > 4 ? (size_t)(M < 128 ? M : 128) 
 // per-row VALU work falls behind the batch MFMA kernels (8192 x 2048 at M = 8: Q8_0 23.3 ->
 // 11.5 us, Q4_K 10.8 -> 9.4 us, Q6_K 17.7 -> 9.5 us). The Q6_K batch kernel already wins at three
 // rows on wide matrices (8192 x 2048: 12.1 -> 9.4 us) but not on narrow ones (2048 x 8192: 10.0
-// against 18.7 us unsplit).
-int gemv_rows(int wtype, int64_t N) { return wtype == kTypeQ6_K && N >= 4096 ? 2 : 4; }
+// against 18.7 us unsplit); tall Q6_K matrices (LM heads, 32768+ rows) keep their MFMA decode
+// kernel up to eight rows (151936 x 2560 at M = 4: 68 us against 120 us on the batch kernel).
+int gemv_rows(int wtype, int64_t N) {
+    if (wtype != kTypeQ6_K) return 4;
+    return N >= 32768 ? 8 : N >= 4096 ? 2 : 4;
+}
 
 // the bytes of a workspace past its first `used` ones, as split-K scratch (none if too small)
 SplitScratch tail_of(void* ws, size_t ws_bytes, size_t used) {

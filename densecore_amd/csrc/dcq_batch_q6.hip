@@ -52,25 +52,20 @@ __device__ __forceinline__ void dma16(const void* g, const void* lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
 
-// One v_mfma_i32_32x32x16_i8 into a zero accumulator. The operands are kept live past the
-// instruction (an empty use that also reads the result): with them dead, the register allocator
-// gave the result registers overlapping both operands (v[0:15] <- v[2:3], v[0:1]), and that form
-// returned wrong sums on gfx950 while the same code with distinct registers was exact.
 __device__ __forceinline__ v16i mfma32k16(long a, long b) {
     v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    const v16i d = __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, z, 0, 0, 0);
-    asm volatile("" ::"v"(a), "v"(b), "v"(d[0]));
-    return d;
+    return __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, z, 0, 0, 0);
 }
 
 // Signed q - 32 bytes of four 6-bit quants: low nibbles from `ql` (bits 0-3 of each byte), the two
 // high bits from `qh2` (bits 0-1 of each byte). (qh2 - 2) << 4 is the high nibble of q - 32: byte
-// qh2 of the table 0x1000F0E0.
+// qh2 of the table 0x1000F0E0. Plain code, not an inline-asm v_bfi_b32: the result is an MFMA
+// operand, and the compiler inserts the wait states between a VALU write and an MFMA read of it
+// only for instructions it can see (with the asm form, an MFMA read its B operand three
+// instructions after the v_bfi wrote it and summed stale bytes).
 __device__ __forceinline__ uint32_t q6_minus32(uint32_t ql, uint32_t qh2) {
     const uint32_t hi = __builtin_amdgcn_perm(0u, 0x1000F0E0u, qh2);
-    uint32_t r;
-    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(0x0F0F0F0Fu), "v"(ql), "v"(hi));
-    return r;
+    return (ql & 0x0F0F0F0Fu) | (hi & 0xF0F0F0F0u);
 }
 
 // LDS byte offset of logical 16-byte slot `slot` (0..15) of activation row `row` (256 B rows)

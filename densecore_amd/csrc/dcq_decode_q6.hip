@@ -419,8 +419,10 @@ __device__ __forceinline__ v16i_t mfma_32x32x16(long a, long b) {
 
 // Signed q - 32 bytes of four 6-bit quants: ql nibbles in bits 0-3 of each byte, the two high
 // bits in bits 0-1 of each byte of qh2 ((qh2 - 2) << 4 is byte qh2 of the table 0x1000F0E0).
+// Plain code, not the inline-asm bfi above: the result is an MFMA operand, and the compiler places
+// the wait states between a VALU write and an MFMA read of it only for instructions it can see.
 __device__ __forceinline__ uint32_t q6_signed(uint32_t ql, uint32_t qh2) {
-    return bfi(0x0F0F0F0Fu, ql, __builtin_amdgcn_perm(0u, 0x1000F0E0u, qh2));
+    return (ql & 0x0F0F0F0Fu) | (__builtin_amdgcn_perm(0u, 0x1000F0E0u, qh2) & 0xF0F0F0F0u);
 }
 
 // 8 bytes at p + SH (p 8-byte aligned, SH 0 or 2): one ds_read_b64, or three dwords realigned
