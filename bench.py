@@ -564,6 +564,37 @@ def bench_lm_head(args, dev, wtype, K, M, N=151936):
     return out
 
 
+# Batched decode (ggml MUL_MAT at small M > 1, core/src/inference.cpp:1049-1063): the batch kernels
+# (and split-K) at ffn shapes of Llama 3.2 1B, 2048 x 8192 (ffn_down, few weight rows) and 8192 x 2048
+BATCHED_SHAPES = [(dc_type, M, N, K) for dc_type in ("Q8_0", "Q4_K", "Q6_K")
+                  for (M, N, K) in ((16, 2048, 8192), (64, 2048, 8192), (16, 8192, 2048))]
+
+
+def bench_batched_decode(args, dev, tname, M, N, K):
+    """One dcq_mul_mat step (activation quantization + product, + the split-K sum where used) at a
+    batched-decode shape, W rotated like the configs; weight GB/s of the step."""
+    import torch
+    import densecore_amd as dc
+    wtype = {"Q8_0": dc.TYPE_Q8_0, "Q4_K": dc.TYPE_Q4_K, "Q6_K": dc.TYPE_Q6_K}[tname]
+    rb = dc.row_size(wtype, K)
+    wbytes = N * rb
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    big = random_weights(dev, wtype, N, K, copies, 31)
+    g = torch.Generator(device=dev)
+    g.manual_seed(32)
+    x = torch.randn((M, K), device=dev, generator=g)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ws = torch.empty(dc.mul_mat_workspace_size(wtype, M, K), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        dc.mul_mat(wtype, big[i % copies], N, K, x, y=y, workspace=ws, stream=torch.cuda.current_stream().cuda_stream)
+
+    step_ms, kern, _ = time_graph(step, max(10, args.steps // 4), args.warmup, args.replays)
+    return {"shape": f"{tname} M={M} N={N} K={K}", "step_us": step_ms * 1e3, "kernels": kern,
+            "weight_GBps": wbytes / (step_ms * 1e-3) / 1e9, "TOPS": 2.0 * M * N * K / (step_ms * 1e-3) / 1e12}
+
+
 def bench_kquant_prefill(args, dev, wtype, M=2048, N=8192, K=2048):
     """A K-quant prompt projection (ggml MUL_MAT at M > 1, core/src/inference.cpp:1049-1063,
     1794-1797) at config 5's shape with Q4_K / Q6_K weights (random valid quants, W rotated like
@@ -1000,6 +1031,10 @@ def main():
             print(f"# {e['shape']}: kernel {e['kernel_us']:.1f} us ({e['TOPS_kernel']:.0f} TOPS, "
                   f"{100 * e['frac_of_int8_peak']:.1f} % of int8 peak), step {e['step_us']:.1f} us "
                   f"({e['kernels']} kernels)", file=sys.stderr, flush=True)
+        for tname, M, N, K in BATCHED_SHAPES:
+            e = extras[f"batched_{tname.lower()}_m{M}_{N}x{K}"] = bench_batched_decode(args, dev, tname, M, N, K)
+            print(f"# batched decode {e['shape']}: {e['step_us']:.2f} us ({e['kernels']} kernels), "
+                  f"{e['weight_GBps']:.0f} GB/s of weights, {e['TOPS']:.1f} TOPS", file=sys.stderr, flush=True)
         extras["gguf_load"] = bench_gguf_load(args, dev)
         print(f"# GGUF ingest: {extras['gguf_load']['GBps']:.1f} GB/s host-to-HBM over "
               f"{extras['gguf_load']['bytes'] >> 20} MiB", file=sys.stderr, flush=True)
