@@ -107,6 +107,10 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
         const int f = 256 * k + 4 * lane;
         d_src[k] = xd + (int64_t)(f / G::kMT) * m_ld + m0 + f % G::kMT;
     }
+    // 4-row activation groups that hold rows < M: only those are loaded. The tile's other LDS rows
+    // keep stale bytes, which only reach outputs of rows >= M (never stored); at M = 8 this loads 2
+    // of the tile's groups instead of 8.
+    const int a_groups = (min(M - m0, G::kMT) + 3) / 4;
     // weight row of this lane (MFMA B operand: column n = lane % 32)
     const uint8_t* wrow = W + (int64_t)min(n0 + col, N - 1) * w_row_bytes;
 
@@ -123,7 +127,8 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
     for (int c = c_begin + wave; c < c_end; c += kWaves) {
         // ---- loads: activation + scales into this wave's LDS region, weights into registers ----
 #pragma unroll
-        for (int i = 0; i < kDA; ++i) dma16(a_src[i] + 256 * c, a_lds + 1024 * i);
+        for (int i = 0; i < kDA; ++i)
+            if (i < a_groups) dma16(a_src[i] + 256 * c, a_lds + 1024 * i);
 #pragma unroll
         for (int k = 0; k < kDD; ++k) dma16(d_src[k] + (int64_t)8 * c * m_ld, d_lds + 256 * k);
         // block pair p: dwords D0..D16 at chunk byte 68p (d_even = low half of D0, the even block's
