@@ -7,7 +7,8 @@
 // off the critical path.
 //
 // Launch shape. A workgroup of 8 waves owns 32 weight rows (one MFMA n-tile) and 64
-// activation rows (two MFMA m-tiles); its waves split K by superblock (wave w takes
+// activation rows (two MFMA m-tiles; 32 rows, one m-tile, at M <= 32); its waves split K by
+// superblock (wave w takes
 // superblocks w, w + 8, ...). Per superblock a wave
 //   - loads the 64 x 256 activation bytes and 64 scales straight into its own LDS
 //     region (global_load_lds_dwordx4: coalesced, no registers in flight, no barrier:
@@ -40,9 +41,13 @@ typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int kWaves = 8;
-constexpr int kMT = 64;         // activation rows per workgroup
+// MTI m-tiles of 32 activation rows per workgroup: 2 (64 rows) in general, 1 at M <= 32
+template <int MTI>
+struct BGeo {
+    static constexpr int kMT = 32 * MTI;                // activation rows per workgroup
+    static constexpr int kRegion = kMT * 256 + 1024;    // per-wave LDS: activation + 1 KB scales
+};
 constexpr int kNT = 32;         // weight rows per workgroup
-constexpr int kRegion = 17408;  // per-wave LDS: 64 rows x 256 B activation + 1 KB scales
 
 // 16 bytes per lane from global memory straight into LDS at base + 16 * lane (base
 // wave-uniform, in M0). Inline asm: the builtin form makes the compiler wait for every
@@ -63,7 +68,7 @@ __device__ __forceinline__ int aswz(int row, int slot) { return row * 256 + 16 *
 
 }  // namespace
 
-template <bool DUMP>
+template <int MTI, bool DUMP>
 __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                                    int N, int nsb, const int8_t* __restrict__ xqs,
                                                                    const float* __restrict__ xd, int64_t m_ld, int M,
@@ -73,6 +78,7 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int K = nsb * 256;
+    constexpr int kMT = BGeo<MTI>::kMT, kRegion = BGeo<MTI>::kRegion, kDA = kMT / 4;
     const int n0 = blockIdx.x * kNT, m0 = blockIdx.y * kMT;
     // workgroup z takes superblocks [z * cpz, (z + 1) * cpz) and stores plane z of Y (planes of M
     // rows; with one plane Y is the output itself)
@@ -81,32 +87,32 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
     const int col = lane & 31, hl = lane >> 5;
     uint8_t* region = smem + wave * kRegion;
     int8_t* a_lds = reinterpret_cast<int8_t*>(region);
-    float* d_lds = reinterpret_cast<float*>(region + 64 * 256);
+    float* d_lds = reinterpret_cast<float*>(region + kMT * 256);
 
-    // activation DMA: instruction i (0..15) fills rows 4i .. 4i+3; lane l the physical slot
+    // activation DMA: instruction i (0..kDA-1) fills rows 4i .. 4i+3; lane l the physical slot
     // l % 16 of row 4i + l / 16, which holds logical slot (l % 16) ^ (row % 16)
-    const int8_t* a_src[16];
+    const int8_t* a_src[kDA];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < kDA; ++i) {
         const int row = 4 * i + (lane >> 4);
         const int slot = (lane & 15) ^ (row & 15);
         a_src[i] = xqs + (int64_t)min(m0 + row, M - 1) * K + 16 * slot;
     }
     // activation scales: lanes 0..15 carry rows 4l .. 4l+3 (the other lanes repeat lane 15)
-    const float* d_src = xd + m0 + 4 * min(lane, 15);
+    const float* d_src = xd + m0 + 4 * min(lane, kMT / 4 - 1);
     // weight row of this lane (MFMA B operand: column n = lane % 32)
     const uint8_t* wrow = W + (int64_t)min(n0 + col, N - 1) * w_row_bytes;
 
-    float acc[2][16];
+    float acc[MTI][16];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MTI; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
 
     for (int s = s_begin + wave; s < s_end; s += kWaves) {
         // ---- loads: activation + scales into this wave's LDS region, weights into registers ----
 #pragma unroll
-        for (int i = 0; i < 16; ++i) dma16(a_src[i] + 256 * s, a_lds + 1024 * i);
+        for (int i = 0; i < kDA; ++i) dma16(a_src[i] + 256 * s, a_lds + 1024 * i);
         dma16(d_src + (int64_t)s * m_ld, d_lds);
         const uint8_t* sb = wrow + (int64_t)s * 144;
         const uint4 hdr = ld16(sb);
@@ -147,7 +153,7 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
             mn[j] = (int)(((mnw[j >> 2] >> (8 * (j & 3))) & 0xFFu) * 0x01010101u);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < MTI; ++i) {
             v16i ahi, alo, amin;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
@@ -200,16 +206,17 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
     // ([i][v][64], 8 KB) goes into its own region, which only it has read, so one barrier ----
     auto part = [&](int w) { return reinterpret_cast<float*>(smem + w * kRegion); };
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MTI; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) part(wave)[(i * 16 + v) * 64 + lane] = acc[i][v];
     __syncthreads();
-    // every wave sums 4 of the 32 (m-tile, value) pairs over the 8 partial tiles, in wave order
+    // every wave sums 2 * MTI of the 16 * MTI (m-tile, value) pairs over the 8 partial tiles, in
+    // wave order
     {
         const int n = n0 + col;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int pv = wave * 4 + k, i = pv >> 4, v = pv & 15;
+        for (int k = 0; k < 2 * MTI; ++k) {
+            const int pv = wave * 2 * MTI + k, i = pv >> 4, v = pv & 15;
             float p8[kWaves];
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) p8[w] = part(w)[(i * 16 + v) * 64 + lane];
@@ -228,6 +235,7 @@ hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64
     if (w_row_bytes % 16 || N > (1 << 30) || M > (1 << 30) || K > (1 << 30)) return hipErrorNotSupported;
     // the per-superblock scale DMA reads 64 scales at [s][m0 .. m0 + 63]: m_ld must cover the
     // last m-tile (it is M rounded up to 128)
+    const int mti = M <= 32 ? 1 : 2, kMT = 32 * mti;
     if (act.m_ld < ((M + kMT - 1) / kMT) * kMT) return hipErrorNotSupported;
     const int nsb = (int)(K / 256);
     const int64_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
@@ -237,8 +245,9 @@ hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64
     float* out = sp.splits > 1 ? sc.p : Y;
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
     dim3 grid((unsigned)((N + kNT - 1) / kNT), (unsigned)((M + kMT - 1) / kMT), (unsigned)sp.splits);
-    const size_t lds = (size_t)kWaves * kRegion;
-    auto fn = block_sums ? batch_q4k_kernel<true> : batch_q4k_kernel<false>;
+    const size_t lds = (size_t)kWaves * (mti == 1 ? BGeo<1>::kRegion : BGeo<2>::kRegion);
+    auto fn = mti == 1 ? (block_sums ? batch_q4k_kernel<1, true> : batch_q4k_kernel<1, false>)
+                       : (block_sums ? batch_q4k_kernel<2, true> : batch_q4k_kernel<2, false>);
     hipLaunchKernelGGL(fn, grid, dim3(64 * kWaves), lds, st, (const uint8_t*)W, w_row_bytes, (int)N, nsb, act.qs,
                        act.d, act.m_ld, (int)M, sp.stps, out, out_stride, block_sums);
     hipError_t e = hipGetLastError();
