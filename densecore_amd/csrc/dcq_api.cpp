@@ -69,6 +69,7 @@ int knob(Knob k) {
         {"DCQ_Q6K_LDS_OFF", 0}, {"DCQ_Q6K_NO_FUSE", 0}, {"DCQ_Q6K_FUSE_NW", -1}, {"DCQ_Q8_SHAPE", -1},
         {"DCQ_GEMV_GENERIC", 0}, {"DCQ_GEMV_LG", -1},   {"DCQ_ATTN_NO_MFMA", 0}, {"DCQ_Q6K_RPW", -1},
         {"DCQ_Q6K_MFMA", 1},    {"DCQ_SPLIT_K", -1},
+        {"DCQ_BATCH_MTI", -1},
     };
     // read once (thread-safe static initialisation), not per call: getenv walks the environment
     static const std::array<int, (int)Knob::kCount> values = [] {

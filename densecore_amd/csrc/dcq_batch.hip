@@ -235,7 +235,8 @@ hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64
     if (w_row_bytes % 16 || N > (1 << 30) || M > (1 << 30) || K > (1 << 30)) return hipErrorNotSupported;
     // the per-superblock scale DMA reads 64 scales at [s][m0 .. m0 + 63]: m_ld must cover the
     // last m-tile (it is M rounded up to 128)
-    const int mti = M <= 32 ? 1 : 2, kMT = 32 * mti;
+    const int forced = knob(Knob::BatchTile);
+    const int mti = forced == 1 || forced == 2 ? forced : M <= 32 ? 1 : 2, kMT = 32 * mti;
     if (act.m_ld < ((M + kMT - 1) / kMT) * kMT) return hipErrorNotSupported;
     const int nsb = (int)(K / 256);
     const int64_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);

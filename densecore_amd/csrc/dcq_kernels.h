@@ -49,6 +49,7 @@ enum class Knob {
     Q6KRows,      // DCQ_Q6K_RPW: rows per wave of the 4-wave Q6_K decode (-1: launch rule)
     Q6KMfma,      // DCQ_Q6K_MFMA: 0 keeps tall Q6_K matrices on the lane-per-superblock kernels
     SplitK,       // DCQ_SPLIT_K: force the K splits of the MFMA prefill kernels (-1: rule, 1: none)
+    BatchTile,    // DCQ_BATCH_MTI: force the Q4_K batch kernel's 32-row m-tiles per workgroup (1 or 2)
     kCount
 };
 int knob(Knob k);
