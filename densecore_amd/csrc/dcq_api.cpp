@@ -59,29 +59,26 @@ SplitScratch tail_of(void* ws, size_t ws_bytes, size_t used) {
     return sc;
 }
 
+#ifdef DCQ_TUNING
+// Tuning build only: the overrides come from the environment, read once (thread-safe static
+// initialisation), not per call. The default build uses the constant knob() in dcq_kernels.h.
 int knob(Knob k) {
-    struct Entry {
-        const char* name;
-        int dflt;
+    static const char* const kNames[(int)Knob::kCount] = {
+        "DCQ_Q4K_SHAPE",    "DCQ_Q4K_NW",  "DCQ_NO_FUSE",      "DCQ_Q6K_DECODE", "DCQ_Q6K_LDS_OFF",
+        "DCQ_Q6K_NO_FUSE",  "DCQ_Q6K_FUSE_NW", "DCQ_Q8_SHAPE", "DCQ_GEMV_GENERIC", "DCQ_GEMV_LG",
+        "DCQ_ATTN_NO_MFMA", "DCQ_Q6K_RPW", "DCQ_Q6K_MFMA",     "DCQ_SPLIT_K",    "DCQ_BATCH_MTI",
     };
-    static const Entry kEntries[(int)Knob::kCount] = {
-        {"DCQ_Q4K_SHAPE", -1}, {"DCQ_Q4K_NW", 4},      {"DCQ_NO_FUSE", 0},      {"DCQ_Q6K_DECODE", 0},
-        {"DCQ_Q6K_LDS_OFF", 0}, {"DCQ_Q6K_NO_FUSE", 0}, {"DCQ_Q6K_FUSE_NW", -1}, {"DCQ_Q8_SHAPE", -1},
-        {"DCQ_GEMV_GENERIC", 0}, {"DCQ_GEMV_LG", -1},   {"DCQ_ATTN_NO_MFMA", 0}, {"DCQ_Q6K_RPW", -1},
-        {"DCQ_Q6K_MFMA", 1},    {"DCQ_SPLIT_K", -1},
-        {"DCQ_BATCH_MTI", -1},
-    };
-    // read once (thread-safe static initialisation), not per call: getenv walks the environment
     static const std::array<int, (int)Knob::kCount> values = [] {
         std::array<int, (int)Knob::kCount> v{};
         for (int i = 0; i < (int)Knob::kCount; ++i) {
-            const char* s = getenv(kEntries[i].name);
-            v[i] = (s && *s) ? atoi(s) : kEntries[i].dflt;
+            const char* s = getenv(kNames[i]);
+            v[i] = (s && *s) ? atoi(s) : kKnobDefault[i];
         }
         return v;
     }();
     return values[(int)k];
 }
+#endif
 
 }  // namespace dcq
 
@@ -467,10 +464,12 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
     const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N));
+    // The workspace is read-only here: products that share one quantization may run on different
+    // streams. So there is no split-K room (it would be written): the MFMA kernels run unsplit,
+    // with the same result bits as dcq_mul_mat given an activation-only workspace.
     hipError_t e = use_gemv ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
                             : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st,
-                                         tail_of((void*)workspace, workspace_bytes,
-                                                 planar_bytes(vdt, M, K, nullptr, nullptr)));
+                                         SplitScratch{});
     return hip_status(e);
 }
 

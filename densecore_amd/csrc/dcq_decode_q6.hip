@@ -40,17 +40,31 @@ namespace {
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Direct-to-LDS loads: lane l writes base + 4*l (dword) or base + 16*l (dwordx4), base
-// wave-uniform in M0. Inline asm: the builtin form waits for every earlier LDS-direct load
-// before the next. The compiler does not count these loads; the kernel issues no other
-// global loads and waits with explicit s_waitcnt. M0 has no other use in the kernel.
+// wave-uniform in M0. Inline asm: the builtin form makes the compiler wait for all of them
+// (vmcnt(0)) before any later use of an ordinary load. The compiler does not count these loads;
+// the kernel waits with explicit s_waitcnt. M0 has no other use in the kernel.
+// PRIVATE: the destination is the issuing wave's own row image, read only by that wave after its
+// own counted wait, and the load may stay in flight across a workgroup barrier. The asm carries a
+// "; wave-private" comment so that the assembly scan in tests/test_isa_hazards.py exempts it from
+// the rule that a barrier must follow a wait for every earlier direct-to-LDS load.
+template <bool PRIVATE = false>
 __device__ __forceinline__ void dma4(const void* g, const void* lds_base) {
     const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+    if constexpr (PRIVATE)
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off ; wave-private" ::"v"(g), "s"(m0)
+                     : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
 // global address 16-byte aligned, base 16-byte aligned
+template <bool PRIVATE = false>
 __device__ __forceinline__ void dma16(const void* g, const void* lds_base) {
     const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+    if constexpr (PRIVATE)
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off ; wave-private" ::"v"(g), "s"(m0)
+                     : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
 }
 
 // A 16-byte global load the compiler does not track, for loads that must sit in the same
@@ -81,6 +95,15 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
         else
             wait_vmcnt_rt<MID + 1, HI>(n);
     }
+}
+// The counted wait for the loads issued before the last n. The ";dcq counted wait" comment after
+// it marks its end in the assembly: the binary search has branches that the assembly scan in
+// tests/test_isa_hazards.py cannot evaluate, so the scan takes the marker as the wait and checks
+// that no instruction touches the registers of an untracked load, and no barrier follows a
+// direct-to-LDS load, on any path before it.
+__device__ __forceinline__ void counted_wait(int n) {
+    wait_vmcnt_rt<0, 63>(n);
+    asm volatile(";dcq counted wait");
 }
 
 // (a & m) | (b & ~m) as one v_bfi_b32 (the compiler otherwise re-derives the masks)
@@ -219,15 +242,15 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
         return r;
     };
     const int tail0 = row_dw > 64 ? row_dw - 64 : 0;
-    auto issue_head = [&](const RowImg& r) { dma4(r.src + 4 * (lane < row_dw ? lane : row_dw - 1), r.img); };
+    auto issue_head = [&](const RowImg& r) { dma4<true>(r.src + 4 * (lane < row_dw ? lane : row_dw - 1), r.img); };
     auto issue_pieces = [&](const RowImg& r, int j0, int j1) {
         for (int j = j0; j < j1; ++j) {
             const int c = 64 * j + lane;
-            dma16(r.src + r.head + 16 * (c < r.nfull ? c : r.nfull - 1), r.lw + 16 + 1024 * j);
+            dma16<true>(r.src + r.head + 16 * (c < r.nfull ? c : r.nfull - 1), r.lw + 16 + 1024 * j);
         }
     };
     auto issue_tail = [&](const RowImg& r) {
-        dma4(r.src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), r.img + 4 * tail0);
+        dma4<true>(r.src + 4 * (tail0 + lane < row_dw ? tail0 + lane : row_dw - 1), r.img + 4 * tail0);
     };
     RowImg cur = row_image(row0, lw0);
     const int issued = cur.issued;
@@ -244,10 +267,14 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     issue_head(cur);
     issue_pieces(cur, 0, n_early);
     if (!split || !stager) issue_tail(cur);
+    // One counted wait on every path. A staging wave of the fused form waits for its activation
+    // loads only (issued before the row): it quantizes the activation while the row streams. Every
+    // other wave waits for the activation share of the unfused form, issued before the row (in
+    // the fused form such a wave issued none, and the wait lets its whole row stay in flight).
+    counted_wait(FUSE && stager && split ? n_early + 1 : issued);
     if (FUSE && stager) {
         // quantize the activation (QC passes of 4 * SW (superblock, row) pairs, one per 16-lane
-        // group) while the row streams: wait for the activation loads only (issued before it)
-        wait_vmcnt_rt<0, 63>(split ? n_early + 1 : issued);
+        // group)
         __builtin_amdgcn_sched_barrier(0);
         const int tid = threadIdx.x, g = tid & 15, last_pair = nsb * MT - 1;
 #pragma unroll
@@ -275,8 +302,6 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
             issue_pieces(cur, n_early, cur.nx4);
             issue_tail(cur);
         }
-    } else {
-        wait_vmcnt_rt<0, 63>(issued);  // the activation share (issued before the row) is in
     }
     __syncthreads();
 
@@ -310,7 +335,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
             const int endb = 3360 * (k + 1) < row_bytes ? 3360 * (k + 1) : row_bytes;
             const int need = (endb - cur.head + 1023) / 1024;
             const int done = k == nsteps - 1 ? cur.issued : 1 + (need < cur.nx4 ? need : cur.nx4);
-            wait_vmcnt_rt<0, 63>(cur.issued - done + after);
+            counted_wait(cur.issued - done + after);
             const int s_raw = kSbStep * k + (lane >> 2);
             const bool valid = s_raw < nsb;
             const int s = valid ? s_raw : nsb - 1;
@@ -404,10 +429,12 @@ __host__ __device__ inline size_t tall_lds_bytes(int MT, int nsb) {
 }
 
 // one dword per lane from global memory (uniform base `g` + per-lane offset) into LDS at
-// lds_base + 4 * lane; the base is an SGPR pair, M0 the LDS base
+// lds_base + 4 * lane; the base is an SGPR pair, M0 the LDS base. Used for the waves' own tile
+// buffers only ("; wave-private", as dma4<true>).
 __device__ __forceinline__ void dma4s(const void* g, uint32_t off, const void* lds_base) {
     const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
-    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(g), "s"(m0) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1 ; wave-private" ::"v"(off), "s"(g), "s"(m0)
+                 : "memory", "m0");
 }
 
 typedef int v16i_t __attribute__((ext_vector_type(16)));
@@ -795,7 +822,7 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
     const int nsb = (int)(K / 256);
     if (nsb % 2 != 0 || w_row_bytes % 4 != 0 || nsb > kMaxNsb || w_row_bytes > INT32_MAX)
         return hipErrorNotSupported;
-    if (knob(Knob::Q6KLdsOff) || knob(Knob::Q6KNoFuse)) return hipErrorNotSupported;
+    if (knob(Knob::Q6KLdsOff) != 0 || knob(Knob::Q6KNoFuse) != 0) return hipErrorNotSupported;
     // tall matrices (M <= 8): the MFMA kernel, every workgroup quantizing the activation
     if (M <= 8 && q6_use_mfma(N, nsb, M))
         return launch_tall_q6k(W, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums, N, st, R,

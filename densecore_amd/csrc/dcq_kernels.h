@@ -32,8 +32,10 @@ hipError_t launch_unpack_ggml_rows(int vdt, const void* in, int64_t in_row_bytes
 // compute units of the current device (cached per device)
 int cu_count();
 
-// Tuning overrides for measurements, read from the environment once per process (the
-// defaults are the measured choices; -1 or 0 means "not set" as listed in dcq_api.cpp).
+// Tuning overrides for measurements. The default build has a fixed dispatch rule: knob() is a
+// constant that returns each knob's default (the measured choice), and the launchers' override
+// branches fold away. Only a tuning build (make TUNING=1, which defines DCQ_TUNING) reads the
+// DCQ_* variables below from the environment, once per process; -1 or 0 means "not set".
 enum class Knob {
     Q4KShape,     // DCQ_Q4K_SHAPE: force a decode shape index (-1: launch rule)
     Q4KWaves,     // DCQ_Q4K_NW: 5 for 5-wave workgroups with a forced shape (default 4)
@@ -52,7 +54,13 @@ enum class Knob {
     BatchTile,    // DCQ_BATCH_MTI: force the Q4_K batch kernel's 32-row m-tiles per workgroup (1 or 2)
     kCount
 };
+// defaults, in Knob order: the launchers' measured rules
+constexpr int kKnobDefault[(int)Knob::kCount] = {-1, 4, 0, 0, 0, 0, -1, -1, 0, -1, 0, -1, 1, -1, -1};
+#ifdef DCQ_TUNING
 int knob(Knob k);
+#else
+constexpr int knob(Knob k) { return kKnobDefault[(int)k]; }
+#endif
 
 hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0, int64_t n1, int64_t K,
                        const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,

@@ -130,10 +130,12 @@ int64_t dcq_block_sums_per_row(int wtype, int64_t k);
  * dcq_quantize_src1 quantizes X once into `workspace` (the library's planar layout, sized by
  * dcq_mul_mat_workspace_size(wtype, M, K)); dcq_mul_mat_q then computes Y from W and that
  * workspace. One quantization can feed several weights that share X (ffn gate and up,
- * core/src/inference.cpp:1794-1797). dcq_mul_mat == dcq_quantize_src1 + dcq_mul_mat_q. The
- * workspace must not be written between the two calls. dcq_mul_mat_q writes the split-K room
- * past the quantized activation (when the workspace has it), so calls that share a workspace
- * must be ordered on one stream. */
+ * core/src/inference.cpp:1794-1797). The workspace must not be written between the two calls.
+ * dcq_mul_mat_q only reads the workspace, so several calls that share one quantization may run
+ * concurrently on different streams. It therefore never splits K (split-K writes partial sums
+ * into workspace room): its result equals dcq_mul_mat's with a workspace that holds only the
+ * quantized activation, bit for bit; dcq_mul_mat with the full workspace may split and differ in
+ * the last fp32 bits. */
 int dcq_quantize_src1(int wtype, const float* X, int64_t M, int64_t K, size_t x_stride_bytes,
                       void* workspace, size_t workspace_bytes, void* stream);
 int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes,
@@ -155,6 +157,12 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
 int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, const float* X,
                         int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes, void* stream);
 
+/* Activation rows up to which dcq_mul_mat's automatic path (and dcq_mul_mat_add and
+ * dcq_ffn_gate_up) takes the decode GEMV kernels: 4 in general; for Q6_K weights 2 when
+ * N >= 4096 and 8 when N >= 32768 (LM heads). Larger M goes to the batched and prefill MFMA
+ * kernels. */
+#define DCQ_DECODE_ROWS(wtype, N) ((wtype) != DCQ_TYPE_Q6_K ? 4 : (N) >= 32768 ? 8 : (N) >= 4096 ? 2 : 4)
+
 /* ---- a projection and its residual or bias ----
  * Y[m][n] = (sum_k W[n][k] x[m][k]) + R[m][n], one fp32 add per element after dcq_mul_mat's
  * product: the reference's residual connections cur = ggml_add(mul_mat(wo, .), inpL) and
@@ -163,8 +171,9 @@ int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w
  * dcq_mul_mat's output plus R bit for bit. r_stride_bytes 0 broadcasts one bias row of N
  * floats; otherwise it is >= N*4. R may be Y itself (r_stride_bytes == y_stride_bytes: the
  * in-place residual) or must not overlap Y. R 4-byte aligned, strides multiples of 4; the rest
- * as dcq_mul_mat. At M <= 8 the add is the fused decode kernel's store; otherwise the product
- * goes to Y (or, when R is Y, a workspace temporary) and one add kernel follows. workspace may
+ * as dcq_mul_mat. Where the decode kernels serve the product (M <= DCQ_DECODE_ROWS(wtype, N))
+ * the add is their store; otherwise the product goes to Y (or, when R is Y, a workspace
+ * temporary) and one add kernel follows. workspace may
  * be NULL; otherwise it should hold dcq_mul_mat_add_workspace_size(wtype, M, N, K) bytes,
  * 256-byte aligned (the split-K room at its end is optional, as in dcq_mul_mat). */
 size_t dcq_mul_mat_add_workspace_size(int wtype, int64_t M, int64_t N, int64_t K);
@@ -177,8 +186,9 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
  * Y[m][n] = silu(sum_k Wg[n][k] x[m][k]) * (sum_k Wu[n][k] x[m][k]), silu(g) = g / (1 + e^-g):
  * the reference FFN's w1 = mul_mat(W1, x), w3 = mul_mat(W3, x), ggml_mul(ggml_silu(w1), w3)
  * (core/src/inference.cpp:1794-1796) in one call. Both weights share wtype, shape and row
- * stride, and X's quantization. At M <= 8 (Q4_K, Q8_0) one fused kernel streams both weight
- * rows; otherwise X is quantized once, both projections run, then the product.
+ * stride, and X's quantization. At M <= DCQ_DECODE_ROWS(wtype, N) (Q4_K, Q8_0) one fused kernel
+ * streams both weight rows; otherwise X is quantized once, both projections run, then the
+ * product.
  * Requirements as dcq_mul_mat's, for both weights. workspace may be NULL; otherwise it should hold
  * dcq_ffn_gate_up_workspace_size(wtype, M, N, K) bytes, 256-byte aligned (the split-K room at its
  * end is optional, as in dcq_mul_mat). */

@@ -262,6 +262,20 @@ def assert_close(y, y_ref, l1, rtol=1e-4, what=""):
     return float(np.max(err / np.maximum(bound / rtol, 1e-30))), float(np.median(rel))
 
 
+def relative_error_stats(y, y_ref, rtol=1e-4):
+    """The plain elementwise relative error |y - y_ref| / |y_ref| over outputs with y_ref != 0:
+    its median, 99th percentile and maximum, and how many outputs exceed rtol (outputs whose fp32
+    terms cancel can, while staying inside the L1-guarded bound of assert_close)."""
+    y = np.asarray(y, dtype=np.float64).ravel()
+    y_ref = np.asarray(y_ref, dtype=np.float64).ravel()
+    nz = y_ref != 0
+    rel = np.abs(y[nz] - y_ref[nz]) / np.abs(y_ref[nz])
+    if rel.size == 0:
+        return {"n": 0, "p50": 0.0, "p99": 0.0, "max": 0.0, "n_above": 0, "n_zero_ref": int(y_ref.size)}
+    return {"n": int(rel.size), "p50": float(np.percentile(rel, 50)), "p99": float(np.percentile(rel, 99)),
+            "max": float(rel.max()), "n_above": int((rel > rtol).sum()), "n_zero_ref": int((~nz).sum())}
+
+
 # ---------------------------------------------------------------- weight-quantizer test hooks
 PLANT_NO_MIN_CLAMP, PLANT_UNIT_WEIGHTS, PLANT_GRID_8 = 1, 2, 4
 

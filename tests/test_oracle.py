@@ -320,3 +320,11 @@ def test_ffn_gate_up_tolerance_catches_a_swapped_pair(O):
     swapped, _ = O.ffn_gate_up(Q4_K, wu, wg, x)
     with pytest.raises(AssertionError):
         O.assert_close_gate_up(swapped.astype(np.float32), y, parts, what="swapped")
+
+
+def test_relative_error_stats_known_values(O):
+    """The reported plain relative error: zeros in the reference are counted apart, not divided by."""
+    st = O.relative_error_stats(np.array([1.0, 2.0, 0.0, 1e-3, 5.0]), np.array([1.0, 2.0002, 0.0, 1.25e-3, 5.0]))
+    assert st["n"] == 4 and st["n_zero_ref"] == 1
+    assert st["max"] == pytest.approx(0.2) and st["n_above"] == 1
+    assert st["p50"] == pytest.approx(0.0002 / 2.0002 / 2, rel=1e-9)  # halfway between 0 and 1e-4
