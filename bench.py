@@ -666,6 +666,31 @@ def bench_gguf_load(args, dev, mib=512):
             "note": "file in the page cache; read into two pinned 32 MB chunks, each copied while the next is read"}
 
 
+def bench_weight_quantizer(args, dev):
+    """dcq_quantize_weights (ggml_quantize_chunk's algorithms on the GPU) at the weight shapes of
+    ms per matrix and GB/s of fp32 input (load-time work, off the hot path)."""
+    import torch
+    import densecore_amd as dc
+    from densecore_amd import synth
+    out = {}
+    for ci in (1, 2, 3):
+        cfg = dc.by_index(ci)
+        w = torch.from_numpy(synth.normal(cfg.N * cfg.K, cfg.w_seed, 0.0, cfg.w_std).reshape(cfg.N, cfg.K)).to(dev)
+        q = dc.quantize_weights(cfg.wtype, w)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
+        e0.record()
+        for _ in range(reps):
+            dc.quantize_weights(cfg.wtype, w, out=q)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[dc.TYPE_NAMES[cfg.wtype].lower()] = {"shape": f"{cfg.N}x{cfg.K}", "ms": ms,
+                                                 "GBps_fp32_in": cfg.N * cfg.K * 4 / (ms * 1e-3) / 1e9}
+    return out
+
+
 def profile_config(cfg, args, dev):
     """Eager steps of one config (counter collection needs plain dispatches)."""
     import torch
@@ -1035,6 +1060,7 @@ def main():
             e = extras[f"batched_{tname.lower()}_m{M}_{N}x{K}"] = bench_batched_decode(args, dev, tname, M, N, K)
             print(f"# batched decode {e['shape']}: {e['step_us']:.2f} us ({e['kernels']} kernels), "
                   f"{e['weight_GBps']:.0f} GB/s of weights, {e['TOPS']:.1f} TOPS", file=sys.stderr, flush=True)
+        extras["weight_quantizer"] = bench_weight_quantizer(args, dev)
         extras["gguf_load"] = bench_gguf_load(args, dev)
         print(f"# GGUF ingest: {extras['gguf_load']['GBps']:.1f} GB/s host-to-HBM over "
               f"{extras['gguf_load']['bytes'] >> 20} MiB", file=sys.stderr, flush=True)

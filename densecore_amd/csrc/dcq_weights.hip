@@ -4,9 +4,14 @@
 // Weight quantization is the offline step before the hot path
 // (core/src/quantize.cpp:214, 285 call ggml_quantize_chunk); dequantization is
 // the reference GEMV's fallback (core/src/inference.cpp:938-945). One thread per
-// block / superblock; the scalar search below is ggml's published algorithm
-// (make_qkx2_quants for Q4_K, make_qx_quants with rmse_type 1 for Q6_K,
-// roundf scaling for Q8_0). This file is compiled with -ffp-contract=off so
+// block / superblock; the search is ggml's published algorithm (make_qkx2_quants for
+// Q4_K, make_qx_quants with rmse_type 1 for Q6_K, roundf scaling for Q8_0), each fit's
+// sums in their sequential order. The Q4_K kernel holds a sub-block in registers and its
+// fits in LDS (no per-thread arrays in scratch memory): 9728 x 2560 took 2.36 ms with the
+// arrays in scratch, 0.39 ms so. The same change to the Q6_K kernel measured slower
+// (0.32 -> 0.36 ms: its final levels need an LDS column per thread, which halves the
+// resident waves), so that kernel keeps its arrays. This file is compiled with
+// -ffp-contract=off so
 // each fp32 operation rounds on its own, as the CPU code does, and the bytes
 // match a CPU build of the same algorithm exactly.
 #include "dcq_common.h"
@@ -44,70 +49,6 @@ __global__ void __launch_bounds__(256) quantize_w_q8_0_kernel(const float* __res
 }
 
 // ---- Q4_K ----
-__device__ float make_qkx2_quants(int n, int nmax, const float* x, const float* weights, uint8_t* L, float* the_min,
-                                  uint8_t* Laux, float rmin, float rdelta, int nstep) {
-    float min = x[0], max = x[0];
-    float sum_w = weights[0];
-    float sum_x = sum_w * x[0];
-    for (int i = 1; i < n; ++i) {
-        if (x[i] < min) min = x[i];
-        if (x[i] > max) max = x[i];
-        float w = weights[i];
-        sum_w += w;
-        sum_x += w * x[i];
-    }
-    if (min > 0) min = 0;
-    if (max == min) {
-        for (int i = 0; i < n; ++i) L[i] = 0;
-        *the_min = -min;
-        return 0.f;
-    }
-    float iscale = nmax / (max - min);
-    float scale = 1 / iscale;
-    float best_error = 0;
-    for (int i = 0; i < n; ++i) {
-        int l = nearest_int(iscale * (x[i] - min));
-        L[i] = (uint8_t)(l < 0 ? 0 : (l > nmax ? nmax : l));
-        float diff = scale * L[i] + min - x[i];
-        best_error += weights[i] * (diff * diff);
-    }
-    for (int is = 0; is <= nstep; ++is) {
-        iscale = (rmin + rdelta * is + nmax) / (max - min);
-        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
-        for (int i = 0; i < n; ++i) {
-            int l = nearest_int(iscale * (x[i] - min));
-            l = l < 0 ? 0 : (l > nmax ? nmax : l);
-            Laux[i] = (uint8_t)l;
-            float w = weights[i];
-            sum_l += w * l;
-            sum_l2 += w * l * l;
-            sum_xl += w * l * x[i];
-        }
-        float D = sum_w * sum_l2 - sum_l * sum_l;
-        if (D > 0) {
-            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
-            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
-            if (this_min > 0) {
-                this_min = 0;
-                this_scale = sum_xl / sum_l2;
-            }
-            float mad = 0;
-            for (int i = 0; i < n; ++i) {
-                float diff = this_scale * Laux[i] + this_min - x[i];
-                mad += weights[i] * (diff * diff);
-            }
-            if (mad < best_error) {
-                for (int i = 0; i < n; ++i) L[i] = Laux[i];
-                best_error = mad;
-                scale = this_scale;
-                min = this_min;
-            }
-        }
-    }
-    *the_min = -min;
-    return scale;
-}
-
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
     if (j < 4) {
         *d = q[j] & 63;
@@ -118,61 +59,178 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint8_t* d
     }
 }
 
-__global__ void __launch_bounds__(64) quantize_w_q4_K_kernel(const float* __restrict__ W, int64_t N, int64_t K,
-                                                             uint8_t* __restrict__ out) {
+// One sub-block's fit for quantize_row_q4_K_ref: ggml's make_qkx2_quants with n = 32, nmax = 15,
+// rmin = -1, rdelta = 0.1, nstep = 20 (the sub-block scale and min of the least weighted squared
+// error over a grid of 21 inverse scales around nmax / (max - min), each refined by a least-squares
+// fit, min clamped to <= 0), the same fp32 operations in the same order, on the sub-block held in
+// registers. The weights av_x + |x_i| are recomputed per use (the
+// same fp32 value each time), and the chosen levels L are not stored: the (iscale, min) they were
+// computed with are returned instead, so the caller recomputes them where it needs them.
+struct Qkx2Fit {
+    float scale, the_min;  // make_qkx2_quants' return value and *the_min
+    float l_iscale, l_min;  // L_i = clamp(nearest_int(l_iscale * (x_i - l_min)), 0, 15)
+    int zero;               // max == min: every L_i is 0
+};
+
+__device__ __forceinline__ int clamp15(int l) { return l < 0 ? 0 : (l > 15 ? 15 : l); }
+
+__device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
+    const int nmax = 15;
+    const float rmin = -1.f, rdelta = 0.1f;
+    const int nstep = 20;
+    float min = x[0], max = x[0];
+    float sum_w = av_x + fabsf(x[0]);
+    float sum_x = sum_w * x[0];
+#pragma unroll
+    for (int i = 1; i < 32; ++i) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        const float w = av_x + fabsf(x[i]);
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (min > 0) min = 0;
+    if (max == min) return {0.f, -min, 0.f, 0.f, 1};
+    float iscale = nmax / (max - min);
+    float scale = 1 / iscale;
+    float best_error = 0;
+    float l_iscale = iscale, l_min = min;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        const int l = clamp15(nearest_int(iscale * (x[i] - min)));
+        const float diff = scale * (float)l + min - x[i];
+        best_error += (av_x + fabsf(x[i])) * (diff * diff);
+    }
+#pragma unroll 1
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * is + nmax) / (max - min);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+            const int l = clamp15(nearest_int(iscale * (x[i] - min)));
+            const float w = av_x + fabsf(x[i]);
+            sum_l += w * l;
+            sum_l2 += w * l * l;
+            sum_xl += w * l * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) {
+                this_min = 0;
+                this_scale = sum_xl / sum_l2;
+            }
+            float mad = 0;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int l = clamp15(nearest_int(iscale * (x[i] - min)));
+                const float diff = this_scale * (float)l + this_min - x[i];
+                mad += (av_x + fabsf(x[i])) * (diff * diff);
+            }
+            if (mad < best_error) {
+                l_iscale = iscale;
+                l_min = min;
+                best_error = mad;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+    return {scale, -min, l_iscale, l_min, 0};
+}
+
+// ---- Q4_K: quantize_row_q4_K_ref, one thread per superblock with no per-thread arrays in scratch:
+// a sub-block's 32 values live in registers, the per-sub-block fits in this thread's LDS slot, and
+// the final levels are recomputed per sub-block pair as they are packed ----
+constexpr int kWq4Threads = 64;
+__global__ void __launch_bounds__(kWq4Threads) quantize_w_q4_K_kernel(const float* __restrict__ W, int64_t N,
+                                                                      int64_t K, uint8_t* __restrict__ out) {
+    __shared__ Qkx2Fit fits[8][kWq4Threads];
     const int64_t nsb = K / QK_K;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= N * nsb) return;
+    const int t = threadIdx.x;
     const int64_t r = gid / nsb, sbi = gid - (gid / nsb) * nsb;
-    const float* x = W + r * K + sbi * QK_K;
-    BlockQ4_K y __attribute__((aligned(16)));
-    uint8_t L[QK_K], Laux[32];
-    float weights[32], mins[8], scales[8];
+    const float* xs = W + r * K + sbi * QK_K;
+    auto load32 = [&](int j, float (&x)[32]) {
+        const float4* p = reinterpret_cast<const float4*>(xs + 32 * j);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 v = p[q];
+            x[4 * q] = v.x, x[4 * q + 1] = v.y, x[4 * q + 2] = v.z, x[4 * q + 3] = v.w;
+        }
+    };
     float max_scale = 0, max_min = 0;
+#pragma unroll 1
     for (int j = 0; j < 8; ++j) {
+        float x[32];
+        load32(j, x);
         float sum_x2 = 0;
-        for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
-        float av_x = sqrtf(sum_x2 / 32);
-        for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
-        scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -1.f, 0.1f, 20);
-        if (scales[j] > max_scale) max_scale = scales[j];
-        if (mins[j] > max_min) max_min = mins[j];
+#pragma unroll
+        for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
+        const float av_x = sqrtf(sum_x2 / 32);
+        const Qkx2Fit f = qkx2_fit32(x, av_x);
+        fits[j][t] = f;
+        if (f.scale > max_scale) max_scale = f.scale;
+        if (f.the_min > max_min) max_min = f.the_min;
     }
-    float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
-    float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
-    for (int i = 0; i < 12; ++i) y.scales[i] = 0;
+    const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    // the 12 scale bytes (get_scale_min_k4's packing), built in three dwords
+    uint32_t scw[3] = {0, 0, 0};
+    auto put = [&](int byte, uint32_t v) { scw[byte >> 2] |= (v & 0xFFu) << (8 * (byte & 3)); };
+    uint8_t ls8[8], lm8[8];
+#pragma unroll
     for (int j = 0; j < 8; ++j) {
-        int ls = nearest_int(inv_scale * scales[j]);
-        int lm = nearest_int(inv_min * mins[j]);
+        int ls = nearest_int(inv_scale * fits[j][t].scale);
+        int lm = nearest_int(inv_min * fits[j][t].the_min);
         ls = ls < 63 ? ls : 63;
         lm = lm < 63 ? lm : 63;
+        ls8[j] = (uint8_t)ls;
+        lm8[j] = (uint8_t)lm;
         if (j < 4) {
-            y.scales[j] = (uint8_t)ls;
-            y.scales[j + 4] = (uint8_t)lm;
+            put(j, (uint32_t)ls);
+            put(j + 4, (uint32_t)lm);
         } else {
-            y.scales[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
-            y.scales[j - 4] |= (uint8_t)((ls >> 4) << 6);
-            y.scales[j - 0] |= (uint8_t)((lm >> 4) << 6);
+            put(j + 4, (uint32_t)((ls & 0xF) | ((lm & 0xF) << 4)));
+            put(j - 4, (uint32_t)((ls >> 4) << 6));
+            put(j, (uint32_t)((lm >> 4) << 6));
         }
     }
-    y.d = float_to_half_bits(max_scale / 63.f);
-    y.dmin = float_to_half_bits(max_min / 63.f);
-    for (int j = 0; j < 8; ++j) {
-        uint8_t sc, m;
-        scale_min_k4(j, y.scales, &sc, &m);
-        const float d = half_bits_to_float(y.d) * sc;
-        if (!d) continue;
-        const float dm = half_bits_to_float(y.dmin) * m;
-        for (int ii = 0; ii < 32; ++ii) {
-            int l = nearest_int((x[32 * j + ii] + dm) / d);
-            L[32 * j + ii] = (uint8_t)(l < 0 ? 0 : (l > 15 ? 15 : l));
-        }
-    }
-    for (int c = 0; c < 4; ++c)
-        for (int l = 0; l < 32; ++l) y.qs[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + l + 32] << 4));
+    const uint16_t dh = float_to_half_bits(max_scale / 63.f), dminh = float_to_half_bits(max_min / 63.f);
     uint32_t* dst = reinterpret_cast<uint32_t*>(out + (r * nsb + sbi) * 144);
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(&y);
-    for (int i = 0; i < 36; ++i) dst[i] = src[i];
+    dst[0] = (uint32_t)dh | ((uint32_t)dminh << 16);
+    dst[1] = scw[0];
+    dst[2] = scw[1];
+    dst[3] = scw[2];
+    const float dsb = half_bits_to_float(dh), dmsb = half_bits_to_float(dminh);
+    // final levels of sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles) of qs[32c .. 32c + 32):
+    // from the 6-bit scales, or, where the scale quantized to 0, the fit's own levels
+#pragma unroll 1
+    for (int c = 0; c < 4; ++c) {
+        uint32_t packed[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int j = 2 * c + h;
+            float x[32];
+            load32(j, x);
+            const float d = dsb * ls8[j];
+            const float dm = dmsb * lm8[j];
+            const Qkx2Fit f = fits[j][t];
+#pragma unroll
+            for (int ii = 0; ii < 32; ++ii) {
+                int l;
+                if (d != 0.0f)
+                    l = clamp15(nearest_int((x[ii] + dm) / d));
+                else
+                    l = f.zero ? 0 : clamp15(nearest_int(f.l_iscale * (x[ii] - f.l_min)));
+                packed[ii >> 2] |= (uint32_t)l << (8 * (ii & 3) + 4 * h);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dst[4 + 8 * c + q] = packed[q];
+    }
 }
 
 // ---- Q6_K ----
@@ -336,8 +394,8 @@ hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t
                            (uint8_t*)Wq);
     } else if (wtype == kTypeQ4_K) {
         const int64_t t = N * (K / QK_K);
-        hipLaunchKernelGGL(quantize_w_q4_K_kernel, dim3((unsigned)((t + 63) / 64)), dim3(64), 0, st, W, N, K,
-                           (uint8_t*)Wq);
+        hipLaunchKernelGGL(quantize_w_q4_K_kernel, dim3((unsigned)((t + kWq4Threads - 1) / kWq4Threads)),
+                           dim3(kWq4Threads), 0, st, W, N, K, (uint8_t*)Wq);
     } else {
         const int64_t t = N * (K / QK_K);
         hipLaunchKernelGGL(quantize_w_q6_K_kernel, dim3((unsigned)((t + 63) / 64)), dim3(64), 0, st, W, N, K,
