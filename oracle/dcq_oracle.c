@@ -36,10 +36,21 @@ typedef struct {
 } blk_q8_0;
 typedef struct {
     uint16_t d;
+    uint8_t qs[QK8_0 / 2]; /* element j: low nibble of qs[j]; element j + 16: its high nibble */
+} blk_q4_0;
+typedef struct {
+    uint16_t d;
     uint16_t dmin;
     uint8_t scales[12];
     uint8_t qs[QK_K / 2];
 } blk_q4_K;
+typedef struct {
+    uint16_t d;
+    uint16_t dmin;
+    uint8_t scales[12];
+    uint8_t qh[QK_K / 8]; /* bit j of qh[l]: the fifth bit of element l of sub-block j */
+    uint8_t qs[QK_K / 2]; /* the low four bits, packed as in Q4_K */
+} blk_q5_K;
 typedef struct {
     uint8_t ql[QK_K / 2];
     uint8_t qh[QK_K / 4];
@@ -53,7 +64,9 @@ typedef struct {
 } blk_q8_K;
 
 _Static_assert(sizeof(blk_q8_0) == 34, "Q8_0 block is 34 bytes");
+_Static_assert(sizeof(blk_q4_0) == 18, "Q4_0 block is 18 bytes");
 _Static_assert(sizeof(blk_q4_K) == 144, "Q4_K block is 144 bytes");
+_Static_assert(sizeof(blk_q5_K) == 176, "Q5_K block is 176 bytes");
 _Static_assert(sizeof(blk_q6_K) == 210, "Q6_K block is 210 bytes");
 _Static_assert(sizeof(blk_q8_K) == 292, "Q8_K block is 292 bytes");
 
@@ -61,8 +74,10 @@ int64_t dcqo_block_size(int type) {
     switch (type) {
         case DCQO_TYPE_F32: return 1;
         case DCQO_TYPE_F16: return 1;
+        case DCQO_TYPE_Q4_0:
         case DCQO_TYPE_Q8_0: return QK8_0;
         case DCQO_TYPE_Q4_K:
+        case DCQO_TYPE_Q5_K:
         case DCQO_TYPE_Q6_K:
         case DCQO_TYPE_Q8_K: return QK_K;
         default: return 0;
@@ -73,8 +88,10 @@ int64_t dcqo_type_size(int type) {
     switch (type) {
         case DCQO_TYPE_F32: return 4;
         case DCQO_TYPE_F16: return 2;
+        case DCQO_TYPE_Q4_0: return (int64_t)sizeof(blk_q4_0);
         case DCQO_TYPE_Q8_0: return (int64_t)sizeof(blk_q8_0);
         case DCQO_TYPE_Q4_K: return (int64_t)sizeof(blk_q4_K);
+        case DCQO_TYPE_Q5_K: return (int64_t)sizeof(blk_q5_K);
         case DCQO_TYPE_Q6_K: return (int64_t)sizeof(blk_q6_K);
         case DCQO_TYPE_Q8_K: return (int64_t)sizeof(blk_q8_K);
         default: return 0;
@@ -87,11 +104,14 @@ int64_t dcqo_row_size(int type, int64_t k) {
     return (k / bs) * dcqo_type_size(type);
 }
 
-/* core/include/simd_ops.h:3298-3305: Q4_K/Q5_K/Q6_K -> Q8_K, Q8_0 -> Q8_0 */
+/* core/include/simd_ops.h:3298-3305: Q4_K/Q5_K/Q6_K -> Q8_K, Q8_0 -> Q8_0; Q4_0 -> Q8_0 is
+ * ggml's type trait for the Q4_0 the reference's quantize tool emits (core/src/quantize.cpp:71-72) */
 int dcqo_vec_dot_type(int type) {
     switch (type) {
+        case DCQO_TYPE_Q4_0:
         case DCQO_TYPE_Q8_0: return DCQO_TYPE_Q8_0;
         case DCQO_TYPE_Q4_K:
+        case DCQO_TYPE_Q5_K:
         case DCQO_TYPE_Q6_K: return DCQO_TYPE_Q8_K;
         default: return -1;
     }
@@ -286,6 +306,31 @@ void dcqo_quantize_row_q8_0_weights(const float* x, void* y, int64_t k) {
     dcqo_quantize_row_q8_0(x, y, k, DCQO_Q8_0_REF);
 }
 
+/* quantize_row_q4_0_ref: max = the first element of largest |x| (strict '<' scan), d = max / -8,
+ * id = 1/d (0 for an all-zero block), q = min(15, (int8)(x*id + 8.5)) truncated toward zero; the
+ * element of largest magnitude maps to 0, i.e. to -8 once the 8 is taken off. */
+void dcqo_quantize_row_q4_0(const float* x, void* vy, int64_t k) {
+    blk_q4_0* y = (blk_q4_0*)vy;
+    for (int64_t i = 0; i < k / QK8_0; ++i) {
+        const float* xb = x + i * QK8_0;
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < QK8_0; ++j) {
+            if (amax < fabsf(xb[j])) {
+                amax = fabsf(xb[j]);
+                max = xb[j];
+            }
+        }
+        const float d = max / -8;
+        const float id = d ? 1.0f / d : 0.0f;
+        y[i].d = dcqo_fp32_to_fp16(d);
+        for (int j = 0; j < QK8_0 / 2; ++j) {
+            const float x0 = xb[j] * id, x1 = xb[QK8_0 / 2 + j] * id;
+            const int q0 = (int)(int8_t)(x0 + 8.5f), q1 = (int)(int8_t)(x1 + 8.5f);
+            y[i].qs[j] = (uint8_t)((q0 < 15 ? q0 : 15) | ((q1 < 15 ? q1 : 15) << 4));
+        }
+    }
+}
+
 /* weighted least-squares fit of x ~ scale*L + min, L in [0,nmax], min <= 0: the best of the
  * rounding at iscale = nmax/(max-min) and the nstep+1 grid points iscale = (rmin + rdelta*is +
  * nmax)/(max-min), each refitted by weighted least squares (min clamped to <= 0).
@@ -382,49 +427,82 @@ static void get_scale_min_k4(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
     }
 }
 
+/* One superblock of quantize_row_q4_K_ref / quantize_row_q5_K_ref: a make_qkx2_quants fit per
+ * 32-element sub-block (weights av_x + |x_i|; nmax 15, rmin -1, nstep 20 for Q4_K; nmax 31,
+ * rmin -0.5, nstep 15 for Q5_K; rdelta 0.1), the fits' scales and mins as 6-bit multiples of
+ * d = max scale / 63 and dmin = max min / 63, then every element re-rounded against its stored
+ * scale and min: L = clamp(nearest_int((x + dmin*m) / (d*sc)), 0, nmax). A sub-block whose stored
+ * scale is 0 keeps its fit's own levels. */
+static void kquant_superblock(const float* x, int nmax, float rmin, int nstep, uint8_t L[QK_K],
+                              uint8_t scales[12], uint16_t* dh, uint16_t* dminh) {
+    uint8_t Laux[32];
+    float weights[32], mins[QK_K / 32], sc_f[QK_K / 32];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < QK_K / 32; ++j) {
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+        float av_x = sqrtf(sum_x2 / 32);
+        for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+        sc_f[j] = make_qkx2_quants(32, nmax, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, rmin, 0.1f,
+                                   nstep, 0);
+        if (sc_f[j] > max_scale) max_scale = sc_f[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
+    float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
+    uint8_t ls[QK_K / 32], lm[QK_K / 32];
+    for (int j = 0; j < QK_K / 32; ++j) {
+        const int a = nearest_int(inv_scale * sc_f[j]);
+        const int b = nearest_int(inv_min * mins[j]);
+        ls[j] = (uint8_t)(a < 63 ? a : 63);
+        lm[j] = (uint8_t)(b < 63 ? b : 63);
+    }
+    dcqo_pack_scale_min_k4(ls, lm, scales);
+    *dh = dcqo_fp32_to_fp16(max_scale / 63.f);
+    *dminh = dcqo_fp32_to_fp16(max_min / 63.f);
+    for (int j = 0; j < QK_K / 32; ++j) {
+        uint8_t sc, m;
+        get_scale_min_k4(j, scales, &sc, &m);
+        const float d = dcqo_fp16_to_fp32(*dh) * sc;
+        if (!d) continue;
+        const float dm = dcqo_fp16_to_fp32(*dminh) * m;
+        for (int ii = 0; ii < 32; ++ii) {
+            int l = nearest_int((x[32 * j + ii] + dm) / d);
+            L[32 * j + ii] = (uint8_t)(l < 0 ? 0 : (l > nmax ? nmax : l));
+        }
+    }
+}
+
 void dcqo_quantize_row_q4_K(const float* x, void* vy, int64_t k) {
     blk_q4_K* y = (blk_q4_K*)vy;
-    const int64_t nb = k / QK_K;
-    uint8_t L[QK_K], Laux[32];
-    float weights[32], mins[QK_K / 32], scales[QK_K / 32];
-    for (int64_t i = 0; i < nb; ++i) {
-        float max_scale = 0, max_min = 0;
-        for (int j = 0; j < QK_K / 32; ++j) {
-            float sum_x2 = 0;
-            for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
-            float av_x = sqrtf(sum_x2 / 32);
-            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
-            scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux,
-                                         -1.f, 0.1f, 20, 0);
-            if (scales[j] > max_scale) max_scale = scales[j];
-            if (mins[j] > max_min) max_min = mins[j];
-        }
-        float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
-        float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
-        uint8_t ls[QK_K / 32], lm[QK_K / 32];
-        for (int j = 0; j < QK_K / 32; ++j) {
-            const int a = nearest_int(inv_scale * scales[j]);
-            const int b = nearest_int(inv_min * mins[j]);
-            ls[j] = (uint8_t)(a < 63 ? a : 63);
-            lm[j] = (uint8_t)(b < 63 ? b : 63);
-        }
-        dcqo_pack_scale_min_k4(ls, lm, y[i].scales);
-        y[i].d = dcqo_fp32_to_fp16(max_scale / 63.f);
-        y[i].dmin = dcqo_fp32_to_fp16(max_min / 63.f);
-        for (int j = 0; j < QK_K / 32; ++j) {
-            uint8_t sc, m;
-            get_scale_min_k4(j, y[i].scales, &sc, &m);
-            const float d = dcqo_fp16_to_fp32(y[i].d) * sc;
-            if (!d) continue;
-            const float dm = dcqo_fp16_to_fp32(y[i].dmin) * m;
-            for (int ii = 0; ii < 32; ++ii) {
-                int l = nearest_int((x[32 * j + ii] + dm) / d);
-                L[32 * j + ii] = (uint8_t)(l < 0 ? 0 : (l > 15 ? 15 : l));
-            }
-        }
+    uint8_t L[QK_K];
+    for (int64_t i = 0; i < k / QK_K; ++i) {
+        kquant_superblock(x, 15, -1.f, 20, L, y[i].scales, &y[i].d, &y[i].dmin);
+        /* sub-block 2c in the low nibbles of qs[32c .. 32c+31], sub-block 2c+1 in the high ones */
         uint8_t* q = y[i].qs;
         for (int j = 0; j < QK_K; j += 64) {
             for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+            q += 32;
+        }
+        x += QK_K;
+    }
+}
+
+void dcqo_quantize_row_q5_K(const float* x, void* vy, int64_t k) {
+    blk_q5_K* y = (blk_q5_K*)vy;
+    uint8_t L[QK_K];
+    for (int64_t i = 0; i < k / QK_K; ++i) {
+        kquant_superblock(x, 31, -0.5f, 15, L, y[i].scales, &y[i].d, &y[i].dmin);
+        /* the low four bits packed as Q4_K's nibbles; bit 4 of element l of sub-block j in bit j of
+         * qh[l] */
+        memset(y[i].qh, 0, sizeof(y[i].qh));
+        uint8_t* q = y[i].qs;
+        for (int j = 0; j < QK_K; j += 64) {
+            for (int l = 0; l < 32; ++l) {
+                const int l1 = L[j + l], l2 = L[j + l + 32];
+                q[l] = (uint8_t)((l1 & 0xF) | ((l2 & 0xF) << 4));
+                y[i].qh[l] |= (uint8_t)(((l1 >> 4) << (j / 32)) | ((l2 >> 4) << (j / 32 + 1)));
+            }
             q += 32;
         }
         x += QK_K;
@@ -571,8 +649,12 @@ static void* qm_worker(void* p) {
         void* yr = (char*)j->y + r * rs;
         if (j->type == DCQO_TYPE_Q8_0)
             dcqo_quantize_row_q8_0_weights(xr, yr, j->k);
+        else if (j->type == DCQO_TYPE_Q4_0)
+            dcqo_quantize_row_q4_0(xr, yr, j->k);
         else if (j->type == DCQO_TYPE_Q4_K)
             dcqo_quantize_row_q4_K(xr, yr, j->k);
+        else if (j->type == DCQO_TYPE_Q5_K)
+            dcqo_quantize_row_q5_K(xr, yr, j->k);
         else if (j->type == DCQO_TYPE_Q6_K)
             dcqo_quantize_row_q6_K(xr, yr, j->k);
     }
@@ -588,7 +670,9 @@ static int auto_threads(int nthreads) {
 }
 
 int dcqo_quantize_matrix(int type, const float* x, int64_t n, int64_t k, void* y, int nthreads) {
-    if (type != DCQO_TYPE_Q8_0 && type != DCQO_TYPE_Q4_K && type != DCQO_TYPE_Q6_K) return -1;
+    if (type != DCQO_TYPE_Q8_0 && type != DCQO_TYPE_Q4_0 && type != DCQO_TYPE_Q4_K && type != DCQO_TYPE_Q5_K &&
+        type != DCQO_TYPE_Q6_K)
+        return -1;
     if (dcqo_row_size(type, k) <= 0) return -2;
     int nt = auto_threads(nthreads);
     if (nt > n) nt = (int)(n > 0 ? n : 1);
@@ -613,6 +697,18 @@ static int q4k_quant(const blk_q4_K* b, int e) {
     uint8_t byte = b->qs[32 * c + l];
     return (w >= 32) ? (byte >> 4) : (byte & 0xF);
 }
+/* element e (0..255) of a Q5_K superblock: the 4-bit part as Q4_K's, plus 16 * bit (e/32) of
+ * qh[e % 32] */
+static int q5k_quant(const blk_q5_K* b, int e) {
+    int c = e / 64, w = e % 64, l = w % 32;
+    uint8_t byte = b->qs[32 * c + l];
+    int lo = (w >= 32) ? (byte >> 4) : (byte & 0xF);
+    return lo + 16 * ((b->qh[l] >> (e / 32)) & 1);
+}
+/* element j (0..31) of a Q4_0 block: unsigned 4-bit quant q (the value is d * (q - 8)) */
+static int q4_0_quant(const blk_q4_0* b, int j) {
+    return j < 16 ? (b->qs[j] & 0xF) : (b->qs[j - 16] >> 4);
+}
 /* element e of a Q6_K superblock: signed 6-bit quant q - 32 */
 static int q6k_quant(const blk_q6_K* b, int e) {
     int h = e / 128, ep = e % 128, t = ep / 32, l = ep % 32;
@@ -629,6 +725,13 @@ int dcqo_dequantize_row(int type, const void* vx, float* y, int64_t k) {
             float d = dcqo_fp16_to_fp32(x[i].d);
             for (int j = 0; j < QK8_0; ++j) y[i * QK8_0 + j] = x[i].qs[j] * d;
         }
+    } else if (type == DCQO_TYPE_Q4_0) {
+        /* dequantize_row_q4_0: (q - 8) * d */
+        const blk_q4_0* x = (const blk_q4_0*)vx;
+        for (int64_t i = 0; i < k / QK8_0; ++i) {
+            float d = dcqo_fp16_to_fp32(x[i].d);
+            for (int j = 0; j < QK8_0; ++j) y[i * QK8_0 + j] = (q4_0_quant(&x[i], j) - 8) * d;
+        }
     } else if (type == DCQO_TYPE_Q4_K) {
         const blk_q4_K* x = (const blk_q4_K*)vx;
         for (int64_t i = 0; i < k / QK_K; ++i) {
@@ -637,6 +740,17 @@ int dcqo_dequantize_row(int type, const void* vx, float* y, int64_t k) {
                 uint8_t sc, m;
                 get_scale_min_k4(e / 32, x[i].scales, &sc, &m);
                 y[i * QK_K + e] = d * sc * q4k_quant(&x[i], e) - dmin * m;
+            }
+        }
+    } else if (type == DCQO_TYPE_Q5_K) {
+        /* dequantize_row_q5_K: (d * sc) * q - dmin * m, q in [0, 31] */
+        const blk_q5_K* x = (const blk_q5_K*)vx;
+        for (int64_t i = 0; i < k / QK_K; ++i) {
+            float d = dcqo_fp16_to_fp32(x[i].d), dmin = dcqo_fp16_to_fp32(x[i].dmin);
+            for (int e = 0; e < QK_K; ++e) {
+                uint8_t sc, m;
+                get_scale_min_k4(e / 32, x[i].scales, &sc, &m);
+                y[i * QK_K + e] = d * sc * q5k_quant(&x[i], e) - dmin * m;
             }
         }
     } else if (type == DCQO_TYPE_Q6_K) {
@@ -668,22 +782,42 @@ static float vec_dot_q8_0_q8_0(int64_t n, const blk_q8_0* x, const blk_q8_0* y) 
     return sumf;
 }
 
-/* integer parts of one Q4_K x Q8_K superblock, as the generic kernel forms
- * them: aux32[8] lanes of sum sc_j*q4*q8 and the mins sum over bsums */
-static void q4k_superblock_ints(const blk_q4_K* x, const blk_q8_K* y, int32_t aux32[8],
-                                int32_t* mins_sum) {
+/* vec_dot_q4_0_q8_0 (generic): per block the integer sum of (q - 8) * q8 over both halves, then
+ * sumf += (sumi * dx) * dy, the products in that order */
+static float vec_dot_q4_0_q8_0(int64_t n, const blk_q4_0* x, const blk_q8_0* y) {
+    float sumf = 0;
+    for (int64_t ib = 0; ib < n / QK8_0; ++ib) {
+        int sumi0 = 0, sumi1 = 0;
+        for (int j = 0; j < QK8_0 / 2; ++j) {
+            sumi0 += ((x[ib].qs[j] & 0x0F) - 8) * y[ib].qs[j];
+            sumi1 += ((x[ib].qs[j] >> 4) - 8) * y[ib].qs[j + QK8_0 / 2];
+        }
+        const int sumi = sumi0 + sumi1;
+        sumf += sumi * dcqo_fp16_to_fp32(x[ib].d) * dcqo_fp16_to_fp32(y[ib].d);
+    }
+    return sumf;
+}
+
+/* integer parts of one Q4_K (qh == NULL) or Q5_K x Q8_K superblock, as the generic kernels form
+ * them: aux32[8] lanes of sum sc_j*q*q8 and the mins sum over bsums. q is the nibble, plus 16
+ * where bit j of qh[l] is set for element l of sub-block j (Q5_K). */
+static void kq_superblock_ints(const uint8_t* qs, const uint8_t* qh, const uint8_t* scales,
+                               const blk_q8_K* y, int32_t aux32[8], int32_t* mins_sum) {
     int8_t a[QK_K];
-    const uint8_t* q4 = x->qs;
+    const uint8_t* q4 = qs;
     int8_t* p = a;
+    uint8_t mbit = 1;
     for (int j = 0; j < QK_K / 64; ++j) {
-        for (int l = 0; l < 32; ++l) p[l] = (int8_t)(q4[l] & 0xF);
+        for (int l = 0; l < 32; ++l) p[l] = (int8_t)((q4[l] & 0xF) + (qh && (qh[l] & mbit) ? 16 : 0));
         p += 32;
-        for (int l = 0; l < 32; ++l) p[l] = (int8_t)(q4[l] >> 4);
+        mbit <<= 1;
+        for (int l = 0; l < 32; ++l) p[l] = (int8_t)((q4[l] >> 4) + (qh && (qh[l] & mbit) ? 16 : 0));
         p += 32;
+        mbit <<= 1;
         q4 += 32;
     }
     uint8_t sc[8], mn[8];
-    for (int j = 0; j < 8; ++j) get_scale_min_k4(j, x->scales, &sc[j], &mn[j]);
+    for (int j = 0; j < 8; ++j) get_scale_min_k4(j, scales, &sc[j], &mn[j]);
     int32_t sumi = 0;
     for (int j = 0; j < QK_K / 16; ++j) sumi += y->bsums[j] * mn[j / 2];
     *mins_sum = sumi;
@@ -700,15 +834,33 @@ static void q4k_superblock_ints(const blk_q4_K* x, const blk_q8_K* y, int32_t au
     }
 }
 
-static float vec_dot_q4_K_q8_K(int64_t n, const blk_q4_K* x, const blk_q8_K* y) {
+static void q4k_superblock_ints(const blk_q4_K* x, const blk_q8_K* y, int32_t aux32[8], int32_t* mins_sum) {
+    kq_superblock_ints(x->qs, NULL, x->scales, y, aux32, mins_sum);
+}
+static void q5k_superblock_ints(const blk_q5_K* x, const blk_q8_K* y, int32_t aux32[8], int32_t* mins_sum) {
+    kq_superblock_ints(x->qs, x->qh, x->scales, y, aux32, mins_sum);
+}
+
+/* vec_dot_q4_K_q8_K and vec_dot_q5_K_q8_K (generic): the same float steps over their integer
+ * parts (the 4-byte d/dmin header sits at the start of both blocks) */
+static float vec_dot_kq_q8_K(int wtype, int64_t n, const void* vx, const blk_q8_K* y) {
     float sums[8] = {0};
     float sumf = 0;
     for (int64_t i = 0; i < n / QK_K; ++i) {
         int32_t aux32[8], mins_sum;
-        q4k_superblock_ints(&x[i], &y[i], aux32, &mins_sum);
-        const float d = dcqo_fp16_to_fp32(x[i].d) * y[i].d;
+        uint16_t xd, xdmin;
+        if (wtype == DCQO_TYPE_Q5_K) {
+            const blk_q5_K* x = (const blk_q5_K*)vx + i;
+            q5k_superblock_ints(x, &y[i], aux32, &mins_sum);
+            xd = x->d, xdmin = x->dmin;
+        } else {
+            const blk_q4_K* x = (const blk_q4_K*)vx + i;
+            q4k_superblock_ints(x, &y[i], aux32, &mins_sum);
+            xd = x->d, xdmin = x->dmin;
+        }
+        const float d = dcqo_fp16_to_fp32(xd) * y[i].d;
         for (int l = 0; l < 8; ++l) sums[l] += d * aux32[l];
-        const float dmin = dcqo_fp16_to_fp32(x[i].dmin) * y[i].d;
+        const float dmin = dcqo_fp16_to_fp32(xdmin) * y[i].d;
         sumf -= dmin * mins_sum;
     }
     for (int l = 0; l < 8; ++l) sumf += sums[l];
@@ -760,7 +912,9 @@ static float vec_dot_q6_K_q8_K(int64_t n, const blk_q6_K* x, const blk_q8_K* y) 
 float dcqo_vec_dot(int wtype, int64_t k, const void* w, const void* xq) {
     switch (wtype) {
         case DCQO_TYPE_Q8_0: return vec_dot_q8_0_q8_0(k, (const blk_q8_0*)w, (const blk_q8_0*)xq);
-        case DCQO_TYPE_Q4_K: return vec_dot_q4_K_q8_K(k, (const blk_q4_K*)w, (const blk_q8_K*)xq);
+        case DCQO_TYPE_Q4_0: return vec_dot_q4_0_q8_0(k, (const blk_q4_0*)w, (const blk_q8_0*)xq);
+        case DCQO_TYPE_Q4_K:
+        case DCQO_TYPE_Q5_K: return vec_dot_kq_q8_K(wtype, k, w, (const blk_q8_K*)xq);
         case DCQO_TYPE_Q6_K: return vec_dot_q6_K_q8_K(k, (const blk_q6_K*)w, (const blk_q8_K*)xq);
         default: return 0.0f;
     }
@@ -768,8 +922,10 @@ float dcqo_vec_dot(int wtype, int64_t k, const void* w, const void* xq) {
 
 int64_t dcqo_block_sums_per_row(int wtype, int64_t k) {
     switch (wtype) {
+        case DCQO_TYPE_Q4_0:
         case DCQO_TYPE_Q8_0: return k / QK8_0;
-        case DCQO_TYPE_Q4_K: return 2 * (k / QK_K);
+        case DCQO_TYPE_Q4_K:
+        case DCQO_TYPE_Q5_K: return 2 * (k / QK_K);
         case DCQO_TYPE_Q6_K: return k / QK_K;
         default: return 0;
     }
@@ -785,12 +941,23 @@ int dcqo_block_sums(int wtype, int64_t k, const void* w, const void* xq, int32_t
             for (int j = 0; j < QK8_0; ++j) s += x[ib].qs[j] * y[ib].qs[j];
             out[ib] = s;
         }
-    } else if (wtype == DCQO_TYPE_Q4_K) {
-        const blk_q4_K* x = (const blk_q4_K*)w;
+    } else if (wtype == DCQO_TYPE_Q4_0) {
+        const blk_q4_0* x = (const blk_q4_0*)w;
+        const blk_q8_0* y = (const blk_q8_0*)xq;
+        for (int64_t ib = 0; ib < k / QK8_0; ++ib) {
+            int s = 0;
+            for (int j = 0; j < QK8_0 / 2; ++j)
+                s += ((x[ib].qs[j] & 0x0F) - 8) * y[ib].qs[j] + ((x[ib].qs[j] >> 4) - 8) * y[ib].qs[j + 16];
+            out[ib] = s;
+        }
+    } else if (wtype == DCQO_TYPE_Q4_K || wtype == DCQO_TYPE_Q5_K) {
         const blk_q8_K* y = (const blk_q8_K*)xq;
         for (int64_t i = 0; i < k / QK_K; ++i) {
             int32_t aux32[8], mins_sum, s = 0;
-            q4k_superblock_ints(&x[i], &y[i], aux32, &mins_sum);
+            if (wtype == DCQO_TYPE_Q5_K)
+                q5k_superblock_ints((const blk_q5_K*)w + i, &y[i], aux32, &mins_sum);
+            else
+                q4k_superblock_ints((const blk_q4_K*)w + i, &y[i], aux32, &mins_sum);
             for (int l = 0; l < 8; ++l) s += aux32[l];
             out[2 * i] = s;
             out[2 * i + 1] = mins_sum;
@@ -823,15 +990,27 @@ int dcqo_block_sums_bruteforce(int wtype, int64_t k, const void* w, const void* 
                 s += (int64_t)x[e / QK8_0].qs[e % QK8_0] * y[e / QK8_0].qs[e % QK8_0];
             out[e0 / QK8_0] = s;
         }
-    } else if (wtype == DCQO_TYPE_Q4_K) {
-        const blk_q4_K* x = (const blk_q4_K*)w;
+    } else if (wtype == DCQO_TYPE_Q4_0) {
+        const blk_q4_0* x = (const blk_q4_0*)w;
+        const blk_q8_0* y = (const blk_q8_0*)xq;
+        for (int64_t e0 = 0; e0 < k; e0 += QK8_0) {
+            int64_t s = 0;
+            for (int64_t e = e0; e < e0 + QK8_0; ++e)
+                s += (int64_t)(q4_0_quant(&x[e / QK8_0], (int)(e % QK8_0)) - 8) * y[e / QK8_0].qs[e % QK8_0];
+            out[e0 / QK8_0] = s;
+        }
+    } else if (wtype == DCQO_TYPE_Q4_K || wtype == DCQO_TYPE_Q5_K) {
         const blk_q8_K* y = (const blk_q8_K*)xq;
         for (int64_t i = 0; i < k / QK_K; ++i) {
+            const blk_q4_K* x4 = (const blk_q4_K*)w + i;
+            const blk_q5_K* x5 = (const blk_q5_K*)w + i;
+            const uint8_t* scales = wtype == DCQO_TYPE_Q5_K ? x5->scales : x4->scales;
             int64_t a = 0, b = 0;
             for (int e = 0; e < QK_K; ++e) {
                 uint8_t sc, m;
-                get_scale_min_k4(e / 32, x[i].scales, &sc, &m);
-                a += (int64_t)sc * q4k_quant(&x[i], e) * y[i].qs[e];
+                get_scale_min_k4(e / 32, scales, &sc, &m);
+                const int q = wtype == DCQO_TYPE_Q5_K ? q5k_quant(x5, e) : q4k_quant(x4, e);
+                a += (int64_t)sc * q * y[i].qs[e];
                 b += (int64_t)m * y[i].qs[e];
             }
             out[2 * i] = a;
@@ -862,6 +1041,14 @@ double dcqo_vec_dot_f64(int wtype, int64_t k, const void* w, const void* xq) {
             double av = (double)dcqo_fp16_to_fp32(y[e / 32].d) * y[e / 32].qs[e % 32];
             s += wv * av;
         }
+    } else if (wtype == DCQO_TYPE_Q4_0) {
+        const blk_q4_0* x = (const blk_q4_0*)w;
+        const blk_q8_0* y = (const blk_q8_0*)xq;
+        for (int64_t e = 0; e < k; ++e) {
+            double wv = (double)dcqo_fp16_to_fp32(x[e / 32].d) * (q4_0_quant(&x[e / 32], (int)(e % 32)) - 8);
+            double av = (double)dcqo_fp16_to_fp32(y[e / 32].d) * y[e / 32].qs[e % 32];
+            s += wv * av;
+        }
     } else if (wtype == DCQO_TYPE_Q4_K) {
         const blk_q4_K* x = (const blk_q4_K*)w;
         const blk_q8_K* y = (const blk_q8_K*)xq;
@@ -870,6 +1057,18 @@ double dcqo_vec_dot_f64(int wtype, int64_t k, const void* w, const void* xq) {
             uint8_t sc, m;
             get_scale_min_k4((int)(e % QK_K) / 32, b->scales, &sc, &m);
             double wv = (double)dcqo_fp16_to_fp32(b->d) * sc * q4k_quant(b, (int)(e % QK_K)) -
+                        (double)dcqo_fp16_to_fp32(b->dmin) * m;
+            double av = (double)y[e / QK_K].d * y[e / QK_K].qs[e % QK_K];
+            s += wv * av;
+        }
+    } else if (wtype == DCQO_TYPE_Q5_K) {
+        const blk_q5_K* x = (const blk_q5_K*)w;
+        const blk_q8_K* y = (const blk_q8_K*)xq;
+        for (int64_t e = 0; e < k; ++e) {
+            const blk_q5_K* b = &x[e / QK_K];
+            uint8_t sc, m;
+            get_scale_min_k4((int)(e % QK_K) / 32, b->scales, &sc, &m);
+            double wv = (double)dcqo_fp16_to_fp32(b->d) * sc * q5k_quant(b, (int)(e % QK_K)) -
                         (double)dcqo_fp16_to_fp32(b->dmin) * m;
             double av = (double)y[e / QK_K].d * y[e / QK_K].qs[e % QK_K];
             s += wv * av;
@@ -890,25 +1089,38 @@ double dcqo_vec_dot_f64(int wtype, int64_t k, const void* w, const void* xq) {
 
 double dcqo_vec_dot_l1(int wtype, int64_t k, const void* w, const void* xq) {
     double s = 0.0;
-    if (wtype == DCQO_TYPE_Q8_0) {
-        const blk_q8_0* x = (const blk_q8_0*)w;
+    if (wtype == DCQO_TYPE_Q8_0 || wtype == DCQO_TYPE_Q4_0) {
+        /* the block terms dW * dA * I_b (the 2-byte fp16 d opens both block layouts) */
+        const size_t wbs = wtype == DCQO_TYPE_Q8_0 ? sizeof(blk_q8_0) : sizeof(blk_q4_0);
         const blk_q8_0* y = (const blk_q8_0*)xq;
         int32_t* ib = (int32_t*)malloc(sizeof(int32_t) * (size_t)(k / 32));
         dcqo_block_sums(wtype, k, w, xq, ib);
-        for (int64_t b = 0; b < k / 32; ++b)
-            s += fabs((double)dcqo_fp16_to_fp32(x[b].d) * dcqo_fp16_to_fp32(y[b].d) * ib[b]);
+        for (int64_t b = 0; b < k / 32; ++b) {
+            uint16_t dw;
+            memcpy(&dw, (const char*)w + b * wbs, 2);
+            s += fabs((double)dcqo_fp16_to_fp32(dw) * dcqo_fp16_to_fp32(y[b].d) * ib[b]);
+        }
         free(ib);
-    } else if (wtype == DCQO_TYPE_Q4_K) {
-        /* the terms vec_dot_q4_K_q8_K adds in fp32: the eight lane sums d * aux32[l] of each
-         * superblock (they can cancel to a much smaller superblock total) and the mins term */
-        const blk_q4_K* x = (const blk_q4_K*)w;
+    } else if (wtype == DCQO_TYPE_Q4_K || wtype == DCQO_TYPE_Q5_K) {
+        /* the terms vec_dot_q4_K_q8_K / vec_dot_q5_K_q8_K add in fp32: the eight lane sums
+         * d * aux32[l] of each superblock (they can cancel to a much smaller superblock total)
+         * and the mins term */
         const blk_q8_K* y = (const blk_q8_K*)xq;
         for (int64_t b = 0; b < k / QK_K; ++b) {
             int32_t aux32[8], mins_sum;
-            q4k_superblock_ints(&x[b], &y[b], aux32, &mins_sum);
-            const double d = (double)dcqo_fp16_to_fp32(x[b].d) * y[b].d;
+            uint16_t xd, xdmin;
+            if (wtype == DCQO_TYPE_Q5_K) {
+                const blk_q5_K* x = (const blk_q5_K*)w + b;
+                q5k_superblock_ints(x, &y[b], aux32, &mins_sum);
+                xd = x->d, xdmin = x->dmin;
+            } else {
+                const blk_q4_K* x = (const blk_q4_K*)w + b;
+                q4k_superblock_ints(x, &y[b], aux32, &mins_sum);
+                xd = x->d, xdmin = x->dmin;
+            }
+            const double d = (double)dcqo_fp16_to_fp32(xd) * y[b].d;
             for (int l = 0; l < 8; ++l) s += fabs(d * aux32[l]);
-            s += fabs((double)dcqo_fp16_to_fp32(x[b].dmin) * y[b].d * mins_sum);
+            s += fabs((double)dcqo_fp16_to_fp32(xdmin) * y[b].d * mins_sum);
         }
     } else if (wtype == DCQO_TYPE_Q6_K) {
         /* the eight lane sums d * aux32[l] of each superblock, as vec_dot_q6_K_q8_K adds them */

@@ -11,11 +11,12 @@
  * reference's own files contribute only the call sites:
  *   - quantize X once with the weight type's vec_dot_type `from_float`, then a
  *     per-row `vec_dot` (core/src/inference.cpp:887-923);
- *   - vec_dot_type mapping Q4_K/Q6_K -> Q8_K, Q8_0 -> Q8_0
- *     (core/include/simd_ops.h:3298-3305);
+ *   - vec_dot_type mapping Q4_K/Q5_K/Q6_K -> Q8_K, Q8_0 -> Q8_0
+ *     (core/include/simd_ops.h:3298-3305); Q4_0 -> Q8_0 (ggml's trait for the
+ *     quantize tool's default type, core/src/quantize.cpp:71-72, 90);
  *   - row-range contract with pre-quantized input (core/src/simd_ops.cpp:140-171).
  * The arithmetic below follows ggml's published algorithms for the GGUF block
- * formats Q8_0 / Q4_K / Q6_K / Q8_K, restated from their definitions.
+ * formats Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K / Q8_K, restated from their definitions.
  *
  * Parity pins (each function lists its own in dcq_oracle.c):
  *   - fp16 conversion: numpy float16 (IEEE RNE) on 2^20+ values and all ties.
@@ -30,7 +31,7 @@
  *   - the choice between the two Q8_0 from_float variants (x86 SIMD vs ref);
  *   - the Q8_K scale constant: iscale = -127/max (ggml's quantize_row_q8_K_ref in the
  *     type-traits-cpu API era the reference's calls imply; older ggml used -128);
- *   - the constants of the Q4_K / Q6_K weight quantizers' grid searches, and so their bytes
+ *   - the constants of the Q4_K / Q5_K / Q6_K weight quantizers' grid searches, and so their bytes
  *     against a ggml build — used only to generate inputs.
  */
 #ifndef DCQ_ORACLE_H
@@ -47,8 +48,10 @@ extern "C" {
 enum {
     DCQO_TYPE_F32 = 0,
     DCQO_TYPE_F16 = 1,
+    DCQO_TYPE_Q4_0 = 2,
     DCQO_TYPE_Q8_0 = 8,
     DCQO_TYPE_Q4_K = 12,
+    DCQO_TYPE_Q5_K = 13,
     DCQO_TYPE_Q6_K = 14,
     DCQO_TYPE_Q8_K = 15,
 };
@@ -80,7 +83,9 @@ void dcqo_quantize_rows(int vec_dot_type, const float* x, int64_t m, int64_t k, 
 
 /* ---- weight quantizers (input generation only) ---- */
 void dcqo_quantize_row_q8_0_weights(const float* x, void* y, int64_t k);
+void dcqo_quantize_row_q4_0(const float* x, void* y, int64_t k);
 void dcqo_quantize_row_q4_K(const float* x, void* y, int64_t k);
+void dcqo_quantize_row_q5_K(const float* x, void* y, int64_t k);
 void dcqo_quantize_row_q6_K(const float* x, void* y, int64_t k);
 /* quantize an [n][k] fp32 matrix to `type`, rows packed; nthreads <= 0 -> auto */
 int dcqo_quantize_matrix(int type, const float* x, int64_t n, int64_t k, void* y, int nthreads);
@@ -115,7 +120,8 @@ int64_t dcqo_block_sums_per_row(int wtype, int64_t k);
 /*
  * Per-block integer sums, the exact integers each vec_dot scales:
  *   Q8_0: I_b = sum_{32} qw*qa                          (k/32 values)
- *   Q4_K: per superblock {sum_j sc_j*I_j, sum_j m_j*S_j} (2*k/256 values)
+ *   Q4_0: I_b = sum_{32} (qw - 8)*qa                    (k/32 values)
+ *   Q4_K, Q5_K: per superblock {sum_j sc_j*I_j, sum_j m_j*S_j} (2*k/256 values)
  *   Q6_K: per superblock sum_g sc_g*I_g                  (k/256 values)
  */
 int dcqo_block_sums(int wtype, int64_t k, const void* w, const void* xq, int32_t* out);

@@ -13,7 +13,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 8, 12, 14, 15
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_K = 0, 1, 2, 8, 12, 13, 14, 15
 Q8_0_X86, Q8_0_REF = 0, 1
 
 _lib = None
@@ -145,8 +145,8 @@ def vec_dot_f64(wt, k, w_row, xq_row):
 
 def vec_dot_l1(wt, k, w_row, xq_row):
     """Sum of the magnitudes of the fp32 terms the reference's vec_dot adds: |d_b * I_b| per
-    Q8_0 block; for Q4_K / Q6_K the eight per-superblock lane sums |d * aux32[l]| (plus the
-    Q4_K mins term), which can cancel to a much smaller superblock total."""
+    Q8_0 / Q4_0 block; for Q4_K / Q5_K / Q6_K the eight per-superblock lane sums |d * aux32[l]|
+    (plus the Q4_K / Q5_K mins term), which can cancel to a much smaller superblock total."""
     w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
     xq_row = np.ascontiguousarray(xq_row, dtype=np.uint8)
     return float(lib().dcqo_vec_dot_l1(wt, k, _p(w_row), _p(xq_row)))
@@ -281,7 +281,8 @@ PLANT_NO_MIN_CLAMP, PLANT_UNIT_WEIGHTS, PLANT_GRID_8 = 1, 2, 4
 
 
 def make_qkx2_quants(x, weights, nmax=15, rmin=-1.0, rdelta=0.1, nstep=20, flags=0):
-    """The Q4_K sub-block fit x ~ scale * L + min (min <= 0): returns (scale, min, L uint8)."""
+    """The Q4_K (defaults) or Q5_K (nmax=31, rmin=-0.5, nstep=15) sub-block fit x ~ scale * L + min
+    (min <= 0): returns (scale, min, L uint8)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     weights = np.ascontiguousarray(weights, dtype=np.float32)
     L = np.zeros(x.size, dtype=np.uint8)

@@ -11,7 +11,7 @@ import pytest
 
 from densecore_amd import synth
 
-Q8_0, Q4_K, Q6_K, Q8_K = 8, 12, 14, 15
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 2, 8, 12, 13, 14, 15
 
 
 # ---------------------------------------------------------------- format parsers (GGUF spec)
@@ -135,7 +135,7 @@ def test_q8_K_zero_block_bsums_and_bounds(O):
 
 
 # ---------------------------------------------------------------- integer block sums
-@pytest.mark.parametrize("wt,k", [(Q8_0, 1024), (Q4_K, 2560), (Q6_K, 2048)])
+@pytest.mark.parametrize("wt,k", [(Q8_0, 1024), (Q4_0, 1024), (Q4_K, 2560), (Q5_K, 2560), (Q6_K, 2048)])
 def test_block_sums_match_bruteforce(O, wt, k):
     """Structured (ggml loop order, bsums for Q4_K mins) vs element-wise int64 brute force."""
     w = synth.normal(6 * k, 11, 0, 0.02).reshape(6, k)
@@ -154,7 +154,7 @@ def test_block_sums_match_bruteforce(O, wt, k):
 def test_block_sums_extreme_magnitudes(O):
     """All-(-128)/127 activations with the largest weight codes stay exact in int32."""
     k = 512
-    for wt in (Q8_0, Q4_K, Q6_K):
+    for wt in (Q8_0, Q4_0, Q4_K, Q5_K, Q6_K):
         w = np.where(np.arange(k) % 2 == 0, 1.0, -1.0).astype(np.float32)[None, :] * 0.05
         wq = O.quantize_matrix(wt, w)
         x = np.full((1, k), -3.0, np.float32)
@@ -164,7 +164,8 @@ def test_block_sums_extreme_magnitudes(O):
 
 
 # ---------------------------------------------------------------- vec_dot vs fp64
-@pytest.mark.parametrize("wt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2560), (Q6_K, 9728)])
+@pytest.mark.parametrize("wt,k", [(Q8_0, 1024), (Q8_0, 96), (Q4_0, 1024), (Q4_0, 96), (Q4_K, 2560),
+                                  (Q5_K, 2560), (Q6_K, 9728)])
 def test_vec_dot_matches_fp64(O, wt, k):
     """The fp32 vec_dot is within fp32 rounding of the exact dequantized dot (catches a dropped
     mins term, a wrong scale index, a sign error)."""
@@ -183,7 +184,7 @@ def test_vec_dot_approximates_float_dot(O):
     """The quantized dot is close to the float dot of the original data (catches an element
     permutation that is consistent between dequantize and vec_dot but wrong)."""
     k = 4096
-    for wt, tol in ((Q8_0, 0.02), (Q6_K, 0.05), (Q4_K, 0.15)):
+    for wt, tol in ((Q8_0, 0.02), (Q6_K, 0.05), (Q5_K, 0.08), (Q4_K, 0.15), (Q4_0, 0.15)):
         w = synth.normal(16 * k, 31, 0, 0.02).reshape(16, k)
         x = synth.normal(k, 32)
         wq = O.quantize_matrix(wt, w)
@@ -195,7 +196,7 @@ def test_vec_dot_approximates_float_dot(O):
 
 
 # ---------------------------------------------------------------- weight quantizers (round trip)
-@pytest.mark.parametrize("wt,bound", [(Q8_0, 0.006), (Q6_K, 0.03), (Q4_K, 0.11)])
+@pytest.mark.parametrize("wt,bound", [(Q8_0, 0.006), (Q6_K, 0.03), (Q5_K, 0.05), (Q4_K, 0.11), (Q4_0, 0.11)])
 def test_weight_quantizer_round_trip(O, wt, bound):
     k = 2048
     w = synth.normal(32 * k, 41, 0, 0.02).reshape(32, k)
@@ -234,6 +235,71 @@ def test_q4_K_element_layout_constructed(O):
     assert np.array_equal(got, want)
 
 
+def test_q5_K_element_layout_constructed(O):
+    """A hand-packed Q5_K block (d = 0.5, dmin = 0.25, distinct 6-bit scales and mins): element e
+    of sub-block j has the 5-bit quant q = (e * 11) % 32, its low four bits in the Q4_K nibble
+    position and its fifth bit in bit j of qh[e % 32]; the value is 0.5 sc_j q - 0.25 m_j."""
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.25], np.float16).view(np.uint8)
+    sc = [1, 2, 3, 4, 37, 45, 50, 63]
+    mn = [63, 0, 17, 5, 33, 48, 1, 20]
+    for j in range(4):
+        blk[4 + j] = sc[j] | ((sc[j + 4] >> 4) << 6)
+        blk[8 + j] = mn[j] | ((mn[j + 4] >> 4) << 6)
+        blk[12 + j] = (sc[j + 4] & 0xF) | ((mn[j + 4] & 0xF) << 4)
+    q = (np.arange(256) * 11) % 32
+    for e in range(256):
+        j, l = divmod(e, 32)
+        blk[48 + 32 * (j // 2) + l] |= (q[e] & 0xF) << (4 * (j % 2))
+        blk[16 + l] |= (q[e] >> 4) << j
+    got = O.dequantize_row(Q5_K, blk, 256)
+    want = np.array([np.float32(0.5 * sc[e // 32]) * np.float32(q[e]) - np.float32(0.25 * mn[e // 32])
+                     for e in range(256)], np.float32)
+    assert np.array_equal(got, want)
+
+
+def test_q4_0_element_layout_constructed(O):
+    """A hand-packed Q4_0 block: element j < 16 in the low nibble of qs[j], element j + 16 in its
+    high nibble, value (q - 8) * d."""
+    q = (np.arange(32) * 5 + 3) % 16
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([-0.375], np.float16).view(np.uint8)
+    blk[2:] = q[:16] | (q[16:] << 4)
+    got = O.dequantize_row(Q4_0, blk, 32)
+    assert np.array_equal(got, ((q - 8) * -0.375).astype(np.float32))
+
+
+def test_q4_0_weight_quantizer_closed_forms(O):
+    """quantize_row_q4_0_ref: d = max / -8 where max is the first element of largest magnitude, so
+    that element stores q = 0; every other q is the nearest of the 16 levels (q - 8) * d to x (a
+    truncation without the + 0.5 fails this), the +8 level clamped to q = 15; an all-zero block is
+    d = 0 with every q = 8. Blocks here hold both signs of the maximum magnitude and ties."""
+    k = 32 * 64
+    w = synth.normal(k, 71, 0, 0.02)
+    w[32:64] = 0.0                                  # all-zero block
+    w[64 + 5], w[64 + 9] = -0.07, 0.07              # both signs of the maximum, negative first
+    w[96 + 3] = 0.05                                # positive maximum
+    w[128:160] = np.float32(0.01) * np.arange(-16, 16, dtype=np.float32) / 8  # exact levels
+    wq = O.quantize_matrix(Q4_0, w[None, :])[0].reshape(-1, 18)
+    d = wq[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    q = np.concatenate([wq[:, 2:] & 0xF, wq[:, 2:] >> 4], axis=1).astype(np.int64)
+    xb = w.reshape(-1, 32)
+    assert d[1] == 0 and np.all(q[1] == 8)
+    for b in range(xb.shape[0]):
+        if not np.any(xb[b]):
+            continue
+        i = int(np.argmax(np.abs(xb[b])))
+        d32 = np.float32(xb[b, i]) / np.float32(-8)
+        assert d[b] == np.float16(d32), b
+        assert q[b, i] == 0, b
+        levels = (np.arange(16) - 8)[None, :] * np.float64(d32)
+        dist = np.abs(xb[b].astype(np.float64)[:, None] - levels)
+        chosen = dist[np.arange(32), q[b]]
+        assert np.all(chosen <= dist.min(axis=1) + 1e-6 * abs(d32)), b
+    assert q[2, 5] == 0 and q[2, 9] == 15  # -0.07 first: d > 0, +0.07 clamps to the top level
+
+
 def test_q6_K_element_layout_constructed(O):
     """A hand-packed Q6_K block: element e has quant (e * 7) % 64 and scale (g + 1) * (-1)^g."""
     q = (np.arange(256) * 7) % 64
@@ -255,7 +321,7 @@ def test_q6_K_element_layout_constructed(O):
 def test_mul_mat_one_hot_columns(O):
     """X = one-hot rows picks columns of the dequantized W (scaled by the Q8 code of 1.0)."""
     k, n = 512, 12
-    for wt in (Q8_0, Q4_K, Q6_K):
+    for wt in (Q8_0, Q4_0, Q4_K, Q5_K, Q6_K):
         w = synth.normal(n * k, 51, 0, 0.02).reshape(n, k)
         wq = O.quantize_matrix(wt, w)
         deq = np.stack([O.dequantize_row(wt, wq[r], k) for r in range(n)])
@@ -266,7 +332,7 @@ def test_mul_mat_one_hot_columns(O):
         y, _ = O.mul_mat(wt, wq, x)
         xq = O.quantize_rows(O.vec_dot_type(wt), x)
         for i, c in enumerate(cols):
-            if wt == Q8_0:
+            if wt in (Q8_0, Q4_0):
                 d, qs = parse_q8_0(xq[i], k)
                 scale = d[c // 32] * qs[c // 32][c % 32]
             else:

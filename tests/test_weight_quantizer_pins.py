@@ -1,4 +1,4 @@
-"""Pins of the oracle's weight quantizers (Q4_K, Q6_K; the ggml_quantize_chunk step of
+"""Pins of the oracle's weight quantizers (Q4_K, Q5_K, Q6_K; the ggml_quantize_chunk step of
 core/src/quantize.cpp:214, 285) by what the mathematics fixes, without ggml.
 
 The published algorithm (ggml's quantize_row_q4_K_ref / quantize_row_q6_K_ref) fits each sub-block
@@ -9,6 +9,7 @@ check each part by its defining property:
     what the search over its 22 candidates gives (the rounding at 15/(max-min), then the 21 grid
     points (-1 + 0.1*is + 15)/(max-min), each refitted by weighted least squares with min <= 0 and
     kept if its weighted squared error is smaller; a kept refit's min offsets the later roundings);
+    Q5_K runs the same search with L in [0, 31], 16 grid points (-0.5 + 0.1*is + 31)/(max-min);
   - make_qx_quants (Q6_K, 16 elements, L in [-32, 31], x ~ scale*L): the result is one of the 19
     candidates (-(32 + 0.1*is)/max, is in [-9, 9]) and maximises the x^2-weighted fit quality;
   - the 6-bit scale/min packing inverts exactly under the GGUF decode formula;
@@ -139,16 +140,21 @@ def _qkx2_outcomes(x, w, nmax=15, rmin=-1.0, rdelta=0.1, nstep=20, limit=256):
     return [(st[0], st[1], st[2]) for st in states]
 
 
-def _check_qkx2(x, scale, mn, L):
+Q4K_SEARCH = dict(nmax=15, rmin=-1.0, rdelta=0.1, nstep=20)
+Q5K_SEARCH = dict(nmax=31, rmin=-0.5, rdelta=0.1, nstep=15)
+
+
+def _check_qkx2(x, scale, mn, L, search=Q4K_SEARCH):
     """None if (scale, min, L) is a result of the grid search, else the reason it is not."""
     w = _q4k_weights(x)
+    nmax = search["nmax"]
     if x.max() == min(x.min(), 0):
         return None if (scale == 0 and np.all(L == 0)) else "constant block"
-    if L.min() < 0 or L.max() > 15:
-        return "L outside [0, 15]"
+    if L.min() < 0 or L.max() > nmax:
+        return f"L outside [0, {nmax}]"
     if mn > 0:
         return f"min {mn} > 0"
-    outs = _qkx2_outcomes(x, w)
+    outs = _qkx2_outcomes(x, w, **search)
     if outs is None:
         return "too many branches"
     match = [o for o in outs if np.array_equal(o[2], L)]
@@ -162,8 +168,8 @@ def _check_qkx2(x, scale, mn, L):
     return None
 
 
-def _branch_count(x):
-    return [len(_qkx2_outcomes(xb, _q4k_weights(xb)) or [0] * 999) for xb in x]
+def _branch_count(x, search=Q4K_SEARCH):
+    return [len(_qkx2_outcomes(xb, _q4k_weights(xb), **search) or [0] * 999) for xb in x]
 
 
 def test_make_qkx2_quants_is_the_grid_optimum(O):
@@ -185,6 +191,31 @@ def test_make_qkx2_quants_planted_mistakes_fail(O, plant):
     for xb in x:
         scale, mn, L = O.make_qkx2_quants(xb, _q4k_weights(xb), **kw)
         failures += _check_qkx2(xb, scale, mn, L.astype(np.int64)) is not None
+    assert failures > 0, f"planted mistake {plant} passed every check"
+
+
+def test_make_qkx2_quants_q5_K_is_the_grid_optimum(O):
+    """The Q5_K sub-block fit (nmax 31, rmin -0.5, nstep 15) is its grid search's result."""
+    x = np.concatenate([_subblocks(32, 300, 15), _clustered(32, 300, 17)])
+    n_out = _branch_count(x, Q5K_SEARCH)
+    assert max(n_out) <= 16 and sum(n > 1 for n in n_out) < 0.1 * len(x), n_out
+    for i, xb in enumerate(x):
+        scale, mn, L = O.make_qkx2_quants(xb, _q4k_weights(xb), **Q5K_SEARCH)
+        r = _check_qkx2(xb, scale, mn, L.astype(np.int64), Q5K_SEARCH)
+        assert r is None, (i, r)
+
+
+@pytest.mark.parametrize("plant", ["q4k_grid", "nstep14", "rmin-1"])
+def test_make_qkx2_quants_q5_K_planted_mistakes_fail(O, plant):
+    """Q5_K fits made with a wrong argument (Q4_K's grid, one grid point short, Q4_K's rmin) are
+    rejected by the Q5_K check."""
+    x = np.concatenate([_subblocks(32, 300, 15), _clustered(32, 300, 17)])
+    kw = {"q4k_grid": dict(Q5K_SEARCH, nstep=20, rmin=-1.0), "nstep14": dict(Q5K_SEARCH, nstep=14),
+          "rmin-1": dict(Q5K_SEARCH, rmin=-1.0)}[plant]
+    failures = 0
+    for xb in x:
+        scale, mn, L = O.make_qkx2_quants(xb, _q4k_weights(xb), **kw)
+        failures += _check_qkx2(xb, scale, mn, L.astype(np.int64), Q5K_SEARCH) is not None
     assert failures > 0, f"planted mistake {plant} passed every check"
 
 
@@ -286,6 +317,39 @@ def test_q4_K_quants_are_nearest_and_scales_rounded(O):
                 grid = dj * np.arange(16)[None, :] - mj
                 dist = np.abs(xj[:, None] - grid)
                 chosen = dist[np.arange(32), nib]
+                assert np.all(chosen <= dist.min(axis=1) + 1e-6 * dj), (n, b, j)
+
+
+def test_q5_K_quants_are_nearest_and_scales_rounded(O):
+    """Final pass of the Q5_K quantizer: each 6-bit sub-block scale is the nearest integer of
+    63 * scale_j / max_j scale_j for the Q5_K fits, and every stored 5-bit quant (low nibble plus
+    the qh bit, read back through dequantize_row) is the nearest of the 32 levels
+    d*sc*L - dmin*m to x."""
+    N, K = 8, 1024
+    w = synth.normal(N * K, 23, 0.0, 0.02).reshape(N, K)
+    w[0, :256] = np.abs(w[0, :256]) + np.float32(0.01)
+    w[2, 300] = np.float32(0.3)
+    q = O.quantize_matrix(13, w).reshape(N, K // 256, 176)
+    for n in range(N):
+        for b in range(K // 256):
+            blk = q[n, b].astype(np.int64)
+            d = O.fp16_to_fp32(q[n, b, 0:2].copy().view(np.uint16))[0]
+            dmin = O.fp16_to_fp32(q[n, b, 2:4].copy().view(np.uint16))[0]
+            xs = w[n, 256 * b:256 * (b + 1)]
+            fits = [O.make_qkx2_quants(xs[32 * j:32 * j + 32], _q4k_weights(xs[32 * j:32 * j + 32]), **Q5K_SEARCH)
+                    for j in range(8)]
+            smax = max(f[0] for f in fits)
+            vals = O.dequantize_row(13, q[n, b], 256).astype(np.float64)
+            for j in range(8):
+                sc, m = _decode_scale_min(blk[4:16], j)
+                assert abs(sc - 63 * fits[j][0] / smax) <= 0.5 + 1e-4, (n, b, j)
+                if sc == 0:
+                    continue
+                dj, mj = np.float64(d) * sc, np.float64(dmin) * m
+                xj = xs[32 * j:32 * j + 32].astype(np.float64)
+                grid = dj * np.arange(32)[None, :] - mj
+                dist = np.abs(xj[:, None] - grid)
+                chosen = np.abs(xj - vals[32 * j:32 * j + 32])
                 assert np.all(chosen <= dist.min(axis=1) + 1e-6 * dj), (n, b, j)
 
 
