@@ -7,8 +7,8 @@ memory and streams). There is no CPU fallback: every compute entry point calls
 the HIP library, and importing the binding fails loudly when libdcq.so is
 missing.
 """
-from .configs import (CONFIGS, TYPE_F16, TYPE_F32, TYPE_NAMES, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0,  # noqa: F401
-                      TYPE_Q8_K, Config, by_index)
+from .configs import (CONFIGS, TYPE_F16, TYPE_F32, TYPE_NAMES, TYPE_Q4_0, TYPE_Q4_K, TYPE_Q5_K,  # noqa: F401
+                      TYPE_Q6_K, TYPE_Q8_0, TYPE_Q8_K, Config, by_index)
 from ._lib import (GGUF, KV_BLOCK_SIZE, PagedKVCache, kv_attention_workspace_size, kv_slot_bytes,  # noqa: F401
                    DcqError, LIB_PATH, block_size, block_sums_per_row, build, dequantize_rows,  # noqa: F401
                    dot_rows, ffn_gate_up, ffn_gate_up_workspace_size, lib, mul_mat, mul_mat_add,
@@ -23,6 +23,7 @@ __all__ = [
     "NOALLOC_SCRATCH_BYTES", "probe_stream_read", "mul_mat_add",
     "mul_mat_add_workspace_size", "dot_rows", "ffn_gate_up",
     "ffn_gate_up_workspace_size", "quantize_weights", "dequantize_rows", "PATH_AUTO",
-    "PATH_GEMV", "PATH_MMQ", "TYPE_F32", "TYPE_F16", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q6_K", "TYPE_Q8_K",
+    "PATH_GEMV", "PATH_MMQ", "TYPE_F32", "TYPE_F16", "TYPE_Q4_0", "TYPE_Q8_0", "TYPE_Q4_K", "TYPE_Q5_K",
+    "TYPE_Q6_K", "TYPE_Q8_K",
     "TYPE_NAMES", "KV_BLOCK_SIZE", "PagedKVCache", "kv_slot_bytes", "kv_attention_workspace_size",
 ]

@@ -8,12 +8,15 @@ from dataclasses import dataclass
 
 TYPE_F32 = 0
 TYPE_F16 = 1
+TYPE_Q4_0 = 2
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
+TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q8_K = 15
 
-TYPE_NAMES = {TYPE_Q8_0: "Q8_0", TYPE_Q4_K: "Q4_K", TYPE_Q6_K: "Q6_K", TYPE_Q8_K: "Q8_K"}
+TYPE_NAMES = {TYPE_Q4_0: "Q4_0", TYPE_Q8_0: "Q8_0", TYPE_Q4_K: "Q4_K", TYPE_Q5_K: "Q5_K", TYPE_Q6_K: "Q6_K",
+              TYPE_Q8_K: "Q8_K"}
 
 
 @dataclass(frozen=True)

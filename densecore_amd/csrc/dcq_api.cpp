@@ -17,7 +17,7 @@
 namespace dcq {
 
 size_t planar_bytes(int vdt, int64_t M, int64_t K, PlanarBuffers* pb, void* base) {
-    const int64_t bs = vdt == kTypeQ8_0 ? QK8_0 : QK_K;
+    const int64_t bs = vdt == kTypeQ8_0 ? QK8_0 : QK_K;  // the activation types: Q8_0 or Q8_K
     const int64_t m_ld = round_up(M, 128);  // >= every MFMA m-tile, so float4 scale loads stay in bounds
     const size_t qs_b = (size_t)round_up(M * K, 256);
     const size_t d_b = (size_t)round_up((K / bs) * m_ld * 4, 256);
@@ -86,7 +86,9 @@ using namespace dcq;
 
 namespace {
 
-bool is_weight_type(int t) { return t == kTypeQ8_0 || t == kTypeQ4_K || t == kTypeQ6_K; }
+bool is_weight_type(int t) {
+    return t == kTypeQ8_0 || t == kTypeQ4_0 || t == kTypeQ4_K || t == kTypeQ5_K || t == kTypeQ6_K;
+}
 
 // The kernels are built for gfx950 only; refuse other devices loudly.
 int check_device() {
@@ -121,7 +123,7 @@ int validate_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_ro
     if (!aligned(W, 16) || !aligned(X, 16) || !aligned(Y, 4)) return DCQ_ERR_MISALIGNED;
     if (x_stride_bytes % 16 || y_stride_bytes % 4) return DCQ_ERR_MISALIGNED;
     if (w_row_bytes % 2) return DCQ_ERR_MISALIGNED;
-    if (wtype == kTypeQ4_K && w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
+    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
     return DCQ_OK;
 }
 
@@ -165,8 +167,10 @@ int64_t dcq_block_size(int type) {
     switch (type) {
         case DCQ_TYPE_F32:
         case DCQ_TYPE_F16: return 1;
+        case DCQ_TYPE_Q4_0:
         case DCQ_TYPE_Q8_0: return QK8_0;
         case DCQ_TYPE_Q4_K:
+        case DCQ_TYPE_Q5_K:
         case DCQ_TYPE_Q6_K:
         case DCQ_TYPE_Q8_K: return QK_K;
         default: return 0;
@@ -177,8 +181,10 @@ int64_t dcq_type_size(int type) {
     switch (type) {
         case DCQ_TYPE_F32: return 4;
         case DCQ_TYPE_F16: return 2;
+        case DCQ_TYPE_Q4_0: return (int64_t)sizeof(BlockQ4_0);
         case DCQ_TYPE_Q8_0: return (int64_t)sizeof(BlockQ8_0);
         case DCQ_TYPE_Q4_K: return (int64_t)sizeof(BlockQ4_K);
+        case DCQ_TYPE_Q5_K: return (int64_t)sizeof(BlockQ5_K);
         case DCQ_TYPE_Q6_K: return (int64_t)sizeof(BlockQ6_K);
         case DCQ_TYPE_Q8_K: return (int64_t)sizeof(BlockQ8_K);
         default: return 0;
@@ -193,8 +199,10 @@ size_t dcq_row_size(int type, int64_t k) {
 
 int dcq_vec_dot_type(int wtype) {
     switch (wtype) {
+        case DCQ_TYPE_Q4_0:
         case DCQ_TYPE_Q8_0: return DCQ_TYPE_Q8_0;
         case DCQ_TYPE_Q4_K:
+        case DCQ_TYPE_Q5_K:
         case DCQ_TYPE_Q6_K: return DCQ_TYPE_Q8_K;
         default: return DCQ_ERR_UNSUPPORTED;
     }
@@ -207,8 +215,10 @@ int dcq_supports_mul_mat(int wtype, int xtype, int ytype) {
 int64_t dcq_block_sums_per_row(int wtype, int64_t k) {
     if (!is_weight_type(wtype) || k <= 0 || k % dcq_block_size(wtype)) return 0;
     switch (wtype) {
+        case DCQ_TYPE_Q4_0:
         case DCQ_TYPE_Q8_0: return k / QK8_0;
-        case DCQ_TYPE_Q4_K: return 2 * (k / QK_K);
+        case DCQ_TYPE_Q4_K:
+        case DCQ_TYPE_Q5_K: return 2 * (k / QK_K);
         default: return k / QK_K;
     }
 }
@@ -481,7 +491,7 @@ int dcq_dot_rows(int wtype, const void* W, size_t w_row_bytes, const void* Xq, i
     if (w_row_bytes < dcq_row_size(wtype, K)) return DCQ_ERR_INVALID_ARG;
     if (!aligned(W, 16) || !aligned(Y, 4)) return DCQ_ERR_MISALIGNED;
     if (w_row_bytes % 2) return DCQ_ERR_MISALIGNED;
-    if (wtype == kTypeQ4_K && w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
+    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
     const int vdt = dcq_vec_dot_type(wtype);
     if (!aligned(Xq, vdt == kTypeQ8_K ? 4 : 2)) return DCQ_ERR_MISALIGNED;
     if (n1 == n0) return DCQ_OK;

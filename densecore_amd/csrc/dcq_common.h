@@ -5,7 +5,11 @@
 // DenseCore's own Metal shader restates for Q8_0
 // (core/shaders/quantized_gemv.metal:85-88):
 //   Q8_0 (32 elems, 34 B):  { half d; int8 qs[32]; }                 value = d*qs[i]
+//   Q4_0 (32 elems, 18 B):  { half d; u8 qs[16]; }  elems i, i+16 = low, high nibble of qs[i];
+//                                                   value = d*(q - 8)
 //   Q4_K (256 elems, 144 B):{ half d; half dmin; u8 scales[12]; u8 qs[128]; }
+//   Q5_K (256 elems, 176 B):{ half d; half dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]; }
+//                           qs as Q4_K's nibbles; bit j of qh[l] = bit 4 of elem l of sub-block j
 //   Q6_K (256 elems, 210 B):{ u8 ql[128]; u8 qh[64]; i8 scales[16]; half d; }
 //   Q8_K (256 elems, 292 B):{ float d; i8 qs[256]; i16 bsums[16]; }
 //
@@ -27,8 +31,10 @@ namespace dcq {
 
 constexpr int kTypeF32 = 0;
 constexpr int kTypeF16 = 1;
+constexpr int kTypeQ4_0 = 2;
 constexpr int kTypeQ8_0 = 8;
 constexpr int kTypeQ4_K = 12;
+constexpr int kTypeQ5_K = 13;
 constexpr int kTypeQ6_K = 14;
 constexpr int kTypeQ8_K = 15;
 
@@ -39,10 +45,21 @@ struct __attribute__((packed)) BlockQ8_0 {
     uint16_t d;
     int8_t qs[QK8_0];
 };
+struct __attribute__((packed)) BlockQ4_0 {
+    uint16_t d;
+    uint8_t qs[QK8_0 / 2];
+};
 struct BlockQ4_K {
     uint16_t d;
     uint16_t dmin;
     uint8_t scales[12];
+    uint8_t qs[QK_K / 2];
+};
+struct BlockQ5_K {
+    uint16_t d;
+    uint16_t dmin;
+    uint8_t scales[12];
+    uint8_t qh[QK_K / 8];
     uint8_t qs[QK_K / 2];
 };
 struct BlockQ6_K {
@@ -57,7 +74,9 @@ struct BlockQ8_K {
     int16_t bsums[QK_K / 16];
 };
 static_assert(sizeof(BlockQ8_0) == 34, "Q8_0 block is 34 bytes");
+static_assert(sizeof(BlockQ4_0) == 18, "Q4_0 block is 18 bytes");
 static_assert(sizeof(BlockQ4_K) == 144, "Q4_K block is 144 bytes");
+static_assert(sizeof(BlockQ5_K) == 176, "Q5_K block is 176 bytes");
 static_assert(sizeof(BlockQ6_K) == 210, "Q6_K block is 210 bytes");
 static_assert(sizeof(BlockQ8_K) == 292, "Q8_K block is 292 bytes");
 
@@ -91,6 +110,16 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
 }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Four unsigned 4-bit values (one per byte, 0..15) to the signed bytes q - 8, per byte without
+// borrows: (q | 0x80) - 8 = 0x78 + q stays in its byte, and the xor turns 0x80 + (q - 8) into
+// the two's complement byte of q - 8.
+__device__ __forceinline__ uint32_t minus8(uint32_t q) { return ((q | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+// Q5_K levels of one sub-block: the nibbles (already shifted down to bits 0..3 of each byte) with
+// bit `bit` of each qh byte as bit 4.
+__device__ __forceinline__ uint32_t q5_levels(uint32_t nib, uint32_t qh, uint32_t bit) {
+    return (nib & 0x0F0F0F0Fu) | (((qh >> bit) & 0x01010101u) << 4);
+}
 
 // (hi:lo) >> (8*shift), low 32 bits; shift in bytes (0..3).
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t shift) {

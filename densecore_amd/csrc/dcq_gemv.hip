@@ -6,21 +6,29 @@
 //
 // Work unit: 64 weight elements of one row.
 //   Q8_0: a pair of 34-byte blocks (68 B, 17 dwords, dword aligned when K % 64 == 0)
+//   Q4_0: a pair of 18-byte blocks (36 B, 9 dwords, dword aligned when K % 64 == 0), or one
+//         block read as 9 halfwords otherwise; nibbles become signed q - 8 bytes per dword
 //   Q4_K: a quarter superblock: 32 B of nibbles (sub-blocks 2c and 2c+1) + the 16 B header
+//   Q5_K: as Q4_K, plus the superblock's 32 B of fifth bits (bits 2c, 2c+1 of each byte)
 //   Q6_K: (half h, column group l0): 16 B ql low, 16 B ql high, 16 B qh + scales + d; the
 //         superblock is only 2-byte aligned, so pieces are re-aligned with v_alignbyte.
 // Each lane issues the loads of all its units before any arithmetic (clamped
 // indices keep every access inside the tensor), so a wave has up to
 // UPL x (48..68) bytes in flight per lane — the decode path is HBM-bound.
 // Integer sums per block are exact (sdot4 with int32 accumulation); the fp32
-// scale products follow vec_dot's form: Q8_0 I*(dW*dA); Q4_K dA*(d*sum sc*I -
-// dmin*sum m*S); Q6_K (dA*d)*sum sc*I. Lanes reduce with shuffles (DPP).
+// scale products follow vec_dot's form: Q8_0 and Q4_0 I*(dW*dA); Q4_K and Q5_K
+// dA*(d*sum sc*I - dmin*sum m*S); Q6_K (dA*d)*sum sc*I. Lanes reduce with shuffles (DPP).
 #include "dcq_common.h"
 #include "dcq_kernels.h"
 
 namespace dcq {
 
-enum GemvFmt { kQ8_0Pair = 0, kQ8_0Single = 1, kQ4K = 2, kQ6K = 3 };
+enum GemvFmt { kQ8_0Pair = 0, kQ8_0Single = 1, kQ4K = 2, kQ6K = 3, kQ4_0Pair = 4, kQ4_0Single = 5, kQ5K = 6 };
+
+// int32 block sums per row (the DUMP layout)
+__host__ __device__ constexpr int64_t sums_per_row(int f, int64_t K) {
+    return (f == kQ4K || f == kQ5K) ? 2 * (K / 256) : f == kQ6K ? K / 256 : K / 32;
+}
 
 // ---------------------------------------------------------------- raw unit loads
 struct RawQ8Pair {
@@ -36,6 +44,16 @@ struct RawQ4K {
 struct RawQ6K {
     uint32_t a[4], b[4], h[4], sc[4];
     uint32_t d;
+};
+struct RawQ4_0Pair {
+    uint32_t w[9];
+};
+struct RawQ4_0Single {
+    uint32_t d;
+    uint32_t q[4];
+};
+struct RawQ5K {
+    uint4 hdr, h0, h1, q0, q1;
 };
 
 template <int F>
@@ -55,6 +73,18 @@ struct RawOf<kQ4K> {
 template <>
 struct RawOf<kQ6K> {
     using T = RawQ6K;
+};
+template <>
+struct RawOf<kQ4_0Pair> {
+    using T = RawQ4_0Pair;
+};
+template <>
+struct RawOf<kQ4_0Single> {
+    using T = RawQ4_0Single;
+};
+template <>
+struct RawOf<kQ5K> {
+    using T = RawQ5K;
 };
 
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, RawQ8Pair& r) {
@@ -79,6 +109,29 @@ __device__ __forceinline__ void load_unit(const uint8_t* row, int u, RawQ4K& r) 
     r.hdr = ld16(sb);
     r.q0 = ld16(sb + 16 + 32 * c);
     r.q1 = ld16(sb + 32 + 32 * c);
+}
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, RawQ4_0Pair& r) {
+    const uint8_t* p = row + (int64_t)u * 36;
+    const U32x4 a = ld4(p), b = ld4(p + 16);
+    r.w[0] = a.x; r.w[1] = a.y; r.w[2] = a.z; r.w[3] = a.w;
+    r.w[4] = b.x; r.w[5] = b.y; r.w[6] = b.z; r.w[7] = b.w;
+    r.w[8] = ld1(p + 32);
+}
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, RawQ4_0Single& r) {
+    // one 18-byte block at 2-byte alignment: 9 halfword loads, never outside the block
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(row + (int64_t)u * 18);
+    r.d = p[0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.q[i] = (uint32_t)p[1 + 2 * i] | ((uint32_t)p[2 + 2 * i] << 16);
+}
+__device__ __forceinline__ void load_unit(const uint8_t* row, int u, RawQ5K& r) {
+    const uint8_t* sb = row + (int64_t)(u >> 2) * 176;
+    const int c = u & 3;
+    r.hdr = ld16(sb);
+    r.h0 = ld16(sb + 16);
+    r.h1 = ld16(sb + 32);
+    r.q0 = ld16(sb + 48 + 32 * c);
+    r.q1 = ld16(sb + 64 + 32 * c);
 }
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, RawQ6K& r) {
     const uint8_t* sb = row + (int64_t)(u >> 2) * 210;
@@ -145,6 +198,34 @@ __device__ __forceinline__ float unit_dot(const RawQ8Single& r, int u, const int
     return (float)i0 * (half_bits_to_float(r.d) * dA);
 }
 
+// The scale step of a Q4_K / Q5_K quarter superblock c of superblock s (the two headers are the
+// same 16 bytes): i0, i1 are the integer sums of sub-blocks 2c, 2c + 1, bsv the activation's
+// four 16-element sums of those sub-blocks. Returns dA * (d * (sc0 i0 + sc1 i1) - dmin * (m0 S0 +
+// m1 S1)).
+template <bool DUMP>
+__device__ __forceinline__ float kq_quarter_finish(const uint4& hdr, int s, int c, uint2 bsv, float dA, int i0,
+                                                   int i1, int32_t* sums_row, bool valid) {
+    // 6-bit scales / mins of sub-blocks j = 2c, 2c+1 (all eight unpacked SWAR-style)
+    const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
+    const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, mn_lo = s1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
+    const uint32_t scw = c < 2 ? sc_lo : sc_hi, mnw = c < 2 ? mn_lo : mn_hi;
+    const uint32_t sh = (uint32_t)(c & 1) * 16u;
+    const int sc0 = (int)((scw >> sh) & 0xFFu), sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
+    const int m0 = (int)((mnw >> sh) & 0xFFu), m1 = (int)((mnw >> (sh + 8)) & 0xFFu);
+    const int S0 = (int)(int16_t)(bsv.x & 0xFFFFu) + (int)(int16_t)(bsv.x >> 16);
+    const int S1 = (int)(int16_t)(bsv.y & 0xFFFFu) + (int)(int16_t)(bsv.y >> 16);
+    const int iA = sc0 * i0 + sc1 * i1;
+    const int iB = m0 * S0 + m1 * S1;
+    if (DUMP && valid) {
+        atomicAdd(sums_row + 2 * s, iA);
+        atomicAdd(sums_row + 2 * s + 1, iB);
+    }
+    const float d = half_bits_to_float(hdr.x & 0xFFFFu), dmin = half_bits_to_float(hdr.x >> 16);
+    return dA * fmaf(-dmin, (float)iB, d * (float)iA);
+}
+
 template <bool DUMP>
 __device__ __forceinline__ float unit_dot(const RawQ4K& r, int u, const int8_t* xrow, const float* xd,
                                           int64_t m_ld, int64_t m, const int16_t* xbs_row, int32_t* sums_row,
@@ -172,25 +253,87 @@ __device__ __forceinline__ float unit_dot(const RawQ4K& r, int u, const int8_t* 
     i1 = sdot4((int)((r.q1.y >> 4) & lo), (int)a3.y, i1);
     i1 = sdot4((int)((r.q1.z >> 4) & lo), (int)a3.z, i1);
     i1 = sdot4((int)((r.q1.w >> 4) & lo), (int)a3.w, i1);
-    // 6-bit scales / mins of sub-blocks j = 2c, 2c+1 (all eight unpacked SWAR-style)
-    const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
-    const uint32_t sc_lo = s0 & 0x3F3F3F3Fu, mn_lo = s1 & 0x3F3F3F3Fu;
-    const uint32_t sc_hi = (s2 & 0x0F0F0F0Fu) | ((s0 >> 2) & 0x30303030u);
-    const uint32_t mn_hi = ((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u);
-    const uint32_t scw = c < 2 ? sc_lo : sc_hi, mnw = c < 2 ? mn_lo : mn_hi;
-    const uint32_t sh = (uint32_t)(c & 1) * 16u;
-    const int sc0 = (int)((scw >> sh) & 0xFFu), sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
-    const int m0 = (int)((mnw >> sh) & 0xFFu), m1 = (int)((mnw >> (sh + 8)) & 0xFFu);
-    const int S0 = (int)(int16_t)(bsv.x & 0xFFFFu) + (int)(int16_t)(bsv.x >> 16);
-    const int S1 = (int)(int16_t)(bsv.y & 0xFFFFu) + (int)(int16_t)(bsv.y >> 16);
-    const int iA = sc0 * i0 + sc1 * i1;
-    const int iB = m0 * S0 + m1 * S1;
+    return kq_quarter_finish<DUMP>(r.hdr, s, c, bsv, dA, i0, i1, sums_row, valid);
+}
+
+template <bool DUMP>
+__device__ __forceinline__ float unit_dot(const RawQ5K& r, int u, const int8_t* xrow, const float* xd,
+                                          int64_t m_ld, int64_t m, const int16_t* xbs_row, int32_t* sums_row,
+                                          bool valid) {
+    const int s = u >> 2, c = u & 3;
+    const int8_t* ap = xrow + 256 * s + 64 * c;
+    const uint4 a0 = ld16(ap), a1 = ld16(ap + 16), a2 = ld16(ap + 32), a3 = ld16(ap + 48);
+    const uint2 bsv = *reinterpret_cast<const uint2*>(xbs_row + 16 * s + 4 * c);
+    const float dA = xd[(int64_t)s * m_ld + m];
+    // sub-block 2c: low nibbles with qh bit 2c; sub-block 2c + 1: high nibbles with bit 2c + 1
+    const uint32_t b0 = 2u * (uint32_t)c, b1 = b0 + 1u;
+    int i0 = 0, i1 = 0;
+    i0 = sdot4((int)q5_levels(r.q0.x, r.h0.x, b0), (int)a0.x, i0);
+    i0 = sdot4((int)q5_levels(r.q0.y, r.h0.y, b0), (int)a0.y, i0);
+    i0 = sdot4((int)q5_levels(r.q0.z, r.h0.z, b0), (int)a0.z, i0);
+    i0 = sdot4((int)q5_levels(r.q0.w, r.h0.w, b0), (int)a0.w, i0);
+    i0 = sdot4((int)q5_levels(r.q1.x, r.h1.x, b0), (int)a1.x, i0);
+    i0 = sdot4((int)q5_levels(r.q1.y, r.h1.y, b0), (int)a1.y, i0);
+    i0 = sdot4((int)q5_levels(r.q1.z, r.h1.z, b0), (int)a1.z, i0);
+    i0 = sdot4((int)q5_levels(r.q1.w, r.h1.w, b0), (int)a1.w, i0);
+    i1 = sdot4((int)q5_levels(r.q0.x >> 4, r.h0.x, b1), (int)a2.x, i1);
+    i1 = sdot4((int)q5_levels(r.q0.y >> 4, r.h0.y, b1), (int)a2.y, i1);
+    i1 = sdot4((int)q5_levels(r.q0.z >> 4, r.h0.z, b1), (int)a2.z, i1);
+    i1 = sdot4((int)q5_levels(r.q0.w >> 4, r.h0.w, b1), (int)a2.w, i1);
+    i1 = sdot4((int)q5_levels(r.q1.x >> 4, r.h1.x, b1), (int)a3.x, i1);
+    i1 = sdot4((int)q5_levels(r.q1.y >> 4, r.h1.y, b1), (int)a3.y, i1);
+    i1 = sdot4((int)q5_levels(r.q1.z >> 4, r.h1.z, b1), (int)a3.z, i1);
+    i1 = sdot4((int)q5_levels(r.q1.w >> 4, r.h1.w, b1), (int)a3.w, i1);
+    return kq_quarter_finish<DUMP>(r.hdr, s, c, bsv, dA, i0, i1, sums_row, valid);
+}
+
+// Q4_0 block: sum over its 32 elements of (q - 8) * a; q[0..3] hold the 16 bytes of nibbles
+// (elements 0..15 low, 16..31 high), lo / hi the activation's elements 0..15 / 16..31.
+__device__ __forceinline__ int q4_0_block_dot(const uint32_t (&q)[4], const uint4& lo, const uint4& hi) {
+    const uint32_t m = 0x0F0F0F0Fu;
+    int i = 0;
+    i = sdot4((int)minus8(q[0] & m), (int)lo.x, i);
+    i = sdot4((int)minus8(q[1] & m), (int)lo.y, i);
+    i = sdot4((int)minus8(q[2] & m), (int)lo.z, i);
+    i = sdot4((int)minus8(q[3] & m), (int)lo.w, i);
+    i = sdot4((int)minus8((q[0] >> 4) & m), (int)hi.x, i);
+    i = sdot4((int)minus8((q[1] >> 4) & m), (int)hi.y, i);
+    i = sdot4((int)minus8((q[2] >> 4) & m), (int)hi.z, i);
+    i = sdot4((int)minus8((q[3] >> 4) & m), (int)hi.w, i);
+    return i;
+}
+
+template <bool DUMP>
+__device__ __forceinline__ float unit_dot(const RawQ4_0Pair& r, int u, const int8_t* xrow, const float* xd,
+                                          int64_t m_ld, int64_t m, const int16_t*, int32_t* sums_row,
+                                          bool valid) {
+    const uint4 a0 = ld16(xrow + 64 * u), a1 = ld16(xrow + 64 * u + 16);
+    const uint4 a2 = ld16(xrow + 64 * u + 32), a3 = ld16(xrow + 64 * u + 48);
+    const float dA0 = xd[(int64_t)(2 * u) * m_ld + m], dA1 = xd[(int64_t)(2 * u + 1) * m_ld + m];
+    const uint32_t* w = r.w;
+    // block 0: d in bytes 0..1, nibbles in bytes 2..17; block 1: d in bytes 18..19, nibbles 20..35
+    const uint32_t q0[4] = {align_bytes(w[1], w[0], 2), align_bytes(w[2], w[1], 2), align_bytes(w[3], w[2], 2),
+                            align_bytes(w[4], w[3], 2)};
+    const uint32_t q1[4] = {w[5], w[6], w[7], w[8]};
+    const int i0 = q4_0_block_dot(q0, a0, a1);
+    const int i1 = q4_0_block_dot(q1, a2, a3);
+    const float dW0 = half_bits_to_float(w[0] & 0xFFFFu), dW1 = half_bits_to_float(w[4] >> 16);
     if (DUMP && valid) {
-        atomicAdd(sums_row + 2 * s, iA);
-        atomicAdd(sums_row + 2 * s + 1, iB);
+        atomicAdd(sums_row + 2 * u, i0);
+        atomicAdd(sums_row + 2 * u + 1, i1);
     }
-    const float d = half_bits_to_float(r.hdr.x & 0xFFFFu), dmin = half_bits_to_float(r.hdr.x >> 16);
-    return dA * fmaf(-dmin, (float)iB, d * (float)iA);
+    return fmaf((float)i1, dW1 * dA1, (float)i0 * (dW0 * dA0));
+}
+
+template <bool DUMP>
+__device__ __forceinline__ float unit_dot(const RawQ4_0Single& r, int u, const int8_t* xrow, const float* xd,
+                                          int64_t m_ld, int64_t m, const int16_t*, int32_t* sums_row,
+                                          bool valid) {
+    const uint4 a0 = ld16(xrow + 32 * u), a1 = ld16(xrow + 32 * u + 16);
+    const float dA = xd[(int64_t)u * m_ld + m];
+    const int i0 = q4_0_block_dot(r.q, a0, a1);
+    if (DUMP && valid) atomicAdd(sums_row + u, i0);
+    return (float)i0 * (half_bits_to_float(r.d) * dA);
 }
 
 template <bool DUMP>
@@ -252,8 +395,8 @@ __global__ void __launch_bounds__(256) gemv_kernel(const uint8_t* __restrict__ W
     const bool row_ok = row < n1;
     const int64_t rowc = row_ok ? row : n1 - 1;
     const uint8_t* wrow = W + rowc * w_row_bytes;
-    const int U = (F == kQ8_0Single) ? K / 32 : K / 64;
-    const int64_t per_row_sums = (F == kQ4K) ? 2 * (K / 256) : (F == kQ6K) ? K / 256 : K / 32;
+    const int U = (F == kQ8_0Single || F == kQ4_0Single) ? K / 32 : K / 64;
+    const int64_t per_row_sums = sums_per_row(F, K);
 
     float acc[MT];
 #pragma unroll
@@ -330,6 +473,9 @@ static GemvFn pick_fmt(int f, int mt, int upl) {
         case kQ8_0Pair: return pick_mt<kQ8_0Pair, DUMP>(mt, upl);
         case kQ8_0Single: return pick_mt<kQ8_0Single, DUMP>(mt, upl);
         case kQ4K: return pick_mt<kQ4K, DUMP>(mt, upl);
+        case kQ4_0Pair: return pick_mt<kQ4_0Pair, DUMP>(mt, upl);
+        case kQ4_0Single: return pick_mt<kQ4_0Single, DUMP>(mt, upl);
+        case kQ5K: return pick_mt<kQ5K, DUMP>(mt, upl);
         default: return pick_mt<kQ6K, DUMP>(mt, upl);
     }
 }
@@ -353,13 +499,18 @@ hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0
     }
     if (R) return hipErrorNotSupported;  // the generic kernels have no add in their store
     int f;
+    const bool pairs = K % 64 == 0 && w_row_bytes % 4 == 0;  // two 32-blocks per unit, dword aligned
     if (wtype == kTypeQ8_0)
-        f = (K % 64 == 0 && w_row_bytes % 4 == 0) ? kQ8_0Pair : kQ8_0Single;
+        f = pairs ? kQ8_0Pair : kQ8_0Single;
+    else if (wtype == kTypeQ4_0)
+        f = pairs ? kQ4_0Pair : kQ4_0Single;
     else if (wtype == kTypeQ4_K)
         f = kQ4K;
+    else if (wtype == kTypeQ5_K)
+        f = kQ5K;
     else
         f = kQ6K;
-    const int U = (f == kQ8_0Single) ? (int)(K / 32) : (int)(K / 64);
+    const int U = (f == kQ8_0Single || f == kQ4_0Single) ? (int)(K / 32) : (int)(K / 64);
     // lanes per row: smallest power of two covering the row's units (capped at a wave)
     int lg = 0;
     while ((1 << lg) < U && lg < 6) ++lg;
@@ -368,7 +519,7 @@ hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0
     const int64_t rows = n1 - n0;
     const int64_t rows_per_block = 4 * (64 / G);
     const unsigned grid = (unsigned)((rows + rows_per_block - 1) / rows_per_block);
-    const int64_t per_row_sums = (wtype == kTypeQ4_K) ? 2 * (K / 256) : (wtype == kTypeQ6_K) ? K / 256 : K / 32;
+    const int64_t per_row_sums = sums_per_row(f, K);
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;

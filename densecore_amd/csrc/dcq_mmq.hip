@@ -3,7 +3,7 @@
 // Replaces ggml's CPU MUL_MAT at M > 1 (core/src/inference.cpp:1049-1063 routes
 // every M > 1 projection there; executed at core/src/worker.cpp:544).
 //
-// Tiling. MFMA v_mfma_i32_32x32x32_i8 (Q8_0, Q4_K) / v_mfma_i32_32x32x16_i8
+// Tiling. MFMA v_mfma_i32_32x32x32_i8 (Q8_0, Q4_0, Q4_K, Q5_K) / v_mfma_i32_32x32x16_i8
 // (Q6_K, whose scales are per 16 elements). Operand roles: A = activations
 // (MFMA rows = m), B = weights (MFMA columns = n), so every lane of the 32x32
 // result owns ONE weight row n = lane % 32 and 16 activation rows
@@ -23,6 +23,8 @@
 //     result read as fp32 is 12582912 + I exactly (|I| <= 32*127*128 < 2^22);
 //     t = fma(F, dW, -dW*12582912) is then dW*I rounded once, and
 //     acc = fma(t, dA, acc): two VALU ops per output per 32-block.
+//   Q4_0: the same, on the nibbles turned into signed q - 8 bytes as they are loaded
+//     (|I| <= 32*8*128 < 2^22 as well).
 //   Q4_K: acc_i += sc_j * I_j (v_mad_i32_i24) per 32-sub-block; the mins term
 //     sum_j m_j * S_j runs on the MFMA against a weight operand whose bytes all
 //     equal m_j; per superblock acc += dA * (d * acc_i - dmin * acc_min).
@@ -32,6 +34,8 @@
 //     int8), and sum_j m_j S_j from the activation's 16-element sums: S_j = 64 hi_j +
 //     lo_j (lo_j in [0, 63], hi_j in [-64, 63]) as int8 bytes against the bytes m_j,
 //     two MFMAs per tile per superblock instead of eight.
+//   Q5_K: the Q4_K steps on the 5-bit levels (nibble plus the qh bit). Levels up to 31 times
+//     sc_hi up to 7 do not fit int8, so Q5_K always takes the per-sub-block form.
 //   Q6_K: acc_i += sc_g * I_g per 16-group (signed q - 32 operands); per
 //     superblock acc += dA * d * acc_i.
 #include "dcq_common.h"
@@ -145,20 +149,32 @@ struct Q8Step {
     uint32_t dw[TN];
 };
 
-template <int TM, int TN>
+// Q40: the weight blocks are Q4_0 (18 B): lane half hl takes the low (hl = 0) or high nibbles of
+// the block's 16 bytes, i.e. its elements 16 hl .. 16 hl + 15, as signed q - 8 bytes.
+template <int TM, int TN, bool Q40>
 __device__ __forceinline__ void q8_load(Q8Step<TM, TN>& s, const int8_t* const* arow, const uint8_t* const* wrow,
                                         int kb, int hl) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) s.a[i] = ld16(arow[i] + 32 * kb + 16 * hl);
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-        const uint8_t* blk = wrow[j] + 34 * (int64_t)kb;
-        ld16_a2(blk + 2 + 16 * hl, s.b[j]);
-        s.dw[j] = ldu16(blk);
+        if constexpr (Q40) {
+            const uint8_t* blk = wrow[j] + 18 * (int64_t)kb;
+            uint32_t raw[4];
+            ld16_a2(blk + 2, raw);
+            const uint32_t sh = 4u * (uint32_t)hl;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s.b[j][e] = minus8((raw[e] >> sh) & 0x0F0F0F0Fu);
+            s.dw[j] = ldu16(blk);
+        } else {
+            const uint8_t* blk = wrow[j] + 34 * (int64_t)kb;
+            ld16_a2(blk + 2 + 16 * hl, s.b[j]);
+            s.dw[j] = ldu16(blk);
+        }
     }
 }
 
-template <int TM, int TN, int WN, int WK, bool DUMP>
+template <int TM, int TN, int WN, int WK, bool DUMP, bool Q40>
 __global__ void __launch_bounds__(256) mmq_q8_0_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t N,
                                                        int64_t K, const int8_t* __restrict__ xqs,
                                                        const float* __restrict__ xd, int64_t m_ld, int64_t M,
@@ -200,10 +216,10 @@ __global__ void __launch_bounds__(256) mmq_q8_0_kernel(const uint8_t* __restrict
 
     Q8Step<TM, TN> cur, nxt;
     int kb = wk;
-    if (kb < nb) q8_load(cur, arow, wrow, kb, hl);
+    if (kb < nb) q8_load<TM, TN, Q40>(cur, arow, wrow, kb, hl);
     for (; kb < nb; kb += WK) {
         const int kn = kb + WK;
-        if (kn < nb) q8_load(nxt, arow, wrow, kn, hl);
+        if (kn < nb) q8_load<TM, TN, Q40>(nxt, arow, wrow, kn, hl);
         const float* xdb = xd + (int64_t)kb * m_ld;
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
@@ -240,14 +256,15 @@ __global__ void __launch_bounds__(256) mmq_q8_0_kernel(const uint8_t* __restrict
     if (reduce_k<TM, TN, WK>(acc, lds, wn, wk, lane)) store_tile<TM, TN>(acc, Y, y_stride, M, N, mbase, nbase, lane);
 }
 
-// ============================================================== Q4_K
-template <int TM, int TN, int WN, int WK, bool DUMP>
+// ============================================================== Q4_K and Q5_K (Q5)
+template <int TM, int TN, int WN, int WK, bool DUMP, bool Q5>
 __global__ void __launch_bounds__(256) mmq_q4_K_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t N,
                                                        int64_t K, const int8_t* __restrict__ xqs,
                                                        const float* __restrict__ xd, int64_t m_ld, int64_t M,
                                                        float* __restrict__ Y, int64_t y_stride,
                                                        int32_t* __restrict__ sums, const int16_t* __restrict__ xbs) {
-    constexpr bool kSplit = TM == 2 && TN == 2;  // see the Q4_K notes at the top
+    constexpr bool kSplit = TM == 2 && TN == 2 && !Q5;  // see the Q4_K / Q5_K notes at the top
+    constexpr int kSbBytes = Q5 ? 176 : 144, kQsOff = Q5 ? 48 : 16;
     extern __shared__ float lds[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wn = wave % WN, wk = wave / WN;
@@ -279,14 +296,17 @@ __global__ void __launch_bounds__(256) mmq_q4_K_kernel(const uint8_t* __restrict
             for (int v = 0; v < 16; ++v) acc.v[i][j][v] = 0.0f;
 
     for (int s = wk; s < nsb; s += WK) {
-        // weight fragments of this superblock: header + 4 x 16 B of nibbles per row
+        // weight fragments of this superblock: header + 4 x 16 B of nibbles per row (Q5_K: and
+        // the 16 qh bytes of this lane half's elements l = 16 hl .. 16 hl + 15)
         uint4 hdr[TN], qw[TN][4];
+        [[maybe_unused]] uint4 qhw[TN];
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const uint8_t* sb = wrow[j] + 144 * (int64_t)s;
+            const uint8_t* sb = wrow[j] + kSbBytes * (int64_t)s;
             hdr[j] = ld16(sb);
 #pragma unroll
-            for (int c = 0; c < 4; ++c) qw[j][c] = ld16(sb + 16 + 32 * c + 16 * hl);
+            for (int c = 0; c < 4; ++c) qw[j][c] = ld16(sb + kQsOff + 32 * c + 16 * hl);
+            if constexpr (Q5) qhw[j] = ld16(sb + 16 + 16 * hl);
         }
         uint4 qa[TM][8];
 #pragma unroll
@@ -394,10 +414,18 @@ __global__ void __launch_bounds__(256) mmq_q4_K_kernel(const uint8_t* __restrict
                     const uint4 q = qw[j][sub >> 1];
                     const uint32_t sh = (sub & 1) ? 4u : 0u;
                     v4i bv;
-                    bv.x = (int)((q.x >> sh) & 0x0F0F0F0Fu);
-                    bv.y = (int)((q.y >> sh) & 0x0F0F0F0Fu);
-                    bv.z = (int)((q.z >> sh) & 0x0F0F0F0Fu);
-                    bv.w = (int)((q.w >> sh) & 0x0F0F0F0Fu);
+                    if constexpr (Q5) {
+                        const uint4 h = qhw[j];
+                        bv.x = (int)q5_levels(q.x >> sh, h.x, (uint32_t)sub);
+                        bv.y = (int)q5_levels(q.y >> sh, h.y, (uint32_t)sub);
+                        bv.z = (int)q5_levels(q.z >> sh, h.z, (uint32_t)sub);
+                        bv.w = (int)q5_levels(q.w >> sh, h.w, (uint32_t)sub);
+                    } else {
+                        bv.x = (int)((q.x >> sh) & 0x0F0F0F0Fu);
+                        bv.y = (int)((q.y >> sh) & 0x0F0F0F0Fu);
+                        bv.z = (int)((q.z >> sh) & 0x0F0F0F0Fu);
+                        bv.w = (int)((q.w >> sh) & 0x0F0F0F0Fu);
+                    }
                     const int sc = (int)((scw[j][sub >> 2] >> (8 * (sub & 3))) & 0xFFu);
                     const uint32_t mb = ((mnw[j][sub >> 2] >> (8 * (sub & 3))) & 0xFFu) * 0x01010101u;
                     v4i bm;
@@ -552,8 +580,10 @@ using MmqFn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, const int8_t*,
 
 template <int TM, int TN, int WN, int WK, bool DUMP>
 static MmqFn pick_fmt(int wtype) {
-    if (wtype == kTypeQ8_0) return mmq_q8_0_kernel<TM, TN, WN, WK, DUMP>;
-    if (wtype == kTypeQ4_K) return mmq_q4_K_kernel<TM, TN, WN, WK, DUMP>;
+    if (wtype == kTypeQ8_0) return mmq_q8_0_kernel<TM, TN, WN, WK, DUMP, false>;
+    if (wtype == kTypeQ4_0) return mmq_q8_0_kernel<TM, TN, WN, WK, DUMP, true>;
+    if (wtype == kTypeQ4_K) return mmq_q4_K_kernel<TM, TN, WN, WK, DUMP, false>;
+    if (wtype == kTypeQ5_K) return mmq_q4_K_kernel<TM, TN, WN, WK, DUMP, true>;
     return mmq_q6_K_kernel<TM, TN, WN, WK, DUMP>;
 }
 
@@ -611,7 +641,7 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
         s = {2, 2, 4, 1};
     else if (M > 32)
         s = {2, 1, 1, 4};
-    else if ((K / (wtype == kTypeQ8_0 ? 32 : 256)) >= 4)
+    else if ((K / (wtype == kTypeQ8_0 || wtype == kTypeQ4_0 ? 32 : 256)) >= 4)
         s = {1, 1, 1, 4};
     else
         s = {1, 2, 4, 1};

@@ -5,8 +5,9 @@
 // (core/src/quantize.cpp:214, 285 call ggml_quantize_chunk); dequantization is
 // the reference GEMV's fallback (core/src/inference.cpp:938-945). One thread per
 // block / superblock; the search is ggml's published algorithm (make_qkx2_quants for
-// Q4_K, make_qx_quants with rmse_type 1 for Q6_K, roundf scaling for Q8_0), each fit's
-// sums in their sequential order. The Q4_K kernel holds a sub-block in registers and its
+// Q4_K and Q5_K, make_qx_quants with rmse_type 1 for Q6_K, roundf scaling for Q8_0, the
+// max / -8 scale with truncation after + 8.5 for Q4_0), each fit's sums in their sequential
+// order. The Q4_K / Q5_K kernel holds a sub-block in registers and its
 // fits in LDS (no per-thread arrays in scratch memory): 9728 x 2560 took 2.36 ms with the
 // arrays in scratch, 0.39 ms so. The same change to the Q6_K kernel measured slower
 // (0.32 -> 0.36 ms: its final levels need an LDS column per thread, which halves the
@@ -48,7 +49,43 @@ __global__ void __launch_bounds__(256) quantize_w_q8_0_kernel(const float* __res
     }
 }
 
-// ---- Q4_K ----
+// ---- Q4_0: quantize_row_q4_0_ref (d = max / -8 for the first element of largest |x|,
+// q = min(15, trunc(x / d + 8.5))) ----
+__global__ void __launch_bounds__(256) quantize_w_q4_0_kernel(const float* __restrict__ W, int64_t N, int64_t K,
+                                                              uint8_t* __restrict__ out) {
+    const int64_t nb = K / QK8_0;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= N * nb) return;
+    const int64_t r = gid / nb, b = gid - (gid / nb) * nb;
+    const float* x = W + r * K + b * QK8_0;
+    float amax = 0.0f, max = 0.0f;
+    for (int j = 0; j < QK8_0; ++j) {
+        if (amax < fabsf(x[j])) {
+            amax = fabsf(x[j]);
+            max = x[j];
+        }
+    }
+    const float d = max / -8;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t* p16 = reinterpret_cast<uint16_t*>(out + r * nb * 18 + b * 18);  // blocks are 2-byte aligned
+    // an all-zero block has d = 0 / -8 = -0.0, stored as fp16 -0.0 (0x8000). The compiler folds the
+    // fp16 conversion of the product max * -0.125 into v_fma_mix with a +0 addend, which turns a
+    // -0 product into +0, so the sign bit is taken from d itself (the product is exact, so the
+    // fold changes nothing else).
+    p16[0] = (uint16_t)(float_to_half_bits(d) | ((__float_as_uint(d) >> 16) & 0x8000u));
+    for (int j = 0; j < QK8_0 / 2; j += 2) {
+        uint32_t two = 0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            // the float -> int8 conversion truncates toward zero; x * id + 8.5 lies in [0, 17)
+            const int q0 = (int)(x[j + t] * id + 8.5f), q1 = (int)(x[16 + j + t] * id + 8.5f);
+            two |= (uint32_t)((q0 < 15 ? q0 : 15) | ((q1 < 15 ? q1 : 15) << 4)) << (8 * t);
+        }
+        p16[1 + j / 2] = (uint16_t)two;
+    }
+}
+
+// ---- Q4_K and Q5_K ----
 __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint8_t* d, uint8_t* m) {
     if (j < 4) {
         *d = q[j] & 63;
@@ -63,7 +100,7 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint8_t* d
 // rmin = -1, rdelta = 0.1, nstep = 20 (the sub-block scale and min of the least weighted squared
 // error over a grid of 21 inverse scales around nmax / (max - min), each refined by a least-squares
 // fit, min clamped to <= 0), the same fp32 operations in the same order, on the sub-block held in
-// registers. The weights av_x + |x_i| are recomputed per use (the
+// registers. quantize_row_q5_K_ref's fit is the same search with nmax = 31, rmin = -0.5, nstep = 15. The weights av_x + |x_i| are recomputed per use (the
 // same fp32 value each time), and the chosen levels L are not stored: the (iscale, min) they were
 // computed with are returned instead, so the caller recomputes them where it needs them.
 struct Qkx2Fit {
@@ -72,12 +109,14 @@ struct Qkx2Fit {
     int zero;               // max == min: every L_i is 0
 };
 
-__device__ __forceinline__ int clamp15(int l) { return l < 0 ? 0 : (l > 15 ? 15 : l); }
+template <int NMAX>
+__device__ __forceinline__ int clampq(int l) { return l < 0 ? 0 : (l > NMAX ? NMAX : l); }
 
+template <bool Q5>
 __device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
-    const int nmax = 15;
-    const float rmin = -1.f, rdelta = 0.1f;
-    const int nstep = 20;
+    constexpr int nmax = Q5 ? 31 : 15;
+    const float rmin = Q5 ? -0.5f : -1.f, rdelta = 0.1f;
+    const int nstep = Q5 ? 15 : 20;
     float min = x[0], max = x[0];
     float sum_w = av_x + fabsf(x[0]);
     float sum_x = sum_w * x[0];
@@ -97,7 +136,7 @@ __device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
     float l_iscale = iscale, l_min = min;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-        const int l = clamp15(nearest_int(iscale * (x[i] - min)));
+        const int l = clampq<nmax>(nearest_int(iscale * (x[i] - min)));
         const float diff = scale * (float)l + min - x[i];
         best_error += (av_x + fabsf(x[i])) * (diff * diff);
     }
@@ -107,7 +146,7 @@ __device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            const int l = clamp15(nearest_int(iscale * (x[i] - min)));
+            const int l = clampq<nmax>(nearest_int(iscale * (x[i] - min)));
             const float w = av_x + fabsf(x[i]);
             sum_l += w * l;
             sum_l2 += w * l * l;
@@ -124,7 +163,7 @@ __device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
             float mad = 0;
 #pragma unroll
             for (int i = 0; i < 32; ++i) {
-                const int l = clamp15(nearest_int(iscale * (x[i] - min)));
+                const int l = clampq<nmax>(nearest_int(iscale * (x[i] - min)));
                 const float diff = this_scale * (float)l + this_min - x[i];
                 mad += (av_x + fabsf(x[i])) * (diff * diff);
             }
@@ -140,12 +179,15 @@ __device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
     return {scale, -min, l_iscale, l_min, 0};
 }
 
-// ---- Q4_K: quantize_row_q4_K_ref, one thread per superblock with no per-thread arrays in scratch:
-// a sub-block's 32 values live in registers, the per-sub-block fits in this thread's LDS slot, and
-// the final levels are recomputed per sub-block pair as they are packed ----
+// ---- Q4_K / Q5_K: quantize_row_q4_K_ref / quantize_row_q5_K_ref, one thread per superblock with no
+// per-thread arrays in scratch: a sub-block's 32 values live in registers, the per-sub-block fits in
+// this thread's LDS slot, and the final levels are recomputed per sub-block pair as they are
+// packed ----
 constexpr int kWq4Threads = 64;
+template <bool Q5>
 __global__ void __launch_bounds__(kWq4Threads) quantize_w_q4_K_kernel(const float* __restrict__ W, int64_t N,
                                                                       int64_t K, uint8_t* __restrict__ out) {
+    constexpr int nmax = Q5 ? 31 : 15, kSb = Q5 ? 176 : 144, kQsDw = Q5 ? 12 : 4;
     __shared__ Qkx2Fit fits[8][kWq4Threads];
     const int64_t nsb = K / QK_K;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -170,7 +212,7 @@ __global__ void __launch_bounds__(kWq4Threads) quantize_w_q4_K_kernel(const floa
 #pragma unroll
         for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
         const float av_x = sqrtf(sum_x2 / 32);
-        const Qkx2Fit f = qkx2_fit32(x, av_x);
+        const Qkx2Fit f = qkx2_fit32<Q5>(x, av_x);
         fits[j][t] = f;
         if (f.scale > max_scale) max_scale = f.scale;
         if (f.the_min > max_min) max_min = f.the_min;
@@ -199,14 +241,16 @@ __global__ void __launch_bounds__(kWq4Threads) quantize_w_q4_K_kernel(const floa
         }
     }
     const uint16_t dh = float_to_half_bits(max_scale / 63.f), dminh = float_to_half_bits(max_min / 63.f);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(out + (r * nsb + sbi) * 144);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out + (r * nsb + sbi) * kSb);
     dst[0] = (uint32_t)dh | ((uint32_t)dminh << 16);
     dst[1] = scw[0];
     dst[2] = scw[1];
     dst[3] = scw[2];
     const float dsb = half_bits_to_float(dh), dmsb = half_bits_to_float(dminh);
     // final levels of sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles) of qs[32c .. 32c + 32):
-    // from the 6-bit scales, or, where the scale quantized to 0, the fit's own levels
+    // from the 6-bit scales, or, where the scale quantized to 0, the fit's own levels. Q5_K: bit 4
+    // of element ii of sub-block j goes to bit j of qh[ii].
+    [[maybe_unused]] uint32_t qh[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll 1
     for (int c = 0; c < 4; ++c) {
         uint32_t packed[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -222,14 +266,19 @@ __global__ void __launch_bounds__(kWq4Threads) quantize_w_q4_K_kernel(const floa
             for (int ii = 0; ii < 32; ++ii) {
                 int l;
                 if (d != 0.0f)
-                    l = clamp15(nearest_int((x[ii] + dm) / d));
+                    l = clampq<nmax>(nearest_int((x[ii] + dm) / d));
                 else
-                    l = f.zero ? 0 : clamp15(nearest_int(f.l_iscale * (x[ii] - f.l_min)));
-                packed[ii >> 2] |= (uint32_t)l << (8 * (ii & 3) + 4 * h);
+                    l = f.zero ? 0 : clampq<nmax>(nearest_int(f.l_iscale * (x[ii] - f.l_min)));
+                packed[ii >> 2] |= (uint32_t)(l & 0xF) << (8 * (ii & 3) + 4 * h);
+                if constexpr (Q5) qh[ii >> 2] |= (uint32_t)(l >> 4) << (8 * (ii & 3) + j);
             }
         }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) dst[4 + 8 * c + q] = packed[q];
+        for (int q = 0; q < 8; ++q) dst[kQsDw + 8 * c + q] = packed[q];
+    }
+    if constexpr (Q5) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dst[4 + q] = qh[q];
     }
 }
 
@@ -370,6 +419,25 @@ __global__ void __launch_bounds__(256) dequantize_kernel(int type, const uint8_t
             const int q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 0xF);
             y[l] = d * q - dm;
         }
+    } else if (type == kTypeQ4_0) {
+        const uint8_t* b = row + c * 18;
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b));
+        for (int j = 0; j < 16; ++j) {
+            y[j] = (float)((int)(b[2 + j] & 0xF) - 8) * d;
+            y[j + 16] = (float)((int)(b[2 + j] >> 4) - 8) * d;
+        }
+    } else if (type == kTypeQ5_K) {
+        const uint8_t* b = row + (c / 8) * 176;
+        const int j = (int)(c % 8);  // sub-block
+        uint8_t sc, m;
+        scale_min_k4(j, b + 4, &sc, &m);
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b)) * sc;
+        const float dm = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b + 2)) * m;
+        const uint8_t* qs = b + 48 + 32 * (j / 2);
+        for (int l = 0; l < 32; ++l) {
+            const int q = ((j & 1) ? (qs[l] >> 4) : (qs[l] & 0xF)) + 16 * ((b[16 + l] >> j) & 1);
+            y[l] = d * q - dm;
+        }
     } else if (type == kTypeQ6_K) {
         const uint8_t* b = row + (c / 8) * 210;
         const float d = half_bits_to_float((uint32_t)b[208] | ((uint32_t)b[209] << 8));
@@ -392,10 +460,15 @@ hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t
         const int64_t t = N * (K / QK8_0);
         hipLaunchKernelGGL(quantize_w_q8_0_kernel, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, W, N, K,
                            (uint8_t*)Wq);
-    } else if (wtype == kTypeQ4_K) {
+    } else if (wtype == kTypeQ4_0) {
+        const int64_t t = N * (K / QK8_0);
+        hipLaunchKernelGGL(quantize_w_q4_0_kernel, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st, W, N, K,
+                           (uint8_t*)Wq);
+    } else if (wtype == kTypeQ4_K || wtype == kTypeQ5_K) {
         const int64_t t = N * (K / QK_K);
-        hipLaunchKernelGGL(quantize_w_q4_K_kernel, dim3((unsigned)((t + kWq4Threads - 1) / kWq4Threads)),
-                           dim3(kWq4Threads), 0, st, W, N, K, (uint8_t*)Wq);
+        hipLaunchKernelGGL(wtype == kTypeQ5_K ? quantize_w_q4_K_kernel<true> : quantize_w_q4_K_kernel<false>,
+                           dim3((unsigned)((t + kWq4Threads - 1) / kWq4Threads)), dim3(kWq4Threads), 0, st, W, N,
+                           K, (uint8_t*)Wq);
     } else {
         const int64_t t = N * (K / QK_K);
         hipLaunchKernelGGL(quantize_w_q6_K_kernel, dim3((unsigned)((t + 63) / 64)), dim3(64), 0, st, W, N, K,

@@ -43,8 +43,10 @@ extern "C" {
 /* ggml type ids */
 #define DCQ_TYPE_F32 0
 #define DCQ_TYPE_F16 1
+#define DCQ_TYPE_Q4_0 2
 #define DCQ_TYPE_Q8_0 8
 #define DCQ_TYPE_Q4_K 12
+#define DCQ_TYPE_Q5_K 13
 #define DCQ_TYPE_Q6_K 14
 #define DCQ_TYPE_Q8_K 15
 
@@ -73,15 +75,18 @@ const char* dcq_version(void);
 const char* dcq_status_string(int status);
 
 /* ---- type traits (ggml_type_traits / ggml_row_size equivalents) ---- */
-/* Elements per block: Q8_0 32, Q4_K/Q6_K/Q8_K 256, F32/F16 1; 0 if unknown. */
+/* Elements per block: Q4_0/Q8_0 32, Q4_K/Q5_K/Q6_K/Q8_K 256, F32/F16 1; 0 if unknown. */
 int64_t dcq_block_size(int type);
-/* Bytes per block: Q8_0 34, Q4_K 144, Q6_K 210, Q8_K 292, F32 4, F16 2; 0 if unknown. */
+/* Bytes per block: Q4_0 18, Q8_0 34, Q4_K 144, Q5_K 176, Q6_K 210, Q8_K 292, F32 4, F16 2;
+ * 0 if unknown. */
 int64_t dcq_type_size(int type);
 /* Bytes of one row of K elements (ggml_row_size, core/src/inference.cpp:977); 0 if K is not
  * a multiple of the block size. */
 size_t dcq_row_size(int type, int64_t k);
 /* vec_dot_type of a weight type (core/src/inference.cpp:970-984, core/include/simd_ops.h:
- * 3298-3305): Q8_0 -> Q8_0, Q4_K/Q6_K -> Q8_K; DCQ_ERR_UNSUPPORTED otherwise. */
+ * 3298-3305): Q8_0 -> Q8_0, Q4_K/Q5_K/Q6_K -> Q8_K; and Q4_0 -> Q8_0, ggml's trait for the type
+ * the reference's quantize tool emits by default (core/src/quantize.cpp:71-72, 90);
+ * DCQ_ERR_UNSUPPORTED otherwise. */
 int dcq_vec_dot_type(int wtype);
 /* 1 if MUL_MAT(src0 = wtype, src1 = xtype) -> ytype is computed by this library, else 0
  * (the check a ggml backend's supports_op answers). */
@@ -95,12 +100,13 @@ int dcq_quantize_rows(int vec_dot_type, const float* X, int64_t M, int64_t K, si
                       void* Xq, void* stream);
 
 /* ---- the operator ----
- * GGML_OP_MUL_MAT for src0 = W (wtype in {Q8_0, Q4_K, Q6_K}), src1 = X (F32), dst = Y (F32):
+ * GGML_OP_MUL_MAT for src0 = W (wtype in {Q8_0, Q4_K, Q6_K}, and the quantize tool's Q4_0 and
+ * Q5_K, core/src/quantize.cpp:71-78), src1 = X (F32), dst = Y (F32):
  * quantizes X once into the workspace, then computes every (m, n) dot
  * (replaces the quantize + chunked vec_dot of ggml's CPU MUL_MAT, executed from
  * core/src/worker.cpp:544, and cb_gemv_custom, core/src/inference.cpp:840-948).
  * Requirements: K % block_size(wtype) == 0; W 16-byte aligned; w_row_bytes >= row_size, even, and
- * a multiple of 16 for Q4_K; X 16-byte aligned with x_stride_bytes % 16 == 0; Y 4-byte aligned
+ * a multiple of 16 for Q4_K and Q5_K; X 16-byte aligned with x_stride_bytes % 16 == 0; Y 4-byte aligned
  * with y_stride_bytes % 4 == 0.
  * workspace may be NULL (the library then takes stream-ordered scratch); otherwise it must be
  * 256-byte aligned and should hold dcq_mul_mat_workspace_size(wtype, M, K) bytes: the quantized
@@ -121,9 +127,9 @@ int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_
                    const float* X, int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes,
                    void* workspace, size_t workspace_bytes, int path, int32_t* block_sums,
                    void* stream);
-/* Number of int32 block sums per (m, n): Q8_0 K/32 (I_b = sum qw*qa over a 32-block);
- * Q4_K 2*K/256 (per superblock: sum_j sc_j*I_j, then sum_j m_j*S_j); Q6_K K/256 (per
- * superblock: sum_g sc_g*I_g). 0 if unsupported. */
+/* Number of int32 block sums per (m, n): Q8_0 K/32 (I_b = sum qw*qa over a 32-block); Q4_0
+ * K/32 (I_b = sum (qw - 8)*qa); Q4_K and Q5_K 2*K/256 (per superblock: sum_j sc_j*I_j, then
+ * sum_j m_j*S_j); Q6_K K/256 (per superblock: sum_g sc_g*I_g). 0 if unsupported. */
 int64_t dcq_block_sums_per_row(int wtype, int64_t k);
 
 /* ---- the operator in two halves (ggml MUL_MAT's wdata step made explicit) ----
@@ -187,8 +193,8 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
  * the reference FFN's w1 = mul_mat(W1, x), w3 = mul_mat(W3, x), ggml_mul(ggml_silu(w1), w3)
  * (core/src/inference.cpp:1794-1796) in one call. Both weights share wtype, shape and row
  * stride, and X's quantization. At M <= DCQ_DECODE_ROWS(wtype, N) (Q4_K, Q8_0) one fused kernel
- * streams both weight rows; otherwise X is quantized once, both projections run, then the
- * product.
+ * streams both weight rows; otherwise (and for Q4_0, Q5_K, Q6_K) X is quantized once, both
+ * projections run, then the product.
  * Requirements as dcq_mul_mat's, for both weights. workspace may be NULL; otherwise it should hold
  * dcq_ffn_gate_up_workspace_size(wtype, M, N, K) bytes, 256-byte aligned (the split-K room at its
  * end is optional, as in dcq_mul_mat). */
@@ -207,8 +213,8 @@ int dcq_dot_rows(int wtype, const void* W, size_t w_row_bytes, const void* Xq, i
 
 /* ---- weight quantization (ggml_quantize_chunk equivalent, core/src/quantize.cpp:285) ----
  * Quantizes an fp32 [N][K] matrix into wtype rows (packed, row stride dcq_row_size):
- * Q8_0 = quantize_row_q8_0_ref, Q4_K = quantize_row_q4_K_ref, Q6_K = quantize_row_q6_K_ref
- * (no importance matrix). */
+ * Q8_0 = quantize_row_q8_0_ref, Q4_0 = quantize_row_q4_0_ref, Q4_K = quantize_row_q4_K_ref,
+ * Q5_K = quantize_row_q5_K_ref, Q6_K = quantize_row_q6_K_ref (no importance matrix). */
 int dcq_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, void* stream);
 
 /* ---- dequantization (type_traits->to_float, core/src/inference.cpp:938-945) ----

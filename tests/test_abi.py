@@ -39,19 +39,24 @@ def test_version_and_status_strings():
 
 
 def test_type_traits_match_gguf():
-    assert [dc.block_size(t) for t in (0, 1, 8, 12, 14, 15, 2)] == [1, 1, 32, 256, 256, 256, 0]
-    assert [dc.type_size(t) for t in (0, 1, 8, 12, 14, 15)] == [4, 2, 34, 144, 210, 292]
+    assert [dc.block_size(t) for t in (0, 1, 2, 8, 12, 13, 14, 15, 3)] == [1, 1, 32, 32, 256, 256, 256, 256, 0]
+    assert [dc.type_size(t) for t in (0, 1, 2, 8, 12, 13, 14, 15)] == [4, 2, 18, 34, 144, 176, 210, 292]
+    assert dc.row_size(2, 2560) == 1440
+    assert dc.row_size(13, 2560) == 1760
     assert dc.row_size(8, 1024) == 1088
     assert dc.row_size(12, 2560) == 1440
     assert dc.row_size(14, 9728) == 7980
     assert dc.row_size(15, 2560) == 2920
     assert dc.row_size(12, 100) == 0
-    assert [dc.vec_dot_type(t) for t in (8, 12, 14)] == [8, 15, 15]
-    assert dc.vec_dot_type(0) == UNSUPPORTED
-    assert dc.supports_mul_mat(12, 0, 0) and not dc.supports_mul_mat(12, 1, 0) and not dc.supports_mul_mat(2, 0, 0)
+    assert [dc.vec_dot_type(t) for t in (2, 8, 12, 13, 14)] == [8, 8, 15, 15, 15]
+    assert dc.vec_dot_type(0) == UNSUPPORTED and dc.vec_dot_type(3) == UNSUPPORTED
+    assert dc.supports_mul_mat(12, 0, 0) and not dc.supports_mul_mat(12, 1, 0) and not dc.supports_mul_mat(3, 0, 0)
+    assert dc.supports_mul_mat(2, 0, 0) and dc.supports_mul_mat(13, 0, 0)
     assert dc.block_sums_per_row(8, 1024) == 32
     assert dc.block_sums_per_row(12, 2560) == 20
     assert dc.block_sums_per_row(14, 9728) == 38
+    assert dc.block_sums_per_row(2, 1024) == 32
+    assert dc.block_sums_per_row(13, 2560) == 20
 
 
 def test_workspace_size():
@@ -76,7 +81,7 @@ def _mm(wt=12, W=0x1000, N=16, K=256, wrb=None, X=0x2000, M=1, xs=None, Y=0x3000
 
 def test_mul_mat_validation_order():
     """Argument errors are reported before any device call."""
-    assert _mm(wt=2) == UNSUPPORTED
+    assert _mm(wt=3) == UNSUPPORTED  # Q4_1: not a weight type of this library
     assert _mm(W=None) == INVALID
     assert _mm(K=100) == BAD_SHAPE
     assert _mm(N=0) == BAD_SHAPE
@@ -86,6 +91,8 @@ def test_mul_mat_validation_order():
     assert _mm(W=0x1004) == MISALIGNED
     assert _mm(X=0x2004) == MISALIGNED
     assert _mm(wt=12, wrb=152) == MISALIGNED  # Q4_K rows must keep 16-byte alignment
+    assert _mm(wt=13, wrb=184) == MISALIGNED  # so must Q5_K rows
+    assert _mm(wt=2, wrb=145) == MISALIGNED   # odd row strides never
     assert _mm(path=7) == INVALID
     assert _mm(ws=0x4000, wsb=16) == WORKSPACE
     assert _mm(ws=0x4010, wsb=1 << 20) == MISALIGNED
@@ -99,7 +106,7 @@ def test_noalloc_validation_and_limit():
 
     def na(wt=8, W=0x1000, N=16, K=1024, M=1, X=0x2000, Y=0x3000):
         return L.dcq_mul_mat_noalloc(wt, W, N, K, dc.row_size(wt, K), X, M, K * 4, Y, N * 4, None)
-    assert na(wt=2) == UNSUPPORTED
+    assert na(wt=3) == UNSUPPORTED
     assert na(W=None) == INVALID
     assert na(K=100) == BAD_SHAPE
     assert na(X=0x2004) == MISALIGNED
@@ -125,14 +132,14 @@ def test_well_formed_call_without_gpu_fails_loudly():
 
 def test_dot_rows_and_quantize_validation():
     L = dc.lib()
-    assert L.dcq_dot_rows(2, 0x1000, 64, 0x2000, 256, 0x3000, 0, 4, None) == UNSUPPORTED
+    assert L.dcq_dot_rows(3, 0x1000, 64, 0x2000, 256, 0x3000, 0, 4, None) == UNSUPPORTED
     assert L.dcq_dot_rows(12, 0x1000, 144, 0x2000, 256, 0x3000, 4, 2, None) == BAD_SHAPE
     assert L.dcq_dot_rows(12, 0x1000, 144, 0x2000, 256, 0x3000, 3, 3, None) == OK  # empty range: no work
     assert L.dcq_quantize_rows(12, 0x1000, 1, 256, 1024, 0x2000, None) == UNSUPPORTED
     assert L.dcq_quantize_rows(15, 0x1000, 1, 100, 1024, 0x2000, None) == BAD_SHAPE
     assert L.dcq_quantize_rows(15, 0x1004, 1, 256, 1024, 0x2000, None) == MISALIGNED
     assert L.dcq_quantize_weights(15, 0x1000, 1, 256, 0x2000, None) == UNSUPPORTED
-    assert L.dcq_dequantize_rows(2, 0x1000, 1, 256, 64, 0x2000, None) == UNSUPPORTED
+    assert L.dcq_dequantize_rows(3, 0x1000, 1, 256, 64, 0x2000, None) == UNSUPPORTED
 
 
 def test_ffn_gate_up_workspace_and_validation():
@@ -147,7 +154,7 @@ def test_ffn_gate_up_workspace_and_validation():
     def ffn(wt=12, Wg=0x1000, Wu=0x5000, N=16, K=256, M=1, ws=None, wsb=0):
         return L.dcq_ffn_gate_up(wt, Wg, Wu, N, K, dc.row_size(wt, K), 0x2000, M, K * 4, 0x3000, N * 4, ws, wsb,
                                  None)
-    assert ffn(wt=2) == UNSUPPORTED
+    assert ffn(wt=3) == UNSUPPORTED
     assert ffn(Wg=None) == INVALID
     assert ffn(Wu=None) == INVALID
     assert ffn(Wu=0x5004) == MISALIGNED

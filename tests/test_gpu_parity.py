@@ -3,7 +3,8 @@
 Bars: quantized activation bytes and per-block int32 sums
 bit-exact; fp32 outputs within |y - y_ref| <= 1e-4 * max(|y_ref|, L1), where L1
 is the sum of the magnitudes of the fp32 terms the reference adds (|scale_b * int_b|
-per Q8_0 block; the eight per-superblock lane sums of Q4_K / Q6_K, plus the mins term):
+per Q8_0 / Q4_0 block; the eight per-superblock lane sums of Q4_K / Q5_K / Q6_K, plus the mins
+term):
 the magnitude the fp32 rounding of both summation orders scales with.
 """
 import numpy as np
@@ -14,7 +15,7 @@ from densecore_amd import synth
 
 pytestmark = pytest.mark.gpu
 
-Q8_0, Q4_K, Q6_K, Q8_K = 8, 12, 14, 15
+Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K = 2, 8, 12, 13, 14, 15
 RTOL = 1e-4
 
 
@@ -162,6 +163,13 @@ CASES = [
     # the 4 passes and take the separate quantize
     (Q6_K, 1, 2048, 9728), (Q6_K, 2, 2560, 9728), (Q6_K, 1, 3000, 5120),
     (Q6_K, 2, 2560, 8192), (Q6_K, 1, 2048, 12288),
+    # the quantize tool's Q4_0 and Q5_K (core/src/quantize.cpp:71-78) on the generic GEMV and MFMA
+    # kernels: Q4_0 in block pairs (K % 64 == 0, dword-aligned rows) and single blocks (K = 96,
+    # 160: 54- and 90-byte rows), Qwen3-4B's ffn width, ragged tiles, several K-steps
+    (Q4_0, 1, 96, 1024), (Q4_0, 3, 70, 2048), (Q4_0, 1, 33, 96), (Q4_0, 2, 40, 160), (Q4_0, 4, 41, 192),
+    (Q4_0, 40, 100, 512), (Q4_0, 130, 257, 256), (Q4_0, 256, 384, 1024), (Q4_0, 1, 9728, 2560),
+    (Q5_K, 1, 97, 2560), (Q5_K, 2, 64, 256), (Q5_K, 5, 40, 512), (Q5_K, 64, 96, 2048), (Q5_K, 70, 33, 768),
+    (Q5_K, 256, 384, 1024), (Q5_K, 1, 9728, 2560), (Q5_K, 3, 2560, 9728),
 ]
 
 
@@ -232,7 +240,8 @@ def test_decode_fused_quantization(O, dev, wt, M, N, K):
 # past the U temporary, one after the other.
 GATE_UP = [(Q4_K, 1, 97, 2560), (Q4_K, 1, 9728, 2560), (Q4_K, 5, 40, 1024), (Q8_0, 1, 96, 1024), (Q8_0, 3, 41, 2048),
            (Q6_K, 1, 50, 1024), (Q6_K, 3, 17, 768), (Q4_K, 33, 64, 512), (Q8_0, 40, 100, 512),
-           (Q8_0, 64, 2048, 8192), (Q6_K, 64, 2048, 8192)]
+           (Q8_0, 64, 2048, 8192), (Q6_K, 64, 2048, 8192),
+           (Q4_0, 1, 96, 1024), (Q4_0, 6, 41, 2048), (Q5_K, 1, 97, 2560), (Q5_K, 40, 64, 512)]
 
 
 @pytest.mark.parametrize("wt,M,N,K", GATE_UP)
@@ -255,7 +264,7 @@ def test_ffn_gate_up(O, dev, wt, M, N, K):
         O.assert_close_gate_up(to_host(y2), y_ref, parts, RTOL, what=f"gate/up with a workspace of {nbytes} B")
 
 
-@pytest.mark.parametrize("wt,M", [(Q4_K, 9), (Q6_K, 3), (Q8_0, 2)])
+@pytest.mark.parametrize("wt,M", [(Q4_K, 9), (Q6_K, 3), (Q8_0, 2), (Q4_0, 3), (Q4_0, 12), (Q5_K, 2), (Q5_K, 9)])
 def test_mul_mat_padded_strides_and_workspace(O, dev, wt, M):
     """Row strides larger than the data (ggml nb[1] > row size) and a caller workspace."""
     import torch
@@ -286,7 +295,8 @@ def test_auto_path_is_consistent(O, dev):
 
 
 # ---------------------------------------------------------------- dot_rows (ComputeDotProductBatch)
-@pytest.mark.parametrize("wt,K", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2560), (Q6_K, 1024)])
+@pytest.mark.parametrize("wt,K", [(Q8_0, 1024), (Q8_0, 96), (Q4_K, 2560), (Q6_K, 1024), (Q4_0, 1024), (Q4_0, 96),
+                                  (Q5_K, 2560)])
 def test_dot_rows(O, dev, wt, K):
     N = 50
     wq, x = make_inputs(O, wt, 1, N, K, seed=K)
@@ -299,7 +309,7 @@ def test_dot_rows(O, dev, wt, K):
 
 
 # ---------------------------------------------------------------- weights
-@pytest.mark.parametrize("wt", [Q8_0, Q4_K, Q6_K])
+@pytest.mark.parametrize("wt", [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K])
 def test_quantize_weights_bit_exact(O, dev, wt):
     N, K = 64, 2048
     w = synth.normal(N * K, 313, 0.0, 0.02).reshape(N, K)
@@ -309,7 +319,7 @@ def test_quantize_weights_bit_exact(O, dev, wt):
     assert np.array_equal(got, O.quantize_matrix(wt, w))
 
 
-@pytest.mark.parametrize("wt", [Q8_0, Q4_K, Q6_K])
+@pytest.mark.parametrize("wt", [Q8_0, Q4_0, Q4_K, Q5_K, Q6_K])
 def test_dequantize_rows(O, dev, wt):
     N, K = 16, 1024
     w = synth.normal(N * K, 314, 0.0, 0.02).reshape(N, K)
@@ -373,7 +383,8 @@ def test_config5_block_sums_full_shape_corner(O, dev):
 # ---------------------------------------------------------------- split operator (shared quantization)
 @pytest.mark.parametrize("path", [dc.PATH_AUTO, dc.PATH_GEMV, dc.PATH_MMQ])
 @pytest.mark.parametrize("wt,M,N,K", [(Q8_0, 1, 70, 1024), (Q4_K, 1, 96, 2560), (Q4_K, 5, 64, 2048),
-                                      (Q4_K, 8, 40, 768), (Q6_K, 3, 33, 1024)])
+                                      (Q4_K, 8, 40, 768), (Q6_K, 3, 33, 1024), (Q4_0, 2, 70, 1024),
+                                      (Q5_K, 6, 40, 768)])
 def test_quantize_src1_then_mul_mat_q(O, dev, wt, M, N, K, path):
     """dcq_quantize_src1 once, then dcq_mul_mat_q for two weights sharing X (ffn gate and up):
     the planar-activation kernels, against the oracle."""
@@ -462,7 +473,8 @@ def test_concatenated_projections_one_call(O, dev, tmp_path, wt):
 # quantizes first (K > 4096) and the batched / prefill MFMA kernels (add kernel after).
 MUL_MAT_ADD = [(Q4_K, 1, 2560, 9728), (Q4_K, 1, 97, 2560), (Q4_K, 5, 40, 1024), (Q8_0, 1, 1024, 2048),
                (Q8_0, 3, 41, 2048), (Q6_K, 1, 1024, 2560), (Q6_K, 1, 2560, 9728), (Q6_K, 2, 70, 4096),
-               (Q4_K, 64, 96, 512), (Q8_0, 130, 64, 1024), (Q6_K, 9, 33, 512)]
+               (Q4_K, 64, 96, 512), (Q8_0, 130, 64, 1024), (Q6_K, 9, 33, 512),
+               (Q4_0, 1, 1024, 2048), (Q4_0, 20, 64, 512), (Q5_K, 1, 2560, 9728), (Q5_K, 9, 33, 512)]
 
 
 @pytest.mark.parametrize("mode", ["residual", "in_place", "bias"])
@@ -507,7 +519,8 @@ def test_mul_mat_add_strided_residual(O, dev):
     assert np.all(yb[:, N:] == -7.0)
 
 
-@pytest.mark.parametrize("wt,M,N,K", [(Q4_K, 520, 16400, 256), (Q6_K, 520, 16400, 256), (Q8_0, 30, 16400, 256)])
+@pytest.mark.parametrize("wt,M,N,K", [(Q4_K, 520, 16400, 256), (Q6_K, 520, 16400, 256), (Q8_0, 30, 16400, 256),
+                                      (Q5_K, 520, 16400, 256), (Q4_0, 520, 16400, 256)])
 def test_mul_mat_large_tiles(O, dev, wt, M, N, K):
     """Shapes that take the large-tile kernels (64 x 256 workgroup tiles for Q4_K / Q6_K at
     >= 512 tiles; ragged M and N): the output against the oracle, and the exact per-block

@@ -274,7 +274,7 @@ def test_q4_0_weight_quantizer_closed_forms(O):
     """quantize_row_q4_0_ref: d = max / -8 where max is the first element of largest magnitude, so
     that element stores q = 0; every other q is the nearest of the 16 levels (q - 8) * d to x (a
     truncation without the + 0.5 fails this), the +8 level clamped to q = 15; an all-zero block is
-    d = 0 with every q = 8. Blocks here hold both signs of the maximum magnitude and ties."""
+    d = -0.0 (0 / -8, the fp16 sign bit set) with every q = 8. Blocks here hold both signs of the maximum magnitude and ties."""
     k = 32 * 64
     w = synth.normal(k, 71, 0, 0.02)
     w[32:64] = 0.0                                  # all-zero block
@@ -285,7 +285,8 @@ def test_q4_0_weight_quantizer_closed_forms(O):
     d = wq[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
     q = np.concatenate([wq[:, 2:] & 0xF, wq[:, 2:] >> 4], axis=1).astype(np.int64)
     xb = w.reshape(-1, 32)
-    assert d[1] == 0 and np.all(q[1] == 8)
+    # d = 0 / -8 is -0.0: stored as fp16 0x8000, the sign bit set
+    assert wq[1, 0] == 0x00 and wq[1, 1] == 0x80 and np.all(q[1] == 8)
     for b in range(xb.shape[0]):
         if not np.any(xb[b]):
             continue
