@@ -505,15 +505,15 @@ def bench_kv_attention(args, dev, ct, n_tokens=1, n_past=4095, n_layer=36, n_hea
 
 def random_weights(dev, wtype, N, K, copies, seed):
     """copies x N rows of valid random quants of `wtype` with small positive fp16 scales (d =
-    0.0004, Q4_K dmin = 0.0002): the kernels' work does not depend on the values, and quantizing
-    hundreds of MB of floats would dominate the run."""
+    0.0004, Q4_K / Q5_K dmin = 0.0002): the kernels' work does not depend on the values, and
+    quantizing hundreds of MB of floats would dominate the run."""
     import torch
     import densecore_amd as dc
     rb = dc.row_size(wtype, K)
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     big = torch.randint(0, 256, (copies, N, rb), dtype=torch.uint8, device=dev, generator=g)
-    bs = {dc.TYPE_Q8_0: 34, dc.TYPE_Q4_K: 144, dc.TYPE_Q6_K: 210}[wtype]
+    bs = {dc.TYPE_Q8_0: 34, dc.TYPE_Q4_0: 18, dc.TYPE_Q4_K: 144, dc.TYPE_Q5_K: 176, dc.TYPE_Q6_K: 210}[wtype]
     blocks = big.view(copies, N, rb // bs, bs)
 
     def f16(v):
@@ -523,7 +523,7 @@ def random_weights(dev, wtype, N, K, copies, seed):
         blocks[..., 208:210] = f16(0.0004)
     else:
         blocks[..., 0:2] = f16(0.0004)
-        if wtype == dc.TYPE_Q4_K:
+        if wtype in (dc.TYPE_Q4_K, dc.TYPE_Q5_K):
             blocks[..., 2:4] = f16(0.0002)
     return big
 
@@ -636,6 +636,47 @@ def bench_kquant_prefill(args, dev, wtype, M=2048, N=8192, K=2048):
     return out
 
 
+# The quantize tool's other output types (core/src/quantize.cpp:71-78: Q4_0, its default, and
+# Q5_K for Q5_K_M) at the shapes of configs 2 (decode), 4 (batched) and 5 (prefill)
+TOOL_TYPE_SHAPES = [(t, M, N, K) for t in ("Q4_0", "Q5_K")
+                    for (M, N, K) in ((1, 9728, 2560), (64, 8192, 2048), (2048, 8192, 2048))]
+
+
+def bench_tool_type(args, dev, tname, M, N, K):
+    """One dcq_mul_mat step with Q4_0 or Q5_K weights (random valid quants, W rotated like the
+    configs): weight GB/s against 8 TB/s and the pure-read time of the same bytes at M = 1, int8
+    TOPS against the int8 MFMA peak otherwise."""
+    import torch
+    import densecore_amd as dc
+    wtype = getattr(dc, "TYPE_" + tname)
+    rb = dc.row_size(wtype, K)
+    wbytes = N * rb
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    big = random_weights(dev, wtype, N, K, copies, 41)
+    g = torch.Generator(device=dev)
+    g.manual_seed(42)
+    x = torch.randn((M, K), device=dev, generator=g)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ws = torch.empty(dc.mul_mat_workspace_size(wtype, M, K), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+
+    def step(i):
+        dc.mul_mat(wtype, big[i % copies], N, K, x, y=y, workspace=ws, stream=torch.cuda.current_stream().cuda_stream)
+
+    ms, kern, _ = time_graph(step, max(10, args.steps // (4 if M < 2048 else 10)), args.warmup, args.replays)
+    out = {"shape": f"{tname} M={M} N={N} K={K}", "step_us": ms * 1e3, "kernels": kern, "w_bytes": wbytes,
+           "weight_GBps": wbytes / (ms * 1e-3) / 1e9, "frac_of_hbm_peak": wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+           "TOPS": 2.0 * M * N * K / (ms * 1e-3) / 1e12,
+           "frac_of_int8_peak": 2.0 * M * N * K / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS}
+    if M == 1 and not args.no_read_ceiling:
+        c = read_ceiling(big.view(copies, -1), wbytes, copies, args)
+        out["read_ceiling_us"] = c["us"]
+        out["frac_of_read_ceiling"] = c["us"] / (ms * 1e3)
+    del big, ws, y, x
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_gguf_load(args, dev, mib=512):
     """GGUF ingest: a file of Q4_K tensors (mib MiB, in the page cache after it is written) loaded
     tensor by tensor into HBM with dcq_gguf_load_tensor; host-to-device GB/s (PCIe bound)."""
@@ -668,26 +709,28 @@ def bench_gguf_load(args, dev, mib=512):
 
 def bench_weight_quantizer(args, dev):
     """dcq_quantize_weights (ggml_quantize_chunk's algorithms on the GPU) at the weight shapes of
-    ms per matrix and GB/s of fp32 input (load-time work, off the hot path)."""
+    BASELINE configs 1-3 (their types), and Q4_0 / Q5_K at config 2's: ms per matrix and GB/s of
+    fp32 input (load-time work, off the hot path)."""
     import torch
     import densecore_amd as dc
     from densecore_amd import synth
     out = {}
-    for ci in (1, 2, 3):
-        cfg = dc.by_index(ci)
+    cases = [(dc.by_index(ci), dc.by_index(ci).wtype) for ci in (1, 2, 3)]
+    cases += [(dc.by_index(2), dc.TYPE_Q4_0), (dc.by_index(2), dc.TYPE_Q5_K)]
+    for cfg, wtype in cases:
         w = torch.from_numpy(synth.normal(cfg.N * cfg.K, cfg.w_seed, 0.0, cfg.w_std).reshape(cfg.N, cfg.K)).to(dev)
-        q = dc.quantize_weights(cfg.wtype, w)
+        q = dc.quantize_weights(wtype, w)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         reps = 5
         e0.record()
         for _ in range(reps):
-            dc.quantize_weights(cfg.wtype, w, out=q)
+            dc.quantize_weights(wtype, w, out=q)
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / reps
-        out[dc.TYPE_NAMES[cfg.wtype].lower()] = {"shape": f"{cfg.N}x{cfg.K}", "ms": ms,
-                                                 "GBps_fp32_in": cfg.N * cfg.K * 4 / (ms * 1e-3) / 1e9}
+        out[dc.TYPE_NAMES[wtype].lower()] = {"shape": f"{cfg.N}x{cfg.K}", "ms": ms,
+                                             "GBps_fp32_in": cfg.N * cfg.K * 4 / (ms * 1e-3) / 1e9}
     return out
 
 
@@ -1060,6 +1103,11 @@ def main():
             e = extras[f"batched_{tname.lower()}_m{M}_{N}x{K}"] = bench_batched_decode(args, dev, tname, M, N, K)
             print(f"# batched decode {e['shape']}: {e['step_us']:.2f} us ({e['kernels']} kernels), "
                   f"{e['weight_GBps']:.0f} GB/s of weights, {e['TOPS']:.1f} TOPS", file=sys.stderr, flush=True)
+        for tname, M, N, K in TOOL_TYPE_SHAPES:
+            e = extras[f"tool_type_{tname.lower()}_m{M}_{N}x{K}"] = bench_tool_type(args, dev, tname, M, N, K)
+            print(f"# {e['shape']}: {e['step_us']:.2f} us ({e['kernels']} kernels), {e['weight_GBps']:.0f} GB/s "
+                  f"of weights ({100 * e['frac_of_hbm_peak']:.1f} % of 8 TB/s; read ceiling "
+                  f"{e.get('read_ceiling_us', 0):.2f} us), {e['TOPS']:.1f} TOPS", file=sys.stderr, flush=True)
         extras["weight_quantizer"] = bench_weight_quantizer(args, dev)
         extras["gguf_load"] = bench_gguf_load(args, dev)
         print(f"# GGUF ingest: {extras['gguf_load']['GBps']:.1f} GB/s host-to-HBM over "

@@ -1,4 +1,5 @@
-// dcq_batch.hip — batched-decode mul_mat (8 < M <= 64 per m-tile) for Q4_K weights on int8 MFMA.
+// dcq_batch.hip — batched-decode mul_mat (8 < M <= 64 per m-tile) for Q4_K and Q5_K weights on int8
+// MFMA.
 //
 // Replaces ggml's CPU MUL_MAT at small M > 1 (continuous-batching decode; every M > 1
 // projection goes there: core/src/inference.cpp:1049-1063, executed at
@@ -22,6 +23,9 @@
 //     m_j * S_j);
 //   - per superblock: acc += dA * (d * sum_j sc_j I_j - dmin * sum_j m_j S_j)
 //     (vec_dot_q4_K_q8_K's per-superblock form).
+// Q5_K (the Q5 variant): the level is q = nib + 16 h with h the element's qh bit, so
+// sum_j sc_j I_j(q) = sum_j sc_j I_j(nib) + 16 sum_j I_j(h sc_j): one more MFMA per sub-block on
+// the bytes h * sc_j (0 or sc_j <= 63), the nibble part as for Q4_K.
 // The 8 partial tiles are summed in wave order through LDS at the end (deterministic), each
 // wave summing an eighth of the tile. With few weight rows the superblocks are also split over
 // workgroups (grid z): each stores its partial tile in a plane of the split-K scratch and
@@ -68,7 +72,7 @@ __device__ __forceinline__ int aswz(int row, int slot) { return row * 256 + 16 *
 
 }  // namespace
 
-template <int MTI, bool DUMP>
+template <int MTI, bool DUMP, bool Q5>
 __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                                    int N, int nsb, const int8_t* __restrict__ xqs,
                                                                    const float* __restrict__ xd, int64_t m_ld, int M,
@@ -114,11 +118,15 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
 #pragma unroll
         for (int i = 0; i < kDA; ++i) dma16(a_src[i] + 256 * s, a_lds + 1024 * i);
         dma16(d_src + (int64_t)s * m_ld, d_lds);
-        const uint8_t* sb = wrow + (int64_t)s * 144;
+        constexpr int kSb = Q5 ? 176 : 144, kQs = Q5 ? 48 : 16;
+        const uint8_t* sb = wrow + (int64_t)s * kSb;
         const uint4 hdr = ld16(sb);
         uint4 qw[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) qw[c] = ld16(sb + 16 + 32 * c + 16 * hl);
+        for (int c = 0; c < 4; ++c) qw[c] = ld16(sb + kQs + 32 * c + 16 * hl);
+        // Q5_K: qh[16hl .. 16hl + 15], the fifth bits of this lane half's elements
+        [[maybe_unused]] uint4 qhw;
+        if constexpr (Q5) qhw = ld16(sb + 16 + 16 * hl);
         __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
         __builtin_amdgcn_wave_barrier();
 
@@ -134,6 +142,7 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
         // packed 16-bit multiply (no byte carries into the next: 15 * 7 < 256). The mins operand
         // (every byte m_j) is rebuilt per use: it would hold 32 registers.
         v4i bhi[8], blo[8];
+        [[maybe_unused]] v4i bhb[8];
         int mn[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -150,16 +159,24 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
                 bhi[j][e] = __builtin_bit_cast(int, (u16x2)(b * s_hi));
                 blo[j][e] = __builtin_bit_cast(int, (u16x2)(b * s_lo));
             }
+            if constexpr (Q5) {
+                // bytes h * sc_j: bit j of each qh byte, times sc (no carries: 0 or sc <= 63)
+                const uint32_t h[4] = {qhw.x, qhw.y, qhw.z, qhw.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bhb[j][e] = (int)(((h[e] >> j) & 0x01010101u) * (uint32_t)sc);
+            }
             mn[j] = (int)(((mnw[j >> 2] >> (8 * (j & 3))) & 0xFFu) * 0x01010101u);
         }
 #pragma unroll
         for (int i = 0; i < MTI; ++i) {
             v16i ahi, alo, amin;
+            [[maybe_unused]] v16i ahb;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 ahi[v] = 0;
                 alo[v] = 0;
                 amin[v] = 0;
+                if constexpr (Q5) ahb[v] = 0;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -170,10 +187,14 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
                 ahi = mfma32(av, bhi[j], ahi);
                 alo = mfma32(av, blo[j], alo);
                 amin = mfma32(av, bm, amin);
+                if constexpr (Q5) ahb = mfma32(av, bhb[j], ahb);
             }
             v16i ai;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) ai[v] = (ahi[v] << 3) + alo[v];
+            for (int v = 0; v < 16; ++v) {
+                ai[v] = (ahi[v] << 3) + alo[v];
+                if constexpr (Q5) ai[v] += ahb[v] << 4;
+            }
             // lane owns weight row n = n0 + col and activation rows m_v = 32i + 8(v/4) + 4hl + v%4
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -229,9 +250,9 @@ __global__ void __launch_bounds__(64 * kWaves, 1) batch_q4k_kernel(const uint8_t
     }
 }
 
-hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                            const SplitScratch& sc) {
+hipError_t launch_batch_q4k(bool q5, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                            const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                            hipStream_t st, const SplitScratch& sc) {
     if (w_row_bytes % 16 || N > (1 << 30) || M > (1 << 30) || K > (1 << 30)) return hipErrorNotSupported;
     // the per-superblock scale DMA reads 64 scales at [s][m0 .. m0 + 63]: m_ld must cover the
     // last m-tile (it is M rounded up to 128)
@@ -247,8 +268,10 @@ hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
     dim3 grid((unsigned)((N + kNT - 1) / kNT), (unsigned)((M + kMT - 1) / kMT), (unsigned)sp.splits);
     const size_t lds = (size_t)kWaves * (mti == 1 ? BGeo<1>::kRegion : BGeo<2>::kRegion);
-    auto fn = mti == 1 ? (block_sums ? batch_q4k_kernel<1, true> : batch_q4k_kernel<1, false>)
-                       : (block_sums ? batch_q4k_kernel<2, true> : batch_q4k_kernel<2, false>);
+    auto fn = q5 ? (mti == 1 ? (block_sums ? batch_q4k_kernel<1, true, true> : batch_q4k_kernel<1, false, true>)
+                             : (block_sums ? batch_q4k_kernel<2, true, true> : batch_q4k_kernel<2, false, true>))
+                 : (mti == 1 ? (block_sums ? batch_q4k_kernel<1, true, false> : batch_q4k_kernel<1, false, false>)
+                             : (block_sums ? batch_q4k_kernel<2, true, false> : batch_q4k_kernel<2, false, false>));
     hipLaunchKernelGGL(fn, grid, dim3(64 * kWaves), lds, st, (const uint8_t*)W, w_row_bytes, (int)N, nsb, act.qs,
                        act.d, act.m_ld, (int)M, sp.stps, out, out_stride, block_sums);
     hipError_t e = hipGetLastError();

@@ -1,4 +1,4 @@
-// dcq_batch_q8.hip — batched-decode mul_mat (4 < M <= 64) for Q8_0 weights on int8 MFMA.
+// dcq_batch_q8.hip — batched-decode mul_mat (4 < M <= 64) for Q8_0 and Q4_0 weights on int8 MFMA.
 //
 // Replaces ggml's CPU MUL_MAT at small M > 1 for Q8_0 weights (continuous-batching decode: every
 // M > 1 projection goes there, core/src/inference.cpp:1049-1063, executed at
@@ -19,6 +19,9 @@
 //     bit pattern of 1.5 * 2^23, so the int32 block sums I_b read as fp32 are 1.5*2^23 + I_b
 //     (|I_b| < 2^22), and accumulates
 //       acc += dA * fma(F, dW, -dW * 1.5*2^23)          (= dA * dW * I_b, vec_dot_q8_0_q8_0's form).
+// Q4_0 weights (Q40): a chunk is 4 pairs of 18-byte blocks (36 bytes, 9 dwords, both lane halves
+// load the pair); lane half hl takes the low (hl = 0) or high nibbles of a block's 16 bytes, its
+// elements 16hl .. 16hl + 15, as signed q - 8 bytes. The rest is the Q8_0 path (|I_b| <= 32*8*128).
 // The 8 partial tiles are summed in wave order through LDS at the end (deterministic). With few
 // weight rows the chunks are also split over workgroups (grid z): each stores its partial tile in
 // a plane of the split-K scratch and launch_sum_splits adds them in order.
@@ -65,10 +68,11 @@ __device__ __forceinline__ int aswz(int row, int slot) { return row * 256 + 16 *
 
 }  // namespace
 
-// W: Q8_0 rows (w_row_bytes % 4 == 0, 16-byte aligned base); xqs: int8 [M][K]; xd: float
-// [K/32][m_ld], m_ld >= M rounded up to the m-tile; K = 256 * nch. Workgroup z computes chunks
-// [z * cpz, (z + 1) * cpz) and stores plane z of Y (planes of M rows; one plane: Y itself).
-template <int MTI, bool DUMP>
+// W: Q8_0 rows, or Q4_0 rows when Q40 (w_row_bytes % 4 == 0, 16-byte aligned base); xqs: int8
+// [M][K]; xd: float [K/32][m_ld], m_ld >= M rounded up to the m-tile; K = 256 * nch. Workgroup z
+// computes chunks [z * cpz, (z + 1) * cpz) and stores plane z of Y (planes of M rows; one plane: Y
+// itself).
+template <int MTI, bool DUMP, bool Q40>
 __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                                  int N, int nch, int cpz,
                                                                  const int8_t* __restrict__ xqs,
@@ -134,16 +138,29 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
         // block pair p: dwords D0..D16 at chunk byte 68p (d_even = low half of D0, the even block's
         // quants at bytes 2..33, d_odd = high half of D8, the odd block's quants at bytes 36..67).
         // Lane half hl: A = D[4hl..4hl+3], e = D[4hl+4], B = D[9+4hl..12+4hl], s = D[8 - 8hl]
+        // (Q4_0: D0..D8 at chunk byte 36p, A = D0..D3, e = D4, B = D5..D8 for both halves)
         uint4 A[4], B[4];
         uint32_t e[4], sx[4];
-        const uint8_t* cb = wrow + (int64_t)c * 272;
+        if constexpr (Q40) {
+            const uint8_t* cb = wrow + (int64_t)c * 144;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const uint8_t* pb = cb + 68 * p;
-            A[p] = ld16(pb + 16 * hl);
-            e[p] = ld1(pb + 16 + 16 * hl);
-            B[p] = ld16(pb + 36 + 16 * hl);
-            sx[p] = ld1(pb + 32 - 32 * hl);
+            for (int p = 0; p < 4; ++p) {
+                const uint8_t* pb = cb + 36 * p;  // dword aligned only
+                const U32x4 lo = ld4(pb), hi = ld4(pb + 16);
+                A[p] = make_uint4(lo.x, lo.y, lo.z, lo.w);  // D0..D3
+                B[p] = make_uint4(hi.x, hi.y, hi.z, hi.w);  // D4..D7
+                e[p] = ld1(pb + 32);                        // D8
+            }
+        } else {
+            const uint8_t* cb = wrow + (int64_t)c * 272;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint8_t* pb = cb + 68 * p;
+                A[p] = ld16(pb + 16 * hl);
+                e[p] = ld1(pb + 16 + 16 * hl);
+                B[p] = ld16(pb + 36 + 16 * hl);
+                sx[p] = ld1(pb + 32 - 32 * hl);
+            }
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads (and the rest) have landed
         __builtin_amdgcn_wave_barrier();
@@ -153,7 +170,25 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
             const int p = j >> 1;
             v4i b;
             uint32_t dbits;
-            if ((j & 1) == 0) {
+            if constexpr (Q40) {
+                // A[p] = D0..D3, B[p] = D4..D7, e[p] = D8; lane half hl takes nibble half hl
+                const uint32_t sh = 4u * (uint32_t)hl, m = 0x0F0F0F0Fu;
+                uint32_t q[4];
+                if ((j & 1) == 0) {
+                    q[0] = align_bytes(A[p].y, A[p].x, 2);
+                    q[1] = align_bytes(A[p].z, A[p].y, 2);
+                    q[2] = align_bytes(A[p].w, A[p].z, 2);
+                    q[3] = align_bytes(B[p].x, A[p].w, 2);
+                    dbits = A[p].x & 0xFFFFu;
+                } else {
+                    q[0] = B[p].y, q[1] = B[p].z, q[2] = B[p].w, q[3] = e[p];
+                    dbits = B[p].x >> 16;
+                }
+                b.x = (int)minus8((q[0] >> sh) & m);
+                b.y = (int)minus8((q[1] >> sh) & m);
+                b.z = (int)minus8((q[2] >> sh) & m);
+                b.w = (int)minus8((q[3] >> sh) & m);
+            } else if ((j & 1) == 0) {
                 b.x = (int)align_bytes(A[p].y, A[p].x, 2);
                 b.y = (int)align_bytes(A[p].z, A[p].y, 2);
                 b.z = (int)align_bytes(A[p].w, A[p].z, 2);
@@ -221,10 +256,10 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
     }
 }
 
-hipError_t launch_batch_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                             int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                             const SplitScratch& sc) {
-    if (K % 256 || w_row_bytes % 4 || w_row_bytes < K / 32 * 34 || (uintptr_t)W % 16 || M > 64 || M < 1 ||
+hipError_t launch_batch_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                             hipStream_t st, const SplitScratch& sc) {
+    if (K % 256 || w_row_bytes % 4 || w_row_bytes < K / 32 * (q40 ? 18 : 34) || (uintptr_t)W % 16 || M > 64 || M < 1 ||
         N > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
     const int mti = M <= 32 ? 1 : 2, mt = 32 * mti;
@@ -239,8 +274,10 @@ hipError_t launch_batch_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int6
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
     dim3 grid((unsigned)tiles_n, 1u, (unsigned)sp.splits);
     const size_t lds = (size_t)kWaves * (mti == 1 ? Geo<1>::kRegion : Geo<2>::kRegion);
-    auto fn = mti == 1 ? (block_sums ? batch_q8_0_kernel<1, true> : batch_q8_0_kernel<1, false>)
-                       : (block_sums ? batch_q8_0_kernel<2, true> : batch_q8_0_kernel<2, false>);
+    auto fn = q40 ? (mti == 1 ? (block_sums ? batch_q8_0_kernel<1, true, true> : batch_q8_0_kernel<1, false, true>)
+                              : (block_sums ? batch_q8_0_kernel<2, true, true> : batch_q8_0_kernel<2, false, true>))
+                  : (mti == 1 ? (block_sums ? batch_q8_0_kernel<1, true, false> : batch_q8_0_kernel<1, false, false>)
+                              : (block_sums ? batch_q8_0_kernel<2, true, false> : batch_q8_0_kernel<2, false, false>));
     hipLaunchKernelGGL(fn, grid, dim3(64 * kWaves), lds, st, (const uint8_t*)W, w_row_bytes, (int)N, nch, sp.stps,
                        act.qs, act.d, act.m_ld, (int)M, out, out_stride, block_sums);
     hipError_t e = hipGetLastError();

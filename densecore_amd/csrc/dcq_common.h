@@ -121,9 +121,39 @@ __device__ __forceinline__ uint32_t q5_levels(uint32_t nib, uint32_t qh, uint32_
     return (nib & 0x0F0F0F0Fu) | (((qh >> bit) & 0x01010101u) << 4);
 }
 
+// Q4_0 block: sum over its 32 elements of (q - 8) * a; q[0..3] hold the 16 bytes of nibbles
+// (elements 0..15 low, 16..31 high), lo / hi the activation's elements 0..15 / 16..31.
+__device__ __forceinline__ int q4_0_block_dot(const uint32_t (&q)[4], const uint4& lo, const uint4& hi) {
+    const uint32_t m = 0x0F0F0F0Fu;
+    int i = 0;
+    i = sdot4((int)minus8(q[0] & m), (int)lo.x, i);
+    i = sdot4((int)minus8(q[1] & m), (int)lo.y, i);
+    i = sdot4((int)minus8(q[2] & m), (int)lo.z, i);
+    i = sdot4((int)minus8(q[3] & m), (int)lo.w, i);
+    i = sdot4((int)minus8((q[0] >> 4) & m), (int)hi.x, i);
+    i = sdot4((int)minus8((q[1] >> 4) & m), (int)hi.y, i);
+    i = sdot4((int)minus8((q[2] >> 4) & m), (int)hi.z, i);
+    i = sdot4((int)minus8((q[3] >> 4) & m), (int)hi.w, i);
+    return i;
+}
+
 // (hi:lo) >> (8*shift), low 32 bits; shift in bytes (0..3).
 __device__ __forceinline__ uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t shift) {
     return __builtin_amdgcn_alignbyte(hi, lo, shift);
+}
+
+// A dword-aligned pair of Q4_0 blocks (36 bytes as 9 dwords: block 0's d in bytes 0..1 and its
+// nibbles in 2..17, block 1's d in 18..19 and nibbles in 20..35) against 64 activation bytes:
+// the two blocks' exact sums and scales.
+__device__ __forceinline__ void q4_0_pair(const uint32_t (&w)[9], const uint4& a0, const uint4& a1, const uint4& a2,
+                                          const uint4& a3, int& i0, int& i1, float& dW0, float& dW1) {
+    const uint32_t q0[4] = {align_bytes(w[1], w[0], 2), align_bytes(w[2], w[1], 2), align_bytes(w[3], w[2], 2),
+                            align_bytes(w[4], w[3], 2)};
+    const uint32_t q1[4] = {w[5], w[6], w[7], w[8]};
+    i0 = q4_0_block_dot(q0, a0, a1);
+    i1 = q4_0_block_dot(q1, a2, a3);
+    dW0 = half_bits_to_float(w[0] & 0xFFFFu);
+    dW1 = half_bits_to_float(w[4] >> 16);
 }
 
 // Global loads with the alignment the data actually has. 16 B at 4-B alignment is a

@@ -1,4 +1,4 @@
-// dcq_decode.hip — decode GEMV (M <= 8 per launch) for the K-quant weights (Q4_K, Q6_K).
+// dcq_decode.hip — decode GEMV (M <= 8 per launch) for the K-quant weights (Q4_K, Q5_K, Q6_K).
 //
 // Replaces the per-row vec_dot loop of cb_gemv_custom (core/src/inference.cpp:896-923)
 // and ggml's CPU MUL_MAT at small M (core/src/inference.cpp:1794-1797, executed at
@@ -22,6 +22,8 @@
 //   the two 6-bit scales applied to exact sums, the mins term from the 16-element bsums:
 //     iA = sc_2c*I_2c + sc_2c+1*I_2c+1,  iB = m_2c*S_2c + m_2c+1*S_2c+1   (exact int32)
 //     acc += dA * (d * iA - dmin * iB)      (vec_dot_q4_K_q8_K's per-superblock form)
+// Q5_K (176 B): as Q4_K, the levels 5-bit: lane c also holds the superblock's 32 qh bytes and
+//   takes bits 2c, 2c+1 of them as bit 4 of its two sub-blocks' levels (vec_dot_q5_K_q8_K)
 // Q6_K (210 B, 2-byte aligned): lane (h, lh) holds elements l in [16lh, 16lh+16) of half h
 //   for all four quarters t: 16 bytes of ql low/high nibbles twice, 16 bytes of qh, the 16
 //   int8 scales and d; q = (nibble | 2 qh bits << 4) - 32 with the -32 taken through the
@@ -65,16 +67,32 @@ size_t act_lds_bytes_q8k(int MT, int64_t K) {
 
 
 // ---------------------------------------------------------------- per-format policies
-struct FmtQ4K {
-    static constexpr int kBytes = 144;    // superblock bytes
-    static constexpr int kSumsPerSb = 2;  // dumped int32 per superblock: sum sc*I, sum m*S
+// Q4_K (Q5 false) and Q5_K (Q5 true): the same header, scales and scale step
+template <bool Q5>
+struct FmtKq {
+    static constexpr int kBytes = Q5 ? 176 : 144;  // superblock bytes
+    static constexpr int kQs = Q5 ? 48 : 16;       // offset of the nibbles
+    static constexpr int kSumsPerSb = 2;           // dumped int32 per superblock: sum sc*I, sum m*S
     struct Raw {
         uint4 hdr, n0, n1;
+        uint4 h0, h1;  // Q5_K: qh[0..15], qh[16..31] (unused for Q4_K)
     };
     __device__ __forceinline__ static void load(const uint8_t* sb, int c, Raw& r) {
         r.hdr = ld16(sb);
-        r.n0 = ld16(sb + 16 + 32 * c);
-        r.n1 = ld16(sb + 32 + 32 * c);
+        r.n0 = ld16(sb + kQs + 32 * c);
+        r.n1 = ld16(sb + kQs + 16 + 32 * c);
+        if constexpr (Q5) {
+            r.h0 = ld16(sb + 16);
+            r.h1 = ld16(sb + 32);
+        }
+    }
+    // the levels of four elements: nibbles (shift 0: sub-block 2c, 4: sub-block 2c + 1), with the
+    // qh bit of that sub-block for Q5_K
+    __device__ __forceinline__ static uint32_t lv(uint32_t n, uint32_t h, uint32_t nsh, int c) {
+        if constexpr (Q5)
+            return q5_levels(n >> nsh, h, 2u * (uint32_t)c + (nsh >> 2));
+        else
+            return (n >> nsh) & 0x0F0F0F0Fu;
     }
     // exact integer sums of this lane's quarter against activation row mi; returns the fp32 term
     __device__ __forceinline__ static float dot(const Raw& r, const ActLds& act, int mi, int s, int c, int K, int MT,
@@ -86,29 +104,28 @@ struct FmtQ4K {
         const uint32_t mnw = lo_sc ? (s1 & 0x3F3F3F3Fu) : (((s2 >> 4) & 0x0F0F0F0Fu) | ((s1 >> 2) & 0x30303030u));
         const int sc0 = (int)((scw >> sh) & 0xFFu), sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
         const int mn0 = (int)((mnw >> sh) & 0xFFu), mn1 = (int)((mnw >> (sh + 8)) & 0xFFu);
-        const uint32_t lo = 0x0F0F0F0Fu;
         const int8_t* aq = act.qs + mi * K + 256 * s + 64 * c;
         const uint4 a0 = *reinterpret_cast<const uint4*>(aq);
         const uint4 a1 = *reinterpret_cast<const uint4*>(aq + 16);
         const uint4 a2 = *reinterpret_cast<const uint4*>(aq + 32);
         const uint4 a3 = *reinterpret_cast<const uint4*>(aq + 48);
         const uint2 bq = *reinterpret_cast<const uint2*>(act.bs + mi * (K / 16) + 16 * s + 4 * c);
-        int il = sdot4((int)(r.n0.x & lo), (int)a0.x, 0);
-        il = sdot4((int)(r.n0.y & lo), (int)a0.y, il);
-        il = sdot4((int)(r.n0.z & lo), (int)a0.z, il);
-        il = sdot4((int)(r.n0.w & lo), (int)a0.w, il);
-        il = sdot4((int)(r.n1.x & lo), (int)a1.x, il);
-        il = sdot4((int)(r.n1.y & lo), (int)a1.y, il);
-        il = sdot4((int)(r.n1.z & lo), (int)a1.z, il);
-        il = sdot4((int)(r.n1.w & lo), (int)a1.w, il);
-        int ih = sdot4((int)((r.n0.x >> 4) & lo), (int)a2.x, 0);
-        ih = sdot4((int)((r.n0.y >> 4) & lo), (int)a2.y, ih);
-        ih = sdot4((int)((r.n0.z >> 4) & lo), (int)a2.z, ih);
-        ih = sdot4((int)((r.n0.w >> 4) & lo), (int)a2.w, ih);
-        ih = sdot4((int)((r.n1.x >> 4) & lo), (int)a3.x, ih);
-        ih = sdot4((int)((r.n1.y >> 4) & lo), (int)a3.y, ih);
-        ih = sdot4((int)((r.n1.z >> 4) & lo), (int)a3.z, ih);
-        ih = sdot4((int)((r.n1.w >> 4) & lo), (int)a3.w, ih);
+        int il = sdot4((int)lv(r.n0.x, r.h0.x, 0, c), (int)a0.x, 0);
+        il = sdot4((int)lv(r.n0.y, r.h0.y, 0, c), (int)a0.y, il);
+        il = sdot4((int)lv(r.n0.z, r.h0.z, 0, c), (int)a0.z, il);
+        il = sdot4((int)lv(r.n0.w, r.h0.w, 0, c), (int)a0.w, il);
+        il = sdot4((int)lv(r.n1.x, r.h1.x, 0, c), (int)a1.x, il);
+        il = sdot4((int)lv(r.n1.y, r.h1.y, 0, c), (int)a1.y, il);
+        il = sdot4((int)lv(r.n1.z, r.h1.z, 0, c), (int)a1.z, il);
+        il = sdot4((int)lv(r.n1.w, r.h1.w, 0, c), (int)a1.w, il);
+        int ih = sdot4((int)lv(r.n0.x, r.h0.x, 4, c), (int)a2.x, 0);
+        ih = sdot4((int)lv(r.n0.y, r.h0.y, 4, c), (int)a2.y, ih);
+        ih = sdot4((int)lv(r.n0.z, r.h0.z, 4, c), (int)a2.z, ih);
+        ih = sdot4((int)lv(r.n0.w, r.h0.w, 4, c), (int)a2.w, ih);
+        ih = sdot4((int)lv(r.n1.x, r.h1.x, 4, c), (int)a3.x, ih);
+        ih = sdot4((int)lv(r.n1.y, r.h1.y, 4, c), (int)a3.y, ih);
+        ih = sdot4((int)lv(r.n1.z, r.h1.z, 4, c), (int)a3.z, ih);
+        ih = sdot4((int)lv(r.n1.w, r.h1.w, 4, c), (int)a3.w, ih);
         // S_2c = bsums[4c] + bsums[4c+1], S_2c+1 = bsums[4c+2] + bsums[4c+3]
         const int S0 = (int)(int16_t)(bq.x & 0xFFFFu) + (int)(int16_t)(bq.x >> 16);
         const int S1 = (int)(int16_t)(bq.y & 0xFFFFu) + (int)(int16_t)(bq.y >> 16);
@@ -121,6 +138,8 @@ struct FmtQ4K {
         return dA * fmaf(-dmin, (float)iB, d * (float)iA);
     }
 };
+using FmtQ4K = FmtKq<false>;
+using FmtQ5K = FmtKq<true>;
 
 struct FmtQ6K {
     static constexpr int kBytes = 210;
@@ -445,10 +464,10 @@ DecodeFn pick_shape(int idx, int mt, int nw) {
     }
 }
 
-// the gate/up pair (GLU) is built for Q4_K with the fused activation only
+// the gate/up pair (GLU) is built for Q4_K and Q5_K with the fused activation only
 template <class Fmt>
 DecodeFn pick_fn(bool fuse, bool dump, bool glu, int idx, int mt, int nw) {
-    if constexpr (std::is_same<Fmt, FmtQ4K>::value) {
+    if constexpr (!std::is_same<Fmt, FmtQ6K>::value) {
         if (glu) return pick_shape<Fmt, true, false, true>(idx, mt, nw);
     }
     return fuse ? (dump ? pick_shape<Fmt, true, true>(idx, mt, nw) : pick_shape<Fmt, true, false>(idx, mt, nw))
@@ -535,16 +554,16 @@ Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
     return {best->idx, best->nw};
 }
 
-// W2 != nullptr: the gate/up pair (Q4_K, fused activation, no block sums): Y = silu(W x) * (W2 x)
+// W2 != nullptr: the gate/up pair (Q4_K or Q5_K, fused activation, no block sums): Y = silu(W x) * (W2 x)
 hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_t w_row_bytes, int64_t n0, int64_t n1,
                      int64_t K, const float* X, int64_t x_stride, const PlanarBuffers* act, int64_t M, float* Y,
                      int64_t y_stride, int32_t* block_sums, int64_t sums_n_stride, hipStream_t st,
                      const float* R = nullptr, int64_t r_stride = 0) {
     const int nsb = (int)(K / 256);
-    if (wtype != kTypeQ4_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
+    if (wtype != kTypeQ4_K && wtype != kTypeQ5_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
     const bool glu = W2 != nullptr;
-    if (glu && (wtype != kTypeQ4_K || !fuse || block_sums)) return hipErrorNotSupported;
-    if (wtype == kTypeQ4_K ? (w_row_bytes % 16 != 0) : (w_row_bytes % 2 != 0)) return hipErrorNotSupported;
+    if (glu && (wtype == kTypeQ6_K || !fuse || block_sums)) return hipErrorNotSupported;
+    if (wtype != kTypeQ6_K ? (w_row_bytes % 16 != 0) : (w_row_bytes % 2 != 0)) return hipErrorNotSupported;
     // the 5-wave variants exist for the fused, sum-free single-row decode and the gate/up pair at
     // M = 1, which take the launch rule (the pair at config 2's shape: 7.44 -> 7.22 us with it,
     // kernel arguments preloaded); other variants keep choose_shape with 4 waves
@@ -553,7 +572,7 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
     const int idx = ln.idx;
     if (idx < 0) return hipErrorNotSupported;
     const int P = kShapes[idx].P;
-    const int64_t per_row_sums = (wtype == kTypeQ4_K ? 2 : 1) * (K / 256);
+    const int64_t per_row_sums = (wtype == kTypeQ6_K ? 1 : 2) * (K / 256);
     // validate every M tile before launching anything
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
@@ -568,8 +587,9 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
         const int nw = ln.nw;
         const int rows_per_block = nw * (64 / (4 * P));
         const unsigned grid = (unsigned)((n1 - n0 + rows_per_block - 1) / rows_per_block);
-        DecodeFn fn = wtype == kTypeQ4_K ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, glu, idx, mt, nw)
-                                         : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, false, idx, mt, nw);
+        DecodeFn fn = wtype == kTypeQ4_K   ? pick_fn<FmtQ4K>(fuse, block_sums != nullptr, glu, idx, mt, nw)
+                      : wtype == kTypeQ5_K ? pick_fn<FmtQ5K>(fuse, block_sums != nullptr, glu, idx, mt, nw)
+                                           : pick_fn<FmtQ6K>(fuse, block_sums != nullptr, false, idx, mt, nw);
         // rows beyond mc in an MT tile stage the last real activation row and are never stored
         hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * nw), lds, st, fuse ? X + m0 * x_stride : nullptr, x_stride,
                            (int)mc, nsb, (const uint8_t*)W, w_row_bytes, n0, n1, (const uint8_t*)W2,
@@ -594,13 +614,13 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
                                int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                hipStream_t st, const float* R, int64_t r_stride) {
     if (knob(Knob::NoFuse)) return hipErrorNotSupported;
-    if (wtype == kTypeQ8_0)
-        return launch_decode_fused_q8_0(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R,
-                                        r_stride);
+    if (wtype == kTypeQ8_0 || wtype == kTypeQ4_0)
+        return launch_decode_fused_q8_0(wtype == kTypeQ4_0, W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride,
+                                        block_sums, st, R, r_stride);
     if (wtype == kTypeQ6_K && !knob(Knob::Q6KDecode))
         return launch_decode_fused_q6k(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R,
                                        r_stride);
-    if (wtype != kTypeQ4_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
+    if (wtype != kTypeQ4_K && wtype != kTypeQ5_K && wtype != kTypeQ6_K) return hipErrorNotSupported;
     return launch_kq(wtype, true, W, nullptr, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, block_sums,
                      N, st, R, r_stride);
 }
@@ -609,9 +629,10 @@ hipError_t launch_decode_fused_glu(int wtype, const void* Wg, const void* Wu, in
                                    const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
                                    hipStream_t st) {
     if (knob(Knob::NoFuse)) return hipErrorNotSupported;
-    if (wtype == kTypeQ8_0)
-        return launch_decode_fused_q8_0_glu(Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, st);
-    if (wtype != kTypeQ4_K) return hipErrorNotSupported;
+    if (wtype == kTypeQ8_0 || wtype == kTypeQ4_0)
+        return launch_decode_fused_q8_0_glu(wtype == kTypeQ4_0, Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y,
+                                            y_stride, st);
+    if (wtype != kTypeQ4_K && wtype != kTypeQ5_K) return hipErrorNotSupported;
     return launch_kq(wtype, true, Wg, Wu, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, nullptr, N, st);
 }
 

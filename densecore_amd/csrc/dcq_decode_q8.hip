@@ -1,4 +1,4 @@
-// dcq_decode_q8.hip — decode GEMV (M <= 8 per launch) for Q8_0 weights with the
+// dcq_decode_q8.hip — decode GEMV (M <= 8 per launch) for Q8_0 and Q4_0 weights with the
 // activation's Q8_0 quantization fused in (one launch per decode step, no workspace).
 //
 // Replaces cb_gemv_custom's quantize-once-then-vec_dot-per-row (core/src/inference.cpp:
@@ -7,8 +7,9 @@
 //
 // Launch shape. A workgroup of NW waves owns NW * 64/G weight rows; G lanes stream a row,
 // lane g holding the block pairs u = g + G*t, t < NS (68 bytes: two 34-byte blocks, dword
-// aligned because K % 64 == 0 and the row stride is a multiple of 4). Every weight load of
-// a lane is issued right after the activation loads, before any arithmetic.
+// aligned because K % 64 == 0 and the row stride is a multiple of 4; Q4_0: 36 bytes, two
+// 18-byte blocks, their nibbles turned into signed q - 8 bytes as they are used). Every weight
+// load of a lane is issued right after the activation loads, before any arithmetic.
 //
 // Activation. Each workgroup quantizes the M fp32 rows into LDS: 8 lanes per 32-element
 // block, 4 floats per lane, the block's max |x| over the 8 lanes by DPP. The arithmetic is
@@ -48,6 +49,14 @@ __device__ __forceinline__ void load_pair(const uint8_t* p, uint32_t (&r)[17]) {
     r[16] = ld1(p + 64);
 }
 
+// 36 bytes (two 18-byte Q4_0 blocks) at a dword aligned address into 9 dwords
+__device__ __forceinline__ void load_pair(const uint8_t* p, uint32_t (&r)[9]) {
+    const U32x4 a = ld4(p), b = ld4(p + 16);
+    r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+    r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+    r[8] = ld1(p + 32);
+}
+
 // exact int32 sums of a block pair (w: 17 dwords, block 0's bytes start at byte 2, block 1's at
 // byte 36) against 64 activation bytes
 __device__ __forceinline__ void pair_sums(const uint32_t* w, uint4 a0, uint4 a1, uint4 a2, uint4 a3, int& i0,
@@ -69,6 +78,17 @@ __device__ __forceinline__ void pair_sums(const uint32_t* w, uint4 a0, uint4 a1,
     i1 = sdot4((int)w[15], (int)a3.z, i1);
     i1 = sdot4((int)w[16], (int)a3.w, i1);
 }
+// the pair's exact sums and its two weight scales, Q8_0 (17 dwords) or Q4_0 (9 dwords)
+__device__ __forceinline__ void pair_terms(const uint32_t (&w)[17], uint4 a0, uint4 a1, uint4 a2, uint4 a3, int& i0,
+                                           int& i1, float& dW0, float& dW1) {
+    pair_sums(w, a0, a1, a2, a3, i0, i1);
+    dW0 = half_bits_to_float(w[0] & 0xFFFFu);
+    dW1 = half_bits_to_float(w[8] >> 16);
+}
+__device__ __forceinline__ void pair_terms(const uint32_t (&w)[9], uint4 a0, uint4 a1, uint4 a2, uint4 a3, int& i0,
+                                           int& i1, float& dW0, float& dW1) {
+    q4_0_pair(w, a0, a1, a2, a3, i0, i1, dW0, dW1);
+}
 
 constexpr int kMaxStagePasses = 8;  // float4 registers of activation per thread
 
@@ -84,7 +104,9 @@ __host__ __device__ constexpr int q8_stage_passes(int G, int NS, int MT, int NW)
 // The arguments the first loads need come first: the first 56 bytes of arguments are preloaded
 // into scalar registers at dispatch (-amdgpu-kernarg-preload-count), the rest take a dependent
 // scalar load.
-template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, int QC = q8_stage_passes(G, NS, MT, NW)>
+// Q40: the weights are Q4_0 (36-byte block pairs) instead of Q8_0 (68-byte pairs).
+template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, bool Q40 = false,
+          int QC = q8_stage_passes(G, NS, MT, NW)>
 __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __restrict__ X, int64_t x_stride,
                                                            const uint8_t* __restrict__ W,
                                                            const uint8_t* __restrict__ W2, int64_t w_row_bytes,
@@ -118,12 +140,13 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
         const bool row_ok = row < N;
         const uint8_t* wrow = W + (row_ok ? row : N - 1) * w_row_bytes;
         const int g = lane % G;
-        uint32_t raw[NS][17], raw2[GLU ? NS : 1][17];
+        constexpr int kPairDw = Q40 ? 9 : 17, kPairBytes = 4 * kPairDw;
+        uint32_t raw[NS][kPairDw], raw2[GLU ? NS : 1][kPairDw];
 #pragma clang loop unroll(full)
         for (int t = 0; t < NS; ++t) {
             int u = g + G * t;
             u = u < U ? u : U - 1;
-            load_pair(wrow + (int64_t)u * 68, raw[t]);
+            load_pair(wrow + (int64_t)u * kPairBytes, raw[t]);
         }
         if constexpr (GLU) {
             const uint8_t* wrow2 = W2 + (row_ok ? row : N - 1) * w_row_bytes;
@@ -131,7 +154,7 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
             for (int t = 0; t < NS; ++t) {
                 int u = g + G * t;
                 u = u < U ? u : U - 1;
-                load_pair(wrow2 + (int64_t)u * 68, raw2[t]);
+                load_pair(wrow2 + (int64_t)u * kPairBytes, raw2[t]);
             }
         }
         // keep the quantizer's first use of the activation (and its wait) behind the weight loads
@@ -171,8 +194,6 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
             const int u_raw = g + G * t;
             const bool valid = u_raw < U;
             const int u = valid ? u_raw : U - 1;
-            const uint32_t* w = raw[t];
-            const float dW0 = half_bits_to_float(w[0] & 0xFFFFu), dW1 = half_bits_to_float(w[8] >> 16);
             // all MT rows, also those >= M (never stored): a guard would let the compiler merge
             // the unrolled steps into one select-fed block
 #pragma unroll
@@ -184,7 +205,8 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
                 const uint4 a3 = *reinterpret_cast<const uint4*>(aq + 48);
                 const float2 dA = *reinterpret_cast<const float2*>(act_d + mi * nb + 2 * u);
                 int i0, i1;
-                pair_sums(w, a0, a1, a2, a3, i0, i1);
+                float dW0, dW1;
+                pair_terms(raw[t], a0, a1, a2, a3, i0, i1, dW0, dW1);
                 if (DUMP && valid && row_ok && mi < M) {
                     int32_t* srow = sums + ((int64_t)mi * sums_n_stride + row) * nb;
                     atomicAdd(srow + 2 * u, i0);
@@ -193,10 +215,9 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
                 const float v = fmaf((float)i1, dW1 * dA.y, (float)i0 * (dW0 * dA.x));
                 acc[mi] = valid ? acc[mi] + v : acc[mi];
                 if constexpr (GLU) {
-                    const uint32_t* w2 = raw2[t];
-                    const float eW0 = half_bits_to_float(w2[0] & 0xFFFFu), eW1 = half_bits_to_float(w2[8] >> 16);
                     int j0, j1;
-                    pair_sums(w2, a0, a1, a2, a3, j0, j1);
+                    float eW0, eW1;
+                    pair_terms(raw2[t], a0, a1, a2, a3, j0, j1, eW0, eW1);
                     const float v2 = fmaf((float)j1, eW1 * dA.y, (float)j0 * (eW0 * dA.x));
                     acc2[mi] = valid ? acc2[mi] + v2 : acc2[mi];
                 }
@@ -235,33 +256,38 @@ static_assert(kNumQ8Shapes == 10, "pick_q8_shape covers every shape");
 #endif
 constexpr int kQ8Waves = DCQ_Q8_NW;
 
-template <int I, int MT, bool DUMP, bool GLU>
+template <int I, int MT, bool DUMP, bool GLU, bool Q40>
 DecodeQ8Fn q8_fn() {
-    return decode_q8_0_kernel<kQ8Shapes[I].G, kQ8Shapes[I].NS, MT, kQ8Waves, DUMP, GLU>;
+    return decode_q8_0_kernel<kQ8Shapes[I].G, kQ8Shapes[I].NS, MT, kQ8Waves, DUMP, GLU, Q40>;
 }
-template <int I, bool DUMP, bool GLU>
+template <int I, bool DUMP, bool GLU, bool Q40>
 DecodeQ8Fn q8_pick_mt(int mt) {
     switch (mt) {
-        case 1: return q8_fn<I, 1, DUMP, GLU>();
-        case 2: return q8_fn<I, 2, DUMP, GLU>();
-        case 4: return q8_fn<I, 4, DUMP, GLU>();
-        default: return q8_fn<I, 8, DUMP, GLU>();
+        case 1: return q8_fn<I, 1, DUMP, GLU, Q40>();
+        case 2: return q8_fn<I, 2, DUMP, GLU, Q40>();
+        case 4: return q8_fn<I, 4, DUMP, GLU, Q40>();
+        default: return q8_fn<I, 8, DUMP, GLU, Q40>();
     }
 }
-template <bool DUMP, bool GLU = false>
+template <bool DUMP, bool GLU, bool Q40>
 DecodeQ8Fn q8_pick_shape(int idx, int mt) {
     switch (idx) {
-        case 0: return q8_pick_mt<0, DUMP, GLU>(mt);
-        case 1: return q8_pick_mt<1, DUMP, GLU>(mt);
-        case 2: return q8_pick_mt<2, DUMP, GLU>(mt);
-        case 3: return q8_pick_mt<3, DUMP, GLU>(mt);
-        case 4: return q8_pick_mt<4, DUMP, GLU>(mt);
-        case 5: return q8_pick_mt<5, DUMP, GLU>(mt);
-        case 6: return q8_pick_mt<6, DUMP, GLU>(mt);
-        case 7: return q8_pick_mt<7, DUMP, GLU>(mt);
-        case 8: return q8_pick_mt<8, DUMP, GLU>(mt);
-        default: return q8_pick_mt<9, DUMP, GLU>(mt);
+        case 0: return q8_pick_mt<0, DUMP, GLU, Q40>(mt);
+        case 1: return q8_pick_mt<1, DUMP, GLU, Q40>(mt);
+        case 2: return q8_pick_mt<2, DUMP, GLU, Q40>(mt);
+        case 3: return q8_pick_mt<3, DUMP, GLU, Q40>(mt);
+        case 4: return q8_pick_mt<4, DUMP, GLU, Q40>(mt);
+        case 5: return q8_pick_mt<5, DUMP, GLU, Q40>(mt);
+        case 6: return q8_pick_mt<6, DUMP, GLU, Q40>(mt);
+        case 7: return q8_pick_mt<7, DUMP, GLU, Q40>(mt);
+        case 8: return q8_pick_mt<8, DUMP, GLU, Q40>(mt);
+        default: return q8_pick_mt<9, DUMP, GLU, Q40>(mt);
     }
+}
+template <bool Q40>
+DecodeQ8Fn q8_pick(bool glu, bool dump, int idx, int mt) {
+    return glu ? q8_pick_shape<false, true, Q40>(idx, mt)
+               : (dump ? q8_pick_shape<true, false, Q40>(idx, mt) : q8_pick_shape<false, false, Q40>(idx, mt));
 }
 
 // fewest steps whose idle pair slots stay within a quarter; then any shape that fits.
@@ -291,10 +317,10 @@ int choose_q8_shape(int U) {
 
 namespace {
 
-// W2 != nullptr: the gate/up pair (no block sums), Y = silu(W x) * (W2 x)
-hipError_t launch_q8(const void* W, const void* W2, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
-                     int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                     const float* R = nullptr, int64_t r_stride = 0) {
+// W2 != nullptr: the gate/up pair (no block sums), Y = silu(W x) * (W2 x). q40: Q4_0 weights.
+hipError_t launch_q8(bool q40, const void* W, const void* W2, int64_t w_row_bytes, int64_t N, int64_t K,
+                     const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                     hipStream_t st, const float* R = nullptr, int64_t r_stride = 0) {
     if (K % 64 != 0 || w_row_bytes % 4 != 0 || x_stride % 4 != 0) return hipErrorNotSupported;
     if (W2 && block_sums) return hipErrorNotSupported;
     const int U = (int)(K / 64);
@@ -315,8 +341,8 @@ hipError_t launch_q8(const void* W, const void* W2, int64_t w_row_bytes, int64_t
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         const size_t lds = (size_t)mt * K * 9 / 8;
-        DecodeQ8Fn fn = W2 ? q8_pick_shape<false, true>(idx, mt)
-                           : (block_sums ? q8_pick_shape<true>(idx, mt) : q8_pick_shape<false>(idx, mt));
+        DecodeQ8Fn fn = q40 ? q8_pick<true>(W2 != nullptr, block_sums != nullptr, idx, mt)
+                            : q8_pick<false>(W2 != nullptr, block_sums != nullptr, idx, mt);
         hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kQ8Waves), lds, st, X + m0 * x_stride, x_stride,
                            (const uint8_t*)W, (const uint8_t*)W2, w_row_bytes, N, (int)K, (int)mc, Y + m0 * y_stride,
                            y_stride,
@@ -328,16 +354,16 @@ hipError_t launch_q8(const void* W, const void* W2, int64_t w_row_bytes, int64_t
 
 }  // namespace
 
-hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
-                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                    hipStream_t st, const float* R, int64_t r_stride) {
-    return launch_q8(W, nullptr, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R, r_stride);
+hipError_t launch_decode_fused_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                                    const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
+                                    int32_t* block_sums, hipStream_t st, const float* R, int64_t r_stride) {
+    return launch_q8(q40, W, nullptr, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R, r_stride);
 }
 
-hipError_t launch_decode_fused_q8_0_glu(const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
-                                        const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
-                                        hipStream_t st) {
-    return launch_q8(Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, nullptr, st);
+hipError_t launch_decode_fused_q8_0_glu(bool q40, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N,
+                                        int64_t K, const float* X, int64_t x_stride, int64_t M, float* Y,
+                                        int64_t y_stride, hipStream_t st) {
+    return launch_q8(q40, Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, nullptr, st);
 }
 
 }  // namespace dcq

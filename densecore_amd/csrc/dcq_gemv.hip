@@ -287,22 +287,6 @@ __device__ __forceinline__ float unit_dot(const RawQ5K& r, int u, const int8_t* 
     return kq_quarter_finish<DUMP>(r.hdr, s, c, bsv, dA, i0, i1, sums_row, valid);
 }
 
-// Q4_0 block: sum over its 32 elements of (q - 8) * a; q[0..3] hold the 16 bytes of nibbles
-// (elements 0..15 low, 16..31 high), lo / hi the activation's elements 0..15 / 16..31.
-__device__ __forceinline__ int q4_0_block_dot(const uint32_t (&q)[4], const uint4& lo, const uint4& hi) {
-    const uint32_t m = 0x0F0F0F0Fu;
-    int i = 0;
-    i = sdot4((int)minus8(q[0] & m), (int)lo.x, i);
-    i = sdot4((int)minus8(q[1] & m), (int)lo.y, i);
-    i = sdot4((int)minus8(q[2] & m), (int)lo.z, i);
-    i = sdot4((int)minus8(q[3] & m), (int)lo.w, i);
-    i = sdot4((int)minus8((q[0] >> 4) & m), (int)hi.x, i);
-    i = sdot4((int)minus8((q[1] >> 4) & m), (int)hi.y, i);
-    i = sdot4((int)minus8((q[2] >> 4) & m), (int)hi.z, i);
-    i = sdot4((int)minus8((q[3] >> 4) & m), (int)hi.w, i);
-    return i;
-}
-
 template <bool DUMP>
 __device__ __forceinline__ float unit_dot(const RawQ4_0Pair& r, int u, const int8_t* xrow, const float* xd,
                                           int64_t m_ld, int64_t m, const int16_t*, int32_t* sums_row,
@@ -310,14 +294,9 @@ __device__ __forceinline__ float unit_dot(const RawQ4_0Pair& r, int u, const int
     const uint4 a0 = ld16(xrow + 64 * u), a1 = ld16(xrow + 64 * u + 16);
     const uint4 a2 = ld16(xrow + 64 * u + 32), a3 = ld16(xrow + 64 * u + 48);
     const float dA0 = xd[(int64_t)(2 * u) * m_ld + m], dA1 = xd[(int64_t)(2 * u + 1) * m_ld + m];
-    const uint32_t* w = r.w;
-    // block 0: d in bytes 0..1, nibbles in bytes 2..17; block 1: d in bytes 18..19, nibbles 20..35
-    const uint32_t q0[4] = {align_bytes(w[1], w[0], 2), align_bytes(w[2], w[1], 2), align_bytes(w[3], w[2], 2),
-                            align_bytes(w[4], w[3], 2)};
-    const uint32_t q1[4] = {w[5], w[6], w[7], w[8]};
-    const int i0 = q4_0_block_dot(q0, a0, a1);
-    const int i1 = q4_0_block_dot(q1, a2, a3);
-    const float dW0 = half_bits_to_float(w[0] & 0xFFFFu), dW1 = half_bits_to_float(w[4] >> 16);
+    int i0, i1;
+    float dW0, dW1;
+    q4_0_pair(r.w, a0, a1, a2, a3, i0, i1, dW0, dW1);
     if (DUMP && valid) {
         atomicAdd(sums_row + 2 * u, i0);
         atomicAdd(sums_row + 2 * u + 1, i1);
@@ -489,7 +468,7 @@ hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0
     // DCQ_Q6K_DECODE=1 selects the lane-direct four-lanes-per-superblock kernel instead
     if (knob(Knob::GemvGeneric) == 0) {
         hipError_t e = hipErrorNotSupported;
-        if (wtype == kTypeQ4_K || (wtype == kTypeQ6_K && knob(Knob::Q6KDecode)))
+        if (wtype == kTypeQ4_K || wtype == kTypeQ5_K || (wtype == kTypeQ6_K && knob(Knob::Q6KDecode)))
             e = launch_decode_kq(wtype, W, w_row_bytes, n0, n1, K, act, M, Y, y_stride, block_sums, sums_n_stride,
                                  st, R, r_stride);
         else if (wtype == kTypeQ6_K)

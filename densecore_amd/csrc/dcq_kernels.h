@@ -27,7 +27,7 @@ hipError_t launch_unpack_ggml_rows(int vdt, const void* in, int64_t in_row_bytes
 // Decode GEMV / small-M: wave-per-row-group int8 dot products.
 // Y[m*y_stride + n] for m < M, n in [n0, n1); block_sums optional (atomics, pre-zeroed).
 // R (optional, indexed like Y, may be Y itself): Y = W x + R, added in the store of the
-// LDS-staged Q4_K / Q6_K kernels; with R given and neither covering the shape, nothing is
+// LDS-staged Q4_K / Q5_K / Q6_K kernels; with R given and neither covering the shape, nothing is
 // launched and the result is hipErrorNotSupported.
 // compute units of the current device (cached per device)
 int cu_count();
@@ -72,14 +72,14 @@ hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64
                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                             int64_t sums_n_stride, hipStream_t st, const float* R = nullptr, int64_t r_stride = 0);
 
-// SwiGLU gate/up pair at M <= 8 with the activation quantization fused in (Q4_K, Q8_0):
+// SwiGLU gate/up pair at M <= 8 with the activation quantization fused in (Q4_K, Q5_K, Q8_0, Q4_0):
 // Y = silu(Wg x) * (Wu x); hipErrorNotSupported when the fused kernels do not cover the shape.
 hipError_t launch_decode_fused_glu(int wtype, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
                                    const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
                                    hipStream_t st);
-hipError_t launch_decode_fused_q8_0_glu(const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
-                                        const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
-                                        hipStream_t st);
+hipError_t launch_decode_fused_q8_0_glu(bool q40, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N,
+                                        int64_t K, const float* X, int64_t x_stride, int64_t M, float* Y,
+                                        int64_t y_stride, hipStream_t st);
 // Y[m][n] = silu(Y[m][n]) * U[m][n] (the SwiGLU product after two separate projections)
 hipError_t launch_silu_mul(float* Y, int64_t y_stride, const float* U, int64_t u_stride, int64_t M, int64_t N,
                            hipStream_t st);
@@ -106,12 +106,13 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
                                hipStream_t st, const float* R = nullptr,
                                    int64_t r_stride = 0);
 
-// Q8_0 decode with the Q8_0 activation quantization fused in (K % 64 == 0, row stride a
-// multiple of 4 bytes, M*K*9/8 bytes of LDS per 8-row tile); hipErrorNotSupported otherwise.
-hipError_t launch_decode_fused_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const float* X,
-                                    int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
-                                    hipStream_t st, const float* R = nullptr,
-                                   int64_t r_stride = 0);
+// Q8_0 (q40 false) or Q4_0 (q40 true) decode with the Q8_0 activation quantization fused in
+// (K % 64 == 0, row stride a multiple of 4 bytes, M*K*9/8 bytes of LDS per 8-row tile);
+// hipErrorNotSupported otherwise.
+hipError_t launch_decode_fused_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                                    const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
+                                    int32_t* block_sums, hipStream_t st, const float* R = nullptr,
+                                    int64_t r_stride = 0);
 
 // Room for the partial tiles of a split-K product (fp32 planes of M x N); bytes == 0: no split.
 struct SplitScratch {
@@ -133,35 +134,35 @@ SplitPlan plan_split_k(int64_t tiles, int nstages, int align, int64_t M, int64_t
 hipError_t launch_sum_splits(const float* P, int splits, int64_t M, int64_t N, float* Y, int64_t y_stride,
                              hipStream_t st);
 
-// Q8_0 prefill: LDS-staged 128 x 128 int8-MFMA tiles (K % 128 == 0, w_row_bytes % 4 == 0);
-// hipErrorNotSupported otherwise (nothing launched).
-hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                               const SplitScratch& sc = SplitScratch());
+// Q8_0 (q40: Q4_0) prefill: LDS-staged 128 x 128 int8-MFMA tiles (K % 128 == 0, w_row_bytes % 4
+// == 0); hipErrorNotSupported otherwise (nothing launched).
+hipError_t launch_prefill_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                               const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                               hipStream_t st, const SplitScratch& sc = SplitScratch());
 
 // Q6_K prefill: the same tiling over the planar Q8_K activation (K % 512 == 0, w_row_bytes % 4
 // == 0, m_ld % 128 == 0); hipErrorNotSupported otherwise (nothing launched).
 hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                                int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
                                const SplitScratch& sc = SplitScratch());
-// Q4_K prefill: the same tiling (K % 256 == 0, w_row_bytes % 16 == 0, m_ld % 128 == 0).
-hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                               const SplitScratch& sc = SplitScratch());
+// Q4_K (q5: Q5_K) prefill: the same tiling (K % 256 == 0, w_row_bytes % 16 == 0, m_ld % 128 == 0).
+hipError_t launch_prefill_q4_k(bool q5, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                               const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                               hipStream_t st, const SplitScratch& sc = SplitScratch());
 
-// Q4_K batched decode (M <= 128): 8-wave workgroups per 32 weight rows x 64 activation
+// Q4_K (q5: Q5_K) batched decode (M <= 128): 8-wave workgroups per 32 weight rows x 64 activation
 // rows, K split over the waves (and over workgroups when the rows are few and sc has room);
 // hipErrorNotSupported when the shape is outside it.
-hipError_t launch_batch_q4k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                            int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                            const SplitScratch& sc = SplitScratch());
+hipError_t launch_batch_q4k(bool q5, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                            const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                            hipStream_t st, const SplitScratch& sc = SplitScratch());
 
-// Q8_0 batched decode (4 < M <= 64): 8-wave workgroups per 32 weight rows x 32 or 64 activation
+// Q8_0 (q40: Q4_0) batched decode (4 < M <= 64): 8-wave workgroups per 32 weight rows x 32 or 64 activation
 // rows, K split over the waves (and over workgroups when the rows are few and sc has room);
 // hipErrorNotSupported when the shape is outside it.
-hipError_t launch_batch_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                             int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                             const SplitScratch& sc);
+hipError_t launch_batch_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                             hipStream_t st, const SplitScratch& sc);
 
 // Q6_K batched decode (4 < M <= 64, K % 512 == 0): the same launch shape, one int8 MFMA per
 // 16-element scale group; hipErrorNotSupported when the shape is outside it.

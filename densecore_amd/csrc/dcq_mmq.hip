@@ -602,35 +602,37 @@ static MmqFn pick(int wtype, const MmqShape& s) {
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                       int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
                       const SplitScratch& sc) {
-    if (wtype == kTypeQ8_0 && M <= 64) {
-        const hipError_t e = launch_batch_q8_0(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
+    const bool q8 = wtype == kTypeQ8_0 || wtype == kTypeQ4_0, q40 = wtype == kTypeQ4_0;  // Q8_0-block kernels
+    if (q8 && M <= 64) {
+        const hipError_t e = launch_batch_q8_0(q40, W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
     if (wtype == kTypeQ6_K && M <= 64) {
         const hipError_t e = launch_batch_q6k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
-    // Q8_0 / Q6_K at 8 < M <= 32 also take the 128 x 128-tile kernels when the MMQ kernel's 32 x 32
-    // tiles would leave most CUs idle and the workspace has room to split K (2048 x 8192 at
-    // M = 16: 70 -> 25 us)
-    const bool starved = (M + 31) / 32 * ((N + 31) / 32) < cu_count() / 2 &&
-                         (wtype == kTypeQ8_0 || wtype == kTypeQ6_K) &&
-                         plan_split_k(((M + 127) / 128) * ((N + 127) / 128), (int)(K / 128),
-                                      wtype == kTypeQ8_0 ? 1 : 2, M, N, sc).splits > 1;
-    if (wtype == kTypeQ8_0 && (M > 32 || starved)) {
-        const hipError_t e = launch_prefill_q8_0(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
+    // Q8_0 / Q4_0 / Q6_K at 8 < M <= 32 also take the 128 x 128-tile kernels when the MMQ kernel's
+    // 32 x 32 tiles would leave most CUs idle and the workspace has room to split K (Q8_0 2048 x 8192
+    // at M = 16: 70 -> 25 us)
+    const bool starved = (M + 31) / 32 * ((N + 31) / 32) < cu_count() / 2 && (q8 || wtype == kTypeQ6_K) &&
+                         plan_split_k(((M + 127) / 128) * ((N + 127) / 128), (int)(K / 128), q8 ? 1 : 2, M, N,
+                                      sc).splits > 1;
+    if (q8 && (M > 32 || starved)) {
+        const hipError_t e = launch_prefill_q8_0(q40, W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
     if (wtype == kTypeQ6_K && (M > 32 || starved)) {
         const hipError_t e = launch_prefill_q6_k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
-    if (wtype == kTypeQ4_K && M > 128) {
-        const hipError_t e = launch_prefill_q4_k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
+    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && M > 128) {
+        const hipError_t e = launch_prefill_q4_k(wtype == kTypeQ5_K, W, w_row_bytes, N, K, act, M, Y, y_stride,
+                                                 block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
-    if (wtype == kTypeQ4_K && M <= 128) {
-        const hipError_t e = launch_batch_q4k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
+    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && M <= 128) {
+        const hipError_t e = launch_batch_q4k(wtype == kTypeQ5_K, W, w_row_bytes, N, K, act, M, Y, y_stride,
+                                              block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
     MmqShape s;

@@ -1,4 +1,4 @@
-// dcq_prefill.hip — prefill / batched mul_mat for Q8_0 weights on gfx950 int8 MFMA.
+// dcq_prefill.hip — prefill / batched mul_mat for Q8_0 (and Q4_0) weights on gfx950 int8 MFMA.
 //
 // Replaces ggml's CPU MUL_MAT at M > 1 for Q8_0 weights (core/src/inference.cpp:1049-1063
 // routes every M > 1 projection there; executed at core/src/worker.cpp:544):
@@ -26,6 +26,10 @@
 // wave64 op against 32 cycles per MFMA: 25 % of the int8 MFMA peak without packed fp32).
 // The seed is held in 16 VGPRs for the whole loop; everything else per block is the LDS
 // reads, four MFMAs and ~4 address instructions (about 37 VALU per MFMA over the kernel).
+//
+// Q4_0 weights (the Q40 variant) take the same path: a thread's block pair is 36 bytes (two
+// 18-byte blocks) and the commit unpacks the nibbles into signed q - 8 bytes, so the LDS tile,
+// MFMAs and epilogue are the Q8_0 ones (|I_b| <= 32*8*128 < 2^22 as well).
 //
 // Workgroup order is XCD-aware: consecutive workgroup ids go to different XCDs, so the
 // id is remapped to give each XCD a contiguous band of n tiles (its weight rows stay in
@@ -85,11 +89,12 @@ __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
 
 }  // namespace
 
-// W: Q8_0 rows (w_row_bytes % 4 == 0); xqs: int8 [M][K]; xd: float [K/32][m_ld]; K % 128 == 0.
+// W: Q8_0 rows, or Q4_0 rows when Q40 (w_row_bytes % 4 == 0); xqs: int8 [M][K]; xd: float
+// [K/32][m_ld]; K % 128 == 0.
 // FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
 // Arguments: the ones the first loads need come first (the first 56 bytes of arguments are
 // preloaded into scalar registers at dispatch).
-template <bool DUMP, bool FULL>
+template <bool DUMP, bool FULL, bool Q40>
 __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
                                                               int w_row_bytes, const uint8_t* __restrict__ W,
                                                               const int8_t* __restrict__ xqs,
@@ -139,18 +144,20 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
     // block (64w + l) / 32, rows 4 * ((64w + l) % 32) .. +4
     const int dc = 64 * (wave_u & 1) + lane;
     const uint32_t da_off = (uint32_t)(((int64_t)(dc >> 5) * m_ld + m0 + 4 * (dc & 31)) * 4);
-    // weight rows: row rw = tid / 2, block pair hw of the stage (68 bytes: d0, q0, d1, q1), through
-    // registers: q0 sits 2 bytes off a dword and is re-sliced; d1 and q1 start on dwords
+    // weight rows: row rw = tid / 2, block pair hw of the stage (68 bytes: d0, q0, d1, q1; Q4_0: 36
+    // bytes, the same order), through registers: q0 sits 2 bytes off a dword and is re-sliced; d1
+    // and q1 start on dwords
+    constexpr int kBlk = Q40 ? 18 : 34;  // weight block bytes
     const int rw = tid >> 1, hw = tid & 1;
-    const uint8_t* w_src = W + (int64_t)(FULL ? n0 + rw : min(n0 + rw, N - 1)) * w_row_bytes + hw * 68;
-    uint32_t gw[17];
+    const uint8_t* w_src = W + (int64_t)(FULL ? n0 + rw : min(n0 + rw, N - 1)) * w_row_bytes + hw * 2 * kBlk;
+    uint32_t gw[17];  // Q4_0 uses gw[0..8]
 #define DCQ_ISSUE(s_, S_)                                                                      \
     do {                                                                                       \
         const int8_t* ab_ = xqs + (int64_t)(s_) * kKS;                                         \
         _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                                       \
             dma16(ab_, a_off[i_], (S_).a + 1024 * (4 * wave_u + i_));                          \
         if (wave_u < 2) dma16(xd + (int64_t)(s_) * kKB * m_ld, da_off, &(S_).da[0][0] + 256 * wave_u); \
-        const uint8_t* wp_ = w_src + (int64_t)(s_) * (kKB * 34);                               \
+        const uint8_t* wp_ = w_src + (int64_t)(s_) * (kKB * kBlk);                             \
         _Pragma("unroll") for (int i_ = 0; i_ < 2; ++i_) {                                     \
             const U32x4 v_ = ld4(wp_ + 16 * i_);                                               \
             gw[4 * i_] = v_.x;                                                                 \
@@ -159,28 +166,53 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
             gw[4 * i_ + 3] = v_.w;                                                             \
         }                                                                                      \
         gw[8] = ld1(wp_ + 32);                                                                 \
-        _Pragma("unroll") for (int i_ = 0; i_ < 2; ++i_) {                                     \
-            const U32x4 v_ = ld4(wp_ + 36 + 16 * i_);                                          \
-            gw[9 + 4 * i_] = v_.x;                                                             \
-            gw[10 + 4 * i_] = v_.y;                                                            \
-            gw[11 + 4 * i_] = v_.z;                                                            \
-            gw[12 + 4 * i_] = v_.w;                                                            \
+        if constexpr (!Q40) {                                                                  \
+            _Pragma("unroll") for (int i_ = 0; i_ < 2; ++i_) {                                 \
+                const U32x4 v_ = ld4(wp_ + 36 + 16 * i_);                                      \
+                gw[9 + 4 * i_] = v_.x;                                                         \
+                gw[10 + 4 * i_] = v_.y;                                                        \
+                gw[11 + 4 * i_] = v_.z;                                                        \
+                gw[12 + 4 * i_] = v_.w;                                                        \
+            }                                                                                  \
         }                                                                                      \
     } while (0)
-    // weight block pair bytes: [0,2) d0, [2,34) q0, [34,36) d1, [36,68) q1;
-    // logical slots 4hw .. 4hw+3 of row rw
+    // weight block pair bytes: [0,2) d0, [2,34) q0, [34,36) d1, [36,68) q1 (Q4_0: [0,2) d0,
+    // [2,18) q0, [18,20) d1, [20,36) q1, each block's 16 nibble bytes holding its elements 0..15 in
+    // the low nibbles and 16..31 in the high ones); logical slots 4hw .. 4hw+3 of row rw
 #define DCQ_COMMIT(S_)                                                                         \
     do {                                                                                       \
-        *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw)) =                                  \
-            make_uint4(align_bytes(gw[1], gw[0], 2), align_bytes(gw[2], gw[1], 2),              \
-                       align_bytes(gw[3], gw[2], 2), align_bytes(gw[4], gw[3], 2));            \
-        *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 1)) =                              \
-            make_uint4(align_bytes(gw[5], gw[4], 2), align_bytes(gw[6], gw[5], 2),              \
-                       align_bytes(gw[7], gw[6], 2), align_bytes(gw[8], gw[7], 2));            \
-        *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 2)) = make_uint4(gw[9], gw[10], gw[11], gw[12]); \
-        *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 3)) = make_uint4(gw[13], gw[14], gw[15], gw[16]); \
-        const float d0_ = half_bits_to_float(gw[0] & 0xFFFFu);                                 \
-        const float d1_ = half_bits_to_float(gw[8] >> 16);                                     \
+        float d0_, d1_;                                                                        \
+        if constexpr (Q40) {                                                                   \
+            const uint32_t m_ = 0x0F0F0F0Fu;                                                   \
+            const uint32_t q0_[4] = {align_bytes(gw[1], gw[0], 2), align_bytes(gw[2], gw[1], 2), \
+                                     align_bytes(gw[3], gw[2], 2), align_bytes(gw[4], gw[3], 2)}; \
+            const uint32_t q1_[4] = {gw[5], gw[6], gw[7], gw[8]};                              \
+            *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw)) =                              \
+                make_uint4(minus8(q0_[0] & m_), minus8(q0_[1] & m_), minus8(q0_[2] & m_), minus8(q0_[3] & m_)); \
+            *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 1)) =                          \
+                make_uint4(minus8((q0_[0] >> 4) & m_), minus8((q0_[1] >> 4) & m_),             \
+                           minus8((q0_[2] >> 4) & m_), minus8((q0_[3] >> 4) & m_));            \
+            *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 2)) =                          \
+                make_uint4(minus8(q1_[0] & m_), minus8(q1_[1] & m_), minus8(q1_[2] & m_), minus8(q1_[3] & m_)); \
+            *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 3)) =                          \
+                make_uint4(minus8((q1_[0] >> 4) & m_), minus8((q1_[1] >> 4) & m_),             \
+                           minus8((q1_[2] >> 4) & m_), minus8((q1_[3] >> 4) & m_));            \
+            d0_ = half_bits_to_float(gw[0] & 0xFFFFu);                                         \
+            d1_ = half_bits_to_float(gw[4] >> 16);                                             \
+        } else {                                                                               \
+            *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw)) =                              \
+                make_uint4(align_bytes(gw[1], gw[0], 2), align_bytes(gw[2], gw[1], 2),          \
+                           align_bytes(gw[3], gw[2], 2), align_bytes(gw[4], gw[3], 2));        \
+            *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 1)) =                          \
+                make_uint4(align_bytes(gw[5], gw[4], 2), align_bytes(gw[6], gw[5], 2),          \
+                           align_bytes(gw[7], gw[6], 2), align_bytes(gw[8], gw[7], 2));        \
+            *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 2)) =                          \
+                make_uint4(gw[9], gw[10], gw[11], gw[12]);                                     \
+            *reinterpret_cast<uint4*>((S_).b + swz(rw, 4 * hw + 3)) =                          \
+                make_uint4(gw[13], gw[14], gw[15], gw[16]);                                    \
+            d0_ = half_bits_to_float(gw[0] & 0xFFFFu);                                         \
+            d1_ = half_bits_to_float(gw[8] >> 16);                                             \
+        }                                                                                      \
         /* -dW * 1.5 * 2^23 is exact: an 11-bit significand times 3 * 2^22 */                  \
         (S_).dwc[2 * hw][rw] = make_float2(d0_, -d0_ * kMagicF);                               \
         (S_).dwc[2 * hw + 1][rw] = make_float2(d1_, -d1_ * kMagicF);                           \
@@ -310,9 +342,9 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
 
 size_t prefill_q8_0_lds_bytes() { return 2 * sizeof(Stage); }
 
-hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                               const SplitScratch& sc) {
+hipError_t launch_prefill_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                               const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                               hipStream_t st, const SplitScratch& sc) {
     if (K % kKS || w_row_bytes % 4 || w_row_bytes > INT32_MAX || act.m_ld > INT32_MAX || N > (1 << 30) ||
         M > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
@@ -322,8 +354,10 @@ hipError_t launch_prefill_q8_0(const void* W, int64_t w_row_bytes, int64_t N, in
     const int tiles_n = (int)((N + kBN - 1) / kBN), tiles_m = (int)((M + kBM - 1) / kBM);
     const size_t lds = prefill_q8_0_lds_bytes();
     const bool full = M % kBM == 0 && N % kBN == 0;
-    auto fn = block_sums ? (full ? prefill_q8_0_kernel<true, true> : prefill_q8_0_kernel<true, false>)
-                         : (full ? prefill_q8_0_kernel<false, true> : prefill_q8_0_kernel<false, false>);
+    auto fn = q40 ? (block_sums ? (full ? prefill_q8_0_kernel<true, true, true> : prefill_q8_0_kernel<true, false, true>)
+                                : (full ? prefill_q8_0_kernel<false, true, true> : prefill_q8_0_kernel<false, false, true>))
+                  : (block_sums ? (full ? prefill_q8_0_kernel<true, true, false> : prefill_q8_0_kernel<true, false, false>)
+                                : (full ? prefill_q8_0_kernel<false, true, false> : prefill_q8_0_kernel<false, false, false>));
     // split-K when the tiles cannot fill the chip: partial planes in the scratch, then their sum
     const SplitPlan sp = plan_split_k((int64_t)tiles_n * tiles_m, (int)(K / kKS), 1, M, N, sc);
     float* out = sp.splits > 1 ? sc.p : Y;

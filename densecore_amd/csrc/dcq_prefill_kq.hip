@@ -1,4 +1,4 @@
-// dcq_prefill_kq.hip — prefill / batched mul_mat for K-quant weights (Q6_K, Q4_K) on gfx950
+// dcq_prefill_kq.hip — prefill / batched mul_mat for K-quant weights (Q6_K, Q4_K, Q5_K) on gfx950
 // int8 MFMA.
 //
 // Replaces ggml's CPU MUL_MAT at M > 1 for K-quant weights (core/src/inference.cpp:1049-1063 and
@@ -31,6 +31,8 @@
 // then iA += sc_j * I_j. iM runs on the MFMA once per superblock: S_j = 64 hi_j + lo_j (lo_j in
 // [0, 63], hi_j in [-64, 63], split at commit from the 16-element bsums) as int8 bytes
 // [hi_0..7, lo_0..7] against the bytes m_j in the first or the second eight k of a K = 16 MFMA.
+// Q5_K (the Q5 variant) is Q4_K with 5-bit levels: the commit also takes the sub-block's qh bit of
+// each element as bit 4 of its level (|I_j| <= 32*31*128 < 2^23, |iA| <= 8*63*2^17 < 2^31).
 //
 // Workgroup order is XCD-aware (consecutive ids go to different XCDs): each XCD takes a
 // contiguous band of n tiles, so its weight rows stay in that XCD's L2.
@@ -60,7 +62,7 @@ struct __align__(16) StageQ6 {
 
 struct __align__(16) StageQ4 {
     int8_t a[kBM * kRow];  // activation int8, [m][k] (swizzled 16-byte slots)
-    int8_t b[kBN * kRow];  // weight nibbles as int8 0..15, [n][k] (swizzled 16-byte slots)
+    int8_t b[kBN * kRow];  // weight levels as int8 0..15 (Q5_K 0..31), [n][k] (swizzled 16-byte slots)
     uint32_t sc[kBN];      // the stage's 4 sub-block scales (6-bit) per weight row
     uint2 mn[kBN];         // the superblock's 8 sub-block mins (6-bit) per weight row
     float2 dw[kBN];        // weight (d, dmin)
@@ -340,7 +342,7 @@ __global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(int tiles_n, int t
 // FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
 // Arguments: the ones the first loads need come first (the first 56 bytes of arguments are
 // preloaded into scalar registers at dispatch).
-template <bool DUMP, bool FULL>
+template <bool DUMP, bool FULL, bool Q5>
 __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
                                                               int w_row_bytes, const uint8_t* __restrict__ W,
                                                               const int8_t* __restrict__ xqs,
@@ -386,25 +388,31 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int t
         a_off[i] = (uint32_t)row * (uint32_t)K + 16u * (uint32_t)a_slot;
     }
     // weight rows: row rw = tid / 2 of the tile, part p = tid % 2: the 32 nibble bytes of chunk
-    // 2h + p of the stage's half h (bytes 16 + 64h + 32p: elements 64p + [0, 32) of the stage in
-    // the low nibbles, 64p + 32 + [0, 32) in the high ones); part 0 also loads the 16-byte header
-    // (d, dmin, 12 bytes of scales and mins). Threads 0..127 load activation row m0 + tid's scale
-    // and its superblock's 16 bsums.
+    // 2h + p of the stage's half h (bytes 16 + 64h + 32p, Q5_K 48 + 64h + 32p: elements 64p + [0, 32)
+    // of the stage in the low nibbles, 64p + 32 + [0, 32) in the high ones, and for Q5_K the 32 qh
+    // bytes); part 0 also loads the 16-byte header (d, dmin, 12 bytes of scales and mins). Threads
+    // 0..127 load activation row m0 + tid's scale and its superblock's 16 bsums.
+    constexpr int kSb = Q5 ? 176 : 144, kQs = Q5 ? 48 : 16;
     const int rw = tid >> 1, p = tid & 1;
     const uint8_t* w_row = W + (int64_t)(FULL ? n0 + rw : min(n0 + rw, N - 1)) * w_row_bytes;
     const int arow = tid & (kBM - 1);
     const int da_row = m0 + arow;  // m_ld >= m0 + 128: in bounds for every tile
     const int16_t* bs_row = xbs + (int64_t)(FULL ? m0 + arow : min(m0 + arow, M - 1)) * (K / 16);
     uint4 gq[2], ghdr, gbs[2];
+    [[maybe_unused]] uint4 gqh[2];
     float gda;
     auto issue = [&](int stg, StageQ4& S) {
         const int8_t* ab = xqs + (int64_t)stg * kKS;
 #pragma unroll
         for (int i = 0; i < 4; ++i) dma16(ab, a_off[i], S.a + 1024 * (4 * wave_u + i));
         const int s = stg >> 1, h = stg & 1;
-        const uint8_t* sb = w_row + 144 * (int64_t)s;
-        gq[0] = ld16(sb + 16 + 64 * h + 32 * p);
-        gq[1] = ld16(sb + 32 + 64 * h + 32 * p);
+        const uint8_t* sb = w_row + kSb * (int64_t)s;
+        gq[0] = ld16(sb + kQs + 64 * h + 32 * p);
+        gq[1] = ld16(sb + kQs + 16 + 64 * h + 32 * p);
+        if constexpr (Q5) {
+            gqh[0] = ld16(sb + 16);
+            gqh[1] = ld16(sb + 32);
+        }
         if (p == 0) ghdr = ld16(sb);
         gda = xd[(int64_t)s * m_ld + da_row];
         gbs[0] = ld16(bs_row + 16 * s);
@@ -414,12 +422,30 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int t
         const int h = stg & 1;
         const uint32_t lo = 0x0F0F0F0Fu;
         const uint32_t q[8] = {gq[0].x, gq[0].y, gq[0].z, gq[0].w, gq[1].x, gq[1].y, gq[1].z, gq[1].w};
-        *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p)) = make_uint4(q[0] & lo, q[1] & lo, q[2] & lo, q[3] & lo);
-        *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 1)) = make_uint4(q[4] & lo, q[5] & lo, q[6] & lo, q[7] & lo);
-        *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 2)) =
-            make_uint4((q[0] >> 4) & lo, (q[1] >> 4) & lo, (q[2] >> 4) & lo, (q[3] >> 4) & lo);
-        *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 3)) =
-            make_uint4((q[4] >> 4) & lo, (q[5] >> 4) & lo, (q[6] >> 4) & lo, (q[7] >> 4) & lo);
+        if constexpr (Q5) {
+            // sub-blocks j = 4h + 2p (low nibbles) and j + 1 (high): bit j / j + 1 of qh[l] is bit 4
+            const uint32_t qh[8] = {gqh[0].x, gqh[0].y, gqh[0].z, gqh[0].w, gqh[1].x, gqh[1].y, gqh[1].z, gqh[1].w};
+            const uint32_t j0 = 4u * (uint32_t)h + 2u * (uint32_t)p, j1 = j0 + 1u;
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p)) =
+                make_uint4(q5_levels(q[0], qh[0], j0), q5_levels(q[1], qh[1], j0), q5_levels(q[2], qh[2], j0),
+                           q5_levels(q[3], qh[3], j0));
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 1)) =
+                make_uint4(q5_levels(q[4], qh[4], j0), q5_levels(q[5], qh[5], j0), q5_levels(q[6], qh[6], j0),
+                           q5_levels(q[7], qh[7], j0));
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 2)) =
+                make_uint4(q5_levels(q[0] >> 4, qh[0], j1), q5_levels(q[1] >> 4, qh[1], j1),
+                           q5_levels(q[2] >> 4, qh[2], j1), q5_levels(q[3] >> 4, qh[3], j1));
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 3)) =
+                make_uint4(q5_levels(q[4] >> 4, qh[4], j1), q5_levels(q[5] >> 4, qh[5], j1),
+                           q5_levels(q[6] >> 4, qh[6], j1), q5_levels(q[7] >> 4, qh[7], j1));
+        } else {
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p)) = make_uint4(q[0] & lo, q[1] & lo, q[2] & lo, q[3] & lo);
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 1)) = make_uint4(q[4] & lo, q[5] & lo, q[6] & lo, q[7] & lo);
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 2)) =
+                make_uint4((q[0] >> 4) & lo, (q[1] >> 4) & lo, (q[2] >> 4) & lo, (q[3] >> 4) & lo);
+            *reinterpret_cast<uint4*>(S.b + swz(rw, 4 * p + 3)) =
+                make_uint4((q[4] >> 4) & lo, (q[5] >> 4) & lo, (q[6] >> 4) & lo, (q[7] >> 4) & lo);
+        }
         if (p == 0) {
             // 6-bit scales and mins of the 8 sub-blocks (get_scale_min_k4): j < 4 from bytes j, j + 4;
             // j >= 4 from the low / high nibble of byte j + 4 and the top two bits of bytes j - 4, j
@@ -487,7 +513,7 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int t
             for (int i = 0; i < 2; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) D[i][j] = mfma32k32(fa[i], fb[j]);
-            // |I_j| <= 32*15*127 < 2^23; |iA| <= 8*63*32*15*127 < 2^31
+            // |I_j| <= 32*31*128 < 2^23; |iA| <= 8*63*32*31*128 < 2^31
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -567,9 +593,9 @@ __global__ void __launch_bounds__(256, 2) prefill_q4_k_kernel(int tiles_n, int t
     }
 }
 
-hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
-                               int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
-                               const SplitScratch& sc) {
+hipError_t launch_prefill_q4_k(bool q5, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+                               const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
+                               hipStream_t st, const SplitScratch& sc) {
     if (K % 256 || w_row_bytes % 16 || w_row_bytes > INT32_MAX || act.m_ld % kBM || act.m_ld > INT32_MAX ||
         !act.bs || N > (1 << 30) || M > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
@@ -577,8 +603,10 @@ hipError_t launch_prefill_q4_k(const void* W, int64_t w_row_bytes, int64_t N, in
     const int tiles_n = (int)((N + kBN - 1) / kBN), tiles_m = (int)((M + kBM - 1) / kBM);
     const size_t lds = 2 * sizeof(StageQ4);
     const bool full = M % kBM == 0 && N % kBN == 0;
-    auto fn = block_sums ? (full ? prefill_q4_k_kernel<true, true> : prefill_q4_k_kernel<true, false>)
-                         : (full ? prefill_q4_k_kernel<false, true> : prefill_q4_k_kernel<false, false>);
+    auto fn = q5 ? (block_sums ? (full ? prefill_q4_k_kernel<true, true, true> : prefill_q4_k_kernel<true, false, true>)
+                               : (full ? prefill_q4_k_kernel<false, true, true> : prefill_q4_k_kernel<false, false, true>))
+                 : (block_sums ? (full ? prefill_q4_k_kernel<true, true, false> : prefill_q4_k_kernel<true, false, false>)
+                               : (full ? prefill_q4_k_kernel<false, true, false> : prefill_q4_k_kernel<false, false, false>));
     // split-K when the tiles cannot fill the chip (ranges of whole superblocks: two stages each)
     const SplitPlan sp = plan_split_k((int64_t)tiles_n * tiles_m, (int)(K / kKS), 2, M, N, sc);
     float* out = sp.splits > 1 ? sc.p : Y;

@@ -212,7 +212,9 @@ def _with_quantizer_ties(x, vdt):
 FUSED = [(Q8_0, 1, 96, 1024), (Q8_0, 8, 50, 1024), (Q8_0, 5, 37, 512), (Q8_0, 2, 41, 4096),
          (Q8_0, 1, 29, 3072), (Q8_0, 1, 70, 8192), (Q8_0, 3, 33, 2048), (Q4_K, 1, 45, 2560),
          (Q4_K, 7, 21, 1024), (Q4_K, 1, 2560, 9728),
-         (Q6_K, 1, 2560, 9728), (Q6_K, 2, 2560, 8192), (Q6_K, 1, 3000, 5120)]
+         (Q6_K, 1, 2560, 9728), (Q6_K, 2, 2560, 8192), (Q6_K, 1, 3000, 5120),
+         (Q4_0, 1, 96, 1024), (Q4_0, 5, 37, 512), (Q4_0, 1, 70, 8192), (Q4_0, 2, 2560, 9728),
+         (Q5_K, 1, 45, 2560), (Q5_K, 7, 21, 1024), (Q5_K, 1, 2560, 9728), (Q5_K, 3, 9728, 2560)]
 
 
 @pytest.mark.parametrize("wt,M,N,K", FUSED)
@@ -234,14 +236,15 @@ def test_decode_fused_quantization(O, dev, wt, M, N, K):
     O.assert_close(to_host(y2), y_ref, l1, RTOL, what="fused production kernel")
 
 
-# SwiGLU gate/up pair: the fused kernels (Q4_K, Q8_0 at M <= 8, shapes of both launch families)
-# and the general path (Q6_K; M > 8: the batched and prefill kernels plus the product kernel).
-# The last two shapes split K (few weight rows, long K): both products then use the split-K room
-# past the U temporary, one after the other.
+# SwiGLU gate/up pair: the fused kernels (Q4_K, Q5_K, Q8_0, Q4_0 at M <= 4, shapes of both launch
+# families) and the general path (Q6_K; larger M: the batched and prefill kernels plus the product
+# kernel). The two 64 x 2048 x 8192 shapes split K (few weight rows, long K): both products then use
+# the split-K room past the U temporary, one after the other.
 GATE_UP = [(Q4_K, 1, 97, 2560), (Q4_K, 1, 9728, 2560), (Q4_K, 5, 40, 1024), (Q8_0, 1, 96, 1024), (Q8_0, 3, 41, 2048),
            (Q6_K, 1, 50, 1024), (Q6_K, 3, 17, 768), (Q4_K, 33, 64, 512), (Q8_0, 40, 100, 512),
            (Q8_0, 64, 2048, 8192), (Q6_K, 64, 2048, 8192),
-           (Q4_0, 1, 96, 1024), (Q4_0, 6, 41, 2048), (Q5_K, 1, 97, 2560), (Q5_K, 40, 64, 512)]
+           (Q4_0, 1, 96, 1024), (Q4_0, 6, 41, 2048), (Q5_K, 1, 97, 2560), (Q5_K, 1, 9728, 2560), (Q5_K, 3, 40, 1024),
+           (Q5_K, 40, 64, 512)]
 
 
 @pytest.mark.parametrize("wt,M,N,K", GATE_UP)
@@ -549,11 +552,11 @@ def _random_blocks(wt, N, K, rng):
     rb = dc.row_size(wt, K)
     q = rng.integers(0, 256, size=(N, rb), dtype=np.uint8)
     scale = np.frombuffer(np.float16(0.0004).tobytes(), dtype=np.uint8)
-    if wt == Q8_0:
-        blk = q.reshape(N, K // 32, 34)
+    if wt in (Q8_0, Q4_0):
+        blk = q.reshape(N, K // 32, 34 if wt == Q8_0 else 18)
         blk[:, :, 0:2] = scale
-    elif wt == Q4_K:  # d, dmin, then 12 bytes of 6-bit scales and mins (random), nibbles
-        blk = q.reshape(N, K // 256, 144)
+    elif wt in (Q4_K, Q5_K):  # d, dmin, then 12 bytes of 6-bit scales and mins (random), (qh,) nibbles
+        blk = q.reshape(N, K // 256, 144 if wt == Q4_K else 176)
         blk[:, :, 0:2] = scale
         blk[:, :, 2:4] = np.frombuffer(np.float16(0.0002).tobytes(), dtype=np.uint8)
     else:  # Q6_K: 16 int8 sub-scales (random), d last
@@ -647,7 +650,8 @@ def test_kquant_prefill_full_shape(O, dev, wt):
 # (no split); repeated calls give the same bits.
 SPLIT_K = [(Q8_0, 64, 2048, 8192), (Q6_K, 64, 2048, 8192), (Q4_K, 256, 2048, 8192), (Q8_0, 40, 1000, 4096),
            (Q6_K, 200, 384, 2048), (Q4_K, 130, 256, 4096), (Q8_0, 16, 2048, 8192), (Q6_K, 9, 2048, 8192),
-           (Q8_0, 256, 8192, 2048)]
+           (Q8_0, 256, 8192, 2048), (Q4_0, 64, 2048, 8192), (Q4_0, 16, 2048, 8192), (Q4_0, 200, 384, 2048),
+           (Q5_K, 64, 2048, 8192), (Q5_K, 256, 2048, 8192), (Q5_K, 130, 256, 4096)]
 
 
 def _split_tail(M):
@@ -680,7 +684,8 @@ def test_split_k_parity(O, dev, wt, M, N, K):
     assert bool((ws[full - _split_tail(M):] == 0xAB).all())
 
 
-@pytest.mark.parametrize("wt,M,N,K", [(Q6_K, 64, 256, 4096), (Q8_0, 48, 384, 2048), (Q4_K, 160, 256, 2048)])
+@pytest.mark.parametrize("wt,M,N,K", [(Q6_K, 64, 256, 4096), (Q8_0, 48, 384, 2048), (Q4_K, 160, 256, 2048),
+                                      (Q4_0, 48, 384, 2048), (Q5_K, 160, 256, 2048), (Q5_K, 64, 256, 4096)])
 def test_split_k_block_sums(O, dev, wt, M, N, K):
     """The per-block int32 sums dumped by split-K ranges: every block written once, bit-exact."""
     import torch
@@ -698,15 +703,17 @@ def test_split_k_block_sums(O, dev, wt, M, N, K):
     O.assert_close(y, y_ref, l1, RTOL, what=f"split-K sums type {wt}")
 
 
-# Batched decode past four rows (Q6_K on matrices of 4096+ rows: past two): Q8_0 and Q6_K on their
-# batch kernels (one or two 32-row m-tiles, K split over the waves and, with few weight rows, over
-# workgroups), Q4_K at M = 5..8 on its own.
+# Batched decode past four rows (Q6_K on matrices of 4096+ rows: past two): Q8_0, Q4_0 and Q6_K on
+# their batch kernels (one or two 32-row m-tiles, K split over the waves and, with few weight rows,
+# over workgroups), Q4_K and Q5_K on theirs (Q5_K: the extra MFMA of the fifth bits).
 # Every output against the oracle, and the per-block int32 sums bit for bit.
 BATCH_SMALL_M = [(Q8_0, 5, 100, 1024), (Q8_0, 8, 8192, 2048), (Q8_0, 16, 2048, 8192), (Q8_0, 32, 96, 256),
                  (Q8_0, 33, 130, 2048), (Q8_0, 64, 2048, 8192), (Q8_0, 64, 8192, 2048), (Q8_0, 7, 33, 4096),
                  (Q4_K, 6, 300, 2048), (Q4_K, 8, 2048, 8192), (Q4_K, 64, 2048, 8192), (Q4_K, 100, 1000, 4096),
                  (Q6_K, 5, 100, 1024), (Q6_K, 8, 8192, 2048), (Q6_K, 16, 2048, 8192), (Q6_K, 33, 130, 2048),
-                 (Q6_K, 64, 2048, 8192), (Q6_K, 20, 77, 512), (Q6_K, 3, 4096, 1024), (Q6_K, 4, 8192, 2048)]
+                 (Q6_K, 64, 2048, 8192), (Q6_K, 20, 77, 512), (Q6_K, 3, 4096, 1024), (Q6_K, 4, 8192, 2048),
+                 (Q4_0, 5, 100, 1024), (Q4_0, 16, 2048, 8192), (Q4_0, 33, 130, 2048), (Q4_0, 64, 8192, 2048),
+                 (Q5_K, 6, 300, 2048), (Q5_K, 8, 2048, 8192), (Q5_K, 64, 8192, 2048), (Q5_K, 100, 1000, 4096)]
 
 
 @pytest.mark.parametrize("wt,M,N,K", BATCH_SMALL_M)
