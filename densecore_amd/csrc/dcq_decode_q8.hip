@@ -247,9 +247,10 @@ using DecodeQ8Fn = void (*)(const float*, int64_t, const uint8_t*, const uint8_t
 struct Q8Shape {
     int G, NS;
 };
-constexpr Q8Shape kQ8Shapes[] = {{16, 1}, {8, 2}, {32, 1}, {16, 2}, {64, 1}, {32, 2}, {16, 4}, {64, 2}, {32, 4}, {64, 4}};
+constexpr Q8Shape kQ8Shapes[] = {{16, 1}, {8, 2}, {32, 1}, {16, 2}, {64, 1}, {32, 2},
+                                 {16, 4}, {64, 2}, {32, 4}, {64, 4}, {16, 3}, {32, 3}};
 constexpr int kNumQ8Shapes = sizeof(kQ8Shapes) / sizeof(kQ8Shapes[0]);
-static_assert(kNumQ8Shapes == 10, "pick_q8_shape covers every shape");
+static_assert(kNumQ8Shapes == 12, "pick_q8_shape covers every shape");
 
 #ifndef DCQ_Q8_NW
 #define DCQ_Q8_NW 4
@@ -281,7 +282,9 @@ DecodeQ8Fn q8_pick_shape(int idx, int mt) {
         case 6: return q8_pick_mt<6, DUMP, GLU, Q40>(mt);
         case 7: return q8_pick_mt<7, DUMP, GLU, Q40>(mt);
         case 8: return q8_pick_mt<8, DUMP, GLU, Q40>(mt);
-        default: return q8_pick_mt<9, DUMP, GLU, Q40>(mt);
+        case 9: return q8_pick_mt<9, DUMP, GLU, Q40>(mt);
+        case 10: return q8_pick_mt<10, DUMP, GLU, Q40>(mt);
+        default: return q8_pick_mt<11, DUMP, GLU, Q40>(mt);
     }
 }
 template <bool Q40>
@@ -290,11 +293,34 @@ DecodeQ8Fn q8_pick(bool glu, bool dump, int idx, int mt) {
                : (dump ? q8_pick_shape<true, false, Q40>(idx, mt) : q8_pick_shape<false, false, Q40>(idx, mt));
 }
 
-// fewest steps whose idle pair slots stay within a quarter; then any shape that fits.
-// DCQ_Q8_SHAPE=<index> forces one (tuning).
-int choose_q8_shape(int U) {
+// The shape for U pairs per row. Measured on MI355X (fused, M = 1, W rotated over 1 GiB; us):
+//   Q8_0  9728 x 2560: {32,2} 6.47  {16,3} 6.88  {64,1} 8.19     4096 x 4096: {32,2} 5.00  {64,1} 5.34
+//        13824 x 5120: {32,3} 15.75 {64,2} 20.31                 2048 x 8192: {64,2} 5.39  {32,4} 5.80
+//   Q4_0  9728 x 2560: {16,3} 5.17  {16,4} 5.74  {32,2} 5.86  {64,1} 7.44
+//         8192 x 3072: {16,3} 4.61  {16,4} 5.12  {32,2} 5.37   2048 x 8192: {32,4} 4.30  {64,2} 4.71
+// Rows of at most 32 lanes win, with a lane's weight bytes in flight up to about 140 (Q8_0: 2
+// pairs of 68 B, then 3; Q4_0: 4 pairs of 36 B): within those limits the shape with the fewest idle
+// pair slots, then the fewest steps. Past them (long rows), the fewest steps whose idle slots stay
+// within a quarter, then any shape that fits. DCQ_Q8_SHAPE=<index> forces one (tuning).
+int choose_q8_shape(int U, bool q40) {
     const int forced = knob(Knob::Q8Shape);
     if (forced >= 0 && forced < kNumQ8Shapes && kQ8Shapes[forced].G * kQ8Shapes[forced].NS >= U) return forced;
+    const int tiers = q40 ? 1 : 2;
+    for (int t = 0; t < tiers; ++t) {
+        const int ns_max = q40 ? 4 : 2 + t;
+        int best = -1, best_waste = 1 << 30, best_ns = 1 << 30;
+        for (int i = 0; i < kNumQ8Shapes; ++i) {
+            const int cap = kQ8Shapes[i].G * kQ8Shapes[i].NS;
+            if (cap < U || kQ8Shapes[i].G > 32 || kQ8Shapes[i].NS > ns_max) continue;
+            const int waste = cap - U;
+            if (waste < best_waste || (waste == best_waste && kQ8Shapes[i].NS < best_ns)) {
+                best = i;
+                best_waste = waste;
+                best_ns = kQ8Shapes[i].NS;
+            }
+        }
+        if (best >= 0) return best;
+    }
     int best = -1;
     for (int pass = 0; pass < 2 && best < 0; ++pass) {
         int best_ns = 1 << 30, best_waste = 1 << 30;
@@ -324,7 +350,7 @@ hipError_t launch_q8(bool q40, const void* W, const void* W2, int64_t w_row_byte
     if (K % 64 != 0 || w_row_bytes % 4 != 0 || x_stride % 4 != 0) return hipErrorNotSupported;
     if (W2 && block_sums) return hipErrorNotSupported;
     const int U = (int)(K / 64);
-    const int idx = choose_q8_shape(U);
+    const int idx = choose_q8_shape(U, q40);
     if (idx < 0) return hipErrorNotSupported;
     const int G = kQ8Shapes[idx].G, NS = kQ8Shapes[idx].NS;
     // validate every M tile before launching anything

@@ -44,7 +44,7 @@ enum class Knob {
     Q6KLdsOff,    // DCQ_Q6K_LDS_OFF: 1 disables the LDS-staged Q6_K kernels
     Q6KNoFuse,    // DCQ_Q6K_NO_FUSE: 1 disables the fused Q6_K decode
     Q6KFuseWaves, // DCQ_Q6K_FUSE_NW: force the fused Q6_K workgroup width (4, 8, 10, 12)
-    Q8Shape,      // DCQ_Q8_SHAPE: force a Q8_0 decode shape index (-1: launch rule)
+    Q8Shape,      // DCQ_Q8_SHAPE: force a Q8_0 / Q4_0 decode shape index (-1: launch rule)
     GemvGeneric,  // DCQ_GEMV_GENERIC: 1 forces the generic GEMV kernel
     GemvLanes,    // DCQ_GEMV_LG: log2 lanes per row of the generic GEMV (-1: rule)
     AttnNoMfma,   // DCQ_ATTN_NO_MFMA: 1 keeps prompts on the VALU attention kernel

@@ -214,6 +214,8 @@ FUSED = [(Q8_0, 1, 96, 1024), (Q8_0, 8, 50, 1024), (Q8_0, 5, 37, 512), (Q8_0, 2,
          (Q4_K, 7, 21, 1024), (Q4_K, 1, 2560, 9728),
          (Q6_K, 1, 2560, 9728), (Q6_K, 2, 2560, 8192), (Q6_K, 1, 3000, 5120),
          (Q4_0, 1, 96, 1024), (Q4_0, 5, 37, 512), (Q4_0, 1, 70, 8192), (Q4_0, 2, 2560, 9728),
+         # shapes of 3 pairs per lane: 16 x 3 (Q4_0 at K = 2560), 32 x 3 (K = 5120)
+         (Q4_0, 1, 300, 2560), (Q4_0, 3, 200, 5120), (Q8_0, 1, 300, 5120), (Q8_0, 2, 97, 3072),
          (Q5_K, 1, 45, 2560), (Q5_K, 7, 21, 1024), (Q5_K, 1, 2560, 9728), (Q5_K, 3, 9728, 2560)]
 
 
@@ -243,7 +245,7 @@ def test_decode_fused_quantization(O, dev, wt, M, N, K):
 GATE_UP = [(Q4_K, 1, 97, 2560), (Q4_K, 1, 9728, 2560), (Q4_K, 5, 40, 1024), (Q8_0, 1, 96, 1024), (Q8_0, 3, 41, 2048),
            (Q6_K, 1, 50, 1024), (Q6_K, 3, 17, 768), (Q4_K, 33, 64, 512), (Q8_0, 40, 100, 512),
            (Q8_0, 64, 2048, 8192), (Q6_K, 64, 2048, 8192),
-           (Q4_0, 1, 96, 1024), (Q4_0, 6, 41, 2048), (Q5_K, 1, 97, 2560), (Q5_K, 1, 9728, 2560), (Q5_K, 3, 40, 1024),
+           (Q4_0, 1, 96, 1024), (Q4_0, 1, 96, 2560), (Q4_0, 6, 41, 2048), (Q5_K, 1, 97, 2560), (Q5_K, 1, 9728, 2560), (Q5_K, 3, 40, 1024),
            (Q5_K, 40, 64, 512)]
 
 
