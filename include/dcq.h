@@ -2,7 +2,8 @@
  * dcq.h — C ABI of libdcq, the MI355X (gfx950) quantized mul_mat backend.
  *
  * It replaces the compute behind ggml's MUL_MAT for GGUF Q8_0 / Q4_K / Q6_K
- * weights times fp32 activations with fp32 output, the operator DenseCore's
+ * weights (and the quantize tool's Q4_0 / Q5_K, core/src/quantize.cpp:71-78)
+ * times fp32 activations with fp32 output, the operator DenseCore's
  * graph emits for every FFN / attention projection:
  *   core/src/inference.cpp:1063, 1794-1797, 1817 (ggml_mul_mat call sites),
  *   core/src/worker.cpp:544 (ggml_backend_graph_compute executes them),
@@ -14,8 +15,8 @@
  *     the null stream). Every call is stream-ordered and asynchronous.
  *   - All data pointers are device pointers owned by the caller; nothing is
  *     freed across the ABI.
- *   - Type ids are ggml's: F32 = 0, F16 = 1, Q8_0 = 8, Q4_K = 12, Q6_K = 14,
- *     Q8_K = 15.
+ *   - Type ids are ggml's: F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12,
+ *     Q5_K = 13, Q6_K = 14, Q8_K = 15.
  *   - Dimensions: W is [N][K] (N output rows, K reduction), row r starts at
  *     W + r * w_row_bytes. X is [M][K] fp32 with row stride x_stride_bytes.
  *     Y is [M][N] fp32 with row stride y_stride_bytes:
