@@ -258,10 +258,10 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
     // out before the activation is waited for (fewer loads ahead of it), the rest once it is
     // quantized (measured at M = 1: 2560 x 9728 9.5 -> 8.7 us; with 4-wave workgroups rows of
     // three 1 KB pieces lose: 1024 x 2560 3.8 -> 4.2 us)
-    // Waves past the first SW stage nothing and issue the whole row at once. The staging
-    // waves are dispatched first, so their activation loads still lead the CU's queue (with
-    // every wave staging, the last-dispatched waves' activation landed about 1.1 us after
-    // the first's, and the barrier waited for them).
+    // Waves past the first SW stage nothing and issue the whole row at once. The launcher has
+    // every wave stage: one quantizer pass each instead of three on four staging waves
+    // (2560 x 9728: 7.94-8.04 -> 7.71-7.72 us; the early share of the row then measured best at
+    // 40 %: 20 % 7.99, 50 % 7.86, 60 % 7.88, the whole row 8.40 us).
     constexpr bool split = FUSE && kWaves > 4;
     const int n_early = split && stager ? (2 * cur.nx4) / 5 : cur.nx4;
     issue_head(cur);
@@ -681,10 +681,10 @@ using Q6Fn = void (*)(const float*, int64_t, const uint8_t*, int64_t, int64_t, i
                       const float*, const int16_t*, int64_t, float*, int64_t, int32_t*, int64_t, const float*,
                       int64_t);
 
-// fused activation: M <= 2 rows, nsb <= 64. 4-wave workgroups: every wave stages, at most 8
-// passes of 16 (superblock, row) pairs. 8..12 waves: the first 4 waves stage, at most 4 passes
-// (nsb * M <= 64; 64 registers of activation per lane)
-constexpr int q6_stage_waves(int nw) { return nw > 4 ? 4 : nw; }
+// fused activation: M <= 2 rows, nsb <= 64. Every wave stages: at most 8 passes of 16 (superblock,
+// row) pairs in 4-wave workgroups, at most 4 passes of 4 * NW pairs in 8..12-wave ones (64
+// registers of activation per lane)
+constexpr int q6_stage_waves(int nw) { return nw; }
 template <int MT, bool DUMP, int NW, int QC>
 Q6Fn q6_fused_qc(int qc) {
     constexpr int SW = q6_stage_waves(NW);
