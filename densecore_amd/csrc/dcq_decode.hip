@@ -517,7 +517,11 @@ int choose_shape(int nsb) {
 struct Launch {
     int idx, nw;
 };
-Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
+// nw5_max_per_cu: 5-wave candidates only up to that many workgroups per CU. Q5_K's steps hold
+// 80 B per lane (Q4_K 48 B): with three or more 5-wave workgroups per CU they lose (14336 x 4096:
+// {4,5} in 5 waves 13.8 us, in 4 waves 11.3 us), while at one or two per CU they still win
+// (9728 x 2560 {4,3}: 5.62 against 6.01 us; 2560 x 9728 {8,5}: 6.82 against 7.79 us).
+Launch choose_launch(int nsb, int64_t rows, bool nw5_ok, int64_t nw5_max_per_cu = INT64_MAX) {
     const int forced = knob(Knob::Q4KShape);
     if (forced >= 0) return {choose_shape(nsb), knob(Knob::Q4KWaves) == 5 ? 5 : 4};
     const int cus = cu_count();
@@ -534,6 +538,7 @@ Launch choose_launch(int nsb, int64_t rows, bool nw5_ok) {
         for (int nw = 4; nw <= (nw5_ok ? 5 : 4); ++nw) {
             const int64_t rpw = nw * (64 / (4 * kShapes[i].P));
             const int64_t wgs = (rows + rpw - 1) / rpw, per_cu = (wgs + cus - 1) / cus;
+            if (nw == 5 && per_cu > nw5_max_per_cu) continue;
             cands[nc++] = {i, nw, per_cu * rpw, per_cu};
             min_busiest = cands[nc - 1].busiest < min_busiest ? cands[nc - 1].busiest : min_busiest;
         }
@@ -568,7 +573,8 @@ hipError_t launch_kq(int wtype, bool fuse, const void* W, const void* W2, int64_
     // M = 1, which take the launch rule (the pair at config 2's shape: 7.44 -> 7.22 us with it,
     // kernel arguments preloaded); other variants keep choose_shape with 4 waves
     const bool single = fuse && !block_sums && M == 1;
-    const Launch ln = single ? choose_launch(nsb, n1 - n0, true) : Launch{choose_shape(nsb), 4};
+    const Launch ln = single ? choose_launch(nsb, n1 - n0, true, wtype == kTypeQ5_K ? 2 : INT64_MAX)
+                             : Launch{choose_shape(nsb), 4};
     const int idx = ln.idx;
     if (idx < 0) return hipErrorNotSupported;
     const int P = kShapes[idx].P;
