@@ -13,7 +13,7 @@ LIB_PATH = os.path.join(HERE, "libdcq.so")
 SYMBOLS = [
     "dcq_version", "dcq_status_string", "dcq_block_size", "dcq_type_size", "dcq_row_size", "dcq_vec_dot_type",
     "dcq_supports_mul_mat", "dcq_quantize_rows", "dcq_mul_mat_workspace_size", "dcq_mul_mat", "dcq_mul_mat_ex",
-    "dcq_block_sums_per_row", "dcq_dot_rows", "dcq_quantize_weights", "dcq_dequantize_rows",
+    "dcq_block_sums_per_row", "dcq_dot_rows", "dcq_quantize_weights", "dcq_repack_weights", "dcq_dequantize_rows",
     "dcq_quantize_src1", "dcq_mul_mat_q", "dcq_mul_mat_add_workspace_size", "dcq_mul_mat_add",
     "dcq_ffn_gate_up_workspace_size", "dcq_ffn_gate_up", "dcq_mul_mat_noalloc",
     "dcq_gguf_open", "dcq_gguf_close", "dcq_gguf_tensor_count", "dcq_gguf_find_tensor", "dcq_gguf_tensor_info",
@@ -64,6 +64,7 @@ def lib():
             "dcq_dot_rows": (i32, [i32, vp, sz, vp, i64, vp, i64, i64, vp]),
             "dcq_quantize_weights": (i32, [i32, vp, i64, i64, vp, vp]),
             "dcq_dequantize_rows": (i32, [i32, vp, i64, i64, sz, vp, vp]),
+            "dcq_repack_weights": (i32, [i32, vp, i64, i64, sz, i32, vp, sz, vp]),
             "dcq_quantize_src1": (i32, [i32, vp, i64, i64, sz, vp, sz, vp]),
             "dcq_mul_mat_q": (i32, [i32, vp, i64, i64, sz, vp, sz, i64, vp, sz, i32, vp]),
             "dcq_mul_mat_add_workspace_size": (sz, [i32, i64, i64, i64]),
@@ -373,6 +374,21 @@ def quantize_weights(wt, w, out=None, stream=None):
     if out is None:
         out = torch.empty((n, row_size(wt, k)), dtype=torch.uint8, device=w.device)
     _check("dcq_quantize_weights", lib().dcq_quantize_weights(wt, _ptr(w), n, k, _ptr(out), _stream(stream)))
+    return out
+
+
+def repack_weights(wt, wq, n, k, out_type, out=None, w_row_bytes=None, stream=None):
+    """Load-time repack (dcq_repack_weights): N rows of `wt` (uint8 cuda) -> uint8 cuda [N, row_size(out_type, K)]
+    rows of out_type (Q8_0 -> row-split Q8_0)."""
+    import torch
+    _u8("wq", wq)
+    if out is None:
+        out = torch.empty((n, row_size(out_type, k)), dtype=torch.uint8, device=wq.device)
+    _u8("out", out)
+    wrb = w_row_bytes if w_row_bytes is not None else row_size(wt, k)
+    orb = out.stride(0) if out.dim() == 2 else row_size(out_type, k)
+    _check("dcq_repack_weights", lib().dcq_repack_weights(wt, _ptr(wq), n, k, wrb, out_type, _ptr(out), orb,
+                                                          _stream(stream)))
     return out
 
 

@@ -14,9 +14,10 @@ TYPE_Q4_K = 12
 TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q8_K = 15
+TYPE_Q8_0_RS = 108  # row-split Q8_0, the library's load-time repack of Q8_0 rows (dcq_repack_weights)
 
 TYPE_NAMES = {TYPE_Q4_0: "Q4_0", TYPE_Q8_0: "Q8_0", TYPE_Q4_K: "Q4_K", TYPE_Q5_K: "Q5_K", TYPE_Q6_K: "Q6_K",
-              TYPE_Q8_K: "Q8_K"}
+              TYPE_Q8_K: "Q8_K", TYPE_Q8_0_RS: "Q8_0_RS"}
 
 
 @dataclass(frozen=True)

@@ -87,7 +87,16 @@ using namespace dcq;
 namespace {
 
 bool is_weight_type(int t) {
-    return t == kTypeQ8_0 || t == kTypeQ4_0 || t == kTypeQ4_K || t == kTypeQ5_K || t == kTypeQ6_K;
+    return t == kTypeQ8_0 || t == kTypeQ4_0 || t == kTypeQ4_K || t == kTypeQ5_K || t == kTypeQ6_K || t == kTypeQ8_0_RS;
+}
+
+// Row-split Q8_0 rows: K % 256 == 0 and 16-byte row strides (every 16-byte piece of the quants
+// plane aligned). DCQ_OK or the status to return.
+int check_rs_rows(int wtype, int64_t K, size_t w_row_bytes) {
+    if (wtype != kTypeQ8_0_RS) return DCQ_OK;
+    if (K % 256) return DCQ_ERR_BAD_SHAPE;
+    if (w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
+    return DCQ_OK;
 }
 
 // The kernels are built for gfx950 only; refuse other devices loudly.
@@ -124,7 +133,7 @@ int validate_mul_mat(int wtype, const void* W, int64_t N, int64_t K, size_t w_ro
     if (x_stride_bytes % 16 || y_stride_bytes % 4) return DCQ_ERR_MISALIGNED;
     if (w_row_bytes % 2) return DCQ_ERR_MISALIGNED;
     if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
-    return DCQ_OK;
+    return check_rs_rows(wtype, K, w_row_bytes);
 }
 
 bool is_cache_type(int t) { return t == kTypeQ8_0 || t == kTypeF16 || t == kTypeF32; }
@@ -168,7 +177,8 @@ int64_t dcq_block_size(int type) {
         case DCQ_TYPE_F32:
         case DCQ_TYPE_F16: return 1;
         case DCQ_TYPE_Q4_0:
-        case DCQ_TYPE_Q8_0: return QK8_0;
+        case DCQ_TYPE_Q8_0:
+        case DCQ_TYPE_Q8_0_RS: return QK8_0;
         case DCQ_TYPE_Q4_K:
         case DCQ_TYPE_Q5_K:
         case DCQ_TYPE_Q6_K:
@@ -182,7 +192,8 @@ int64_t dcq_type_size(int type) {
         case DCQ_TYPE_F32: return 4;
         case DCQ_TYPE_F16: return 2;
         case DCQ_TYPE_Q4_0: return (int64_t)sizeof(BlockQ4_0);
-        case DCQ_TYPE_Q8_0: return (int64_t)sizeof(BlockQ8_0);
+        case DCQ_TYPE_Q8_0:
+        case DCQ_TYPE_Q8_0_RS: return (int64_t)sizeof(BlockQ8_0);
         case DCQ_TYPE_Q4_K: return (int64_t)sizeof(BlockQ4_K);
         case DCQ_TYPE_Q5_K: return (int64_t)sizeof(BlockQ5_K);
         case DCQ_TYPE_Q6_K: return (int64_t)sizeof(BlockQ6_K);
@@ -200,7 +211,8 @@ size_t dcq_row_size(int type, int64_t k) {
 int dcq_vec_dot_type(int wtype) {
     switch (wtype) {
         case DCQ_TYPE_Q4_0:
-        case DCQ_TYPE_Q8_0: return DCQ_TYPE_Q8_0;
+        case DCQ_TYPE_Q8_0:
+        case DCQ_TYPE_Q8_0_RS: return DCQ_TYPE_Q8_0;
         case DCQ_TYPE_Q4_K:
         case DCQ_TYPE_Q5_K:
         case DCQ_TYPE_Q6_K: return DCQ_TYPE_Q8_K;
@@ -216,7 +228,8 @@ int64_t dcq_block_sums_per_row(int wtype, int64_t k) {
     if (!is_weight_type(wtype) || k <= 0 || k % dcq_block_size(wtype)) return 0;
     switch (wtype) {
         case DCQ_TYPE_Q4_0:
-        case DCQ_TYPE_Q8_0: return k / QK8_0;
+        case DCQ_TYPE_Q8_0:
+        case DCQ_TYPE_Q8_0_RS: return k / QK8_0;
         case DCQ_TYPE_Q4_K:
         case DCQ_TYPE_Q5_K: return 2 * (k / QK_K);
         default: return k / QK_K;
@@ -492,6 +505,7 @@ int dcq_dot_rows(int wtype, const void* W, size_t w_row_bytes, const void* Xq, i
     if (!aligned(W, 16) || !aligned(Y, 4)) return DCQ_ERR_MISALIGNED;
     if (w_row_bytes % 2) return DCQ_ERR_MISALIGNED;
     if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && w_row_bytes % 16) return DCQ_ERR_MISALIGNED;
+    if (int rs = check_rs_rows(wtype, K, w_row_bytes)) return rs;
     const int vdt = dcq_vec_dot_type(wtype);
     if (!aligned(Xq, vdt == kTypeQ8_K ? 4 : 2)) return DCQ_ERR_MISALIGNED;
     if (n1 == n0) return DCQ_OK;
@@ -513,13 +527,30 @@ int dcq_dot_rows(int wtype, const void* W, size_t w_row_bytes, const void* Xq, i
 }
 
 int dcq_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, void* stream) {
-    if (!is_weight_type(wtype)) return DCQ_ERR_UNSUPPORTED;
+    if (!is_weight_type(wtype) || wtype == kTypeQ8_0_RS) return DCQ_ERR_UNSUPPORTED;
     if (!W || !Wq) return DCQ_ERR_INVALID_ARG;
     if (N <= 0 || K <= 0 || K % dcq_block_size(wtype)) return DCQ_ERR_BAD_SHAPE;
     if (!aligned(W, 4) || !aligned(Wq, 16)) return DCQ_ERR_MISALIGNED;
     int rc = check_device();
     if (rc) return rc;
     return hip_status(launch_quantize_weights(wtype, W, N, K, Wq, (hipStream_t)stream));
+}
+
+int dcq_repack_weights(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, int out_type, void* Wr,
+                       size_t wr_row_bytes, void* stream) {
+    if (wtype != DCQ_TYPE_Q8_0 || out_type != DCQ_TYPE_Q8_0_RS) return DCQ_ERR_UNSUPPORTED;
+    if (!W || !Wr) return DCQ_ERR_INVALID_ARG;
+    if (N <= 0 || K <= 0 || K % 256 || K > (int64_t)1 << 30 || N > (int64_t)1 << 31) return DCQ_ERR_BAD_SHAPE;
+    if (w_row_bytes < dcq_row_size(wtype, K) || wr_row_bytes < dcq_row_size(out_type, K)) return DCQ_ERR_INVALID_ARG;
+    if (!aligned(W, 2) || w_row_bytes % 2 || !aligned(Wr, 16) || wr_row_bytes % 16) return DCQ_ERR_MISALIGNED;
+    // the source and destination must not overlap (rows are rearranged, not moved in place)
+    const uintptr_t a0 = (uintptr_t)W, a1 = a0 + (uintptr_t)((N - 1) * (int64_t)w_row_bytes + dcq_row_size(wtype, K));
+    const uintptr_t b0 = (uintptr_t)Wr, b1 = b0 + (uintptr_t)((N - 1) * (int64_t)wr_row_bytes + dcq_row_size(out_type, K));
+    if (a0 < b1 && b0 < a1) return DCQ_ERR_INVALID_ARG;
+    int rc = check_device();
+    if (rc) return rc;
+    return hip_status(launch_repack_q8_0_rs(W, (int64_t)w_row_bytes, N, K, Wr, (int64_t)wr_row_bytes,
+                                            (hipStream_t)stream));
 }
 
 int dcq_dequantize_rows(int type, const void* Wq, int64_t N, int64_t K, size_t w_row_bytes, float* Y, void* stream) {

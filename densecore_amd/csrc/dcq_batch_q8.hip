@@ -22,11 +22,16 @@
 // Q4_0 weights (Q40): a chunk is 4 pairs of 18-byte blocks (36 bytes, 9 dwords, both lane halves
 // load the pair); lane half hl takes the low (hl = 0) or high nibbles of a block's 16 bytes, its
 // elements 16hl .. 16hl + 15, as signed q - 8 bytes. The rest is the Q8_0 path (|I_b| <= 32*8*128).
+// Row-split Q8_0 (RS): lane half hl loads bytes 16hl .. 16hl + 16 of each block's 32 quants from the
+// row's quants plane (16-byte aligned, no re-slicing) and the chunk's eight fp16 scales as one
+// 16-byte load from its scales plane.
 // The 8 partial tiles are summed in wave order through LDS at the end (deterministic). With few
 // weight rows the chunks are also split over workgroups (grid z): each stores its partial tile in
 // a plane of the split-K scratch and launch_sum_splits adds them in order.
 #include "dcq_common.h"
 #include "dcq_kernels.h"
+
+#include <type_traits>
 
 #pragma clang diagnostic ignored "-Winline-asm"  // M0 in the clobber list (see dma16)
 
@@ -68,11 +73,12 @@ __device__ __forceinline__ int aswz(int row, int slot) { return row * 256 + 16 *
 
 }  // namespace
 
-// W: Q8_0 rows, or Q4_0 rows when Q40 (w_row_bytes % 4 == 0, 16-byte aligned base); xqs: int8
+// W: Q8_0, Q4_0 or row-split Q8_0 rows (FMT; w_row_bytes % 4 == 0, row-split % 16; 16-byte aligned
+// base); xqs: int8
 // [M][K]; xd: float [K/32][m_ld], m_ld >= M rounded up to the m-tile; K = 256 * nch. Workgroup z
 // computes chunks [z * cpz, (z + 1) * cpz) and stores plane z of Y (planes of M rows; one plane: Y
 // itself).
-template <int MTI, bool DUMP, bool Q40>
+template <int MTI, bool DUMP, int FMT>
 __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
                                                                  int N, int nch, int cpz,
                                                                  const int8_t* __restrict__ xqs,
@@ -80,6 +86,7 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
                                                                  float* __restrict__ Y, int64_t y_stride,
                                                                  int32_t* __restrict__ sums) {
     using G = Geo<MTI>;
+    constexpr bool Q40 = FMT == kFmtQ4_0, RS = FMT == kFmtQ8_0RS;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -141,7 +148,17 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
         // (Q4_0: D0..D8 at chunk byte 36p, A = D0..D3, e = D4, B = D5..D8 for both halves)
         uint4 A[4], B[4];
         uint32_t e[4], sx[4];
-        if constexpr (Q40) {
+        [[maybe_unused]] uint4 scl;
+        if constexpr (RS) {
+            // block 2p's half hl in A[p], block 2p + 1's in B[p]; the chunk's 8 scales in scl
+            const uint8_t* cb = wrow + (int64_t)c * 256 + 16 * hl;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                A[p] = ld16(cb + 64 * p);
+                B[p] = ld16(cb + 64 * p + 32);
+            }
+            scl = ld16(wrow + K + (int64_t)c * 16);
+        } else if constexpr (Q40) {
             const uint8_t* cb = wrow + (int64_t)c * 144;
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
@@ -170,7 +187,12 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
             const int p = j >> 1;
             v4i b;
             uint32_t dbits;
-            if constexpr (Q40) {
+            if constexpr (RS) {
+                const uint4 q = (j & 1) ? B[p] : A[p];
+                b.x = (int)q.x, b.y = (int)q.y, b.z = (int)q.z, b.w = (int)q.w;
+                const uint32_t sw = p == 0 ? scl.x : p == 1 ? scl.y : p == 2 ? scl.z : scl.w;
+                dbits = (sw >> (16 * (j & 1))) & 0xFFFFu;
+            } else if constexpr (Q40) {
                 // A[p] = D0..D3, B[p] = D4..D7, e[p] = D8; lane half hl takes nibble half hl
                 const uint32_t sh = 4u * (uint32_t)hl, m = 0x0F0F0F0Fu;
                 uint32_t q[4];
@@ -256,11 +278,12 @@ __global__ void __launch_bounds__(64 * kWaves) batch_q8_0_kernel(const uint8_t* 
     }
 }
 
-hipError_t launch_batch_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+hipError_t launch_batch_q8_0(int fmt, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
                              const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                              hipStream_t st, const SplitScratch& sc) {
+    const bool q40 = fmt == kFmtQ4_0;
     if (K % 256 || w_row_bytes % 4 || w_row_bytes < K / 32 * (q40 ? 18 : 34) || (uintptr_t)W % 16 || M > 64 || M < 1 ||
-        N > (1 << 30) || K > (1 << 30))
+        N > (1 << 30) || K > (1 << 30) || (fmt == kFmtQ8_0RS && w_row_bytes % 16))
         return hipErrorNotSupported;
     const int mti = M <= 32 ? 1 : 2, mt = 32 * mti;
     // the scale DMA reads rows m0 .. m0 + mt - 1 of every block: m_ld must cover the m-tile
@@ -274,10 +297,14 @@ hipError_t launch_batch_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
     dim3 grid((unsigned)tiles_n, 1u, (unsigned)sp.splits);
     const size_t lds = (size_t)kWaves * (mti == 1 ? Geo<1>::kRegion : Geo<2>::kRegion);
-    auto fn = q40 ? (mti == 1 ? (block_sums ? batch_q8_0_kernel<1, true, true> : batch_q8_0_kernel<1, false, true>)
-                              : (block_sums ? batch_q8_0_kernel<2, true, true> : batch_q8_0_kernel<2, false, true>))
-                  : (mti == 1 ? (block_sums ? batch_q8_0_kernel<1, true, false> : batch_q8_0_kernel<1, false, false>)
-                              : (block_sums ? batch_q8_0_kernel<2, true, false> : batch_q8_0_kernel<2, false, false>));
+    auto pick = [&](auto f) {
+        constexpr int F = decltype(f)::value;
+        return mti == 1 ? (block_sums ? batch_q8_0_kernel<1, true, F> : batch_q8_0_kernel<1, false, F>)
+                        : (block_sums ? batch_q8_0_kernel<2, true, F> : batch_q8_0_kernel<2, false, F>);
+    };
+    auto fn = fmt == kFmtQ4_0     ? pick(std::integral_constant<int, kFmtQ4_0>{})
+              : fmt == kFmtQ8_0RS ? pick(std::integral_constant<int, kFmtQ8_0RS>{})
+                                  : pick(std::integral_constant<int, kFmtQ8_0>{});
     hipLaunchKernelGGL(fn, grid, dim3(64 * kWaves), lds, st, (const uint8_t*)W, w_row_bytes, (int)N, nch, sp.stps,
                        act.qs, act.d, act.m_ld, (int)M, out, out_stride, block_sums);
     hipError_t e = hipGetLastError();

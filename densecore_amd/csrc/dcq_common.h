@@ -37,6 +37,11 @@ constexpr int kTypeQ4_K = 12;
 constexpr int kTypeQ5_K = 13;
 constexpr int kTypeQ6_K = 14;
 constexpr int kTypeQ8_K = 15;
+// Library layout, not a ggml type: Q8_0 rows split into planes (dcq_repack_weights writes it from
+// Q8_0 rows). A row of K elements holds the K int8 quants first (block b's 32 at byte 32b, so
+// every 16-byte piece is 16-byte aligned), then the K/32 fp16 scales (block b's at byte K + 2b):
+// the same 34 bytes per block as Q8_0, the same values.
+constexpr int kTypeQ8_0_RS = 108;
 
 constexpr int QK8_0 = 32;
 constexpr int QK_K = 256;

@@ -620,8 +620,8 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
                                int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                hipStream_t st, const float* R, int64_t r_stride) {
     if (knob(Knob::NoFuse)) return hipErrorNotSupported;
-    if (wtype == kTypeQ8_0 || wtype == kTypeQ4_0)
-        return launch_decode_fused_q8_0(wtype == kTypeQ4_0, W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride,
+    if (wtype == kTypeQ8_0 || wtype == kTypeQ4_0 || wtype == kTypeQ8_0_RS)
+        return launch_decode_fused_q8_0(q8_fmt(wtype), W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride,
                                         block_sums, st, R, r_stride);
     if (wtype == kTypeQ6_K && !knob(Knob::Q6KDecode))
         return launch_decode_fused_q6k(W, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R,
@@ -636,7 +636,7 @@ hipError_t launch_decode_fused_glu(int wtype, const void* Wg, const void* Wu, in
                                    hipStream_t st) {
     if (knob(Knob::NoFuse)) return hipErrorNotSupported;
     if (wtype == kTypeQ8_0 || wtype == kTypeQ4_0)
-        return launch_decode_fused_q8_0_glu(wtype == kTypeQ4_0, Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y,
+        return launch_decode_fused_q8_0_glu(q8_fmt(wtype), Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y,
                                             y_stride, st);
     if (wtype != kTypeQ4_K && wtype != kTypeQ5_K) return hipErrorNotSupported;
     return launch_kq(wtype, true, Wg, Wu, w_row_bytes, 0, N, K, X, x_stride, nullptr, M, Y, y_stride, nullptr, N, st);

@@ -49,6 +49,18 @@ __device__ __forceinline__ void load_pair(const uint8_t* p, uint32_t (&r)[17]) {
     r[16] = ld1(p + 64);
 }
 
+// a row-split pair u (two 32-blocks): the 64 quants at row + 64u (16-byte aligned) into r[0..15],
+// the two fp16 scales at row + K + 4u into r[16]
+__device__ __forceinline__ void load_pair_rs(const uint8_t* row, int u, int K, uint32_t (&r)[17]) {
+    const uint8_t* p = row + (int64_t)u * 64;
+    const U32x4 a = ld4(p), b = ld4(p + 16), c = ld4(p + 32), d = ld4(p + 48);
+    r[0] = a.x; r[1] = a.y; r[2] = a.z; r[3] = a.w;
+    r[4] = b.x; r[5] = b.y; r[6] = b.z; r[7] = b.w;
+    r[8] = c.x; r[9] = c.y; r[10] = c.z; r[11] = c.w;
+    r[12] = d.x; r[13] = d.y; r[14] = d.z; r[15] = d.w;
+    r[16] = ld1(row + K + (int64_t)u * 4);
+}
+
 // 36 bytes (two 18-byte Q4_0 blocks) at a dword aligned address into 9 dwords
 __device__ __forceinline__ void load_pair(const uint8_t* p, uint32_t (&r)[9]) {
     const U32x4 a = ld4(p), b = ld4(p + 16);
@@ -89,6 +101,28 @@ __device__ __forceinline__ void pair_terms(const uint32_t (&w)[9], uint4 a0, uin
                                            int& i1, float& dW0, float& dW1) {
     q4_0_pair(w, a0, a1, a2, a3, i0, i1, dW0, dW1);
 }
+// row-split pair (load_pair_rs): the quants need no re-slicing
+__device__ __forceinline__ void pair_terms_rs(const uint32_t (&w)[17], uint4 a0, uint4 a1, uint4 a2, uint4 a3, int& i0,
+                                              int& i1, float& dW0, float& dW1) {
+    i0 = sdot4((int)w[0], (int)a0.x, 0);
+    i0 = sdot4((int)w[1], (int)a0.y, i0);
+    i0 = sdot4((int)w[2], (int)a0.z, i0);
+    i0 = sdot4((int)w[3], (int)a0.w, i0);
+    i0 = sdot4((int)w[4], (int)a1.x, i0);
+    i0 = sdot4((int)w[5], (int)a1.y, i0);
+    i0 = sdot4((int)w[6], (int)a1.z, i0);
+    i0 = sdot4((int)w[7], (int)a1.w, i0);
+    i1 = sdot4((int)w[8], (int)a2.x, 0);
+    i1 = sdot4((int)w[9], (int)a2.y, i1);
+    i1 = sdot4((int)w[10], (int)a2.z, i1);
+    i1 = sdot4((int)w[11], (int)a2.w, i1);
+    i1 = sdot4((int)w[12], (int)a3.x, i1);
+    i1 = sdot4((int)w[13], (int)a3.y, i1);
+    i1 = sdot4((int)w[14], (int)a3.z, i1);
+    i1 = sdot4((int)w[15], (int)a3.w, i1);
+    dW0 = half_bits_to_float(w[16] & 0xFFFFu);
+    dW1 = half_bits_to_float(w[16] >> 16);
+}
 
 constexpr int kMaxStagePasses = 8;  // float4 registers of activation per thread
 
@@ -104,8 +138,9 @@ __host__ __device__ constexpr int q8_stage_passes(int G, int NS, int MT, int NW)
 // The arguments the first loads need come first: the first 56 bytes of arguments are preloaded
 // into scalar registers at dispatch (-amdgpu-kernarg-preload-count), the rest take a dependent
 // scalar load.
-// Q40: the weights are Q4_0 (36-byte block pairs) instead of Q8_0 (68-byte pairs).
-template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, bool Q40 = false,
+// FMT: Q8_0 (68-byte block pairs), Q4_0 (36-byte pairs) or row-split Q8_0 (64 quant bytes and 4 scale
+// bytes from the row's two planes).
+template <int G, int NS, int MT, int NW, bool DUMP, bool GLU = false, int FMT = kFmtQ8_0,
           int QC = q8_stage_passes(G, NS, MT, NW)>
 __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __restrict__ X, int64_t x_stride,
                                                            const uint8_t* __restrict__ W,
@@ -113,6 +148,7 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
                                                            int64_t N, int K, int M, float* Y,  // R may alias Y
                                                            int64_t y_stride, int32_t* __restrict__ sums,
                                                            int64_t sums_n_stride, const float* R, int64_t r_stride) {
+    constexpr bool Q40 = FMT == kFmtQ4_0, RS = FMT == kFmtQ8_0RS;
     if constexpr (QC <= kMaxStagePasses) {
         extern __shared__ __align__(16) uint8_t smem[];
         constexpr int RPW = 64 / G;  // rows per wave
@@ -146,7 +182,10 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
         for (int t = 0; t < NS; ++t) {
             int u = g + G * t;
             u = u < U ? u : U - 1;
-            load_pair(wrow + (int64_t)u * kPairBytes, raw[t]);
+            if constexpr (RS)
+                load_pair_rs(wrow, u, K, raw[t]);
+            else
+                load_pair(wrow + (int64_t)u * kPairBytes, raw[t]);
         }
         if constexpr (GLU) {
             const uint8_t* wrow2 = W2 + (row_ok ? row : N - 1) * w_row_bytes;
@@ -154,7 +193,10 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
             for (int t = 0; t < NS; ++t) {
                 int u = g + G * t;
                 u = u < U ? u : U - 1;
-                load_pair(wrow2 + (int64_t)u * kPairBytes, raw2[t]);
+                if constexpr (RS)
+                    load_pair_rs(wrow2, u, K, raw2[t]);
+                else
+                    load_pair(wrow2 + (int64_t)u * kPairBytes, raw2[t]);
             }
         }
         // keep the quantizer's first use of the activation (and its wait) behind the weight loads
@@ -206,7 +248,10 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
                 const float2 dA = *reinterpret_cast<const float2*>(act_d + mi * nb + 2 * u);
                 int i0, i1;
                 float dW0, dW1;
-                pair_terms(raw[t], a0, a1, a2, a3, i0, i1, dW0, dW1);
+                if constexpr (RS)
+                    pair_terms_rs(raw[t], a0, a1, a2, a3, i0, i1, dW0, dW1);
+                else
+                    pair_terms(raw[t], a0, a1, a2, a3, i0, i1, dW0, dW1);
                 if (DUMP && valid && row_ok && mi < M) {
                     int32_t* srow = sums + ((int64_t)mi * sums_n_stride + row) * nb;
                     atomicAdd(srow + 2 * u, i0);
@@ -217,7 +262,10 @@ __global__ void __launch_bounds__(64 * NW) decode_q8_0_kernel(const float* __res
                 if constexpr (GLU) {
                     int j0, j1;
                     float eW0, eW1;
-                    pair_terms(raw2[t], a0, a1, a2, a3, j0, j1, eW0, eW1);
+                    if constexpr (RS)
+                        pair_terms_rs(raw2[t], a0, a1, a2, a3, j0, j1, eW0, eW1);
+                    else
+                        pair_terms(raw2[t], a0, a1, a2, a3, j0, j1, eW0, eW1);
                     const float v2 = fmaf((float)j1, eW1 * dA.y, (float)j0 * (eW0 * dA.x));
                     acc2[mi] = valid ? acc2[mi] + v2 : acc2[mi];
                 }
@@ -257,40 +305,45 @@ static_assert(kNumQ8Shapes == 12, "pick_q8_shape covers every shape");
 #endif
 constexpr int kQ8Waves = DCQ_Q8_NW;
 
-template <int I, int MT, bool DUMP, bool GLU, bool Q40>
+template <int I, int MT, bool DUMP, bool GLU, int FMT>
 DecodeQ8Fn q8_fn() {
-    return decode_q8_0_kernel<kQ8Shapes[I].G, kQ8Shapes[I].NS, MT, kQ8Waves, DUMP, GLU, Q40>;
+    return decode_q8_0_kernel<kQ8Shapes[I].G, kQ8Shapes[I].NS, MT, kQ8Waves, DUMP, GLU, FMT>;
 }
-template <int I, bool DUMP, bool GLU, bool Q40>
+template <int I, bool DUMP, bool GLU, int FMT>
 DecodeQ8Fn q8_pick_mt(int mt) {
     switch (mt) {
-        case 1: return q8_fn<I, 1, DUMP, GLU, Q40>();
-        case 2: return q8_fn<I, 2, DUMP, GLU, Q40>();
-        case 4: return q8_fn<I, 4, DUMP, GLU, Q40>();
-        default: return q8_fn<I, 8, DUMP, GLU, Q40>();
+        case 1: return q8_fn<I, 1, DUMP, GLU, FMT>();
+        case 2: return q8_fn<I, 2, DUMP, GLU, FMT>();
+        case 4: return q8_fn<I, 4, DUMP, GLU, FMT>();
+        default: return q8_fn<I, 8, DUMP, GLU, FMT>();
     }
 }
-template <bool DUMP, bool GLU, bool Q40>
+template <bool DUMP, bool GLU, int FMT>
 DecodeQ8Fn q8_pick_shape(int idx, int mt) {
     switch (idx) {
-        case 0: return q8_pick_mt<0, DUMP, GLU, Q40>(mt);
-        case 1: return q8_pick_mt<1, DUMP, GLU, Q40>(mt);
-        case 2: return q8_pick_mt<2, DUMP, GLU, Q40>(mt);
-        case 3: return q8_pick_mt<3, DUMP, GLU, Q40>(mt);
-        case 4: return q8_pick_mt<4, DUMP, GLU, Q40>(mt);
-        case 5: return q8_pick_mt<5, DUMP, GLU, Q40>(mt);
-        case 6: return q8_pick_mt<6, DUMP, GLU, Q40>(mt);
-        case 7: return q8_pick_mt<7, DUMP, GLU, Q40>(mt);
-        case 8: return q8_pick_mt<8, DUMP, GLU, Q40>(mt);
-        case 9: return q8_pick_mt<9, DUMP, GLU, Q40>(mt);
-        case 10: return q8_pick_mt<10, DUMP, GLU, Q40>(mt);
-        default: return q8_pick_mt<11, DUMP, GLU, Q40>(mt);
+        case 0: return q8_pick_mt<0, DUMP, GLU, FMT>(mt);
+        case 1: return q8_pick_mt<1, DUMP, GLU, FMT>(mt);
+        case 2: return q8_pick_mt<2, DUMP, GLU, FMT>(mt);
+        case 3: return q8_pick_mt<3, DUMP, GLU, FMT>(mt);
+        case 4: return q8_pick_mt<4, DUMP, GLU, FMT>(mt);
+        case 5: return q8_pick_mt<5, DUMP, GLU, FMT>(mt);
+        case 6: return q8_pick_mt<6, DUMP, GLU, FMT>(mt);
+        case 7: return q8_pick_mt<7, DUMP, GLU, FMT>(mt);
+        case 8: return q8_pick_mt<8, DUMP, GLU, FMT>(mt);
+        case 9: return q8_pick_mt<9, DUMP, GLU, FMT>(mt);
+        case 10: return q8_pick_mt<10, DUMP, GLU, FMT>(mt);
+        default: return q8_pick_mt<11, DUMP, GLU, FMT>(mt);
     }
 }
-template <bool Q40>
+template <int FMT>
 DecodeQ8Fn q8_pick(bool glu, bool dump, int idx, int mt) {
-    return glu ? q8_pick_shape<false, true, Q40>(idx, mt)
-               : (dump ? q8_pick_shape<true, false, Q40>(idx, mt) : q8_pick_shape<false, false, Q40>(idx, mt));
+    if constexpr (FMT == kFmtQ8_0RS) {
+        // the gate/up pair takes GGUF rows only
+        return dump ? q8_pick_shape<true, false, FMT>(idx, mt) : q8_pick_shape<false, false, FMT>(idx, mt);
+    } else {
+        return glu ? q8_pick_shape<false, true, FMT>(idx, mt)
+                   : (dump ? q8_pick_shape<true, false, FMT>(idx, mt) : q8_pick_shape<false, false, FMT>(idx, mt));
+    }
 }
 
 // The shape for U pairs per row. Measured on MI355X (fused, M = 1, W rotated over 1 GiB; us):
@@ -344,13 +397,14 @@ int choose_q8_shape(int U, bool q40) {
 namespace {
 
 // W2 != nullptr: the gate/up pair (no block sums), Y = silu(W x) * (W2 x). q40: Q4_0 weights.
-hipError_t launch_q8(bool q40, const void* W, const void* W2, int64_t w_row_bytes, int64_t N, int64_t K,
+hipError_t launch_q8(int fmt, const void* W, const void* W2, int64_t w_row_bytes, int64_t N, int64_t K,
                      const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                      hipStream_t st, const float* R = nullptr, int64_t r_stride = 0) {
     if (K % 64 != 0 || w_row_bytes % 4 != 0 || x_stride % 4 != 0) return hipErrorNotSupported;
-    if (W2 && block_sums) return hipErrorNotSupported;
+    if (W2 && (block_sums || fmt == kFmtQ8_0RS)) return hipErrorNotSupported;
+    if (fmt == kFmtQ8_0RS && w_row_bytes % 16 != 0) return hipErrorNotSupported;
     const int U = (int)(K / 64);
-    const int idx = choose_q8_shape(U, q40);
+    const int idx = choose_q8_shape(U, fmt == kFmtQ4_0);
     if (idx < 0) return hipErrorNotSupported;
     const int G = kQ8Shapes[idx].G, NS = kQ8Shapes[idx].NS;
     // validate every M tile before launching anything
@@ -367,8 +421,10 @@ hipError_t launch_q8(bool q40, const void* W, const void* W2, int64_t w_row_byte
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         const size_t lds = (size_t)mt * K * 9 / 8;
-        DecodeQ8Fn fn = q40 ? q8_pick<true>(W2 != nullptr, block_sums != nullptr, idx, mt)
-                            : q8_pick<false>(W2 != nullptr, block_sums != nullptr, idx, mt);
+        const bool glu = W2 != nullptr, dump = block_sums != nullptr;
+        DecodeQ8Fn fn = fmt == kFmtQ4_0     ? q8_pick<kFmtQ4_0>(glu, dump, idx, mt)
+                        : fmt == kFmtQ8_0RS ? q8_pick<kFmtQ8_0RS>(glu, dump, idx, mt)
+                                            : q8_pick<kFmtQ8_0>(glu, dump, idx, mt);
         hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kQ8Waves), lds, st, X + m0 * x_stride, x_stride,
                            (const uint8_t*)W, (const uint8_t*)W2, w_row_bytes, N, (int)K, (int)mc, Y + m0 * y_stride,
                            y_stride,
@@ -380,16 +436,16 @@ hipError_t launch_q8(bool q40, const void* W, const void* W2, int64_t w_row_byte
 
 }  // namespace
 
-hipError_t launch_decode_fused_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+hipError_t launch_decode_fused_q8_0(int fmt, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
                                     const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
                                     int32_t* block_sums, hipStream_t st, const float* R, int64_t r_stride) {
-    return launch_q8(q40, W, nullptr, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R, r_stride);
+    return launch_q8(fmt, W, nullptr, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, block_sums, st, R, r_stride);
 }
 
-hipError_t launch_decode_fused_q8_0_glu(bool q40, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N,
+hipError_t launch_decode_fused_q8_0_glu(int fmt, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N,
                                         int64_t K, const float* X, int64_t x_stride, int64_t M, float* Y,
                                         int64_t y_stride, hipStream_t st) {
-    return launch_q8(q40, Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, nullptr, st);
+    return launch_q8(fmt, Wg, Wu, w_row_bytes, N, K, X, x_stride, M, Y, y_stride, nullptr, st);
 }
 
 }  // namespace dcq

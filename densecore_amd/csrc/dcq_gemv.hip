@@ -23,7 +23,16 @@
 
 namespace dcq {
 
-enum GemvFmt { kQ8_0Pair = 0, kQ8_0Single = 1, kQ4K = 2, kQ6K = 3, kQ4_0Pair = 4, kQ4_0Single = 5, kQ5K = 6 };
+enum GemvFmt {
+    kQ8_0Pair = 0,
+    kQ8_0Single = 1,
+    kQ4K = 2,
+    kQ6K = 3,
+    kQ4_0Pair = 4,
+    kQ4_0Single = 5,
+    kQ5K = 6,
+    kQ8_0RSPair = 7  // row-split Q8_0: two blocks' 64 quants and their two scales
+};
 
 // int32 block sums per row (the DUMP layout)
 __host__ __device__ constexpr int64_t sums_per_row(int f, int64_t K) {
@@ -47,6 +56,10 @@ struct RawQ6K {
 };
 struct RawQ4_0Pair {
     uint32_t w[9];
+};
+struct RawQ8RSPair {
+    uint32_t q[16];
+    uint32_t d;  // the two fp16 scales
 };
 struct RawQ4_0Single {
     uint32_t d;
@@ -85,6 +98,10 @@ struct RawOf<kQ4_0Single> {
 template <>
 struct RawOf<kQ5K> {
     using T = RawQ5K;
+};
+template <>
+struct RawOf<kQ8_0RSPair> {
+    using T = RawQ8RSPair;
 };
 
 __device__ __forceinline__ void load_unit(const uint8_t* row, int u, RawQ8Pair& r) {
@@ -172,6 +189,29 @@ __device__ __forceinline__ float unit_dot(const RawQ8Pair& r, int u, const int8_
     i1 = sdot4((int)w[15], (int)a3.z, i1);
     i1 = sdot4((int)w[16], (int)a3.w, i1);
     const float dW0 = half_bits_to_float(w[0] & 0xFFFFu), dW1 = half_bits_to_float(w[8] >> 16);
+    if (DUMP && valid) {
+        atomicAdd(sums_row + 2 * u, i0);
+        atomicAdd(sums_row + 2 * u + 1, i1);
+    }
+    return fmaf((float)i1, dW1 * dA1, (float)i0 * (dW0 * dA0));
+}
+
+template <bool DUMP>
+__device__ __forceinline__ float unit_dot(const RawQ8RSPair& r, int u, const int8_t* xrow, const float* xd,
+                                          int64_t m_ld, int64_t m, const int16_t*, int32_t* sums_row,
+                                          bool valid) {
+    const uint4 a0 = ld16(xrow + 64 * u), a1 = ld16(xrow + 64 * u + 16);
+    const uint4 a2 = ld16(xrow + 64 * u + 32), a3 = ld16(xrow + 64 * u + 48);
+    const float dA0 = xd[(int64_t)(2 * u) * m_ld + m], dA1 = xd[(int64_t)(2 * u + 1) * m_ld + m];
+    const uint32_t a[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                            a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+    int i0 = 0, i1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        i0 = sdot4((int)r.q[k], (int)a[k], i0);
+        i1 = sdot4((int)r.q[8 + k], (int)a[8 + k], i1);
+    }
+    const float dW0 = half_bits_to_float(r.d & 0xFFFFu), dW1 = half_bits_to_float(r.d >> 16);
     if (DUMP && valid) {
         atomicAdd(sums_row + 2 * u, i0);
         atomicAdd(sums_row + 2 * u + 1, i1);
@@ -386,7 +426,19 @@ __global__ void __launch_bounds__(256) gemv_kernel(const uint8_t* __restrict__ W
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
             const int u = u0 + g + t * G;
-            load_unit(wrow, u < U ? u : U - 1, raw[t]);
+            const int uc = u < U ? u : U - 1;
+            if constexpr (F == kQ8_0RSPair) {
+                // the pair's 64 quants at row + 64u (16-byte aligned), its two scales at row + K + 4u
+                const uint8_t* p = wrow + (int64_t)uc * 64;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const U32x4 v = ld4(p + 16 * i);
+                    raw[t].q[4 * i] = v.x, raw[t].q[4 * i + 1] = v.y, raw[t].q[4 * i + 2] = v.z, raw[t].q[4 * i + 3] = v.w;
+                }
+                raw[t].d = ld1(wrow + K + (int64_t)uc * 4);
+            } else {
+                load_unit(wrow, uc, raw[t]);
+            }
         }
 #pragma unroll
         for (int t = 0; t < UPL; ++t) {
@@ -455,6 +507,7 @@ static GemvFn pick_fmt(int f, int mt, int upl) {
         case kQ4_0Pair: return pick_mt<kQ4_0Pair, DUMP>(mt, upl);
         case kQ4_0Single: return pick_mt<kQ4_0Single, DUMP>(mt, upl);
         case kQ5K: return pick_mt<kQ5K, DUMP>(mt, upl);
+        case kQ8_0RSPair: return pick_mt<kQ8_0RSPair, DUMP>(mt, upl);
         default: return pick_mt<kQ6K, DUMP>(mt, upl);
     }
 }
@@ -479,7 +532,10 @@ hipError_t launch_gemv(int wtype, const void* W, int64_t w_row_bytes, int64_t n0
     if (R) return hipErrorNotSupported;  // the generic kernels have no add in their store
     int f;
     const bool pairs = K % 64 == 0 && w_row_bytes % 4 == 0;  // two 32-blocks per unit, dword aligned
-    if (wtype == kTypeQ8_0)
+    if (wtype == kTypeQ8_0_RS) {
+        if (K % 64 || w_row_bytes % 16) return hipErrorNotSupported;
+        f = kQ8_0RSPair;
+    } else if (wtype == kTypeQ8_0)
         f = pairs ? kQ8_0Pair : kQ8_0Single;
     else if (wtype == kTypeQ4_0)
         f = pairs ? kQ4_0Pair : kQ4_0Single;

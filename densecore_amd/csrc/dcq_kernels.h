@@ -4,7 +4,14 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "dcq_common.h"
+
 namespace dcq {
+
+// Weight formats of the Q8_0-block kernels: GGUF Q8_0 and Q4_0 rows, and row-split Q8_0
+// (kTypeQ8_0_RS).
+enum Q8Fmt { kFmtQ8_0 = 0, kFmtQ4_0 = 1, kFmtQ8_0RS = 2 };
+inline int q8_fmt(int wtype) { return wtype == kTypeQ4_0 ? kFmtQ4_0 : wtype == kTypeQ8_0_RS ? kFmtQ8_0RS : kFmtQ8_0; }
 
 // Planar quantized activations inside a workspace (see dcq_common.h for the layout).
 struct PlanarBuffers {
@@ -77,7 +84,7 @@ hipError_t launch_decode_kq(int wtype, const void* W, int64_t w_row_bytes, int64
 hipError_t launch_decode_fused_glu(int wtype, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N, int64_t K,
                                    const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
                                    hipStream_t st);
-hipError_t launch_decode_fused_q8_0_glu(bool q40, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N,
+hipError_t launch_decode_fused_q8_0_glu(int fmt, const void* Wg, const void* Wu, int64_t w_row_bytes, int64_t N,
                                         int64_t K, const float* X, int64_t x_stride, int64_t M, float* Y,
                                         int64_t y_stride, hipStream_t st);
 // Y[m][n] = silu(Y[m][n]) * U[m][n] (the SwiGLU product after two separate projections)
@@ -106,10 +113,10 @@ hipError_t launch_decode_fused(int wtype, const void* W, int64_t w_row_bytes, in
                                hipStream_t st, const float* R = nullptr,
                                    int64_t r_stride = 0);
 
-// Q8_0 (q40 false) or Q4_0 (q40 true) decode with the Q8_0 activation quantization fused in
-// (K % 64 == 0, row stride a multiple of 4 bytes, M*K*9/8 bytes of LDS per 8-row tile);
-// hipErrorNotSupported otherwise.
-hipError_t launch_decode_fused_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+// Q8_0, Q4_0 or row-split Q8_0 (fmt, a Q8Fmt) decode with the Q8_0 activation quantization fused in
+// (K % 64 == 0, row stride a multiple of 4 bytes (row-split: 16), M*K*9/8 bytes of LDS per 8-row
+// tile; the gate/up pair takes Q8_0 and Q4_0); hipErrorNotSupported otherwise.
+hipError_t launch_decode_fused_q8_0(int fmt, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
                                     const float* X, int64_t x_stride, int64_t M, float* Y, int64_t y_stride,
                                     int32_t* block_sums, hipStream_t st, const float* R = nullptr,
                                     int64_t r_stride = 0);
@@ -134,9 +141,10 @@ SplitPlan plan_split_k(int64_t tiles, int nstages, int align, int64_t M, int64_t
 hipError_t launch_sum_splits(const float* P, int splits, int64_t M, int64_t N, float* Y, int64_t y_stride,
                              hipStream_t st);
 
-// Q8_0 (q40: Q4_0) prefill: LDS-staged 128 x 128 int8-MFMA tiles (K % 128 == 0, w_row_bytes % 4
-// == 0); hipErrorNotSupported otherwise (nothing launched).
-hipError_t launch_prefill_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+// Q8_0 / Q4_0 / row-split Q8_0 (fmt) prefill: LDS-staged 128 x 128 int8-MFMA tiles (K % 128 == 0,
+// w_row_bytes % 4 == 0; row-split: % 16 == 0 and N * w_row_bytes < 4 GiB); hipErrorNotSupported
+// otherwise (nothing launched).
+hipError_t launch_prefill_q8_0(int fmt, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
                                const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                hipStream_t st, const SplitScratch& sc = SplitScratch());
 
@@ -157,10 +165,10 @@ hipError_t launch_batch_q4k(bool q5, const void* W, int64_t w_row_bytes, int64_t
                             const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                             hipStream_t st, const SplitScratch& sc = SplitScratch());
 
-// Q8_0 (q40: Q4_0) batched decode (4 < M <= 64): 8-wave workgroups per 32 weight rows x 32 or 64 activation
-// rows, K split over the waves (and over workgroups when the rows are few and sc has room);
-// hipErrorNotSupported when the shape is outside it.
-hipError_t launch_batch_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+// Q8_0 / Q4_0 / row-split Q8_0 (fmt) batched decode (4 < M <= 64): 8-wave workgroups per 32 weight
+// rows x 32 or 64 activation rows, K split over the waves (and over workgroups when the rows are few
+// and sc has room); hipErrorNotSupported when the shape is outside it.
+hipError_t launch_batch_q8_0(int fmt, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
                              const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                              hipStream_t st, const SplitScratch& sc);
 
@@ -199,5 +207,8 @@ int noalloc_scratch(void** ptr, size_t* bytes);
 hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, hipStream_t st);
 hipError_t launch_dequantize(int type, const void* Wq, int64_t N, int64_t K, int64_t w_row_bytes, float* Y,
                              hipStream_t st);
+// Q8_0 rows -> row-split rows (out rows 16-byte aligned, out_row_bytes >= 34 * K / 32)
+hipError_t launch_repack_q8_0_rs(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, void* out,
+                                 int64_t out_row_bytes, hipStream_t st);
 
 }  // namespace dcq

@@ -602,9 +602,18 @@ static MmqFn pick(int wtype, const MmqShape& s) {
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                       int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
                       const SplitScratch& sc) {
-    const bool q8 = wtype == kTypeQ8_0 || wtype == kTypeQ4_0, q40 = wtype == kTypeQ4_0;  // Q8_0-block kernels
+    // row-split Q8_0: the batched and the 128 x 128-tile kernels (no generic MMQ form)
+    if (wtype == kTypeQ8_0_RS) {
+        if (M <= 64) {
+            const hipError_t e = launch_batch_q8_0(kFmtQ8_0RS, W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums,
+                                                   st, sc);
+            if (e != hipErrorNotSupported) return e;
+        }
+        return launch_prefill_q8_0(kFmtQ8_0RS, W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
+    }
+    const bool q8 = wtype == kTypeQ8_0 || wtype == kTypeQ4_0;  // Q8_0-block kernels
     if (q8 && M <= 64) {
-        const hipError_t e = launch_batch_q8_0(q40, W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
+        const hipError_t e = launch_batch_q8_0(q8_fmt(wtype), W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
     if (wtype == kTypeQ6_K && M <= 64) {
@@ -618,7 +627,8 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
                          plan_split_k(((M + 127) / 128) * ((N + 127) / 128), (int)(K / 128), q8 ? 1 : 2, M, N,
                                       sc).splits > 1;
     if (q8 && (M > 32 || starved)) {
-        const hipError_t e = launch_prefill_q8_0(q40, W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
+        const hipError_t e = launch_prefill_q8_0(q8_fmt(wtype), W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums,
+                                                 st, sc);
         if (e != hipErrorNotSupported) return e;
     }
     if (wtype == kTypeQ6_K && (M > 32 || starved)) {

@@ -59,6 +59,7 @@ struct __align__(16) Stage {
     int8_t b[kBN * kRow];    // weight int8, [n][k] (swizzled 16-byte slots)
     float2 dwc[kKB][kBN];    // per weight row and block: (dW, -dW * 1.5*2^23), the epilogue's constants
     float da[kKB][kBM];      // activation block scales
+    uint2 dw16[kBN];         // row-split weights: the stage's four fp16 block scales per row, as loaded
 };
 
 // LDS byte offset of logical 16-byte slot `slot` (= 2*block + half) of tile row `row`.
@@ -69,6 +70,13 @@ __device__ __forceinline__ int swz_key(int row) { return (row & 7) ^ ((row >> 3)
 __device__ __forceinline__ int swz(int row, int slot) { return row * kRow + 16 * (slot ^ swz_key(row)); }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 4 bytes per lane from global memory (uniform base `g` + per-lane byte offset `off`) into LDS at
+// lds_base + 4 * lane, as dma16 below.
+__device__ __forceinline__ void dma4(const void* g, uint32_t off, const void* lds_base) {
+    const uint32_t m0 = (uint32_t)(uintptr_t)(lds_ptr_t)lds_base;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(g), "s"(m0) : "memory", "m0");
+}
 
 // 16 bytes per lane from global memory (uniform base `g` + per-lane byte offset `off`) straight
 // into LDS at lds_base + 16 * lane (lds_base wave-uniform, in M0): global_load_lds_dwordx4 with an
@@ -94,13 +102,14 @@ __device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
 // FULL: M and N are multiples of the 128 x 128 tile (no row clamps, unguarded stores).
 // Arguments: the ones the first loads need come first (the first 56 bytes of arguments are
 // preloaded into scalar registers at dispatch).
-template <bool DUMP, bool FULL, bool Q40>
+template <bool DUMP, bool FULL, int FMT>
 __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
                                                               int w_row_bytes, const uint8_t* __restrict__ W,
                                                               const int8_t* __restrict__ xqs,
                                                               const float* __restrict__ xd, int M, int stps,
                                                               float* __restrict__ Y, int64_t y_stride,
                                                               int32_t* __restrict__ sums) {
+    constexpr bool Q40 = FMT == kFmtQ4_0, RS = FMT == kFmtQ8_0RS;
     extern __shared__ __align__(16) uint8_t smem[];
     Stage* st = reinterpret_cast<Stage*>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -151,12 +160,33 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
     const int rw = tid >> 1, hw = tid & 1;
     const uint8_t* w_src = W + (int64_t)(FULL ? n0 + rw : min(n0 + rw, N - 1)) * w_row_bytes + hw * 2 * kBlk;
     uint32_t gw[17];  // Q4_0 uses gw[0..8]
+    // row-split weights (RS): the quants go straight to LDS like the activation rows (instruction i
+    // of wave w fills tile rows 8*(4w+i) .. +8), and each wave's 32 rows' four fp16 scales per stage
+    // by one dword instruction (lane l: row 32w + l/2, scales 2(l%2), 2(l%2)+1); the rows' byte
+    // offsets fit 32 bits (the launcher checks N * w_row_bytes < 4 GiB)
+    uint32_t b_off[4], bd_off;
+    if constexpr (RS) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int b_slot = (lane & 7) ^ swz_key(a_row0 + 8 * i);
+            const int row = FULL ? n0 + a_row0 + 8 * i : min(n0 + a_row0 + 8 * i, N - 1);
+            b_off[i] = (uint32_t)row * (uint32_t)w_row_bytes + 16u * (uint32_t)b_slot;
+        }
+        const int row = FULL ? n0 + 32 * wave_u + (lane >> 1) : min(n0 + 32 * wave_u + (lane >> 1), N - 1);
+        bd_off = (uint32_t)row * (uint32_t)w_row_bytes + 4u * (uint32_t)(lane & 1);
+    }
 #define DCQ_ISSUE(s_, S_)                                                                      \
     do {                                                                                       \
         const int8_t* ab_ = xqs + (int64_t)(s_) * kKS;                                         \
         _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                                       \
             dma16(ab_, a_off[i_], (S_).a + 1024 * (4 * wave_u + i_));                          \
         if (wave_u < 2) dma16(xd + (int64_t)(s_) * kKB * m_ld, da_off, &(S_).da[0][0] + 256 * wave_u); \
+        if constexpr (RS) {                                                                    \
+            _Pragma("unroll") for (int i_ = 0; i_ < 4; ++i_)                                   \
+                dma16(W + (int64_t)(s_) * kKS, b_off[i_], (S_).b + 1024 * (4 * wave_u + i_));  \
+            dma4(W + K + (int64_t)(s_) * (2 * kKB), bd_off, &(S_).dw16[32 * wave_u]);          \
+            break;                                                                             \
+        }                                                                                      \
         const uint8_t* wp_ = w_src + (int64_t)(s_) * (kKB * kBlk);                             \
         _Pragma("unroll") for (int i_ = 0; i_ < 2; ++i_) {                                     \
             const U32x4 v_ = ld4(wp_ + 16 * i_);                                               \
@@ -181,6 +211,7 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
     // the low nibbles and 16..31 in the high ones); logical slots 4hw .. 4hw+3 of row rw
 #define DCQ_COMMIT(S_)                                                                         \
     do {                                                                                       \
+        if constexpr (RS) break; /* staged by DMA; the scales are widened by DCQ_WIDEN */      \
         float d0_, d1_;                                                                        \
         if constexpr (Q40) {                                                                   \
             const uint32_t m_ = 0x0F0F0F0Fu;                                                   \
@@ -217,6 +248,19 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
         (S_).dwc[2 * hw][rw] = make_float2(d0_, -d0_ * kMagicF);                               \
         (S_).dwc[2 * hw + 1][rw] = make_float2(d1_, -d1_ * kMagicF);                           \
     } while (0)
+    // row-split weights, after the wait for this wave's loads: each lane widens the two fp16 scales
+    // its own dword load brought (row 32w + l/2, blocks 2(l%2) and 2(l%2)+1) into the epilogue's
+    // constants; the barrier that follows publishes them
+#define DCQ_WIDEN(S_)                                                                          \
+    do {                                                                                       \
+        if constexpr (RS) {                                                                    \
+            const int r_ = 32 * wave_u + (lane >> 1), k_ = 2 * (lane & 1);                     \
+            const uint32_t h_ = reinterpret_cast<const uint32_t*>(&(S_).dw16[r_])[lane & 1];   \
+            const float e0_ = half_bits_to_float(h_ & 0xFFFFu), e1_ = half_bits_to_float(h_ >> 16); \
+            (S_).dwc[k_][r_] = make_float2(e0_, -e0_ * kMagicF);                               \
+            (S_).dwc[k_ + 1][r_] = make_float2(e1_, -e1_ * kMagicF);                           \
+        }                                                                                      \
+    } while (0)
 
     // ---- wave tile: 64 x 64 at (wm, wn) inside the workgroup tile ----
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
@@ -238,6 +282,7 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
     DCQ_ISSUE(s_begin, st[s_begin & 1]);
     DCQ_COMMIT(st[s_begin & 1]);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
+    DCQ_WIDEN(st[s_begin & 1]);
     __syncthreads();
 
     // Fragments of block kb: this lane's fragment rows wm + 32i + col and wn + 32j + col share
@@ -318,6 +363,7 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
                 // the barrier that ended stage s - 1: one barrier per stage is enough
                 DCQ_COMMIT(st[(s + 1) & 1]);
                 __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
+                DCQ_WIDEN(st[(s + 1) & 1]);
                 __syncthreads();
             }
         }
@@ -359,12 +405,14 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
             if (more) {
                 DCQ_COMMIT(st[(s + 1) & 1]);
                 __builtin_amdgcn_s_waitcnt(0);
+                DCQ_WIDEN(st[(s + 1) & 1]);
                 __syncthreads();
             }
         }
     }
 #undef DCQ_ISSUE
 #undef DCQ_COMMIT
+#undef DCQ_WIDEN
 
     // ---- store: lane owns column n, rows m_v = m0 + wm + 32i + 8(v/4) + 4hl + v%4; the row
     // offsets beyond the lane's first row are uniform multiples of y_stride (scalar arithmetic) ----
@@ -384,11 +432,22 @@ __global__ void __launch_bounds__(256, 2) prefill_q8_0_kernel(int tiles_n, int t
 
 size_t prefill_q8_0_lds_bytes() { return 2 * sizeof(Stage); }
 
-hipError_t launch_prefill_q8_0(bool q40, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
+template <int FMT>
+using PrefillQ8Fn = decltype(&prefill_q8_0_kernel<false, true, FMT>);
+template <int FMT>
+PrefillQ8Fn<FMT> prefill_q8_pick(bool dump, bool full) {
+    return dump ? (full ? prefill_q8_0_kernel<true, true, FMT> : prefill_q8_0_kernel<true, false, FMT>)
+                : (full ? prefill_q8_0_kernel<false, true, FMT> : prefill_q8_0_kernel<false, false, FMT>);
+}
+
+hipError_t launch_prefill_q8_0(int fmt, const void* W, int64_t w_row_bytes, int64_t N, int64_t K,
                                const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                                hipStream_t st, const SplitScratch& sc) {
     if (K % kKS || w_row_bytes % 4 || w_row_bytes > INT32_MAX || act.m_ld > INT32_MAX || N > (1 << 30) ||
         M > (1 << 30) || K > (1 << 30))
+        return hipErrorNotSupported;
+    // row-split weights: 16-byte pieces straight to LDS (rows 16-byte aligned), 32-bit row offsets
+    if (fmt == kFmtQ8_0RS && (w_row_bytes % 16 || (uint64_t)N * (uint64_t)w_row_bytes >= (1ull << 32)))
         return hipErrorNotSupported;
     // the DMA offsets are 32-bit: every activation row, weight row and scale row must lie within 4 GiB
     if ((uint64_t)M * (uint64_t)K >= (1ull << 32) || (uint64_t)(K / 32) * (uint64_t)act.m_ld * 4 >= (1ull << 32))
@@ -396,10 +455,10 @@ hipError_t launch_prefill_q8_0(bool q40, const void* W, int64_t w_row_bytes, int
     const int tiles_n = (int)((N + kBN - 1) / kBN), tiles_m = (int)((M + kBM - 1) / kBM);
     const size_t lds = prefill_q8_0_lds_bytes();
     const bool full = M % kBM == 0 && N % kBN == 0;
-    auto fn = q40 ? (block_sums ? (full ? prefill_q8_0_kernel<true, true, true> : prefill_q8_0_kernel<true, false, true>)
-                                : (full ? prefill_q8_0_kernel<false, true, true> : prefill_q8_0_kernel<false, false, true>))
-                  : (block_sums ? (full ? prefill_q8_0_kernel<true, true, false> : prefill_q8_0_kernel<true, false, false>)
-                                : (full ? prefill_q8_0_kernel<false, true, false> : prefill_q8_0_kernel<false, false, false>));
+    const bool dump = block_sums != nullptr;
+    auto fn = fmt == kFmtQ4_0     ? prefill_q8_pick<kFmtQ4_0>(dump, full)
+              : fmt == kFmtQ8_0RS ? prefill_q8_pick<kFmtQ8_0RS>(dump, full)
+                                  : prefill_q8_pick<kFmtQ8_0>(dump, full);
     // split-K when the tiles cannot fill the chip: partial planes in the scratch, then their sum
     const SplitPlan sp = plan_split_k((int64_t)tiles_n * tiles_m, (int)(K / kKS), 1, M, N, sc);
     float* out = sp.splits > 1 ? sc.p : Y;

@@ -407,6 +407,9 @@ __global__ void __launch_bounds__(256) dequantize_kernel(int type, const uint8_t
         const uint8_t* b = row + c * 34;
         const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(b));
         for (int j = 0; j < 32; ++j) y[j] = (float)(int8_t)b[2 + j] * d;
+    } else if (type == kTypeQ8_0_RS) {
+        const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(row + K + 2 * c));
+        for (int j = 0; j < 32; ++j) y[j] = (float)(int8_t)row[32 * c + j] * d;
     } else if (type == kTypeQ4_K) {
         const uint8_t* b = row + (c / 8) * 144;
         const int j = (int)(c % 8);  // sub-block
@@ -453,6 +456,34 @@ __global__ void __launch_bounds__(256) dequantize_kernel(int type, const uint8_t
         const float d = *reinterpret_cast<const float*>(b);
         for (int l = 0; l < 32; ++l) y[l] = d * (float)(int8_t)b[4 + (c % 8) * 32 + l];
     }
+}
+
+// ---- load-time repack: Q8_0 rows into row-split rows (quants plane, then scales plane) ----
+// One thread per 32-element block: the block's 34 bytes (2-byte aligned) as 17 halfwords; the 32
+// quants go out as two 16-byte stores (out rows 16-byte aligned), the scale as one halfword.
+__global__ void __launch_bounds__(256) repack_q8_0_rs_kernel(const uint8_t* __restrict__ W, int64_t w_row_bytes,
+                                                             int64_t N, int64_t K, uint8_t* __restrict__ out,
+                                                             int64_t out_row_bytes) {
+    const int64_t nb = K / 32;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= N * nb) return;
+    const int64_t r = gid / nb, b = gid - r * nb;
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(W + r * w_row_bytes + b * 34);
+    uint32_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = (uint32_t)p[1 + 2 * i] | ((uint32_t)p[2 + 2 * i] << 16);
+    uint8_t* o = out + r * out_row_bytes;
+    *reinterpret_cast<uint4*>(o + 32 * b) = make_uint4(q[0], q[1], q[2], q[3]);
+    *reinterpret_cast<uint4*>(o + 32 * b + 16) = make_uint4(q[4], q[5], q[6], q[7]);
+    *reinterpret_cast<uint16_t*>(o + K + 2 * b) = p[0];
+}
+
+hipError_t launch_repack_q8_0_rs(const void* W, int64_t w_row_bytes, int64_t N, int64_t K, void* out,
+                                 int64_t out_row_bytes, hipStream_t st) {
+    const int64_t t = N * (K / 32);
+    hipLaunchKernelGGL(repack_q8_0_rs_kernel, dim3((unsigned)((t + 255) / 256)), dim3(256), 0, st,
+                       (const uint8_t*)W, w_row_bytes, N, K, (uint8_t*)out, out_row_bytes);
+    return hipGetLastError();
 }
 
 hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, hipStream_t st) {

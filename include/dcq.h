@@ -16,7 +16,8 @@
  *   - All data pointers are device pointers owned by the caller; nothing is
  *     freed across the ABI.
  *   - Type ids are ggml's: F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q4_K = 12,
- *     Q5_K = 13, Q6_K = 14, Q8_K = 15.
+ *     Q5_K = 13, Q6_K = 14, Q8_K = 15; and one layout of this library's own,
+ *     DCQ_TYPE_Q8_0_RS (Q8_0 rows repacked at load time, see dcq_repack_weights).
  *   - Dimensions: W is [N][K] (N output rows, K reduction), row r starts at
  *     W + r * w_row_bytes. X is [M][K] fp32 with row stride x_stride_bytes.
  *     Y is [M][N] fp32 with row stride y_stride_bytes:
@@ -50,6 +51,11 @@ extern "C" {
 #define DCQ_TYPE_Q5_K 13
 #define DCQ_TYPE_Q6_K 14
 #define DCQ_TYPE_Q8_K 15
+/* Row-split Q8_0 (not a ggml type): a row of K elements holds its K int8 quants first (block b's 32
+ * at byte 32b), then its K/32 fp16 scales (block b's at byte K + 2b): Q8_0's 34 bytes per block and
+ * values, split into two planes so that every 16-byte piece of quants is 16-byte aligned. Written by
+ * dcq_repack_weights; K % 256 == 0 and row strides multiples of 16 bytes. */
+#define DCQ_TYPE_Q8_0_RS 108
 
 /* status codes */
 #define DCQ_OK 0
@@ -217,6 +223,22 @@ int dcq_dot_rows(int wtype, const void* W, size_t w_row_bytes, const void* Xq, i
  * Q8_0 = quantize_row_q8_0_ref, Q4_0 = quantize_row_q4_0_ref, Q4_K = quantize_row_q4_K_ref,
  * Q5_K = quantize_row_q5_K_ref, Q6_K = quantize_row_q6_K_ref (no importance matrix). */
 int dcq_quantize_weights(int wtype, const float* W, int64_t N, int64_t K, void* Wq, void* stream);
+
+/* ---- load-time weight repack ----
+ * The reference keeps GGUF blocks in plain host buffers (core/src/model_loader.cpp:103-105); a ggml
+ * backend may instead store a tensor in its own layout when the loader hands it over (the role of
+ * ggml's extra buffer types, e.g. the CPU backend's repacked weights). This converts N Q8_0 rows
+ * (wtype = DCQ_TYPE_Q8_0) into DCQ_TYPE_Q8_0_RS rows (out_type) at Wr, row stride wr_row_bytes >=
+ * dcq_row_size(DCQ_TYPE_Q8_0_RS, K), a multiple of 16; K % 256 == 0; W 2-byte aligned with an even
+ * row stride, Wr 16-byte aligned, the two not overlapping. dcq_mul_mat (and _ex, _q, _add, _noalloc,
+ * dcq_ffn_gate_up, dcq_dot_rows, dcq_dequantize_rows) take DCQ_TYPE_Q8_0_RS weights: the prefill MFMA
+ * kernel then loads the quants straight into LDS (no register pass) and the other kernels read
+ * aligned quants. The kernels and their arithmetic are the Q8_0 rows' (the same exact block sums
+ * and fp32 steps), so dcq_mul_mat, _ex, _q, _add, _noalloc and dcq_dot_rows return the Q8_0 rows'
+ * result bits; dcq_ffn_gate_up at M <= DCQ_DECODE_ROWS runs the pair as two products (the fused pair
+ * kernel takes GGUF rows only), equal to the Q8_0 result up to summation order. */
+int dcq_repack_weights(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_bytes, int out_type, void* Wr,
+                       size_t wr_row_bytes, void* stream);
 
 /* ---- dequantization (type_traits->to_float, core/src/inference.cpp:938-945) ----
  * Y[r][k] = value of element k of row r; N rows of K elements, Y rows packed. */

@@ -208,6 +208,22 @@ def mul_mat(wt, wq, x, variant=Q8_0_X86, nthreads=0, want_l1=True):
     return (y, l1) if want_l1 else y
 
 
+def repack_q8_0_rs(wq, k):
+    """Row-split layout of Q8_0 rows (the library's own load-time layout, no reference counterpart):
+    [N][34*K/32] GGUF Q8_0 rows -> [N][34*K/32] rows holding the K int8 quants first (block b's 32 at
+    byte 32b), then the K/32 fp16 scales (block b's at byte K + 2b). A plain byte rearrangement:
+    its values are the Q8_0 rows' (the tests check dequantization and every product against the
+    Q8_0 rows as well)."""
+    wq = np.ascontiguousarray(wq, dtype=np.uint8)
+    n = wq.shape[0]
+    nb = k // 32
+    blocks = wq[:, :34 * nb].reshape(n, nb, 34)
+    out = np.empty((n, 34 * nb), dtype=np.uint8)
+    out[:, :k] = blocks[:, :, 2:].reshape(n, k)
+    out[:, k:] = blocks[:, :, :2].reshape(n, 2 * nb)
+    return out
+
+
 def silu(g):
     """ggml_silu, the SwiGLU gate nonlinearity g / (1 + e^-g), in float64 (ggml's definition;
     reference call ggml_silu at core/src/inference.cpp:1796)."""

@@ -98,6 +98,37 @@ def test_mul_mat_validation_order():
     assert _mm(ws=0x4010, wsb=1 << 20) == MISALIGNED
 
 
+def test_row_split_q8_0_traits_and_validation():
+    """DCQ_TYPE_Q8_0_RS (108): Q8_0's block traits and activation type; rows K % 256 == 0 and 16-byte
+    row strides; the repack takes Q8_0 -> row-split only, rejects overlap, all before any device call."""
+    L = dc.lib()
+    RS = dc.TYPE_Q8_0_RS
+    assert RS == 108
+    assert (dc.block_size(RS), dc.type_size(RS), dc.row_size(RS, 2048)) == (32, 34, 2176)
+    assert dc.vec_dot_type(RS) == 8 and dc.supports_mul_mat(RS, 0, 0)
+    assert dc.block_sums_per_row(RS, 2048) == 64
+    assert dc.mul_mat_workspace_size(RS, 5, 2048) == dc.mul_mat_workspace_size(8, 5, 2048)
+    assert _mm(wt=RS, K=96) == BAD_SHAPE           # K % 256
+    assert _mm(wt=RS, K=1024, wrb=1096) == MISALIGNED  # row stride % 16
+    assert L.dcq_dot_rows(RS, 0x1000, 1096, 0x2000, 1024, 0x3000, 0, 4, None) == MISALIGNED
+    assert L.dcq_quantize_weights(RS, 0x1000, 1, 256, 0x2000, None) == UNSUPPORTED
+
+    def rp(wt=8, W=0x1000, N=4, K=1024, wrb=None, out=RS, Wr=0x100000, wrrb=None):
+        wrb = dc.row_size(8, K) if wrb is None else wrb
+        wrrb = dc.row_size(RS, K) if wrrb is None else wrrb
+        return L.dcq_repack_weights(wt, W, N, K, wrb, out, Wr, wrrb, None)
+    assert rp(wt=12) == UNSUPPORTED and rp(out=8) == UNSUPPORTED
+    assert rp(W=None) == INVALID
+    assert rp(K=96) == BAD_SHAPE and rp(N=0) == BAD_SHAPE
+    assert rp(wrb=1000) == INVALID and rp(wrrb=1000) == INVALID
+    assert rp(W=0x1001) == MISALIGNED and rp(Wr=0x100008) == MISALIGNED and rp(wrrb=1096) == MISALIGNED
+    assert rp(Wr=0x1000 + 1088) == INVALID  # overlaps the source rows
+    import torch
+    if not torch.cuda.is_available():  # well-formed calls reach the device check (no pointer is used)
+        assert rp() == NO_DEVICE
+        assert _mm(wt=RS, K=1024) == NO_DEVICE
+
+
 def test_noalloc_validation_and_limit():
     """dcq_mul_mat_noalloc validates like dcq_mul_mat, and refuses a product whose activation
     workspace exceeds the static scratch (DCQ_ERR_SCRATCH_LIMIT), all before any device call."""

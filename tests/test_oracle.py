@@ -395,3 +395,32 @@ def test_relative_error_stats_known_values(O):
     assert st["n"] == 4 and st["n_zero_ref"] == 1
     assert st["max"] == pytest.approx(0.2) and st["n_above"] == 1
     assert st["p50"] == pytest.approx(0.0002 / 2.0002 / 2, rel=1e-9)  # halfway between 0 and 1e-4
+
+
+def test_row_split_layout_closed_form(O):
+    """The row-split layout on hand-made Q8_0 rows: quants plane (block order), then the scales
+    plane (block order), and back; a swapped plane or block order fails."""
+    k = 64
+    row = np.zeros((2, 68), dtype=np.uint8)
+    row[0, 0:2] = [0x11, 0x22]
+    row[0, 2:34] = np.arange(0, 32)
+    row[0, 34:36] = [0x33, 0x44]
+    row[0, 36:68] = np.arange(100, 132)
+    row[1] = row[0][::-1]
+    rs = O.repack_q8_0_rs(row, k)
+    assert rs.shape == (2, 68)
+    assert list(rs[0, :64]) == list(range(0, 32)) + list(range(100, 132))
+    assert list(rs[0, 64:]) == [0x11, 0x22, 0x33, 0x44]
+    # the inverse reconstructs the rows (a bijection on the bytes)
+    back = np.empty_like(rs)
+    for b in range(2):
+        back[:, 34 * b:34 * b + 2] = rs[:, k + 2 * b:k + 2 * b + 2]
+        back[:, 34 * b + 2:34 * b + 34] = rs[:, 32 * b:32 * b + 32]
+    assert np.array_equal(back, row)
+    # dequantized values agree with the Q8_0 rows' (the oracle's own decoder)
+    q = O.quantize_matrix(8, synth.normal(3 * 512, 91, 0.0, 0.02).reshape(3, 512))
+    r = O.repack_q8_0_rs(q, 512)
+    for n in range(3):
+        d = np.frombuffer(r[n, 512:].tobytes(), dtype=np.float16).astype(np.float32)
+        vals = r[n, :512].view(np.int8).astype(np.float32).reshape(16, 32) * d[:, None]
+        assert np.array_equal(vals.reshape(-1), O.dequantize_row(8, q[n], 512))
