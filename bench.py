@@ -677,6 +677,45 @@ def bench_tool_type(args, dev, tname, M, N, K):
     return out
 
 
+# Row-split Q8_0 (the load-time repack, dcq_repack_weights) against the GGUF Q8_0 rows: config 5's
+# prefill, config 4's batched shape and config 1's decode shape
+ROW_SPLIT_SHAPES = [(2048, 8192, 2048), (64, 8192, 2048), (1, 3072, 1024)]
+
+
+def bench_q8_0_row_split(args, dev, M, N, K):
+    """One dcq_mul_mat step on Q8_0 rows and on the same rows repacked (random valid quants, W rotated
+    like the configs), alternating the two layouts twice; the repack itself is load-time work,
+    outside the timed steps."""
+    import torch
+    import densecore_amd as dc
+    q8, rs = dc.TYPE_Q8_0, dc.TYPE_Q8_0_RS
+    wbytes = N * dc.row_size(q8, K)
+    copies = max(2, int(np.ceil(args.rotate_mb * 2 ** 20 / wbytes)))
+    big8 = random_weights(dev, q8, N, K, copies, 43)
+    bigr = torch.empty((copies, N, dc.row_size(rs, K)), dtype=torch.uint8, device=dev)
+    for r in range(copies):
+        dc.repack_weights(q8, big8[r], N, K, rs, out=bigr[r])
+    g = torch.Generator(device=dev)
+    g.manual_seed(44)
+    x = torch.randn((M, K), device=dev, generator=g)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ws = torch.empty(dc.mul_mat_workspace_size(q8, M, K), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    steps = max(10, args.steps // (4 if M < 2048 else 10))
+    best = {}
+    for _ in range(2):
+        for t, big in ((q8, big8), (rs, bigr)):
+            def step(i, t=t, big=big):
+                dc.mul_mat(t, big[i % copies], N, K, x, y=y, workspace=ws, stream=torch.cuda.current_stream().cuda_stream)
+            ms, _, _ = time_graph(step, steps, args.warmup, args.replays)
+            best[t] = min(best.get(t, float("inf")), ms)
+    out = {"shape": f"Q8_0 M={M} N={N} K={K}", "gguf_step_us": best[q8] * 1e3, "row_split_step_us": best[rs] * 1e3,
+           "row_split_speedup": best[q8] / best[rs], "w_bytes": wbytes}
+    del big8, bigr, ws, y, x
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_gguf_load(args, dev, mib=512):
     """GGUF ingest: a file of Q4_K tensors (mib MiB, in the page cache after it is written) loaded
     tensor by tensor into HBM with dcq_gguf_load_tensor; host-to-device GB/s (PCIe bound)."""
@@ -1108,6 +1147,10 @@ def main():
             print(f"# {e['shape']}: {e['step_us']:.2f} us ({e['kernels']} kernels), {e['weight_GBps']:.0f} GB/s "
                   f"of weights ({100 * e['frac_of_hbm_peak']:.1f} % of 8 TB/s; read ceiling "
                   f"{e.get('read_ceiling_us', 0):.2f} us), {e['TOPS']:.1f} TOPS", file=sys.stderr, flush=True)
+        for M, N, K in ROW_SPLIT_SHAPES:
+            e = extras[f"q8_0_row_split_m{M}_{N}x{K}"] = bench_q8_0_row_split(args, dev, M, N, K)
+            print(f"# {e['shape']}: GGUF rows {e['gguf_step_us']:.2f} us, row-split {e['row_split_step_us']:.2f} us "
+                  f"({e['row_split_speedup']:.3f}x)", file=sys.stderr, flush=True)
         extras["weight_quantizer"] = bench_weight_quantizer(args, dev)
         extras["gguf_load"] = bench_gguf_load(args, dev)
         print(f"# GGUF ingest: {extras['gguf_load']['GBps']:.1f} GB/s host-to-HBM over "
