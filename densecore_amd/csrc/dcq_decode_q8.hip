@@ -8,8 +8,9 @@
 // Launch shape. A workgroup of NW waves owns NW * 64/G weight rows; G lanes stream a row,
 // lane g holding the block pairs u = g + G*t, t < NS (68 bytes: two 34-byte blocks, dword
 // aligned because K % 64 == 0 and the row stride is a multiple of 4; Q4_0: 36 bytes, two
-// 18-byte blocks, their nibbles turned into signed q - 8 bytes as they are used). Every weight
-// load of a lane is issued right after the activation loads, before any arithmetic.
+// 18-byte blocks, their nibbles turned into signed q - 8 bytes as they are used; row-split Q8_0:
+// the pair's 64 quants from the row's quants plane and its two scales from its scales plane).
+// Every weight load of a lane is issued right after the activation loads, before any arithmetic.
 //
 // Activation. Each workgroup quantizes the M fp32 rows into LDS: 8 lanes per 32-element
 // block, 4 floats per lane, the block's max |x| over the 8 lanes by DPP. The arithmetic is

@@ -6,6 +6,8 @@
 //
 // Work unit: 64 weight elements of one row.
 //   Q8_0: a pair of 34-byte blocks (68 B, 17 dwords, dword aligned when K % 64 == 0)
+//   row-split Q8_0: a pair's 64 quants (16-byte aligned) and its two fp16 scales from the row's
+//         scales plane (17 dwords, no re-slicing)
 //   Q4_0: a pair of 18-byte blocks (36 B, 9 dwords, dword aligned when K % 64 == 0), or one
 //         block read as 9 halfwords otherwise; nibbles become signed q - 8 bytes per dword
 //   Q4_K: a quarter superblock: 32 B of nibbles (sub-blocks 2c and 2c+1) + the 16 B header

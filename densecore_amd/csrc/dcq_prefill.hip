@@ -27,9 +27,16 @@
 // The seed is held in 16 VGPRs for the whole loop; everything else per block is the LDS
 // reads, four MFMAs and ~4 address instructions (about 37 VALU per MFMA over the kernel).
 //
-// Q4_0 weights (the Q40 variant) take the same path: a thread's block pair is 36 bytes (two
+// Q4_0 weights (FMT kFmtQ4_0) take the same path: a thread's block pair is 36 bytes (two
 // 18-byte blocks) and the commit unpacks the nibbles into signed q - 8 bytes, so the LDS tile,
 // MFMAs and epilogue are the Q8_0 ones (|I_b| <= 32*8*128 < 2^22 as well).
+// Row-split Q8_0 weights (FMT kFmtQ8_0RS: each row's quants, then its fp16 scales) skip the
+// register pass: the quants go global -> LDS directly like the activation rows, and each lane
+// widens the two scales its own dword load brought into the (dW, -dW * 1.5*2^23) pairs after its
+// wait, before the stage's barrier.
+//
+// The MFMAs of block kb + 1 are issued tile by tile, each right after block kb's epilogue of that
+// tile, so the matrix unit runs one block ahead of the VALU within a wave.
 //
 // Workgroup order is XCD-aware: consecutive workgroup ids go to different XCDs, so the
 // id is remapped to give each XCD a contiguous band of n tiles (its weight rows stay in
