@@ -210,6 +210,48 @@ __device__ __forceinline__ void load_value_dims(const uint8_t* head, int e0, flo
     }
 }
 
+// F16 / F32: the words holding DPL consecutive dims of a value row from element e0 (as
+// load_value_dims), unconverted; value_from_raw converts them (zeros where `ok` is false).
+template <int CT, int DPL>
+__device__ __forceinline__ void load_value_raw(const uint8_t* head, int e0, uint32_t (&w)[CT == kTypeF16 ? (DPL + 1) / 2 : DPL]) {
+    static_assert(CT == kTypeF16 || CT == kTypeF32, "Q8_0 values are staged through LDS");
+    if constexpr (CT == kTypeF16) {
+        const uint8_t* h = head + 2 * e0;
+        if constexpr (DPL == 1) {
+            w[0] = ldu16(h);
+        } else if constexpr (DPL == 2) {
+            w[0] = ld1(h);
+        } else {
+            const uint2 u = *reinterpret_cast<const uint2*>(h);
+            w[0] = u.x, w[1] = u.y;
+        }
+    } else {
+        const uint8_t* f = head + 4 * e0;
+        if constexpr (DPL == 1) {
+            w[0] = ld1(f);
+        } else if constexpr (DPL == 2) {
+            const uint2 u = *reinterpret_cast<const uint2*>(f);
+            w[0] = u.x, w[1] = u.y;
+        } else {
+            const uint4 u = *reinterpret_cast<const uint4*>(f);
+            w[0] = u.x, w[1] = u.y, w[2] = u.z, w[3] = u.w;
+        }
+    }
+}
+template <int CT, int DPL>
+__device__ __forceinline__ void value_from_raw(const uint32_t (&w)[CT == kTypeF16 ? (DPL + 1) / 2 : DPL], bool ok,
+                                               float (&v)[DPL]) {
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) {
+        float x;
+        if constexpr (CT == kTypeF16)
+            x = half_bits_to_float((w[k / 2] >> (16 * (k & 1))) & 0xFFFFu);
+        else
+            x = __uint_as_float(w[k]);
+        v[k] = ok ? x : 0.0f;
+    }
+}
+
 template <int CT>
 __device__ __forceinline__ int64_t head_bytes(int hd) {
     return CT == kTypeQ8_0 ? (int64_t)(hd / 32) * 34 : (int64_t)hd * (CT == kTypeF16 ? 2 : 4);
@@ -254,6 +296,9 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
     constexpr int LPK = S::LPK, KPW = S::KPW, KC = S::KC, DPL = S::DPL;
     constexpr int HBW = AttnSmem<HD, RM>::HBW, NST = AttnSmem<HD, RM>::NST;
     constexpr bool STAGED = SRC == kTypeQ8_0 && !FROM_CUR;
+    // F16 / F32 history: K and V loaded as raw words by every lane of a wave with a present key,
+    // converted at use (see the loads below)
+    constexpr bool RAWV = !STAGED && !FROM_CUR;
     const int wave = w.wave, lane = w.lane;
 
     // ---- this lane's key (score mapping) and where its head piece lives: a byte offset into
@@ -283,8 +328,8 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
     constexpr int KRAW = STAGED ? 2 : (SRC == kTypeF16 ? 4 : 8);  // 16-byte words of the block
     uint4 kraw[KRAW];
     float sc = 0.0f;
-    if (have) {
-        if constexpr (STAGED) {
+    if constexpr (STAGED) {
+        if (have) {
             const uint8_t* p = kbase_p + off + b * 34;
             sc = half_bits_to_float(ldu16(p));
             uint32_t w[8];
@@ -293,18 +338,30 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
             kraw[0] = make_uint4(w[0], w[1], w[2], w[3]);
             kraw[1] = make_uint4(w[4], w[5], w[6], w[7]);
         } else {
-            // the key's piece as 16-byte words, interleaved over its LPK lanes (word b + LPK*j to
-            // lane b): each load instruction reads contiguous bytes across the lanes of a key
-            sc = 1.0f;
-            const uint8_t* p = kbase_p + off + 16 * b;
-#pragma unroll
-            for (int j = 0; j < KRAW; ++j) kraw[j] = ld16(p + 16 * LPK * j);
+            kraw[0] = kraw[1] = make_uint4(0u, 0u, 0u, 0u);
         }
+    } else if (RAWV ? present != 0 : have) {
+        // the key's piece as 16-byte words, interleaved over its LPK lanes (word b + LPK*j to
+        // lane b): each load instruction reads contiguous bytes across the lanes of a key. History:
+        // every lane of a wave with a present key loads (a missing key's offset is 0, in bounds),
+        // and its values are zeroed when converted, so that no branch splits the loads (the waits
+        // below then count exactly).
+        sc = 1.0f;
+        const uint8_t* p = kbase_p + off + 16 * b;
+#pragma unroll
+        for (int j = 0; j < KRAW; ++j) kraw[j] = ld16(p + 16 * LPK * j);
     } else {
 #pragma unroll
         for (int j = 0; j < KRAW; ++j) kraw[j] = make_uint4(0u, 0u, 0u, 0u);
     }
+    // F16 / F32: the K loads stay ahead of the V loads (the scheduler otherwise issues the V loads
+    // first, and the scores would wait for both); they are waited for first (loads retire in order)
+    if constexpr (RAWV) __builtin_amdgcn_sched_barrier(0);
     float v[KPW][DPL];
+    // F16 / F32: the raw words of each key's DPL dims, converted after the softmax (a conversion
+    // here would make each key's load wait for the one before)
+    constexpr int VRW = SRC == kTypeF16 ? (DPL + 1) / 2 : DPL;
+    uint32_t vraw[RAWV ? KPW : 1][VRW];
     const int e0 = DPL * lane;
     uint32_t vst[STAGED ? NST : 1];
     if constexpr (STAGED) {
@@ -332,6 +389,21 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
             const bool ok = f < KPW * HBW && ((present >> (pkc * LPK)) & 1);
             vst[j] = ok ? ld1(vbase_p + op + 4 * dw) : 0u;
         }
+    } else if constexpr (RAWV) {
+        if (present != 0) {
+#pragma unroll
+            for (int tt = 0; tt < KPW; ++tt) {
+                // every lane loads: a missing key's offset is 0, in bounds (masked when converted)
+                const int64_t o_tt = ((int64_t)__builtin_amdgcn_readlane((int)(off >> 32), tt * LPK) << 32) |
+                                     (uint32_t)__builtin_amdgcn_readlane((int)off, tt * LPK);
+                load_value_raw<SRC, DPL>(vbase_p + o_tt, e0, vraw[tt]);
+            }
+        } else {
+#pragma unroll
+            for (int tt = 0; tt < KPW; ++tt)
+#pragma unroll
+                for (int k = 0; k < VRW; ++k) vraw[tt][k] = 0u;
+        }
     } else {
 #pragma unroll
         for (int tt = 0; tt < KPW; ++tt) {
@@ -357,7 +429,8 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
     } else if constexpr (SRC == kTypeF16) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t hw[4] = {kraw[j].x, kraw[j].y, kraw[j].z, kraw[j].w};
+            const uint32_t hw[4] = {have ? kraw[j].x : 0u, have ? kraw[j].y : 0u, have ? kraw[j].z : 0u,
+                                    have ? kraw[j].w : 0u};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 x[8 * j + 2 * k] = half_bits_to_float(hw[k] & 0xFFFF);
@@ -367,8 +440,8 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            x[4 * j] = __uint_as_float(kraw[j].x), x[4 * j + 1] = __uint_as_float(kraw[j].y);
-            x[4 * j + 2] = __uint_as_float(kraw[j].z), x[4 * j + 3] = __uint_as_float(kraw[j].w);
+            x[4 * j] = have ? __uint_as_float(kraw[j].x) : 0.0f, x[4 * j + 1] = have ? __uint_as_float(kraw[j].y) : 0.0f;
+            x[4 * j + 2] = have ? __uint_as_float(kraw[j].z) : 0.0f, x[4 * j + 3] = have ? __uint_as_float(kraw[j].w) : 0.0f;
         }
     }
 
@@ -459,6 +532,10 @@ __device__ __forceinline__ void attn_chunk(const AttnArgs& a, const AttnTile& w,
         const uint8_t* vb = reinterpret_cast<const uint8_t*>(&sm.v[wave][0]);
 #pragma unroll
         for (int tt = 0; tt < KPW; ++tt) load_value_dims<kTypeQ8_0, DPL>(vb + tt * HBW * 4, e0, v[tt]);
+    }
+    if constexpr (RAWV) {
+#pragma unroll
+        for (int tt = 0; tt < KPW; ++tt) value_from_raw<SRC, DPL>(vraw[tt], ((present >> (tt * LPK)) & 1) != 0, v[tt]);
     }
     auto v_row = [&](int r) {
         float acc[DPL];
