@@ -8,25 +8,28 @@
 //   I_g = sum over the 16 elements k of group g of qa[m][k] * (q[n][k] - 32)
 //
 // Tiling (as the Q8_0 prefill). A 256-thread workgroup computes a 128 (m) x 128 (n) tile of Y;
-// each wave owns 64 x 64 = 2 x 2 MFMA tiles. K advances in stages of 128 (half a superblock:
-// 8 groups of 16), double-buffered in LDS; the next stage's loads are issued before the current
-// stage's MFMAs. Activation rows go global -> LDS directly (global_load_lds_dwordx4 from a
-// scalar base); weight bytes pass through registers: thread (row, part) holds the ql, qh bytes of
-// 64 of the stage's elements and, at commit, writes them to LDS as signed int8 q - 32, so the
-// MFMA reads weight operands like activation operands. Per dword the conversion is a v_perm table
-// lookup (the two qh bits select the high nibble of q - 32: 0xE0, 0xF0, 0x00, 0x10) and a v_bfi
-// that merges the ql nibble. LDS rows are 128 bytes of 16-byte slots (one group each) XOR-swizzled
-// by row % 8.
+// each wave owns 64 x 64 = 2 x 2 MFMA tiles. Activation rows go global -> LDS directly
+// (global_load_lds_dwordx4 from a scalar base); weight bytes pass through registers.
 //
-// Per group: v_mfma_i32_32x32x16_i8 (K = 16, one group) into a zero accumulator, then
-// iS += sc_g * I_g with v_mad_i32_i24 (|I_g| <= 16*32*127 < 2^23; |iS| <= 256*128*32*127 < 2^31);
-// per superblock acc += (d * dA) * iS. The 16 integer multiply-adds per lane and group (against
-// 4 MFMAs per wave and group) are the VALU work that bounds the kernel.
+// Q6_K, group scales folded into the weights. The workgroup is 8 waves, each owning 64 x 32 (two
+// MFMA tiles), so that the two accumulator planes below fit the registers; one workgroup per CU.
+// K advances in stages of 128 (half a superblock, 8 groups of 16), double-buffered in LDS, the next
+// stage's loads issued before the current stage's MFMAs. At commit, thread (row, part) turns the 32
+// weights of its two groups into
+// w = (q - 32) * sc_g (|w| <= 4096) and writes them as two int8 planes, w = 64 hi + lo with
+// hi = w >> 6 in [-64, 64] and lo = w & 63 (packed 16-bit arithmetic, two weights per VALU
+// instruction). The MFMA then sums whole superblocks with no VALU between groups:
+//   H = sum_k qa * hi, L = sum_k qa * lo over the superblock's 256 k (v_mfma_i32_32x32x32_i8 into
+//   running accumulators), iS = 64 H + L = sum_g sc_g * I_g exactly (|H| <= 256*64*128 < 2^22,
+//   |iS| <= 256*4096*128 < 2^31), and per superblock acc += (d * dA) * iS.
+// The per-group integer multiply-add of each output (16 VALU instructions per group per MFMA tile)
+// becomes the fold at commit, once per weight element per workgroup. LDS rows are 128 bytes of
+// 16-byte slots (one group each), slot XOR (row % 8).
 //
 // Q4_K, vec_dot_q4_K_q8_K's arithmetic, has 8 sub-blocks of 32 with 6-bit scales and mins:
 //   Y[m][n] = sum_s dA[m][s] * (d[n][s] * iA - dmin[n][s] * iM)
 //   iA = sum_j sc_j * I_j,  iM = sum_j m_j * S_j   (exact int32; S_j = the activation's sub-block sum)
-// Same tiling and stages (half a superblock: 4 sub-blocks); the nibbles are unpacked to one int8
+// Stages of 128 (half a superblock: 4 sub-blocks) in 128-byte LDS rows; the nibbles are unpacked to one int8
 // per element at commit. Per sub-block: v_mfma_i32_32x32x32_i8 (K = 32) into a zero accumulator,
 // then iA += sc_j * I_j. iM runs on the MFMA once per superblock: S_j = 64 hi_j + lo_j (lo_j in
 // [0, 63], hi_j in [-64, 63], split at commit from the 16-element bsums) as int8 bytes
@@ -52,13 +55,17 @@ constexpr int kKS = 128;             // k per stage: half a Q6_K superblock, 8 g
 constexpr int kRow = kKS;            // LDS row: 8 slots of 16 bytes (one group each), slot XOR (row % 8)
 constexpr int kXcds = 8;
 
+constexpr int kKS6 = 128;   // Q6_K: k per stage, half a superblock (8 groups of 16)
+constexpr int kRow6 = kKS6;  // Q6_K LDS row: 8 slots of 16 bytes, slot XOR (row % 8)
+
 struct __align__(16) StageQ6 {
-    int8_t a[kBM * kRow];  // activation int8, [m][k] (swizzled 16-byte slots)
-    int8_t b[kBN * kRow];  // weight q - 32 as int8, [n][k] (swizzled 16-byte slots)
-    uint2 sc[kBN];         // the stage's 8 int8 group scales per weight row
-    float dw[kBN];         // weight superblock scale d
-    float da[kBM];         // activation superblock scale
+    int8_t a[kBM * kRow6];   // activation int8, [m][k] (swizzled 16-byte slots)
+    int8_t bh[kBN * kRow6];  // weight (q - 32) * sc >> 6 as int8, [n][k]
+    int8_t bl[kBN * kRow6];  // weight (q - 32) * sc & 63 as int8, [n][k]
+    float dw[kBN];           // weight superblock scale d
+    float da[kBM];           // activation superblock scale
 };
+__device__ __forceinline__ int swz6(int row, int slot) { return row * kRow6 + 16 * (slot ^ (row & 7)); }
 
 struct __align__(16) StageQ4 {
     int8_t a[kBM * kRow];  // activation int8, [m][k] (swizzled 16-byte slots)
@@ -92,6 +99,10 @@ __device__ __forceinline__ v16i mfma32k32(v4i a, v4i b) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
 }
 
+__device__ __forceinline__ v16i mfma32k32_acc(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ v16i mfma32k16(long a, long b) {
     v16i z = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
     return __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, z, 0, 0, 0);
@@ -107,6 +118,24 @@ __device__ __forceinline__ uint32_t q6_minus32(uint32_t ql, uint32_t qh2) {
     return r;
 }
 
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// Four signed bytes v times the scale sc2 (replicated in both 16-bit halves) as two int8 planes:
+// for each byte b, w = b * sc (|w| <= 4096), hi byte = w >> 6, lo byte = w & 63. Each byte pair is
+// widened by placing the bytes in the high halves of two 16-bit lanes and shifting right
+// arithmetically, then multiplied with packed 16-bit arithmetic.
+__device__ __forceinline__ void fold4(uint32_t v, s16x2 sc2, uint32_t& hi, uint32_t& lo) {
+    const s16x2 a01 = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v, 0x010C000Cu)) >> (s16x2){8, 8};
+    const s16x2 a23 = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v, 0x030C020Cu)) >> (s16x2){8, 8};
+    const s16x2 w01 = a01 * sc2, w23 = a23 * sc2;
+    const uint32_t h01 = __builtin_bit_cast(uint32_t, w01 >> (s16x2){6, 6});
+    const uint32_t h23 = __builtin_bit_cast(uint32_t, w23 >> (s16x2){6, 6});
+    const uint32_t l01 = __builtin_bit_cast(uint32_t, w01) & 0x003F003Fu;
+    const uint32_t l23 = __builtin_bit_cast(uint32_t, w23) & 0x003F003Fu;
+    hi = __builtin_amdgcn_perm(h23, h01, 0x06040200u);
+    lo = __builtin_amdgcn_perm(l23, l01, 0x06040200u);
+}
+
 }  // namespace
 
 // W: Q6_K rows (w_row_bytes % 4 == 0, 16-byte aligned base); xqs: int8 [M][K]; xd: float
@@ -115,7 +144,7 @@ __device__ __forceinline__ uint32_t q6_minus32(uint32_t ql, uint32_t qh2) {
 // Arguments: the ones the first loads need come first (the first 56 bytes of arguments are
 // preloaded into scalar registers at dispatch).
 template <bool DUMP, bool FULL>
-__global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
+__global__ void __launch_bounds__(512, 1) prefill_q6_k_kernel(int tiles_n, int tiles_m, int N, int K, int m_ld,
                                                               int w_row_bytes, const uint8_t* __restrict__ W,
                                                               const int8_t* __restrict__ xqs,
                                                               const float* __restrict__ xd, int M, int stps,
@@ -143,42 +172,43 @@ __global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(int tiles_n, int t
         tile_m = bid / tiles_n;
     }
     const int m0 = tile_m * kBM, n0 = tile_n * kBN;
-    const int nstages = K / kKS, nsb = K / 256;
+    const int nstages = K / kKS6, nsb = K / 256;
     // stps is even: a split covers whole superblocks (two stages each)
     const int s_begin = split * stps, s_end = min(nstages, s_begin + stps);
     Y += (int64_t)split * M * y_stride;
 
     // ---- staging assignment (fixed for the whole K loop) ----
-    // activation rows: instruction i of wave w fills tile rows 8*(4w+i) .. +8, lane l the 16-byte
-    // slot (l % 8) of row 8*(4w+i) + l/8, which holds logical slot (l % 8) ^ (row % 8)
+    // activation rows: instruction i of wave w fills tile rows 8(2w + i) .. + 8, lane l the 16-byte
+    // slot (l % 8) of row 8(2w + i) + l/8, which holds logical slot (l % 8) ^ (row % 8)
     const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    const int a_row0 = 8 * (4 * wave_u) + (lane >> 3);
-    const int a_slot = (lane & 7) ^ (a_row0 & 7);
-    uint32_t a_off[4];
+    uint32_t a_off[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int row = FULL ? m0 + a_row0 + 8 * i : min(m0 + a_row0 + 8 * i, M - 1);
-        a_off[i] = (uint32_t)row * (uint32_t)K + 16u * (uint32_t)a_slot;
+    for (int i = 0; i < 2; ++i) {
+        const int r = 8 * (2 * wave_u + i) + (lane >> 3);
+        const int slot = (lane & 7) ^ (r & 7);
+        const int row = FULL ? m0 + r : min(m0 + r, M - 1);
+        a_off[i] = (uint32_t)row * (uint32_t)K + 16u * (uint32_t)slot;
     }
-    // weight rows: row rw = tid / 2 of the tile, part p = tid % 2: elements 32t + 16p + [0, 16) of
-    // the stage's half h for t = 0..3 (ql bytes 64h + 16p and 64h + 32 + 16p, qh bytes
-    // 128 + 32h + 16p, 16 each); part 0 also loads the half's 8 scales, part 1 the fp16 d.
+    // weight rows: row rw = tid / 4 of the tile, pp = tid % 4 = 2e + p. Of the stage's half h the
+    // thread holds elements 32t + 16p + [0, 16) for t = e and t = e + 2 (groups 2t + p, LDS slots pp
+    // and pp + 4): the ql bytes 64h + 32e + 16p (low nibbles for t = e, high for t = e + 2) and the
+    // qh bytes 128 + 32h + 16p. Every thread loads the half's 8 scales, slot 0 the fp16 d.
     // Superblock s starts 210 s bytes into the row (rows are dword aligned): its dword offset
     // sh = (210 s) & 3 is 0 or 2 for every row of the stage; loads start at the dword below.
-    const int rw = tid >> 1, p = tid & 1;
+    const int rw = tid >> 2, pp = tid & 3, e = pp >> 1, p = pp & 1;
     const uint8_t* w_row = W + (int64_t)(FULL ? n0 + rw : min(n0 + rw, N - 1)) * w_row_bytes;
     const int da_row = m0 + (tid & (kBM - 1));  // m_ld >= m0 + 128: in bounds for every tile
-    uint32_t gw[15], gx[3];
+    uint32_t gw[10], gx[4];
     float gda;
     auto issue = [&](int stg, StageQ6& S) {
-        const int8_t* ab = xqs + (int64_t)stg * kKS;
+        const int8_t* ab = xqs + (int64_t)stg * kKS6;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dma16(ab, a_off[i], S.a + 1024 * (4 * wave_u + i));
+        for (int i = 0; i < 2; ++i) dma16(ab, a_off[i], S.a + 1024 * (2 * wave_u + i));
         const int s = stg >> 1, h = stg & 1;
         const uint8_t* sb = w_row + 210 * s - ((210 * s) & 3);
 #pragma unroll
-        for (int piece = 0; piece < 3; ++piece) {
-            const uint8_t* q = sb + (piece == 2 ? 128 + 32 * h : 64 * h + 32 * piece) + 16 * p;
+        for (int piece = 0; piece < 2; ++piece) {
+            const uint8_t* q = sb + (piece == 1 ? 128 + 32 * h : 64 * h + 32 * e) + 16 * p;
             const U32x4 v = ld4(q);
             gw[5 * piece] = v.x;
             gw[5 * piece + 1] = v.y;
@@ -186,155 +216,124 @@ __global__ void __launch_bounds__(256, 2) prefill_q6_k_kernel(int tiles_n, int t
             gw[5 * piece + 3] = v.w;
             gw[5 * piece + 4] = ld1(q + 16);
         }
-        if (p == 0) {
-            gx[0] = ld1(sb + 192 + 8 * h);
-            gx[1] = ld1(sb + 196 + 8 * h);
-            gx[2] = ld1(sb + 200 + 8 * h);
-        } else {
-            gx[0] = ld1(sb + 208);
-        }
-        gda = xd[(int64_t)s * m_ld + da_row];
+        gx[0] = ld1(sb + 192 + 8 * h);
+        gx[1] = ld1(sb + 196 + 8 * h);
+        gx[2] = ld1(sb + 200 + 8 * h);
+        if (pp == 0) gx[3] = ld1(sb + 208);
+        if (tid < kBM) gda = xd[(int64_t)s * m_ld + da_row];
     };
     auto commit = [&](int stg, StageQ6& S) {
         const uint32_t sh = (uint32_t)((210 * (stg >> 1)) & 3);
-        uint32_t qa[4], qb[4], qh[4];
+        const uint32_t sc_lo = align_bytes(gx[1], gx[0], sh), sc_hi = align_bytes(gx[2], gx[1], sh);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            qa[i] = align_bytes(gw[i + 1], gw[i], sh);
-            qb[i] = align_bytes(gw[i + 6], gw[i + 5], sh);
-            qh[i] = align_bytes(gw[i + 11], gw[i + 10], sh);
+        for (int c = 0; c < 2; ++c) {  // t = e + 2c: group 2t + p, scale byte 2t + p = pp + 4c
+            const int sc = __builtin_amdgcn_sbfe((int)(c ? sc_hi : sc_lo), 8 * pp, 8);
+            const s16x2 sc2 = {(short)sc, (short)sc};
+            const uint32_t nsh = 4u * (uint32_t)c, hsh = 2u * (uint32_t)(e + 2 * c);
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ql = align_bytes(gw[i + 1], gw[i], sh);
+                const uint32_t qh = align_bytes(gw[5 + i + 1], gw[5 + i], sh);
+                fold4(q6_minus32(ql >> nsh, (qh >> hsh) & 0x03030303u), sc2, hi[i], lo[i]);
+            }
+            *reinterpret_cast<uint4*>(S.bh + swz6(rw, pp + 4 * c)) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            *reinterpret_cast<uint4*>(S.bl + swz6(rw, pp + 4 * c)) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
         }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint32_t* src = (t & 1) ? qb : qa;
-            uint32_t v[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                v[i] = q6_minus32(src[i] >> (4 * (t >> 1)), (qh[i] >> (2 * t)) & 0x03030303u);
-            *reinterpret_cast<uint4*>(S.b + swz(rw, 2 * t + p)) = make_uint4(v[0], v[1], v[2], v[3]);
-        }
-        if (p == 0)
-            S.sc[rw] = make_uint2(align_bytes(gx[1], gx[0], sh), align_bytes(gx[2], gx[1], sh));
-        else
-            S.dw[rw] = half_bits_to_float((gx[0] >> (8 * sh)) & 0xFFFFu);
+        if (pp == 0) S.dw[rw] = half_bits_to_float((gx[3] >> (8 * sh)) & 0xFFFFu);
         if (tid < kBM) S.da[tid] = gda;
     };
 
-    // ---- wave tile: 64 x 64 at (wm, wn) inside the workgroup tile ----
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    // ---- wave tile: 64 (m) x 32 (n) at (wm, wn) inside the workgroup tile: 2 MFMA tiles ----
+    const int wm = (wave >> 2) * 64, wn = (wave & 3) * 32;
     const int col = lane & 31, hl = lane >> 5;
-    float acc[2][2][16];
-    int ai[2][2][16];
+    float acc[2][16];
+    v16i H[2], L[2];  // set by a superblock's first MFMAs
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f, ai[i][j][v] = 0;
+        for (int v = 0; v < 16; ++v) acc[i][v] = 0.0f;
+    }
 
-    issue(s_begin, st[s_begin & 1]);
-    commit(s_begin, st[s_begin & 1]);
+    issue(s_begin, st[0]);
+    commit(s_begin, st[0]);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
     __syncthreads();
 
-    for (int stg = s_begin; stg < s_end; ++stg) {
-        const StageQ6& S = st[stg & 1];
-        const bool more = stg + 1 < s_end;
-        if (more) issue(stg + 1, st[(stg + 1) & 1]);  // in flight while this stage computes
-        uint2 scw[2];
+    // superblocks of two stages, unrolled: stage u of a superblock reads buffer u (s_begin is even),
+    // its first MFMAs start from zero, its second ends with the epilogue
+    for (int sb0 = s_begin; sb0 < s_end; sb0 += 2) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) scw[j] = S.sc[wn + 32 * j + col];
+        for (int u = 0; u < 2; ++u) {
+            const int stg = sb0 + u;
+            const StageQ6& S = st[u];
+            const bool more = stg + 1 < s_end;
+            if (more) issue(stg + 1, st[u ^ 1]);  // in flight while this stage computes
 #pragma unroll
-        for (int kg = 0; kg < 8; ++kg) {
-            // fragment rows wm + 32i + col and wn + 32j + col share row % 8 = col % 8; lane half hl
-            // takes bytes 8hl .. 8hl + 8 of the group's slot
-            const int fo = col * kRow + 16 * (kg ^ (col & 7)) + 8 * hl;
-            long fa[2], fb[2];
+            for (int kb = 0; kb < 4; ++kb) {
+                // k 32 kb .. 32 kb + 32 of the stage: lane half hl takes the 16-byte slot 2 kb + hl;
+                // fragment rows wm + 32i + col and wn + col share row % 8 = col % 8
+                const int fo = col * kRow6 + 16 * ((2 * kb + hl) ^ (col & 7));
+                v4i fa[2];
 #pragma unroll
-            for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const long*>(S.a + fo + (wm + 32 * ii) * kRow);
+                for (int ii = 0; ii < 2; ++ii) fa[ii] = *reinterpret_cast<const v4i*>(S.a + fo + (wm + 32 * ii) * kRow6);
+                const v4i fh = *reinterpret_cast<const v4i*>(S.bh + fo + wn * kRow6);
+                const v4i fl = *reinterpret_cast<const v4i*>(S.bl + fo + wn * kRow6);
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) fb[jj] = *reinterpret_cast<const long*>(S.b + fo + (wn + 32 * jj) * kRow);
-            int sc[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint32_t w = kg < 4 ? scw[j].x : scw[j].y;
-                sc[j] = __builtin_amdgcn_sbfe((int)w, 8 * (kg & 3), 8);
-            }
-            v16i D[2][2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) D[i][j] = mfma32k16(fa[i], fb[j]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) ai[i][j][v] = __mul24(sc[j], D[i][j][v]) + ai[i][j][v];
-        }
-        if (stg & 1) {
-            // end of superblock s: acc += (d * dA) * iS, the scales from this (second-half) stage
-            const int s = stg >> 1;
-            float dwj[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) dwj[j] = S.dw[wn + 32 * j + col];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float4 v4 = *reinterpret_cast<const float4*>(&S.da[wm + 32 * i + 8 * q + 4 * hl]);
-                    const float da4[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-#pragma unroll
-                        for (int j = 0; j < 2; ++j) {
-                            const int v = 4 * q + e;
-                            acc[i][j][v] = fmaf(dwj[j] * da4[e], (float)ai[i][j][v], acc[i][j][v]);
-                        }
+                for (int i = 0; i < 2; ++i) {
+                    if (u == 0 && kb == 0) {
+                        H[i] = mfma32k32(fa[i], fh);
+                        L[i] = mfma32k32(fa[i], fl);
+                    } else {
+                        H[i] = mfma32k32_acc(fa[i], fh, H[i]);
+                        L[i] = mfma32k32_acc(fa[i], fl, L[i]);
+                    }
                 }
             }
-            if (DUMP) {
+            if (u == 1) {
+                // end of superblock s: iS = 64 H + L, acc += (d * dA) * iS, the scales from this stage
+                const int s = stg >> 1;
+                const float dwj = S.dw[wn + col];
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                for (int i = 0; i < 2; ++i) {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const int n = n0 + wn + 32 * j + col;
+                    for (int q = 0; q < 4; ++q) {
+                        const float4 v4 = *reinterpret_cast<const float4*>(&S.da[wm + 32 * i + 8 * q + 4 * hl]);
+                        const float da4[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const int m = m0 + wm + 32 * i + 8 * (v >> 2) + 4 * hl + (v & 3);
-                            if (m < M && n < N) sums[((int64_t)m * N + n) * nsb + s] = ai[i][j][v];
+                        for (int k = 0; k < 4; ++k) {
+                            const int v = 4 * q + k;
+                            const int iS = (H[i][v] << 6) + L[i][v];
+                            acc[i][v] = fmaf(dwj * da4[k], (float)iS, acc[i][v]);
+                            if (DUMP) {
+                                const int n = n0 + wn + col;
+                                const int m = m0 + wm + 32 * i + 8 * q + 4 * hl + k;
+                                if (m < M && n < N) sums[((int64_t)m * N + n) * nsb + s] = iS;
+                            }
                         }
                     }
+                }
             }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) ai[i][j][v] = 0;
-        }
-        if (more) {
-            // the other buffer was last read in stage stg - 1, which every wave finished before
-            // the barrier that ended it: one barrier per stage is enough
-            commit(stg + 1, st[(stg + 1) & 1]);
-            __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
-            __syncthreads();
+            if (more) {
+                // the other buffer was last read in stage stg - 1, which every wave finished before
+                // the barrier that ended it: one barrier per stage is enough
+                commit(stg + 1, st[u ^ 1]);
+                __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS-direct loads have landed
+                __syncthreads();
+            }
         }
     }
 
     // ---- store: lane owns column n, rows m0 + wm + 32i + 8(v/4) + 4hl + v%4 ----
+    if (!FULL && n0 + wn + col >= N) return;
     float* yl = Y + (int64_t)(m0 + wm + 4 * hl) * y_stride + (n0 + wn + col);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        if (!FULL && n0 + wn + 32 * j + col >= N) continue;
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = 32 * i + 8 * (v >> 2) + (v & 3);
-                if (FULL || m0 + wm + 4 * hl + r < M) yl[(int64_t)r * y_stride + 32 * j] = acc[i][j][v];
-            }
-    }
+        for (int v = 0; v < 16; ++v) {
+            const int r = 32 * i + 8 * (v >> 2) + (v & 3);
+            if (FULL || m0 + wm + 4 * hl + r < M) yl[(int64_t)r * y_stride] = acc[i][v];
+        }
 }
 
 // W: Q4_K rows (w_row_bytes % 16 == 0, 16-byte aligned base); xqs: int8 [M][K]; xd: float
@@ -634,10 +633,11 @@ hipError_t launch_prefill_q6_k(const void* W, int64_t w_row_bytes, int64_t N, in
     const bool full = M % kBM == 0 && N % kBN == 0;
     auto fn = block_sums ? (full ? prefill_q6_k_kernel<true, true> : prefill_q6_k_kernel<true, false>)
                          : (full ? prefill_q6_k_kernel<false, true> : prefill_q6_k_kernel<false, false>);
-    const SplitPlan sp = plan_split_k((int64_t)tiles_n * tiles_m, (int)(K / kKS), 2, M, N, sc);
+    // stages of half a superblock (splits cover whole superblocks)
+    const SplitPlan sp = plan_split_k((int64_t)tiles_n * tiles_m, (int)(K / kKS6), 2, M, N, sc);
     float* out = sp.splits > 1 ? sc.p : Y;
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
-    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m * sp.splits)), dim3(256), lds, st, tiles_n, tiles_m,
+    hipLaunchKernelGGL(fn, dim3((unsigned)(tiles_n * tiles_m * sp.splits)), dim3(512), lds, st, tiles_n, tiles_m,
                        (int)N, (int)K, (int)act.m_ld, (int)w_row_bytes, (const uint8_t*)W, act.qs, act.d, (int)M,
                        sp.stps, out, out_stride, block_sums);
     hipError_t e = hipGetLastError();
