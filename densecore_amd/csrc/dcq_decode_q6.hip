@@ -414,8 +414,16 @@ __global__ void __launch_bounds__(64 * kWaves) decode_q6k_lds_kernel(
 // (210 s = 2 mod 4) sits 2 bytes into its LDS row; the next superblock's 32 loads are in flight
 // while the current one computes. The activation (planar Q8_K: qs and d; the bsums
 // are not needed, the -32 is in the operand) is staged once per workgroup. A workgroup owns tiles
-// blockIdx.x + k * gridDim.x; its 8 waves take k from an LDS counter, so the tiles of a CU spread
-// over its waves whatever their count.
+// blockIdx.x + k * gridDim.x; its 8 waves take work from an LDS counter, so the tiles of a CU
+// spread over its waves whatever their count.
+//
+// Halves (PAIR): with whole tiles as the unit of work, a head of fewer tiles than waves (32768
+// rows: 1024 tiles for 2048 waves) leaves waves idle. With PAIR the unit is half a tile's
+// superblocks; the wave finishing a tile's first half parks its partial sums in an
+// LDS slot (kTallSlots slots, tile k in slot k % kTallSlots once its earlier occupants are done),
+// and the wave finishing the second half adds the two (a two-term fp32 sum: the same bits
+// whichever half finishes first) and stores Y. A wave waits (s_sleep) only for a slot's earlier
+// tile, whose second half another wave is computing, or for the partner's partial being written.
 constexpr int kTallWaves = 8;
 constexpr int kTallPitch = 264;             // LDS bytes per staged row (66 dwords)
 constexpr int kTallBuf = 32 * kTallPitch;   // one superblock of a 32-row tile
@@ -424,8 +432,18 @@ constexpr int64_t kTallMinRows = 32768;     // rows from which the MFMA form is 
 __host__ __device__ inline size_t tall_act_bytes(int MT, int nsb) {
     return (size_t)round_up((int64_t)MT * 256 * nsb + (int64_t)nsb * MT * 4 + 16, 256);
 }
-__host__ __device__ inline size_t tall_lds_bytes(int MT, int nsb) {
-    return tall_act_bytes(MT, nsb) + (size_t)kTallWaves * 2 * kTallBuf;
+constexpr int kTallSlots = 8;  // PAIR: parked half-tile partials (64 lanes x 4 floats each)
+constexpr size_t kTallPairBytes = (size_t)kTallSlots * 1024 + 3 * kTallSlots * 4;
+__host__ __device__ inline size_t tall_lds_bytes(int MT, int nsb, bool pair) {
+    return tall_act_bytes(MT, nsb) + (size_t)kTallWaves * 2 * kTallBuf + (pair ? kTallPairBytes : 0);
+}
+// Bounded spin of one lane on an LDS word (an exit every wave reaches, whatever the word holds:
+// 2^22 sleeps, far beyond any wait here)
+__device__ __forceinline__ void lds_spin_until(const int* p, int v) {
+    for (int it = 0; it < (1 << 22); ++it) {
+        if (__hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == v) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
 }
 
 // one dword per lane from global memory (uniform base `g` + per-lane offset) into LDS at
@@ -538,7 +556,7 @@ __device__ __forceinline__ void tall_superblock(const uint8_t* row, const int8_t
 // FUSE: X is fp32 [M][x_stride] and every workgroup quantizes the rows it needs to Q8_K itself (the
 // shared 16-lane quantizer: the same bytes as the quantize kernel), saving that launch; else the
 // planar workspace (xqs, xd).
-template <int MT, bool DUMP, bool FUSE>
+template <int MT, bool DUMP, bool FUSE, bool PAIR>
 __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
     const uint8_t* __restrict__ W, int64_t w_row_bytes, int64_t n0, int64_t n1, int nsb,
     const int8_t* __restrict__ xqs, const float* __restrict__ xd, int64_t m_ld, const float* __restrict__ X,
@@ -554,6 +572,12 @@ __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
     float* ad = reinterpret_cast<float*>(smem + (size_t)MT * K);         // [nsb][MT]
     int* ctr = reinterpret_cast<int*>(smem + (size_t)MT * K + (size_t)nsb * MT * 4);
     uint8_t* wb = smem + tall_act_bytes(MT, nsb) + (size_t)wave * 2 * kTallBuf;
+    // PAIR: parked partials [slot][lane] (float4), then per slot: arrivals, partial ready, generation
+    uint8_t* pair_base = smem + tall_act_bytes(MT, nsb) + (size_t)kTallWaves * 2 * kTallBuf;
+    float4* parked = reinterpret_cast<float4*>(pair_base);
+    int* slot_cnt = reinterpret_cast<int*>(pair_base + kTallSlots * 1024);
+    int* slot_ready = slot_cnt + kTallSlots;
+    int* slot_gen = slot_ready + kTallSlots;
 
     // ---- activation: MT rows of qs (rows >= M repeat row M - 1) and the superblock scales ----
     if constexpr (FUSE) {
@@ -585,6 +609,7 @@ __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
         for (int i = tid; i < nsb * MT; i += 64 * kTallWaves) ad[i] = xd[(int64_t)(i / MT) * m_ld + i % MT];
     }
     if (tid == 0) *ctr = 0;
+    if (PAIR && tid < 3 * kTallSlots) slot_cnt[tid] = 0;
     __syncthreads();
 
     const int64_t tiles = (n1 - n0 + 31) / 32;
@@ -616,24 +641,30 @@ __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
         }
     };
 
-    int k_cur = claim();
-    if (k_cur >= cnt) return;  // no barrier follows: a wave without a tile may leave
-    int k_next = claim();
+    // units: whole tiles, or (PAIR) halves: unit u is tile u >> 1, superblocks from (u & 1) * per
+    const int per = PAIR ? nsb / 2 : nsb;
+    const int units = PAIR ? 2 * cnt : cnt;
+    auto tile_of = [&](int u) { return PAIR ? u >> 1 : u; };
+    auto sb0_of = [&](int u) { return PAIR ? (u & 1) * per : 0; };
+    int u_cur = claim();
+    if (u_cur >= units) return;  // no barrier follows: a wave without work may leave
+    int u_next = claim();
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     int ai[4] = {0, 0, 0, 0};
     const int8_t* arow = aq + (size_t)(col < MT ? col : MT - 1) * K + 8 * hl;
-    issue(k_cur, 0, 0, 0, 32);
-    int s = 0, b = 0;
+    issue(tile_of(u_cur), sb0_of(u_cur), 0, 0, 32);
+    int i = 0, b = 0;  // superblock i of the unit, in buffer b
     for (;;) {
-        const bool last_sb = s + 1 == nsb;
-        const bool more = !last_sb || k_next < cnt;
+        const bool last_sb = i + 1 == per;
+        const bool more = !last_sb || u_next < units;
+        const int s = sb0_of(u_cur) + i;
         if (more) {
-            const int nk = last_sb ? k_next : k_cur, ns = last_sb ? 0 : s + 1;
+            const int nu = last_sb ? u_next : u_cur, ns = last_sb ? sb0_of(u_next) : s + 1;
             // the other buffer's previous reads have returned (lgkmcnt(0)) before it is refilled
             __builtin_amdgcn_s_waitcnt(0xC07F);
-            issue(nk, ns, b ^ 1, 0, 31);
+            issue(tile_of(nu), ns, b ^ 1, 0, 31);
             wait_vmcnt<31>();  // this superblock's 32 loads (issued before the next one's) are in
-            issue(nk, ns, b ^ 1, 31, 32);
+            issue(tile_of(nu), ns, b ^ 1, 31, 32);
         } else {
             wait_vmcnt<0>();
         }
@@ -644,7 +675,8 @@ __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
         else
             tall_superblock<MT, 0>(row, arow + 256 * s, hl, ai);
         const float dW = half_bits_to_float(*reinterpret_cast<const uint16_t*>(row + 208 + ((210 * s) & 3)));
-        const int64_t n = n0 + (int64_t)(c0 + (int64_t)k_cur * G) * 32 + col;
+        const int k = tile_of(u_cur);
+        const int64_t n = n0 + (int64_t)(c0 + (int64_t)k * G) * 32 + col;
 #pragma unroll
         for (int v = 0; v < MV; ++v) {
             const int m = 4 * hl + v;
@@ -653,7 +685,34 @@ __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
             ai[v] = 0;
         }
         if (last_sb) {
-            if (n < n1) {
+            bool store = true;
+            if constexpr (PAIR) {
+                const int j = k % kTallSlots, gen = k / kTallSlots;
+                // the slot's earlier tiles are done
+                if (lane == 0) lds_spin_until(slot_gen + j, gen);
+                int first = 0;
+                if (lane == 0) first = atomicAdd(slot_cnt + j, 1) == 0;
+                first = __builtin_amdgcn_readfirstlane(first);
+                if (first) {
+                    parked[j * 64 + lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+                    __builtin_amdgcn_s_waitcnt(0xC07F);  // the partial is in LDS
+                    if (lane == 0) __hip_atomic_store(slot_ready + j, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    store = false;
+                } else {
+                    if (lane == 0) lds_spin_until(slot_ready + j, 1);
+                    __builtin_amdgcn_sched_barrier(0);
+                    asm volatile("" ::: "memory");
+                    const float4 o = parked[j * 64 + lane];
+                    acc[0] += o.x, acc[1] += o.y, acc[2] += o.z, acc[3] += o.w;
+                    __builtin_amdgcn_s_waitcnt(0xC07F);  // the partial has been read
+                    if (lane == 0) {
+                        slot_cnt[j] = 0;
+                        slot_ready[j] = 0;
+                        __hip_atomic_store(slot_gen + j, gen + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    }
+                }
+            }
+            if (store && n < n1) {
 #pragma unroll
                 for (int v = 0; v < MV; ++v) {
                     const int m = 4 * hl + v;
@@ -665,11 +724,11 @@ __global__ void __launch_bounds__(64 * kTallWaves, 1) decode_q6k_mfma_kernel(
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[v] = 0.0f;
             if (!more) break;
-            k_cur = k_next;
-            k_next = claim();
-            s = 0;
+            u_cur = u_next;
+            u_next = claim();
+            i = 0;
         } else {
-            ++s;
+            ++i;
         }
         b ^= 1;
     }
@@ -726,14 +785,18 @@ int q6_rows_per_wave(int64_t rows, int nw) {
 using TallFn = void (*)(const uint8_t*, int64_t, int64_t, int64_t, int, const int8_t*, const float*, int64_t,
                         const float*, int64_t, int, float*, int64_t, int32_t*, int64_t, const float*, int64_t);
 
-template <bool DUMP, bool FUSE>
+template <bool DUMP, bool FUSE, bool PAIR>
 TallFn tall_pick(int mt) {
     switch (mt) {
-        case 1: return decode_q6k_mfma_kernel<1, DUMP, FUSE>;
-        case 2: return decode_q6k_mfma_kernel<2, DUMP, FUSE>;
-        case 4: return decode_q6k_mfma_kernel<4, DUMP, FUSE>;
-        default: return decode_q6k_mfma_kernel<8, DUMP, FUSE>;
+        case 1: return decode_q6k_mfma_kernel<1, DUMP, FUSE, PAIR>;
+        case 2: return decode_q6k_mfma_kernel<2, DUMP, FUSE, PAIR>;
+        case 4: return decode_q6k_mfma_kernel<4, DUMP, FUSE, PAIR>;
+        default: return decode_q6k_mfma_kernel<8, DUMP, FUSE, PAIR>;
     }
+}
+template <bool DUMP, bool FUSE>
+TallFn tall_pick(int mt, bool pair) {
+    return pair ? tall_pick<DUMP, FUSE, true>(mt) : tall_pick<DUMP, FUSE, false>(mt);
 }
 
 // Tall matrices: the MFMA kernel over rows [n0, n1), M tiled by 8; X (fp32, quantized in every
@@ -748,9 +811,12 @@ hipError_t launch_tall_q6k(const void* W, int64_t w_row_bytes, int64_t n0, int64
         const int64_t mc = M - m0 < 8 ? M - m0 : 8;
         const int mt = mc == 1 ? 1 : mc == 2 ? 2 : mc <= 4 ? 4 : 8;
         const bool fuse = X != nullptr;
-        TallFn fn = block_sums ? (fuse ? tall_pick<true, true>(mt) : tall_pick<true, false>(mt))
-                               : (fuse ? tall_pick<false, true>(mt) : tall_pick<false, false>(mt));
-        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kTallWaves), tall_lds_bytes(mt, nsb), st, (const uint8_t*)W,
+        // halves where whole tiles would leave waves idle and the slots fit in LDS (151936 x 2560:
+        // 2.3 tiles per wave, halves 63.6 -> 64.8 us; 32768 x 4096: 0.5, halves 32.1 -> 27.5 us)
+        const bool pair = tiles < (int64_t)grid * kTallWaves && tall_lds_bytes(mt, nsb, true) <= kMaxLds;
+        TallFn fn = block_sums ? (fuse ? tall_pick<true, true>(mt, pair) : tall_pick<true, false>(mt, pair))
+                               : (fuse ? tall_pick<false, true>(mt, pair) : tall_pick<false, false>(mt, pair));
+        hipLaunchKernelGGL(fn, dim3(grid), dim3(64 * kTallWaves), tall_lds_bytes(mt, nsb, pair), st, (const uint8_t*)W,
                            w_row_bytes, n0, n1, nsb, fuse ? nullptr : act->qs + m0 * K, fuse ? nullptr : act->d + m0,
                            fuse ? (int64_t)0 : act->m_ld, fuse ? X + m0 * x_stride : nullptr, x_stride, (int)mc,
                            Y + m0 * y_stride, y_stride, block_sums ? block_sums + m0 * sums_n_stride * nsb : nullptr,
@@ -765,7 +831,7 @@ hipError_t launch_tall_q6k(const void* W, int64_t w_row_bytes, int64_t n0, int64
 bool q6_use_mfma(int64_t rows, int nsb, int64_t M) {
     if (rows < kTallMinRows || nsb % 2 != 0 || knob(Knob::Q6KMfma) == 0) return false;
     const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
-    return tall_lds_bytes(mt, nsb) <= kMaxLds;
+    return tall_lds_bytes(mt, nsb, false) <= kMaxLds;
 }
 
 template <bool DUMP>

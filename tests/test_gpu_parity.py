@@ -587,7 +587,10 @@ def test_lm_head_parity(O, dev, wt, K, M):
 # Tall Q6_K matrices (32768+ rows at K <= 4096): each wave streams 2, 4 or 8 rows through two LDS
 # images, the next row's loads in flight while the current one computes. Rows not a multiple of
 # the rows per workgroup (tails of every length), the fused kernel (M <= 2) and the one over a
-# quantized activation (M = 3, M = 9: two tiles of rows), block sums and the residual add.
+# quantized activation (M = 3, M = 9: two tiles of rows), block sums and the residual add. The
+# MFMA kernel for tall matrices splits each 32-row tile into two halves of its superblocks, summed
+# in LDS, when the tiles are fewer than its waves (40001 and 40003 rows: 1251 tiles for 2048
+# waves); 70001+ rows keep whole tiles.
 TALL_Q6 = [(1, 40001, 1024), (2, 70003, 512), (3, 70001, 1024), (9, 40003, 512), (1, 139999, 1536)]
 
 
