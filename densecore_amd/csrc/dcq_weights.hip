@@ -3,18 +3,20 @@
 //
 // Weight quantization is the offline step before the hot path
 // (core/src/quantize.cpp:214, 285 call ggml_quantize_chunk); dequantization is
-// the reference GEMV's fallback (core/src/inference.cpp:938-945). One thread per
-// block / superblock; the search is ggml's published algorithm (make_qkx2_quants for
-// Q4_K and Q5_K, make_qx_quants with rmse_type 1 for Q6_K, roundf scaling for Q8_0, the
-// max / -8 scale with truncation after + 8.5 for Q4_0), each fit's sums in their sequential
-// order. The Q4_K / Q5_K kernel holds a sub-block in registers and its
-// fits in LDS (no per-thread arrays in scratch memory): 9728 x 2560 took 2.36 ms with the
-// arrays in scratch, 0.39 ms so. The same change to the Q6_K kernel measured slower
-// (0.32 -> 0.36 ms: its final levels need an LDS column per thread, which halves the
-// resident waves), so that kernel keeps its arrays. This file is compiled with
-// -ffp-contract=off so
-// each fp32 operation rounds on its own, as the CPU code does, and the bytes
-// match a CPU build of the same algorithm exactly.
+// the reference GEMV's fallback (core/src/inference.cpp:938-945). The search is ggml's published
+// algorithm (make_qkx2_quants for Q4_K and Q5_K, make_qx_quants with rmse_type 1 for Q6_K, roundf
+// scaling for Q8_0, the max / -8 scale with truncation after + 8.5 for Q4_0), each fit's sums in
+// their sequential order. Q8_0 and Q4_0 take one thread per block. The K-quants take one lane per
+// independent fit: eight lanes per Q4_K / Q5_K superblock (a 32-element sub-block each), sixteen per
+// Q6_K superblock (a 16-element group each), each fit on values in registers; what a superblock
+// shares (its largest scale and min, Q6_K's first group of the largest |scale|, the packed scale
+// bytes, bytes built from several fits' levels) comes from lane exchanges within the superblock's
+// lanes. ggml's fits within a sub-block depend on each other (a better candidate moves the next
+// candidates' offset), so they stay sequential in their lane. 9728 x 2560: Q4_K one thread per
+// superblock with the sub-block fits in LDS 0.39 ms (2.36 ms with per-thread arrays in scratch
+// memory); Q6_K one thread per superblock 0.33 ms. This file is compiled with -ffp-contract=off so
+// each fp32 operation rounds on its own, as the CPU code does, and the bytes match a CPU build of
+// the same algorithm exactly.
 #include "dcq_common.h"
 #include "dcq_kernels.h"
 
@@ -100,8 +102,7 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, uint8_t* d
 // rmin = -1, rdelta = 0.1, nstep = 20 (the sub-block scale and min of the least weighted squared
 // error over a grid of 21 inverse scales around nmax / (max - min), each refined by a least-squares
 // fit, min clamped to <= 0), the same fp32 operations in the same order, on the sub-block held in
-// registers. quantize_row_q5_K_ref's fit is the same search with nmax = 31, rmin = -0.5, nstep = 15. The weights av_x + |x_i| are recomputed per use (the
-// same fp32 value each time), and the chosen levels L are not stored: the (iscale, min) they were
+// registers. quantize_row_q5_K_ref's fit is the same search with nmax = 31, rmin = -0.5, nstep = 15. The chosen levels L are not stored: the (iscale, min) they were
 // computed with are returned instead, so the caller recomputes them where it needs them.
 struct Qkx2Fit {
     float scale, the_min;  // make_qkx2_quants' return value and *the_min
@@ -113,20 +114,22 @@ template <int NMAX>
 __device__ __forceinline__ int clampq(int l) { return l < 0 ? 0 : (l > NMAX ? NMAX : l); }
 
 template <bool Q5>
-__device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
+__device__ __forceinline__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
     constexpr int nmax = Q5 ? 31 : 15;
     const float rmin = Q5 ? -0.5f : -1.f, rdelta = 0.1f;
     const int nstep = Q5 ? 15 : 20;
+    float w[32];  // the weights av_x + |x_i|, each computed once (the same fp32 value at every use)
+#pragma unroll
+    for (int i = 0; i < 32; ++i) w[i] = av_x + fabsf(x[i]);
     float min = x[0], max = x[0];
-    float sum_w = av_x + fabsf(x[0]);
+    float sum_w = w[0];
     float sum_x = sum_w * x[0];
 #pragma unroll
     for (int i = 1; i < 32; ++i) {
         if (x[i] < min) min = x[i];
         if (x[i] > max) max = x[i];
-        const float w = av_x + fabsf(x[i]);
-        sum_w += w;
-        sum_x += w * x[i];
+        sum_w += w[i];
+        sum_x += w[i] * x[i];
     }
     if (min > 0) min = 0;
     if (max == min) return {0.f, -min, 0.f, 0.f, 1};
@@ -138,19 +141,19 @@ __device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
     for (int i = 0; i < 32; ++i) {
         const int l = clampq<nmax>(nearest_int(iscale * (x[i] - min)));
         const float diff = scale * (float)l + min - x[i];
-        best_error += (av_x + fabsf(x[i])) * (diff * diff);
+        best_error += w[i] * (diff * diff);
     }
 #pragma unroll 1
     for (int is = 0; is <= nstep; ++is) {
         iscale = (rmin + rdelta * is + nmax) / (max - min);
         float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        float lf[32];  // this candidate's levels, reused by its error sum
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
-            const int l = clampq<nmax>(nearest_int(iscale * (x[i] - min)));
-            const float w = av_x + fabsf(x[i]);
-            sum_l += w * l;
-            sum_l2 += w * l * l;
-            sum_xl += w * l * x[i];
+            lf[i] = (float)clampq<nmax>(nearest_int(iscale * (x[i] - min)));
+            sum_l += w[i] * lf[i];
+            sum_l2 += w[i] * lf[i] * lf[i];
+            sum_xl += w[i] * lf[i] * x[i];
         }
         const float D = sum_w * sum_l2 - sum_l * sum_l;
         if (D > 0) {
@@ -163,9 +166,8 @@ __device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
             float mad = 0;
 #pragma unroll
             for (int i = 0; i < 32; ++i) {
-                const int l = clampq<nmax>(nearest_int(iscale * (x[i] - min)));
-                const float diff = this_scale * (float)l + this_min - x[i];
-                mad += (av_x + fabsf(x[i])) * (diff * diff);
+                const float diff = this_scale * lf[i] + this_min - x[i];
+                mad += w[i] * (diff * diff);
             }
             if (mad < best_error) {
                 l_iscale = iscale;
@@ -179,151 +181,167 @@ __device__ Qkx2Fit qkx2_fit32(const float (&x)[32], float av_x) {
     return {scale, -min, l_iscale, l_min, 0};
 }
 
-// ---- Q4_K / Q5_K: quantize_row_q4_K_ref / quantize_row_q5_K_ref, one thread per superblock with no
-// per-thread arrays in scratch: a sub-block's 32 values live in registers, the per-sub-block fits in
-// this thread's LDS slot, and the final levels are recomputed per sub-block pair as they are
-// packed ----
-constexpr int kWq4Threads = 64;
+// ---- Q4_K / Q5_K: quantize_row_q4_K_ref / quantize_row_q5_K_ref with eight lanes per superblock,
+// one per 32-element sub-block. Each lane runs its sub-block's fit on its values in registers; the
+// superblock's largest scale and min, and the packed scale bytes, come from exchanges within the
+// eight lanes; each lane then forms its sub-block's final levels, and the even lane of a pair writes
+// the pair's 32 nibble bytes. The maxima are exact in any order, so the bytes are those of ggml's
+// sequential loop. ----
+constexpr int kWqThreads = 256;
 template <bool Q5>
-__global__ void __launch_bounds__(kWq4Threads) quantize_w_q4_K_kernel(const float* __restrict__ W, int64_t N,
-                                                                      int64_t K, uint8_t* __restrict__ out) {
+__global__ void __launch_bounds__(kWqThreads) quantize_w_q4_K_kernel(const float* __restrict__ W, int64_t N,
+                                                                     int64_t K, uint8_t* __restrict__ out) {
     constexpr int nmax = Q5 ? 31 : 15, kSb = Q5 ? 176 : 144, kQsDw = Q5 ? 12 : 4;
-    __shared__ Qkx2Fit fits[8][kWq4Threads];
     const int64_t nsb = K / QK_K;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= N * nsb) return;
-    const int t = threadIdx.x;
-    const int64_t r = gid / nsb, sbi = gid - (gid / nsb) * nsb;
-    const float* xs = W + r * K + sbi * QK_K;
-    auto load32 = [&](int j, float (&x)[32]) {
-        const float4* p = reinterpret_cast<const float4*>(xs + 32 * j);
+    const int64_t sg = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 3;  // superblock over [N][nsb]
+    const int j = (int)(threadIdx.x & 7);                                       // its sub-block
+    if (sg >= N * nsb) return;  // the eight lanes of a superblock leave together
+    const int64_t r = sg / nsb, sbi = sg - r * nsb;
+    float x[32];
+    {
+        const float4* p = reinterpret_cast<const float4*>(W + r * K + sbi * QK_K + 32 * j);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const float4 v = p[q];
             x[4 * q] = v.x, x[4 * q + 1] = v.y, x[4 * q + 2] = v.z, x[4 * q + 3] = v.w;
         }
-    };
-    float max_scale = 0, max_min = 0;
-#pragma unroll 1
-    for (int j = 0; j < 8; ++j) {
-        float x[32];
-        load32(j, x);
-        float sum_x2 = 0;
+    }
+    float sum_x2 = 0;
 #pragma unroll
-        for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
-        const float av_x = sqrtf(sum_x2 / 32);
-        const Qkx2Fit f = qkx2_fit32<Q5>(x, av_x);
-        fits[j][t] = f;
-        if (f.scale > max_scale) max_scale = f.scale;
-        if (f.the_min > max_min) max_min = f.the_min;
+    for (int l = 0; l < 32; ++l) sum_x2 += x[l] * x[l];
+    const float av_x = sqrtf(sum_x2 / 32);
+    const Qkx2Fit f = qkx2_fit32<Q5>(x, av_x);
+    // the superblock's largest scale and min, from 0 (ggml's running maxima)
+    float max_scale = f.scale > 0 ? f.scale : 0.f, max_min = f.the_min > 0 ? f.the_min : 0.f;
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+        const float a = __shfl_xor(max_scale, o, 8), c = __shfl_xor(max_min, o, 8);
+        max_scale = a > max_scale ? a : max_scale;
+        max_min = c > max_min ? c : max_min;
     }
     const float inv_scale = max_scale > 0 ? 63.f / max_scale : 0.f;
     const float inv_min = max_min > 0 ? 63.f / max_min : 0.f;
-    // the 12 scale bytes (get_scale_min_k4's packing), built in three dwords
+    int ls = nearest_int(inv_scale * f.scale);
+    int lm = nearest_int(inv_min * f.the_min);
+    ls = ls < 63 ? ls : 63;
+    lm = lm < 63 ? lm : 63;
+    const uint16_t dh = float_to_half_bits(max_scale / 63.f), dminh = float_to_half_bits(max_min / 63.f);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(out + sg * kSb);
+    // the 12 scale bytes (get_scale_min_k4's packing) from the eight lanes' (ls, lm)
+    const int pk = (ls & 0xFFFF) | (lm << 16);
     uint32_t scw[3] = {0, 0, 0};
     auto put = [&](int byte, uint32_t v) { scw[byte >> 2] |= (v & 0xFFu) << (8 * (byte & 3)); };
-    uint8_t ls8[8], lm8[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        int ls = nearest_int(inv_scale * fits[j][t].scale);
-        int lm = nearest_int(inv_min * fits[j][t].the_min);
-        ls = ls < 63 ? ls : 63;
-        lm = lm < 63 ? lm : 63;
-        ls8[j] = (uint8_t)ls;
-        lm8[j] = (uint8_t)lm;
-        if (j < 4) {
-            put(j, (uint32_t)ls);
-            put(j + 4, (uint32_t)lm);
+    for (int k = 0; k < 8; ++k) {
+        const int v = __shfl(pk, k, 8);
+        const int lsk = (int)(int16_t)(v & 0xFFFF), lmk = v >> 16;
+        if (k < 4) {
+            put(k, (uint32_t)lsk);
+            put(k + 4, (uint32_t)lmk);
         } else {
-            put(j + 4, (uint32_t)((ls & 0xF) | ((lm & 0xF) << 4)));
-            put(j - 4, (uint32_t)((ls >> 4) << 6));
-            put(j, (uint32_t)((lm >> 4) << 6));
+            put(k + 4, (uint32_t)((lsk & 0xF) | ((lmk & 0xF) << 4)));
+            put(k - 4, (uint32_t)((lsk >> 4) << 6));
+            put(k, (uint32_t)((lmk >> 4) << 6));
         }
     }
-    const uint16_t dh = float_to_half_bits(max_scale / 63.f), dminh = float_to_half_bits(max_min / 63.f);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(out + (r * nsb + sbi) * kSb);
-    dst[0] = (uint32_t)dh | ((uint32_t)dminh << 16);
-    dst[1] = scw[0];
-    dst[2] = scw[1];
-    dst[3] = scw[2];
-    const float dsb = half_bits_to_float(dh), dmsb = half_bits_to_float(dminh);
-    // final levels of sub-blocks 2c (low nibbles) and 2c + 1 (high nibbles) of qs[32c .. 32c + 32):
-    // from the 6-bit scales, or, where the scale quantized to 0, the fit's own levels. Q5_K: bit 4
-    // of element ii of sub-block j goes to bit j of qh[ii].
-    [[maybe_unused]] uint32_t qh[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll 1
-    for (int c = 0; c < 4; ++c) {
-        uint32_t packed[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (j == 0) {
+        dst[0] = (uint32_t)dh | ((uint32_t)dminh << 16);
+        dst[1] = scw[0];
+        dst[2] = scw[1];
+        dst[3] = scw[2];
+    }
+    // final levels: from the 6-bit scales, or, where the scale quantized to 0, the fit's own levels.
+    // Sub-blocks 2c and 2c + 1 are the low and high nibbles of qs[32c .. 32c + 32); Q5_K: bit 4 of
+    // element ii of sub-block j goes to bit j of qh[ii].
+    const float d = half_bits_to_float(dh) * (float)(uint8_t)ls;
+    const float dm = half_bits_to_float(dminh) * (float)(uint8_t)lm;
+    const int h = j & 1;
+    uint32_t nib[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    [[maybe_unused]] uint32_t hb[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int j = 2 * c + h;
-            float x[32];
-            load32(j, x);
-            const float d = dsb * ls8[j];
-            const float dm = dmsb * lm8[j];
-            const Qkx2Fit f = fits[j][t];
+    for (int ii = 0; ii < 32; ++ii) {
+        int l;
+        if (d != 0.0f)
+            l = clampq<nmax>(nearest_int((x[ii] + dm) / d));
+        else
+            l = f.zero ? 0 : clampq<nmax>(nearest_int(f.l_iscale * (x[ii] - f.l_min)));
+        nib[ii >> 2] |= (uint32_t)(l & 0xF) << (8 * (ii & 3) + 4 * h);
+        if constexpr (Q5) hb[ii >> 2] |= (uint32_t)(l >> 4) << (8 * (ii & 3) + j);
+    }
 #pragma unroll
-            for (int ii = 0; ii < 32; ++ii) {
-                int l;
-                if (d != 0.0f)
-                    l = clampq<nmax>(nearest_int((x[ii] + dm) / d));
-                else
-                    l = f.zero ? 0 : clampq<nmax>(nearest_int(f.l_iscale * (x[ii] - f.l_min)));
-                packed[ii >> 2] |= (uint32_t)(l & 0xF) << (8 * (ii & 3) + 4 * h);
-                if constexpr (Q5) qh[ii >> 2] |= (uint32_t)(l >> 4) << (8 * (ii & 3) + j);
-            }
-        }
+    for (int q = 0; q < 8; ++q) nib[q] |= (uint32_t)__shfl_xor((int)nib[q], 1, 8);
+    if (h == 0) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) dst[kQsDw + 8 * c + q] = packed[q];
+        for (int q = 0; q < 8; ++q) dst[kQsDw + 8 * (j >> 1) + q] = nib[q];
     }
     if constexpr (Q5) {
 #pragma unroll
-        for (int q = 0; q < 8; ++q) dst[4 + q] = qh[q];
+        for (int o = 1; o < 8; o <<= 1)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) hb[q] |= (uint32_t)__shfl_xor((int)hb[q], o, 8);
+        if (j == 0) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) dst[4 + q] = hb[q];
+        }
     }
 }
 
-// ---- Q6_K ----
-__device__ float make_qx_quants_rmse1(int n, int nmax, const float* x, int8_t* L) {
+// ---- Q6_K: quantize_row_q6_K_ref with sixteen lanes per superblock, one per 16-element group ----
+// make_qx_quants with n = 16, nmax = 32, rmse_type 1 on one group held in registers (the levels L
+// are l + 32 in [0, 63]); the candidate loop is ggml's, in order.
+__device__ __forceinline__ float qx_fit16(const float (&x)[16], int (&L)[16]) {
+    constexpr int nmax = 32;
     float max = 0, amax = 0;
-    for (int i = 0; i < n; ++i) {
-        float ax = fabsf(x[i]);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const float ax = fabsf(x[i]);
         if (ax > amax) {
             amax = ax;
             max = x[i];
         }
     }
     if (amax < 1e-15f) {
-        for (int i = 0; i < n; ++i) L[i] = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) L[i] = 0;
         return 0.f;
     }
     float iscale = -nmax / max;
     float sumlx = 0, suml2 = 0;
-    for (int i = 0; i < n; ++i) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
         int l = nearest_int(iscale * x[i]);
         l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
-        L[i] = (int8_t)(l + nmax);
-        float w = x[i] * x[i];
+        L[i] = l + nmax;
+        const float w = x[i] * x[i];
         sumlx += w * x[i] * l;
         suml2 += w * l * l;
     }
     float scale = suml2 ? sumlx / suml2 : 0.0f;
     float best = scale * sumlx;
+    float w[16], wx[16];  // x_i^2 and x_i^2 * x_i, the first factors of the sums below
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        w[i] = x[i] * x[i];
+        wx[i] = w[i] * x[i];
+    }
+#pragma unroll 1
     for (int is = -9; is <= 9; ++is) {
         if (is == 0) continue;
         iscale = -(nmax + 0.1f * is) / max;
         sumlx = suml2 = 0;
-        for (int i = 0; i < n; ++i) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
             int l = nearest_int(iscale * x[i]);
             l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
-            float w = x[i] * x[i];
-            sumlx += w * x[i] * l;
-            suml2 += w * l * l;
+            sumlx += wx[i] * l;
+            suml2 += w[i] * l * l;
         }
         if (suml2 > 0 && sumlx * sumlx > best * suml2) {
-            for (int i = 0; i < n; ++i) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
                 int l = nearest_int(iscale * x[i]);
                 l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
-                L[i] = (int8_t)(l + nmax);
+                L[i] = l + nmax;
             }
             scale = sumlx / suml2;
             best = scale * sumlx;
@@ -332,66 +350,96 @@ __device__ float make_qx_quants_rmse1(int n, int nmax, const float* x, int8_t* L
     return scale;
 }
 
-__global__ void __launch_bounds__(64) quantize_w_q6_K_kernel(const float* __restrict__ W, int64_t N, int64_t K,
-                                                             uint8_t* __restrict__ out) {
+// Lane ib fits group ib; the superblock scale is the scale of the first group of the largest |scale|
+// (ggml's strict running maximum), found by exchanges within the sixteen lanes; each lane forms its
+// group's scale byte and final levels. In the 210-byte superblock, element 128 jh + 32 qd + l of half
+// jh and quarter qd is the low (qd 0, 1) or high (qd 2, 3) nibble of ql[64 jh + 32 (qd & 1) + l] and
+// bits 2 qd of qh[32 jh + l]: group ib = 8 jh + 2 qd + (l >> 4). The lanes of one ql byte (ib, ib ^ 4)
+// and of one qh byte (ib, ib ^ 2, ib ^ 4, ib ^ 6) combine by exchange; superblocks are 2-byte aligned,
+// so the bytes go out as 16-bit stores.
+__global__ void __launch_bounds__(kWqThreads) quantize_w_q6_K_kernel(const float* __restrict__ W, int64_t N, int64_t K,
+                                                                     uint8_t* __restrict__ out) {
     const int64_t nsb = K / QK_K;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (gid >= N * nsb) return;
-    const int64_t r = gid / nsb, sbi = gid - (gid / nsb) * nsb;
-    const float* x = W + r * K + sbi * QK_K;
-    uint8_t* dstb = out + (r * nsb + sbi) * 210;
-    int8_t L[QK_K];
-    float scales[16];
-    float max_scale = 0, max_abs_scale = 0;
-    for (int ib = 0; ib < 16; ++ib) {
-        const float scale = make_qx_quants_rmse1(16, 32, x + 16 * ib, L + 16 * ib);
-        scales[ib] = scale;
-        const float abs_scale = fabsf(scale);
-        if (abs_scale > max_abs_scale) {
-            max_abs_scale = abs_scale;
-            max_scale = scale;
+    const int64_t sg = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // superblock over [N][nsb]
+    const int ib = (int)(threadIdx.x & 15);                                      // its group
+    if (sg >= N * nsb) return;  // the sixteen lanes of a superblock leave together
+    const int64_t r = sg / nsb, sbi = sg - r * nsb;
+    float x[16];
+    {
+        const float4* p = reinterpret_cast<const float4*>(W + r * K + sbi * QK_K + 16 * ib);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = p[q];
+            x[4 * q] = v.x, x[4 * q + 1] = v.y, x[4 * q + 2] = v.z, x[4 * q + 3] = v.w;
         }
     }
-    uint8_t y[210];
-    for (int i = 0; i < 210; ++i) y[i] = 0;
-    if (!(max_abs_scale < 1e-15f)) {
-        float iscale = -128.f / max_scale;
-        const uint16_t dh = float_to_half_bits(1 / iscale);
-        y[208] = (uint8_t)dh;
-        y[209] = (uint8_t)(dh >> 8);
-        int8_t* ysc = reinterpret_cast<int8_t*>(y + 192);
-        for (int ib = 0; ib < 16; ++ib) {
-            int v = nearest_int(iscale * scales[ib]);
-            ysc[ib] = (int8_t)(v < 127 ? v : 127);
-        }
-        for (int j = 0; j < 16; ++j) {
-            float d = half_bits_to_float(dh) * ysc[j];
-            if (!d) continue;
-            for (int ii = 0; ii < 16; ++ii) {
-                int l = nearest_int(x[16 * j + ii] / d);
-                l = l < -32 ? -32 : (l > 31 ? 31 : l);
-                L[16 * j + ii] = (int8_t)(l + 32);
-            }
-        }
-        uint8_t* ql = y;
-        uint8_t* qh = y + 128;
-        for (int j = 0; j < QK_K; j += 128) {
-            for (int l = 0; l < 32; ++l) {
-                const uint8_t q1 = L[j + l + 0] & 0xF;
-                const uint8_t q2 = L[j + l + 32] & 0xF;
-                const uint8_t q3 = L[j + l + 64] & 0xF;
-                const uint8_t q4 = L[j + l + 96] & 0xF;
-                ql[l + 0] = (uint8_t)(q1 | (q3 << 4));
-                ql[l + 32] = (uint8_t)(q2 | (q4 << 4));
-                qh[l] = (uint8_t)((L[j + l] >> 4) | ((L[j + l + 32] >> 4) << 2) | ((L[j + l + 64] >> 4) << 4) |
-                                  ((L[j + l + 96] >> 4) << 6));
-            }
-            ql += 64;
-            qh += 32;
+    int L[16];
+    const float scale = qx_fit16(x, L);
+    // the first group of the largest |scale|
+    float best_abs = fabsf(scale), best_scale = scale;
+    int best_ib = ib;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        const float a = __shfl_xor(best_abs, o, 16), sc = __shfl_xor(best_scale, o, 16);
+        const int i2 = __shfl_xor(best_ib, o, 16);
+        if (a > best_abs || (a == best_abs && i2 < best_ib)) {
+            best_abs = a;
+            best_scale = sc;
+            best_ib = i2;
         }
     }
-    uint16_t* d16 = reinterpret_cast<uint16_t*>(dstb);  // superblocks are 2-byte aligned
-    for (int i = 0; i < 105; ++i) d16[i] = (uint16_t)(y[2 * i] | (y[2 * i + 1] << 8));
+    uint16_t* d16 = reinterpret_cast<uint16_t*>(out + sg * 210);
+    if (best_abs < 1e-15f) {  // an all-zero superblock: 105 zero halfwords over the sixteen lanes
+        for (int k = ib; k < 105; k += 16) d16[k] = 0;
+        return;
+    }
+    const float iscale = -128.f / best_scale;
+    const uint16_t dh = float_to_half_bits(1 / iscale);
+    const int v = nearest_int(iscale * scale);
+    const int sc8 = v < 127 ? v : 127;  // the group's int8 scale
+    const float d = half_bits_to_float(dh) * (float)(int8_t)sc8;
+    if (d != 0.0f) {
+#pragma unroll
+        for (int ii = 0; ii < 16; ++ii) {
+            int l = nearest_int(x[ii] / d);
+            l = l < -32 ? -32 : (l > 31 ? 31 : l);
+            L[ii] = l + 32;
+        }
+    }
+    const int jh = ib >> 3, g = ib & 7, qd = g >> 1, l0 = 16 * (g & 1);
+    uint32_t ql[4] = {0, 0, 0, 0}, qh[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int ii = 0; ii < 16; ++ii) {
+        ql[ii >> 2] |= (uint32_t)(L[ii] & 0xF) << (8 * (ii & 3) + 4 * (qd >> 1));
+        qh[ii >> 2] |= (uint32_t)(L[ii] >> 4) << (8 * (ii & 3) + 2 * qd);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        ql[q] |= (uint32_t)__shfl_xor((int)ql[q], 4, 16);
+        qh[q] |= (uint32_t)__shfl_xor((int)qh[q], 2, 16);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) qh[q] |= (uint32_t)__shfl_xor((int)qh[q], 4, 16);
+    if ((qd >> 1) == 0) {  // ql bytes 64 jh + 32 qd + l0 ..
+        uint16_t* p = d16 + (64 * jh + 32 * qd + l0) / 2;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            p[2 * q] = (uint16_t)ql[q];
+            p[2 * q + 1] = (uint16_t)(ql[q] >> 16);
+        }
+    }
+    if (qd == 0) {  // qh bytes 128 + 32 jh + l0 ..
+        uint16_t* p = d16 + (128 + 32 * jh + l0) / 2;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            p[2 * q] = (uint16_t)qh[q];
+            p[2 * q + 1] = (uint16_t)(qh[q] >> 16);
+        }
+    }
+    // scale bytes 192 + ib (pairs as halfwords), then d
+    const int sc_pair = (sc8 & 0xFF) | ((__shfl_xor(sc8, 1, 16) & 0xFF) << 8);
+    if ((ib & 1) == 0) d16[(192 + ib) / 2] = (uint16_t)sc_pair;
+    if (ib == 0) d16[104] = dh;
 }
 
 // ---- dequantization: one thread per 32 output elements ----
@@ -498,12 +546,12 @@ hipError_t launch_quantize_weights(int wtype, const float* W, int64_t N, int64_t
     } else if (wtype == kTypeQ4_K || wtype == kTypeQ5_K) {
         const int64_t t = N * (K / QK_K);
         hipLaunchKernelGGL(wtype == kTypeQ5_K ? quantize_w_q4_K_kernel<true> : quantize_w_q4_K_kernel<false>,
-                           dim3((unsigned)((t + kWq4Threads - 1) / kWq4Threads)), dim3(kWq4Threads), 0, st, W, N,
+                           dim3((unsigned)((8 * t + kWqThreads - 1) / kWqThreads)), dim3(kWqThreads), 0, st, W, N,
                            K, (uint8_t*)Wq);
     } else {
         const int64_t t = N * (K / QK_K);
-        hipLaunchKernelGGL(quantize_w_q6_K_kernel, dim3((unsigned)((t + 63) / 64)), dim3(64), 0, st, W, N, K,
-                           (uint8_t*)Wq);
+        hipLaunchKernelGGL(quantize_w_q6_K_kernel, dim3((unsigned)((16 * t + kWqThreads - 1) / kWqThreads)),
+                           dim3(kWqThreads), 0, st, W, N, K, (uint8_t*)Wq);
     }
     return hipGetLastError();
 }
