@@ -262,8 +262,8 @@ hipError_t launch_batch_q4k(bool q5, const void* W, int64_t w_row_bytes, int64_t
     const int nsb = (int)(K / 256);
     const int64_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
     // with few weight rows the superblocks are also split over workgroups (at least one per wave;
-    // about 0.25 us per superblock of a workgroup)
-    const SplitPlan sp = plan_split_k(tiles, nsb, kWaves, M, N, sc, 0.25);
+    // about 0.6 us per superblock of a workgroup: 4096 x 4096 at M = 64, 128 workgroups, 10.1 us)
+    const SplitPlan sp = plan_split_k(tiles, nsb, kWaves, M, N, sc, 0.6);
     float* out = sp.splits > 1 ? sc.p : Y;
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
     dim3 grid((unsigned)((N + kNT - 1) / kNT), (unsigned)((M + kMT - 1) / kMT), (unsigned)sp.splits);

@@ -244,7 +244,8 @@ hipError_t launch_batch_q6k(const void* W, int64_t w_row_bytes, int64_t N, int64
     if (act.m_ld < ((M + mt - 1) / mt) * mt) return hipErrorNotSupported;
     const int nsb = (int)(K / 256);
     const int64_t tiles_n = (N + kNT - 1) / kNT;
-    const SplitPlan sp = plan_split_k(tiles_n, nsb, kWaves, M, N, sc, 0.25);
+    // about 1 us per superblock of a workgroup (4096 x 4096 at M = 64, 128 workgroups: 16.8 us)
+    const SplitPlan sp = plan_split_k(tiles_n, nsb, kWaves, M, N, sc, 1.0);
     float* out = sp.splits > 1 ? sc.p : Y;
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
     dim3 grid((unsigned)tiles_n, 1u, (unsigned)sp.splits);

@@ -290,9 +290,10 @@ hipError_t launch_batch_q8_0(int fmt, const void* W, int64_t w_row_bytes, int64_
     if (act.m_ld < ((M + mt - 1) / mt) * mt) return hipErrorNotSupported;
     const int nch = (int)(K / 256);
     const int64_t tiles_n = (N + kNT - 1) / kNT;
-    // a chunk range per workgroup of at least one chunk per wave; about 0.25 us per chunk of a
-    // workgroup (8 waves, one chunk each, in about 2 us)
-    const SplitPlan sp = plan_split_k(tiles_n, nch, kWaves, M, N, sc, 0.25);
+    // a chunk range per workgroup of at least one chunk per wave; about 1 us per chunk of a
+    // workgroup (4096 x 4096 at M = 64, 128 workgroups of 16 chunks: 17.0 us; with 0.25 us the rule
+    // left that shape and 2048 x 5632 unsplit, 2.4 - 2.9 us slower per step than two ranges)
+    const SplitPlan sp = plan_split_k(tiles_n, nch, kWaves, M, N, sc, 1.0);
     float* out = sp.splits > 1 ? sc.p : Y;
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
     dim3 grid((unsigned)tiles_n, 1u, (unsigned)sp.splits);
