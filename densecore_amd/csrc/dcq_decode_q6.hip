@@ -912,7 +912,17 @@ hipError_t launch_decode_fused_q6k(const void* W, int64_t w_row_bytes, int64_t N
     const int mt = M == 1 ? 1 : 2;
     const int sw = q6_stage_waves(kWaves);
     const int qc = (nsb * mt + 4 * sw - 1) / (4 * sw);
-    const int rpw = kWaves == 4 && nsb <= kSbStep ? q6_rows_per_wave(N, kWaves) : 1;
+    // Rows per wave of the fused 4-wave kernel: every workgroup quantizes the activation again, so
+    // from 6144 rows fewer, longer workgroups win, four rows per wave from 128 k superblocks (per
+    // step, 1 / 2 / 4 rows per wave: 8192 x 2048 6.98 / 6.50 / 7.24 us; 8192 x 4096 9.0 / 9.6 /
+    // 8.6 us; 24576 x 2048 16.9 / 14.9 / 14.2 us; 32000 x 2048 21.3 / 18.0 / 16.7 us; M = 2,
+    // 8192 x 4096 13.9 / 12.5 / 10.9 us; below 6144 rows one row per wave: 2048 x 2048 3.8 / 4.2 /
+    // 6.1 us)
+    int rpw = 1;
+    if (kWaves == 4 && nsb <= kSbStep) {
+        rpw = (int64_t)N * nsb >= 131072 ? 4 : N >= 6144 ? 2 : 1;
+        if (knob(Knob::Q6KRows) >= 1) rpw = q6_rows_per_wave(N, kWaves);
+    }
     const Q6Lds lds(nsb, mt, kWaves, rpw > 1 ? 2 : 1);
     if (lds.total > kMaxLds) return hipErrorNotSupported;
     Q6Fn fn = block_sums ? q6_pick_fused<true>(mt, qc, kWaves) : q6_pick_fused<false>(mt, qc, kWaves);
