@@ -256,8 +256,14 @@ hipError_t launch_batch_q4k(bool q5, const void* W, int64_t w_row_bytes, int64_t
     if (w_row_bytes % 16 || N > (1 << 30) || M > (1 << 30) || K > (1 << 30)) return hipErrorNotSupported;
     // the per-superblock scale DMA reads 64 scales at [s][m0 .. m0 + 63]: m_ld must cover the
     // last m-tile (it is M rounded up to 128)
+    // 64-row m-tiles (two MFMA m-tiles per workgroup) above 32 rows, except where 64-row tiles would
+    // leave CUs idle and 32-row ones give every CU at most one workgroup (4096 x 4096 at M = 64: 128
+    // workgroups with split K 13.2 us, 256 of 32 rows 10.7 us; but 6144 x 4096: 192 workgroups
+    // 13.5 us against 384 of 32 rows 15.7 us)
     const int forced = knob(Knob::BatchTile);
-    const int mti = forced == 1 || forced == 2 ? forced : M <= 32 ? 1 : 2, kMT = 32 * mti;
+    const int64_t n_tiles = (N + kNT - 1) / kNT;
+    const bool fill32 = n_tiles * ((M + 63) / 64) < cu_count() && n_tiles * ((M + 31) / 32) <= cu_count();
+    const int mti = forced == 1 || forced == 2 ? forced : M <= 32 || fill32 ? 1 : 2, kMT = 32 * mti;
     if (act.m_ld < ((M + kMT - 1) / kMT) * kMT) return hipErrorNotSupported;
     const int nsb = (int)(K / 256);
     const int64_t tiles = ((N + kNT - 1) / kNT) * ((M + kMT - 1) / kMT);
