@@ -240,15 +240,26 @@ hipError_t launch_batch_q6k(const void* W, int64_t w_row_bytes, int64_t N, int64
     if (K % 512 || w_row_bytes % 4 || w_row_bytes < K / 256 * 210 || (uintptr_t)W % 16 || M > 64 || M < 1 ||
         N > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
-    const int mti = M <= 32 ? 1 : 2, mt = 32 * mti;
+    // 64-row m-tiles above 32 rows, except where 32-row tiles give every CU at most one workgroup,
+    // 64-row ones would leave CUs idle, and the 32-row tiles would not need split K themselves (each
+    // m-tile reads the weights again, which a split does not make up for at these weights' 0.8-1.1
+    // bytes per element: 2048 x 8192 Q8_0 at M = 64 17.4 -> 18.5 us). 4096 x 4096 at M = 64: Q6_K
+    // 17.3 -> 13.3 us, Q8_0 16.8 -> 16.2 us; 3072 x 3072 Q8_0 15.6 -> 12.3 us; M = 48 2048 x 2048
+    // Q6_K 12.9 -> 9.0 us.
+    const int64_t n_tiles = (N + kNT - 1) / kNT;
+    const int64_t t32 = n_tiles * ((M + 31) / 32);
+    const bool fill32 = n_tiles * ((M + 63) / 64) < cu_count() && t32 <= cu_count() &&
+                        (2 * t32 > cu_count() || K / 256 < 2 * kWaves);
+    const int mti = M <= 32 || fill32 ? 1 : 2, mt = 32 * mti;
+    const int m_tiles = (int)((M + mt - 1) / mt);
     if (act.m_ld < ((M + mt - 1) / mt) * mt) return hipErrorNotSupported;
     const int nsb = (int)(K / 256);
     const int64_t tiles_n = (N + kNT - 1) / kNT;
     // about 1 us per superblock of a workgroup (4096 x 4096 at M = 64, 128 workgroups: 16.8 us)
-    const SplitPlan sp = plan_split_k(tiles_n, nsb, kWaves, M, N, sc, 1.0);
+    const SplitPlan sp = plan_split_k(tiles_n * m_tiles, nsb, kWaves, M, N, sc, 1.0);
     float* out = sp.splits > 1 ? sc.p : Y;
     const int64_t out_stride = sp.splits > 1 ? N : y_stride;
-    dim3 grid((unsigned)tiles_n, 1u, (unsigned)sp.splits);
+    dim3 grid((unsigned)tiles_n, (unsigned)m_tiles, (unsigned)sp.splits);
     const size_t lds = (size_t)kWaves * (mti == 1 ? Geo<1>::kRegion : Geo<2>::kRegion);
     auto fn = mti == 1 ? (block_sums ? batch_q6k_kernel<1, true> : batch_q6k_kernel<1, false>)
                        : (block_sums ? batch_q6k_kernel<2, true> : batch_q6k_kernel<2, false>);
