@@ -39,13 +39,22 @@ size_t split_tail_bytes(int64_t M) { return M > 4 ? (size_t)(M < 128 ? M : 128) 
 
 // Activation rows up to which the decode (GEMV) kernels serve a product. Past four rows their
 // per-row VALU work falls behind the batch MFMA kernels (8192 x 2048 at M = 8: Q8_0 23.3 ->
-// 11.5 us, Q4_K 10.8 -> 9.4 us, Q6_K 17.7 -> 9.5 us). The Q6_K batch kernel already wins at three
-// rows on wide matrices (8192 x 2048: 12.1 -> 9.4 us) but not on narrow ones (2048 x 8192: 10.0
-// against 18.7 us unsplit); tall Q6_K matrices (LM heads, 32768+ rows) keep their MFMA decode
-// kernel up to eight rows (151936 x 2560 at M = 4: 68 us against 120 us on the batch kernel).
-int gemv_rows(int wtype, int64_t N) {
-    if (wtype != kTypeQ6_K) return 4;
-    return N >= 32768 ? 8 : N >= 4096 ? 2 : 4;
+// 11.5 us, Q4_K 10.8 -> 9.4 us, Q6_K 17.7 -> 9.5 us). At three and four rows (steps, GEMV against
+// batch kernel, one box): Q6_K keeps the GEMV from 10 to 16 superblocks per row and below 4096
+// rows (4096 x 4096 9.6 against 12.7 us, 8192 x 4096 13.9 against 14.5 us, 2560 x 9728 21.1 against
+// 22.1 us) and takes the batch kernel elsewhere (8192 x 2048 12.1 against 9.7 us, 5120 x 5120 14.8
+// against 14.0 us, 4096 x 14336 33.6 against 28.4 us); Q4_0 keeps the GEMV up to K = 2048 (8192 x
+// 2048 7.5 against 9.5 us) but not beyond (9728 x 2560 20.6 against 11.9 us). Tall Q6_K matrices
+// (LM heads, 32768+ rows) keep their MFMA decode kernel up to eight rows (151936 x 2560 at M = 4:
+// 68 us against 120 us on the batch kernel).
+int gemv_rows(int wtype, int64_t N, int64_t K) {
+    if (wtype == kTypeQ6_K) {
+        if (N >= 32768) return 8;
+        const int64_t nsb = K / 256;
+        return N < 4096 || (nsb >= 10 && nsb <= 16) ? 4 : 2;
+    }
+    if (wtype == kTypeQ4_0) return K <= 2048 ? 4 : 2;
+    return 4;
 }
 
 // the bytes of a workspace past its first `used` ones, as split-K scratch (none if too small)
@@ -271,7 +280,7 @@ int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_
     rc = check_device();
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
-    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N));
+    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N, K));
     if (use_gemv) {
         // decode: the activation quantization runs inside the GEMV kernel where it can
         hipError_t e = launch_decode_fused(wtype, W, (int64_t)w_row_bytes, N, K, X, (int64_t)(x_stride_bytes / 4), M,
@@ -358,7 +367,7 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4), r_stride = (int64_t)(r_stride_bytes / 4);
-    if (M <= gemv_rows(wtype, N)) {
+    if (M <= gemv_rows(wtype, N, K)) {
         // decode: the add is the fused kernel's store epilogue
         hipError_t e = launch_decode_fused(wtype, W, (int64_t)w_row_bytes, N, K, X, (int64_t)(x_stride_bytes / 4), M,
                                            Y, y_stride, nullptr, st, R, r_stride);
@@ -378,14 +387,14 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
     const SplitScratch sc = tail_of(ws, workspace ? workspace_bytes : need, act_bytes + (size_t)M * N * 4);
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
     bool added = false;
-    if (e == hipSuccess && M <= gemv_rows(wtype, N)) {
+    if (e == hipSuccess && M <= gemv_rows(wtype, N, K)) {
         // the LDS-staged decode kernels add R in their store
         e = launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st, R, r_stride);
         added = e != hipErrorNotSupported;
         if (!added) e = hipSuccess;
     }
     if (e == hipSuccess && !added) {
-        e = M <= gemv_rows(wtype, N)
+        e = M <= gemv_rows(wtype, N, K)
                 ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, T, t_stride, nullptr, N, st)
                 : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, T, t_stride, nullptr, st, sc);
         if (e == hipSuccess) e = launch_add_rows(Y, y_stride, T, t_stride, R, r_stride, M, N, st);
@@ -420,7 +429,7 @@ int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
-    if (M <= gemv_rows(wtype, N)) {
+    if (M <= gemv_rows(wtype, N, K)) {
         // one launch: both weight rows per lane group, the activation quantized in the workgroup
         hipError_t e = launch_decode_fused_glu(wtype, Wg, Wu, (int64_t)w_row_bytes, N, K, X,
                                                (int64_t)(x_stride_bytes / 4), M, Y, y_stride, st);
@@ -437,7 +446,7 @@ int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_
     // split-K partial sums after U (the two products run one after the other on the stream)
     const SplitScratch sc = tail_of(ws, workspace ? workspace_bytes : need, act_bytes + (size_t)M * N * 4);
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
-    const bool use_gemv = M <= gemv_rows(wtype, N);
+    const bool use_gemv = M <= gemv_rows(wtype, N, K);
     if (e == hipSuccess)
         e = use_gemv ? launch_gemv(wtype, Wg, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
                      : launch_mmq(wtype, Wg, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st, sc);
@@ -486,7 +495,7 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
     planar_bytes(vdt, M, K, &pb, (void*)workspace);
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
-    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N));
+    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N, K));
     // The workspace is read-only here: products that share one quantization may run on different
     // streams. So there is no split-K room (it would be written): the MFMA kernels run unsplit,
     // with the same result bits as dcq_mul_mat given an activation-only workspace.

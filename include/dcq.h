@@ -171,10 +171,13 @@ int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w
                         int64_t M, size_t x_stride_bytes, float* Y, size_t y_stride_bytes, void* stream);
 
 /* Activation rows up to which dcq_mul_mat's automatic path (and dcq_mul_mat_add and
- * dcq_ffn_gate_up) takes the decode GEMV kernels: 4 in general; for Q6_K weights 2 when
- * N >= 4096 and 8 when N >= 32768 (LM heads). Larger M goes to the batched and prefill MFMA
- * kernels. */
-#define DCQ_DECODE_ROWS(wtype, N) ((wtype) != DCQ_TYPE_Q6_K ? 4 : (N) >= 32768 ? 8 : (N) >= 4096 ? 2 : 4)
+ * dcq_ffn_gate_up) takes the decode GEMV kernels: 4 in general; for Q6_K weights 8 when
+ * N >= 32768 (LM heads), else 4 when N < 4096 or K/256 is 10..16, else 2; for Q4_0 weights 4 when
+ * K <= 2048, else 2. Larger M goes to the batched and prefill MFMA kernels. */
+#define DCQ_DECODE_ROWS(wtype, N, K)                                                               \
+    ((wtype) == DCQ_TYPE_Q6_K                                                                      \
+         ? ((N) >= 32768 ? 8 : ((N) < 4096 || ((K) / 256 >= 10 && (K) / 256 <= 16)) ? 4 : 2)       \
+         : (wtype) == DCQ_TYPE_Q4_0 ? ((K) <= 2048 ? 4 : 2) : 4)
 
 /* ---- a projection and its residual or bias ----
  * Y[m][n] = (sum_k W[n][k] x[m][k]) + R[m][n], one fp32 add per element after dcq_mul_mat's
