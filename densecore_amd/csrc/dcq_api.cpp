@@ -47,12 +47,22 @@ size_t split_tail_bytes(int64_t M) { return M > 4 ? (size_t)(M < 128 ? M : 128) 
 // 2048 7.5 against 9.5 us) but not beyond (9728 x 2560 20.6 against 11.9 us). Tall Q6_K matrices
 // (LM heads, 32768+ rows) keep their MFMA decode kernel up to eight rows (151936 x 2560 at M = 4:
 // 68 us against 120 us on the batch kernel).
-int gemv_rows(int wtype, int64_t N, int64_t K) {
+// fused: the activation quantization runs inside the GEMV kernel (the small-matrix extension to
+// eight rows pays only there: on a pre-quantized activation, Q8_0 M = 5 3072 x 1024 took 8.2 us on
+// the GEMV against 5.3 us on the batch kernel)
+int gemv_rows(int wtype, int64_t N, int64_t K, bool fused) {
     if (wtype == kTypeQ6_K) {
         if (N >= 32768) return 8;
         const int64_t nsb = K / 256;
         return N < 4096 || (nsb >= 10 && nsb <= 16) ? 4 : 2;
     }
+    // small matrices keep the GEMV up to eight rows, where the batch kernel has few tiles and too
+    // little K to split (M = 5-8: Q8_0 3072 x 1024 4.6 against 7.6 us, Q4_K 2048 x 2048 5.1-5.4
+    // against 6.7 us; not Q8_0 at K = 2048: 2048 x 2048 11.2 against 10.1 us)
+    // (row-split Q8_0 rows as their Q8_0 originals, so both give the same bits)
+    if (fused && (((wtype == kTypeQ8_0 || wtype == kTypeQ8_0_RS || wtype == kTypeQ4_0) && K <= 1024 && N <= 4096) ||
+                  ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && N * K <= (int64_t)2048 * 2048)))
+        return 8;
     if (wtype == kTypeQ4_0) return K <= 2048 ? 4 : 2;
     return 4;
 }
@@ -280,8 +290,8 @@ int dcq_mul_mat_ex(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_
     rc = check_device();
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
-    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N, K));
-    if (use_gemv) {
+    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N, K, false));
+    if (path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N, K, true))) {
         // decode: the activation quantization runs inside the GEMV kernel where it can
         hipError_t e = launch_decode_fused(wtype, W, (int64_t)w_row_bytes, N, K, X, (int64_t)(x_stride_bytes / 4), M,
                                            Y, (int64_t)(y_stride_bytes / 4), block_sums, st);
@@ -367,7 +377,7 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4), r_stride = (int64_t)(r_stride_bytes / 4);
-    if (M <= gemv_rows(wtype, N, K)) {
+    if (M <= gemv_rows(wtype, N, K, true)) {
         // decode: the add is the fused kernel's store epilogue
         hipError_t e = launch_decode_fused(wtype, W, (int64_t)w_row_bytes, N, K, X, (int64_t)(x_stride_bytes / 4), M,
                                            Y, y_stride, nullptr, st, R, r_stride);
@@ -387,14 +397,14 @@ int dcq_mul_mat_add(int wtype, const void* W, int64_t N, int64_t K, size_t w_row
     const SplitScratch sc = tail_of(ws, workspace ? workspace_bytes : need, act_bytes + (size_t)M * N * 4);
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
     bool added = false;
-    if (e == hipSuccess && M <= gemv_rows(wtype, N, K)) {
+    if (e == hipSuccess && M <= gemv_rows(wtype, N, K, false)) {
         // the LDS-staged decode kernels add R in their store
         e = launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st, R, r_stride);
         added = e != hipErrorNotSupported;
         if (!added) e = hipSuccess;
     }
     if (e == hipSuccess && !added) {
-        e = M <= gemv_rows(wtype, N, K)
+        e = M <= gemv_rows(wtype, N, K, false)
                 ? launch_gemv(wtype, W, (int64_t)w_row_bytes, 0, N, K, pb, M, T, t_stride, nullptr, N, st)
                 : launch_mmq(wtype, W, (int64_t)w_row_bytes, N, K, pb, M, T, t_stride, nullptr, st, sc);
         if (e == hipSuccess) e = launch_add_rows(Y, y_stride, T, t_stride, R, r_stride, M, N, st);
@@ -429,7 +439,7 @@ int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
-    if (M <= gemv_rows(wtype, N, K)) {
+    if (M <= gemv_rows(wtype, N, K, true)) {
         // one launch: both weight rows per lane group, the activation quantized in the workgroup
         hipError_t e = launch_decode_fused_glu(wtype, Wg, Wu, (int64_t)w_row_bytes, N, K, X,
                                                (int64_t)(x_stride_bytes / 4), M, Y, y_stride, st);
@@ -446,7 +456,7 @@ int dcq_ffn_gate_up(int wtype, const void* Wg, const void* Wu, int64_t N, int64_
     // split-K partial sums after U (the two products run one after the other on the stream)
     const SplitScratch sc = tail_of(ws, workspace ? workspace_bytes : need, act_bytes + (size_t)M * N * 4);
     hipError_t e = launch_quantize_planar(vdt, X, (int64_t)(x_stride_bytes / 4), M, K, pb, st);
-    const bool use_gemv = M <= gemv_rows(wtype, N, K);
+    const bool use_gemv = M <= gemv_rows(wtype, N, K, false);
     if (e == hipSuccess)
         e = use_gemv ? launch_gemv(wtype, Wg, (int64_t)w_row_bytes, 0, N, K, pb, M, Y, y_stride, nullptr, N, st)
                      : launch_mmq(wtype, Wg, (int64_t)w_row_bytes, N, K, pb, M, Y, y_stride, nullptr, st, sc);
@@ -495,7 +505,7 @@ int dcq_mul_mat_q(int wtype, const void* W, int64_t N, int64_t K, size_t w_row_b
     planar_bytes(vdt, M, K, &pb, (void*)workspace);
     hipStream_t st = (hipStream_t)stream;
     const int64_t y_stride = (int64_t)(y_stride_bytes / 4);
-    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N, K));
+    const bool use_gemv = path == DCQ_PATH_GEMV || (path == DCQ_PATH_AUTO && M <= gemv_rows(wtype, N, K, false));
     // The workspace is read-only here: products that share one quantization may run on different
     // streams. So there is no split-K room (it would be written): the MFMA kernels run unsplit,
     // with the same result bits as dcq_mul_mat given an activation-only workspace.
