@@ -635,12 +635,19 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
         const hipError_t e = launch_prefill_q6_k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
-    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && M > 128) {
+    // Q4_K / Q5_K: the batch kernel (64-row m-tiles) up to 256 rows, and up to 512 while the
+    // prefill kernel's 128 x 128 tiles would not give every CU one (steps: 192 x 8192 x 2048 19.9
+    // against 27.8 us on the prefill kernel, 512 x 2048 x 8192 37.5 against 47.4 us, 384 x 8192 x
+    // 2048 36.5 against 39.1 us; but 512 x 8192 x 2048, 256 prefill tiles, 46.3 against 40.6 us, and
+    // from 768 rows the prefill kernel)
+    const bool q4_batch =
+        M <= 256 || (M <= 512 && ((M + 127) / 128) * ((N + 127) / 128) < (int64_t)cu_count());
+    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && !q4_batch) {
         const hipError_t e = launch_prefill_q4_k(wtype == kTypeQ5_K, W, w_row_bytes, N, K, act, M, Y, y_stride,
                                                  block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
-    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && M <= 128) {
+    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && q4_batch) {
         const hipError_t e = launch_batch_q4k(wtype == kTypeQ5_K, W, w_row_bytes, N, K, act, M, Y, y_stride,
                                               block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;

@@ -170,6 +170,9 @@ CASES = [
     (Q4_0, 40, 100, 512), (Q4_0, 130, 257, 256), (Q4_0, 256, 384, 1024), (Q4_0, 1, 9728, 2560),
     (Q5_K, 1, 97, 2560), (Q5_K, 2, 64, 256), (Q5_K, 5, 40, 512), (Q5_K, 64, 96, 2048), (Q5_K, 70, 33, 768),
     (Q5_K, 256, 384, 1024), (Q5_K, 1, 9728, 2560), (Q5_K, 3, 2560, 9728),
+    # the Q4_K / Q5_K batch kernel past 256 rows while the prefill tiles would not fill the CUs
+    # (eight 64-row m-tiles, ragged last one), and the prefill kernel from 512 rows over 256+ tiles
+    (Q4_K, 500, 320, 1024), (Q5_K, 384, 200, 512), (Q4_K, 512, 8192, 256),
 ]
 
 
