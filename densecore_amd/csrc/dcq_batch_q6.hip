@@ -237,7 +237,7 @@ hipError_t launch_batch_q6k(const void* W, int64_t w_row_bytes, int64_t N, int64
                             const SplitScratch& sc) {
     // K % 512: an even superblock count, so the dword reads past an even superblock's byte 209 stay
     // inside the next one
-    if (K % 512 || w_row_bytes % 4 || w_row_bytes < K / 256 * 210 || (uintptr_t)W % 16 || M > 64 || M < 1 ||
+    if (K % 512 || w_row_bytes % 4 || w_row_bytes < K / 256 * 210 || (uintptr_t)W % 16 || M < 1 ||
         N > (1 << 30) || K > (1 << 30))
         return hipErrorNotSupported;
     // 64-row m-tiles above 32 rows, except where 32-row tiles give every CU at most one workgroup,

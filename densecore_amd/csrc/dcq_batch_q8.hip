@@ -282,7 +282,7 @@ hipError_t launch_batch_q8_0(int fmt, const void* W, int64_t w_row_bytes, int64_
                              const PlanarBuffers& act, int64_t M, float* Y, int64_t y_stride, int32_t* block_sums,
                              hipStream_t st, const SplitScratch& sc) {
     const bool q40 = fmt == kFmtQ4_0;
-    if (K % 256 || w_row_bytes % 4 || w_row_bytes < K / 32 * (q40 ? 18 : 34) || (uintptr_t)W % 16 || M > 64 || M < 1 ||
+    if (K % 256 || w_row_bytes % 4 || w_row_bytes < K / 32 * (q40 ? 18 : 34) || (uintptr_t)W % 16 || M < 1 ||
         N > (1 << 30) || K > (1 << 30) || (fmt == kFmtQ8_0RS && w_row_bytes % 16))
         return hipErrorNotSupported;
     // 64-row m-tiles above 32 rows, except where 32-row tiles give every CU at most one workgroup,

@@ -602,9 +602,16 @@ static MmqFn pick(int wtype, const MmqShape& s) {
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                       int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
                       const SplitScratch& sc) {
+    // Q8_0 / Q4_0 / Q6_K past 64 rows: the batch kernel up to 128 rows where its tiles give every CU
+    // at most one workgroup and K <= 4096, else the 128 x 128-tile kernels (steps at 80 and 128
+    // rows: batch kernel faster on all 14 such shapes, 2048 x 2048 Q6_K 16.1 -> 9.1 us, 4096 x 2048
+    // Q8_0 22.7 -> 13.8 us; slower past one workgroup per CU, 6144 x 4096 25.5 -> 33.3 us, and at
+    // K >= 8192 from 128 rows)
+    const bool batch_past_64 =
+        M <= 128 && K <= 4096 && ((N + 31) / 32) * ((M + 63) / 64) <= (int64_t)cu_count();
     // row-split Q8_0: the batched and the 128 x 128-tile kernels (no generic MMQ form)
     if (wtype == kTypeQ8_0_RS) {
-        if (M <= 64) {
+        if (M <= 64 || batch_past_64) {
             const hipError_t e = launch_batch_q8_0(kFmtQ8_0RS, W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums,
                                                    st, sc);
             if (e != hipErrorNotSupported) return e;
@@ -612,11 +619,11 @@ hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, 
         return launch_prefill_q8_0(kFmtQ8_0RS, W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
     }
     const bool q8 = wtype == kTypeQ8_0 || wtype == kTypeQ4_0;  // Q8_0-block kernels
-    if (q8 && M <= 64) {
+    if (q8 && (M <= 64 || batch_past_64)) {
         const hipError_t e = launch_batch_q8_0(q8_fmt(wtype), W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
-    if (wtype == kTypeQ6_K && M <= 64) {
+    if (wtype == kTypeQ6_K && (M <= 64 || batch_past_64)) {
         const hipError_t e = launch_batch_q6k(W, w_row_bytes, N, K, act, M, Y, y_stride, block_sums, st, sc);
         if (e != hipErrorNotSupported) return e;
     }
