@@ -602,13 +602,13 @@ static MmqFn pick(int wtype, const MmqShape& s) {
 hipError_t launch_mmq(int wtype, const void* W, int64_t w_row_bytes, int64_t N, int64_t K, const PlanarBuffers& act,
                       int64_t M, float* Y, int64_t y_stride, int32_t* block_sums, hipStream_t st,
                       const SplitScratch& sc) {
-    // Q8_0 / Q4_0 / Q6_K past 64 rows: the batch kernel up to 128 rows where its tiles give every CU
-    // at most one workgroup and K <= 4096, else the 128 x 128-tile kernels (steps at 80 and 128
-    // rows: batch kernel faster on all 14 such shapes, 2048 x 2048 Q6_K 16.1 -> 9.1 us, 4096 x 2048
-    // Q8_0 22.7 -> 13.8 us; slower past one workgroup per CU, 6144 x 4096 25.5 -> 33.3 us, and at
-    // K >= 8192 from 128 rows)
+    // Q8_0 / Q4_0 / Q6_K past 64 rows: the batch kernel up to 256 rows where its tiles give every CU
+    // at most one workgroup and K <= 4096, else the 128 x 128-tile kernels (steps at 80 to 256 rows:
+    // batch kernel faster on all 26 such shapes, 2048 x 2048 Q6_K at 128 rows 16.1 -> 9.1 us, Q8_0
+    // at 256 rows 22.1 -> 13.9 us; slower past one workgroup per CU, 6144 x 4096 at 128 rows
+    // 25.5 -> 33.3 us, and at K >= 8192 from 128 rows)
     const bool batch_past_64 =
-        M <= 128 && K <= 4096 && ((N + 31) / 32) * ((M + 63) / 64) <= (int64_t)cu_count();
+        M <= 256 && K <= 4096 && ((N + 31) / 32) * ((M + 63) / 64) <= (int64_t)cu_count();
     // row-split Q8_0: the batched and the 128 x 128-tile kernels (no generic MMQ form)
     if (wtype == kTypeQ8_0_RS) {
         if (M <= 64 || batch_past_64) {
