@@ -830,6 +830,10 @@ hipError_t launch_tall_q6k(const void* W, int64_t w_row_bytes, int64_t n0, int64
 // and the activation tile within the LDS left by the weight buffers.
 bool q6_use_mfma(int64_t rows, int nsb, int64_t M) {
     if (rows < kTallMinRows || nsb % 2 != 0 || knob(Knob::Q6KMfma) == 0) return false;
+    // one activation row up to 16 superblocks: the fused LDS kernel (four rows per wave) stays
+    // faster below 65536 rows (49152 x 4096: 36.8 against 40.8 us per step; 32768 x 4096 26.0
+    // against 26.7 us), the MFMA kernel from there (65536 x 2048: 27.6 against 30.6 us)
+    if (M == 1 && nsb <= kSbStep && rows < 65536) return false;
     const int mt = M == 1 ? 1 : M == 2 ? 2 : M <= 4 ? 4 : 8;
     return tall_lds_bytes(mt, nsb, false) <= kMaxLds;
 }

@@ -592,8 +592,9 @@ def test_lm_head_parity(O, dev, wt, K, M):
 # the rows per workgroup (tails of every length), the fused kernel (M <= 2) and the one over a
 # quantized activation (M = 3, M = 9: two tiles of rows), block sums and the residual add. The
 # MFMA kernel for tall matrices splits each 32-row tile into two halves of its superblocks, summed
-# in LDS, when the tiles are fewer than its waves (40001 and 40003 rows: 1251 tiles for 2048
-# waves); 70001+ rows keep whole tiles.
+# in LDS, when the tiles are fewer than its waves (40003 rows at M = 9: 1251 tiles for 2048 waves);
+# 70001+ rows keep whole tiles. One activation row over fewer than 65536 rows of up to 16
+# superblocks (40001 x 1024) takes the fused LDS kernel instead.
 TALL_Q6 = [(1, 40001, 1024), (2, 70003, 512), (3, 70001, 1024), (9, 40003, 512), (1, 139999, 1536)]
 
 
