@@ -58,11 +58,17 @@ int gemv_rows(int wtype, int64_t N, int64_t K, bool fused) {
     }
     // small matrices keep the GEMV up to eight rows, where the batch kernel has few tiles and too
     // little K to split (M = 5-8: Q8_0 3072 x 1024 4.6 against 7.6 us, Q4_K 2048 x 2048 5.1-5.4
-    // against 6.7 us; not Q8_0 at K = 2048: 2048 x 2048 11.2 against 10.1 us)
+    // against 6.7 us; not Q8_0 at K = 2048: 2048 x 2048 11.2 against 10.1 us), and Q8_0 rows of
+    // 1024 elements at any height (151936 x 1024 at M = 6: 58.0 against 77.7 us)
     // (row-split Q8_0 rows as their Q8_0 originals, so both give the same bits)
-    if (fused && (((wtype == kTypeQ8_0 || wtype == kTypeQ8_0_RS || wtype == kTypeQ4_0) && K <= 1024 && N <= 4096) ||
+    const bool q8 = wtype == kTypeQ8_0 || wtype == kTypeQ8_0_RS;
+    if (fused && ((q8 && K <= 1024) || (wtype == kTypeQ4_0 && K <= 1024 && N <= 4096) ||
                   ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && N * K <= (int64_t)2048 * 2048)))
         return 8;
+    // Q8_0 rows of 4096+ elements over 4096+ rows: the batch kernel from three rows (M = 3:
+    // 32000 x 4096 86.3 against 47.1 us; M = 4: 4096 x 4096 16.6 against 14.6 us; but 2048 x 8192
+    // 16.0 against 22.1 us on the GEMV)
+    if (q8 && K >= 4096 && N >= 4096) return 2;
     if (wtype == kTypeQ4_0) return K <= 2048 ? 4 : 2;
     return 4;
 }

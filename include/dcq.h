@@ -172,16 +172,18 @@ int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w
 
 /* Activation rows up to which dcq_mul_mat's automatic path (and dcq_mul_mat_add and
  * dcq_ffn_gate_up) takes the decode GEMV kernels: 4 in general; for Q6_K weights 8 when
- * N >= 32768 (LM heads), else 4 when N < 4096 or K/256 is 10..16, else 2; 8 for small matrices
- * (Q8_0, row-split Q8_0 and Q4_0 with K <= 1024 and N <= 4096, Q4_K and Q5_K with
- * N * K <= 2048 * 2048) where the GEMV quantizes the activation itself (dcq_mul_mat_q, on a
- * pre-quantized activation, keeps 4 there); for other Q4_0 weights 4 when K <= 2048, else 2.
- * Larger M goes to the batched and prefill MFMA kernels. */
+ * N >= 32768 (LM heads), else 4 when N < 4096 or K/256 is 10..16, else 2; for Q8_0 and row-split
+ * Q8_0 weights 8 when K <= 1024, 2 when K >= 4096 and N >= 4096; 8 for other small matrices (Q4_0
+ * with K <= 1024 and N <= 4096, Q4_K and Q5_K with N * K <= 2048 * 2048); for other Q4_0 weights 4
+ * when K <= 2048, else 2. The eight-row cases hold where the GEMV quantizes the activation itself
+ * (dcq_mul_mat_q, on a pre-quantized activation, keeps 4 there). Larger M goes to the batched and
+ * prefill MFMA kernels. */
 #define DCQ_DECODE_ROWS(wtype, N, K)                                                                 \
     ((wtype) == DCQ_TYPE_Q6_K                                                                        \
          ? ((N) >= 32768 ? 8 : ((N) < 4096 || ((K) / 256 >= 10 && (K) / 256 <= 16)) ? 4 : 2)         \
-     : (((wtype) == DCQ_TYPE_Q8_0 || (wtype) == DCQ_TYPE_Q8_0_RS || (wtype) == DCQ_TYPE_Q4_0) &&    \
-        (K) <= 1024 && (N) <= 4096) ||                                                               \
+     : ((wtype) == DCQ_TYPE_Q8_0 || (wtype) == DCQ_TYPE_Q8_0_RS)                                     \
+         ? ((K) <= 1024 ? 8 : ((K) >= 4096 && (N) >= 4096) ? 2 : 4)                                  \
+     : ((wtype) == DCQ_TYPE_Q4_0 && (K) <= 1024 && (N) <= 4096) ||                                   \
              (((wtype) == DCQ_TYPE_Q4_K || (wtype) == DCQ_TYPE_Q5_K) && (int64_t)(N) * (K) <= 2048 * 2048) \
          ? 8                                                                                         \
      : (wtype) == DCQ_TYPE_Q4_0 ? ((K) <= 2048 ? 4 : 2)                                               \
