@@ -69,6 +69,10 @@ int gemv_rows(int wtype, int64_t N, int64_t K, bool fused) {
     // 32000 x 4096 86.3 against 47.1 us; M = 4: 4096 x 4096 16.6 against 14.6 us; but 2048 x 8192
     // 16.0 against 22.1 us on the GEMV)
     if (q8 && K >= 4096 && N >= 4096) return 2;
+    // Q4_K / Q5_K: likewise for large matrices of 4096+ element rows (M = 3: 14336 x 4096 23.4
+    // against 15.7 us, 4096 x 14336 47.6 against 18.7 us, 8192 x 8192 31.7 against 14.8 us; the
+    // GEMV stays for 9728 x 2560, 4096 x 4096 and 151936 x 1024)
+    if ((wtype == kTypeQ4_K || wtype == kTypeQ5_K) && K >= 4096 && N * K >= ((int64_t)1 << 25)) return 2;
     if (wtype == kTypeQ4_0) return K <= 2048 ? 4 : 2;
     return 4;
 }

@@ -173,7 +173,8 @@ int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w
 /* Activation rows up to which dcq_mul_mat's automatic path (and dcq_mul_mat_add and
  * dcq_ffn_gate_up) takes the decode GEMV kernels: 4 in general; for Q6_K weights 8 when
  * N >= 32768 (LM heads), else 4 when N < 4096 or K/256 is 10..16, else 2; for Q8_0 and row-split
- * Q8_0 weights 8 when K <= 1024, 2 when K >= 4096 and N >= 4096; 8 for other small matrices (Q4_0
+ * Q8_0 weights 8 when K <= 1024, 2 when K >= 4096 and N >= 4096; for Q4_K and Q5_K weights 2 when
+ * K >= 4096 and N * K >= 2^25; 8 for other small matrices (Q4_0
  * with K <= 1024 and N <= 4096, Q4_K and Q5_K with N * K <= 2048 * 2048); for other Q4_0 weights 4
  * when K <= 2048, else 2. The eight-row cases hold where the GEMV quantizes the activation itself
  * (dcq_mul_mat_q, on a pre-quantized activation, keeps 4 there). Larger M goes to the batched and
@@ -187,7 +188,10 @@ int dcq_mul_mat_noalloc(int wtype, const void* W, int64_t N, int64_t K, size_t w
              (((wtype) == DCQ_TYPE_Q4_K || (wtype) == DCQ_TYPE_Q5_K) && (int64_t)(N) * (K) <= 2048 * 2048) \
          ? 8                                                                                         \
      : (wtype) == DCQ_TYPE_Q4_0 ? ((K) <= 2048 ? 4 : 2)                                               \
-                                : 4)
+     : (((wtype) == DCQ_TYPE_Q4_K || (wtype) == DCQ_TYPE_Q5_K) && (K) >= 4096 &&                      \
+        (int64_t)(N) * (K) >= ((int64_t)1 << 25))                                                    \
+         ? 2                                                                                         \
+         : 4)
 
 /* ---- a projection and its residual or bias ----
  * Y[m][n] = (sum_k W[n][k] x[m][k]) + R[m][n], one fp32 add per element after dcq_mul_mat's
